@@ -1,0 +1,309 @@
+/*
+ * tenzor_hip.h — C-ABI of the MI355X (gfx950) backend for tenzor's
+ * lazy elementwise/broadcast/reduce evaluation and the int8-weight
+ * Arctic-embed-xs encoder forward.
+ *
+ * Conventions (mirroring the Zig surfaces this library replaces):
+ *   - Every entry point returns 0 (TZH_OK) on success and a negative status
+ *     on failure; tzh_last_error() returns a thread-local message for the
+ *     last failure.  No C++ exception crosses this boundary.
+ *   - The caller owns output buffers (tensor.zig:129-134 semantics).
+ *   - "device pointer" arguments are HBM addresses (hipMalloc'd, by
+ *     tzh_malloc or by any HIP allocator such as torch's caching allocator on
+ *     the same device).  Host pointers are marked "host".
+ *   - A tzh_ctx enqueues all work asynchronously on one HIP stream chosen
+ *     at tzh_init (NULL = the default stream).  tzh_sync() waits for it.  A context is not
+ *     thread-safe (one per thread), like arctic.InferenceContext
+ *     (arctic.zig:407-482).
+ */
+#ifndef TENZOR_HIP_H
+#define TENZOR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TZH_ABI_VERSION 1
+#define TZH_MAX_RANK 8 /* shape.zig:10 MAX_RANK */
+
+/* ------------------------------------------------------------------ */
+/* Status codes.  The Zig error names they stand for are cited.        */
+/* ------------------------------------------------------------------ */
+enum {
+    TZH_OK = 0,
+    TZH_ERR_INVALID_ARGS = -1,      /* std.debug.assert preconditions, e.g. matmul_w8a32.zig:24-29 */
+    TZH_ERR_OUT_OF_MEMORY = -2,     /* error.OutOfMemory */
+    TZH_ERR_DEVICE = -3,            /* HIP runtime failure */
+    TZH_ERR_MISSING_WEIGHT = -4,    /* error.MissingWeight, arctic.zig:194-197 */
+    TZH_ERR_WRONG_DTYPE = -5,       /* error.WrongDtype, arctic.zig:198-201 */
+    TZH_ERR_UNSUPPORTED_DTYPE = -6, /* error.UnsupportedDtype, arctic.zig:282-285 */
+    TZH_ERR_INVALID_FORMAT = -7,    /* error.InvalidFormat, safetensors.zig:173-180 */
+    TZH_ERR_IO = -8,                /* file system errors */
+    TZH_ERR_UNSUPPORTED_OP = -9,    /* @compileError("Unsupported ... operation"), elementwise.zig:143,191 */
+    TZH_ERR_SHAPE = -10,            /* "Shapes not broadcast compatible", expr.zig:366-375 */
+    TZH_ERR_TOO_LARGE = -11         /* input beyond a documented size limit */
+};
+
+/* Element types; numbering follows safetensors DType order (safetensors.zig:13-26). */
+enum {
+    TZH_F16 = 0, TZH_BF16 = 1, TZH_F32 = 2, TZH_F64 = 3,
+    TZH_I8 = 4, TZH_I16 = 5, TZH_I32 = 6, TZH_I64 = 7,
+    TZH_U8 = 8, TZH_U16 = 9, TZH_U32 = 10, TZH_U64 = 11, TZH_BOOL = 12
+};
+
+/* Operation tags; numbering is the ordinal of ops.OpTag (expr.zig:19-91),
+ * so a Zig caller passes @intFromEnum(Expr.operation) unchanged. */
+enum {
+    TZH_OP_NEG = 0, TZH_OP_ABS = 1, TZH_OP_EXP = 2, TZH_OP_EXP2 = 3, TZH_OP_LOG = 4,
+    TZH_OP_LOG2 = 5, TZH_OP_LOG10 = 6, TZH_OP_SQRT = 7, TZH_OP_RSQRT = 8, TZH_OP_SIN = 9,
+    TZH_OP_COS = 10, TZH_OP_TAN = 11, TZH_OP_TANH = 12, TZH_OP_SINH = 13, TZH_OP_COSH = 14,
+    TZH_OP_ASIN = 15, TZH_OP_ACOS = 16, TZH_OP_ATAN = 17, TZH_OP_SIGMOID = 18, TZH_OP_RELU = 19,
+    TZH_OP_LEAKY_RELU = 20, TZH_OP_GELU = 21, TZH_OP_SILU = 22, TZH_OP_SOFTPLUS = 23,
+    TZH_OP_CEIL = 24, TZH_OP_FLOOR = 25, TZH_OP_ROUND = 26, TZH_OP_SIGN = 27,
+    TZH_OP_ADD = 28, TZH_OP_SUB = 29, TZH_OP_MUL = 30, TZH_OP_DIV = 31, TZH_OP_POW = 32,
+    TZH_OP_MAX = 33, TZH_OP_MIN = 34, TZH_OP_MOD = 35, TZH_OP_ATAN2 = 36,
+    TZH_OP_EQ = 37, TZH_OP_NE = 38, TZH_OP_LT = 39, TZH_OP_LE = 40, TZH_OP_GT = 41, TZH_OP_GE = 42,
+    TZH_OP_MATMUL = 43, TZH_OP_TRANSPOSE = 44,
+    TZH_OP_SUM = 45, TZH_OP_PROD = 46, TZH_OP_REDUCE_MAX = 47, TZH_OP_REDUCE_MIN = 48,
+    TZH_OP_MEAN = 49, TZH_OP_VARIANCE = 50
+};
+
+/* Node kinds; numbering is the ordinal of ops.NodeKind (expr.zig:137-149). */
+enum {
+    TZH_NODE_TENSOR = 0, TZH_NODE_CONSTANT = 1, TZH_NODE_UNARY = 2, TZH_NODE_BINARY = 3,
+    TZH_NODE_MATMUL = 4, TZH_NODE_REDUCE = 5, TZH_NODE_RESHAPE = 6, TZH_NODE_TRANSPOSE = 7,
+    TZH_NODE_SOFTMAX = 8, TZH_NODE_LAYERNORM = 9, TZH_NODE_GATHER = 10
+};
+
+/* ------------------------------------------------------------------ */
+/* Errors, version, context, memory                                    */
+/* ------------------------------------------------------------------ */
+const char *tzh_last_error(void);
+int tzh_abi_version(void);
+
+typedef struct tzh_ctx tzh_ctx;
+
+/* Create a context on `device`.  `stream` is the hipStream_t to enqueue on;
+ * NULL is the device's default stream (the caller keeps ownership).
+ * Replaces InferenceContext.init/initWithPool (arctic.zig:436-465) and the
+ * allocator argument of executor.eval/evalInto (executor.zig:29-54). */
+int tzh_init(int device, void *stream, tzh_ctx **out);
+int tzh_destroy(tzh_ctx *ctx);
+int tzh_sync(tzh_ctx *ctx);
+void *tzh_stream(tzh_ctx *ctx);
+
+int tzh_malloc(tzh_ctx *ctx, size_t bytes, void **dptr);
+int tzh_free(tzh_ctx *ctx, void *dptr);
+int tzh_memcpy_h2d(tzh_ctx *ctx, void *dst_device, const void *src_host, size_t bytes);
+int tzh_memcpy_d2h(tzh_ctx *ctx, void *dst_host, const void *src_device, size_t bytes);
+
+/* ------------------------------------------------------------------ */
+/* Lazy expression evaluation (replaces executor.eval/evalInto,        */
+/* executor.zig:29-93, for NodeKind tensor/constant/unary/binary/reduce)*/
+/* ------------------------------------------------------------------ */
+
+/* One node of an expression DAG in post-order (children before parents,
+ * root last).  This is what a comptime walk over an Expr type emits. */
+typedef struct {
+    int32_t kind;     /* TZH_NODE_* */
+    int32_t op;       /* TZH_OP_* for unary / binary / reduce */
+    int32_t lhs;      /* index of the input (unary/reduce) or left operand node */
+    int32_t rhs;      /* index of the right operand node (binary), else -1 */
+    int32_t leaf;     /* TZH_NODE_TENSOR: index into the leaves array */
+    int32_t axis;     /* TZH_NODE_REDUCE: reduced axis, or -1 for all axes (ReduceExpr .{}) */
+    int32_t keepdims; /* TZH_NODE_REDUCE: keep_dims */
+    int32_t ndim;     /* rank of this node's result */
+    int64_t shape[TZH_MAX_RANK]; /* result shape (expr.zig ShapeOf) */
+    double value;     /* TZH_NODE_CONSTANT: ScalarExpr.value (converted to dtype) */
+} tzh_node;
+
+/* A leaf tensor: contiguous row-major device data (Tensor.data, tensor.zig:28-60). */
+typedef struct {
+    const void *data; /* device pointer */
+    int32_t ndim;
+    int32_t pad_;
+    int64_t shape[TZH_MAX_RANK];
+} tzh_leaf;
+
+/* Evaluate the DAG rooted at tape[n_nodes-1] into `out` (device, numel of
+ * the root shape elements of `dtype`).  dtype is TZH_F32 or TZH_F64 (the
+ * element type shared by every node, expr.zig:358-364).  Elementwise chains
+ * are evaluated in a single pass without temporaries; a reduce node fuses
+ * the chain below it into its reduction.  Broadcasting follows NumPy rules
+ * (shape.zig:168-204, strides.zig:92-121). */
+int tzh_eval_into(tzh_ctx *ctx, const tzh_node *tape, int32_t n_nodes,
+                  const tzh_leaf *leaves, int32_t n_leaves, int32_t dtype, void *out);
+
+/* ------------------------------------------------------------------ */
+/* Kernel-level entry points                                           */
+/* ------------------------------------------------------------------ */
+
+/* c[i,j] = (sum_k a[i,k]*f32(wq[j,k])) * f32(scale[j]) + bias[j]
+ * Replaces matmulTransposeB_f32_i8_rowScale_bias (matmul_w8a32.zig:14-57).
+ * a f32 [m,k], wq i8 [n,k] row-major, scale f16 bits [n], bias f32 [n] (may be
+ * NULL = zeros), c f32 [m,n]; all device pointers.  k must be a multiple of 32. */
+int tzh_matmul_w8a32(tzh_ctx *ctx, const float *a, const int8_t *wq, const uint16_t *scale,
+                     const float *bias, float *c, int64_t m, int64_t k, int64_t n);
+
+/* Epilogues for tzh_linear_w8. */
+enum {
+    TZH_EPI_BIAS = 0,          /* y = acc*s + b                         (arctic.zig:622-633) */
+    TZH_EPI_BIAS_GELU = 1,     /* y = gelu(acc*s + b)                   (arctic.zig:771-776) */
+    TZH_EPI_BIAS_RES_LN = 2    /* y = LN(res + (acc*s + b)), N == 384   (arctic.zig:716-746, 779-809) */
+};
+
+/* General int8-weight linear with fused epilogue.  a_dtype and c_dtype are
+ * TZH_F32 or TZH_F16; residual (EPI_BIAS_RES_LN only) has res_dtype
+ * TZH_F32 or TZH_F16 and shape [m,n]; gamma/beta f32 [n].
+ * Activations are rounded to f16 for the MFMA; accumulation is f32. */
+int tzh_linear_w8(tzh_ctx *ctx, const void *a, int32_t a_dtype, const int8_t *wq,
+                  const uint16_t *scale, const float *bias, void *c, int32_t c_dtype,
+                  int64_t m, int64_t k, int64_t n, int32_t epilogue,
+                  const void *residual, int32_t res_dtype, const float *gamma,
+                  const float *beta, float eps);
+
+/* y = ((x-mean)*inv_std)*gamma + beta over the last dim, two-pass mean /
+ * biased variance, inv_std = 1/sqrt(var+eps).  Replaces layerNormLastDim
+ * (layernorm.zig:26-117).  x, y f32 [rows, n] (may alias). */
+int tzh_layernorm_last_dim(tzh_ctx *ctx, const float *x, const float *gamma, const float *beta,
+                           float *y, int64_t rows, int64_t n, float eps);
+
+/* Multi-head self-attention core of selfAttention (arctic.zig:660-713) over
+ * packed variable-length sequences: for every sequence b (tokens
+ * cu_seqlens[b] .. cu_seqlens[b+1]) and head h, softmax(Q_h K_h^T /
+ * sqrt(32)) V_h.  qkv: device f16 [T, 3*hidden] (Q | K | V columns), out:
+ * device f16 [T, hidden], cu_seqlens: device int32 [batch+1].  head_dim must
+ * be 32 and sequences at most 512 tokens. */
+int tzh_attention_varlen(tzh_ctx *ctx, const uint16_t *qkv, uint16_t *out, const int32_t *cu_seqlens,
+                         int32_t batch, int32_t n_heads, int32_t hidden);
+
+/* Per-row symmetric int8 quantization with f16 scale, bit-exact to
+ * quantize_arctic_xs.zig:152-173.  Device pointers: w f32 [rows,cols],
+ * q i8 [rows,cols], scale f16 bits [rows]. */
+int tzh_quantize_rows(tzh_ctx *ctx, const float *w, int64_t rows, int64_t cols,
+                      int8_t *q, uint16_t *scale);
+
+/* Host-side version of the same quantizer (host pointers, no device work). */
+int tzh_quantize_rows_host(const float *w, int64_t rows, int64_t cols, int8_t *q, uint16_t *scale);
+
+/* The quantize_arctic_xs tool (quantize_arctic_xs.zig:100-203): read a
+ * safetensors file, quantize every tensor shouldQuantize() selects
+ * (quantize_arctic_xs.zig:80-92), write I8 `<name>` + F16 `<name>.scale`,
+ * copy the rest.  If n_quantized is not NULL it receives the count. */
+int tzh_quantize_safetensors(const char *in_path, const char *out_path, int32_t *n_quantized);
+
+/* ------------------------------------------------------------------ */
+/* Arctic-embed-xs model (replaces arctic.zig ModelWeights / forward*) */
+/* ------------------------------------------------------------------ */
+
+/* arctic.Config (arctic.zig:29-42). */
+typedef struct {
+    int32_t hidden_size;             /* 384 */
+    int32_t num_hidden_layers;       /* 6 */
+    int32_t num_attention_heads;     /* 12 */
+    int32_t intermediate_size;       /* 1536 */
+    int32_t vocab_size;              /* 30522 */
+    int32_t max_position_embeddings; /* 512 */
+    int32_t type_vocab_size;         /* 2 */
+    float layer_norm_eps;            /* 1e-12 */
+} tzh_arctic_config;
+
+/* One weight matrix, arctic.MatWeight (arctic.zig:47-58): either F32 data or
+ * I8 data [rows, cols] row-major with F16 per-row scale. Host pointers. */
+typedef struct {
+    const void *data;
+    const uint16_t *scale; /* F16 bits [rows] when dtype == TZH_I8, else NULL */
+    int32_t dtype;         /* TZH_F32 or TZH_I8 */
+    int32_t rows;
+    int32_t cols;
+    int32_t pad_;
+} tzh_mat_view;
+
+/* arctic.AttentionWeights (arctic.zig:70-81). Host pointers. */
+typedef struct {
+    tzh_mat_view query_weight;  const float *query_bias;
+    tzh_mat_view key_weight;    const float *key_bias;
+    tzh_mat_view value_weight;  const float *value_bias;
+    tzh_mat_view output_weight; const float *output_bias;
+    const float *output_ln_gamma;
+    const float *output_ln_beta;
+} tzh_attention_weights;
+
+/* arctic.FeedForwardWeights (arctic.zig:84-91). Host pointers. */
+typedef struct {
+    tzh_mat_view intermediate_weight; const float *intermediate_bias;
+    tzh_mat_view output_weight;       const float *output_bias;
+    const float *output_ln_gamma;
+    const float *output_ln_beta;
+} tzh_ffn_weights;
+
+typedef struct {
+    tzh_attention_weights attention;
+    tzh_ffn_weights ffn;
+} tzh_layer_weights;
+
+/* arctic.ModelWeights (arctic.zig:100-108) as host views. */
+typedef struct {
+    tzh_arctic_config config;
+    tzh_mat_view word_embeddings;       /* [vocab, hidden] */
+    tzh_mat_view position_embeddings;   /* [max_pos, hidden] */
+    tzh_mat_view token_type_embeddings; /* [type_vocab, hidden] */
+    const float *layer_norm_gamma;
+    const float *layer_norm_beta;
+    const tzh_layer_weights *layers;    /* [num_hidden_layers] */
+} tzh_arctic_weights;
+
+typedef struct tzh_model tzh_model;
+
+/* Upload host weights to HBM (int8 linears stay int8; f32 linears are kept
+ * f32 in HBM and rounded to f16 per tile on load).  The model is bound to
+ * ctx's device and stream. */
+int tzh_arctic_upload(tzh_ctx *ctx, const tzh_arctic_weights *weights, tzh_model **out);
+
+/* ModelWeights.fromSafeTensors (arctic.zig:113-166): "bert." prefix
+ * optional, LayerNorm weight|gamma and bias|beta, I8 weights need an F16
+ * "<name>.scale".  Errors: TZH_ERR_MISSING_WEIGHT, TZH_ERR_WRONG_DTYPE,
+ * TZH_ERR_UNSUPPORTED_DTYPE, TZH_ERR_INVALID_FORMAT, TZH_ERR_IO. */
+int tzh_arctic_load_safetensors(tzh_ctx *ctx, const char *path, const tzh_arctic_config *config,
+                                tzh_model **out);
+int tzh_arctic_free(tzh_model *model);
+
+/* Batched forward: arctic.forwardBatch / forwardBatchParallel
+ * (arctic.zig:902-918, 959-1013).  Sequence b has lengths[b] tokens
+ * (host int32 array, 1..max_position_embeddings) whose ids are at
+ * ids + b*ids_stride (device u32; ids_stride == 0 means the sequences are
+ * packed back to back).  Each sequence is forwarded at its own length, the
+ * reference's semantics for a padded+masked batch.  outputs: device f32
+ * [batch, hidden], each row the L2-normalised CLS embedding. */
+int tzh_arctic_forward_batch(tzh_model *model, float *outputs, const uint32_t *ids,
+                             const int32_t *lengths, int32_t batch, int64_t ids_stride);
+
+/* Hidden state after the embeddings and the first n_layers encoder layers
+ * (arctic.zig:830-848 stopped early; n_layers == 0 gives the embedding
+ * LayerNorm output), for every token of the packed batch: hidden device f32
+ * [sum(lengths), hidden_size].  Same batch arguments as
+ * tzh_arctic_forward_batch. */
+int tzh_arctic_hidden(tzh_model *model, float *hidden, const uint32_t *ids, const int32_t *lengths,
+                      int32_t batch, int64_t ids_stride, int32_t n_layers);
+
+/* Single sequence (arctic.forward, arctic.zig:874-898): ids device u32 [seq_len]. */
+int tzh_arctic_forward(tzh_model *model, float *output, const uint32_t *token_ids, int64_t seq_len);
+
+/* Number of out-of-range token ids (>= vocab_size) seen since the model was
+ * created.  Such ids are clamped to vocab_size-1 so the gather stays in
+ * bounds (the reference panics on the slice bounds check in safe builds).
+ * Synchronises the model's stream. */
+int tzh_arctic_bad_id_count(tzh_model *model, int32_t *count);
+
+/* Last-batch timing hook: number of kernel launches the previous
+ * tzh_arctic_forward_batch enqueued (for launch-overhead accounting). */
+int tzh_arctic_last_launch_count(tzh_model *model);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TENZOR_HIP_H */

@@ -1,0 +1,82 @@
+"""Arctic-embed-xs on the GPU: the mirror of model/arctic.zig's entry points.
+
+    ctx = InferenceContext(device=0)                       # arctic.zig:436-465
+    weights = ModelWeights.fromSafeTensors(ctx, path)      # arctic.zig:113-166
+    forward(out, token_ids, weights, ctx)                  # arctic.zig:874-898
+    forwardBatch(outs, ids, lengths, weights, ctx)         # arctic.zig:902-918 / 959-1013
+
+Outputs are L2-normalised CLS embeddings [hidden] per sequence.  Device
+tensors are torch tensors on the context's device; ids are uint32 values
+stored in an int32 tensor.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import Context, check, lib
+from .synth import Config, HostWeights
+
+InferenceContext = Context
+arctic_embed_xs_config = Config()
+
+
+class ModelWeights:
+    """Device-resident weights (tzh_model)."""
+
+    def __init__(self, handle: C.c_void_p, ctx: Context, config: Config):
+        self.handle, self.ctx, self.config = handle, ctx, config
+
+    @staticmethod
+    def fromSafeTensors(ctx: Context, path: str, config: Config = Config()) -> "ModelWeights":
+        h = C.c_void_p()
+        cfg = config.to_c()
+        check(lib().tzh_arctic_load_safetensors(ctx.handle, str(path).encode(), C.byref(cfg), C.byref(h)))
+        return ModelWeights(h, ctx, config)
+
+    @staticmethod
+    def fromHost(ctx: Context, weights: dict, config: Config = Config()) -> "ModelWeights":
+        hw = HostWeights(weights, config)
+        h = C.c_void_p()
+        check(lib().tzh_arctic_upload(ctx.handle, C.byref(hw.struct), C.byref(h)))
+        return ModelWeights(h, ctx, config)
+
+    def bad_id_count(self) -> int:
+        n = C.c_int32()
+        check(lib().tzh_arctic_bad_id_count(self.handle, C.byref(n)))
+        return n.value
+
+    def last_launch_count(self) -> int:
+        return lib().tzh_arctic_last_launch_count(self.handle)
+
+    def deinit(self) -> None:
+        if self.handle:
+            lib().tzh_arctic_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.deinit()
+        except Exception:
+            pass
+
+
+def forward(output, token_ids, weights: ModelWeights, ctx: Context | None = None) -> None:
+    """Embed one sequence: output f32 [hidden] (device), token_ids [L] (device)."""
+    if output.numel() != weights.config.hidden_size:
+        raise ValueError("output must hold hidden_size floats")
+    check(lib().tzh_arctic_forward(weights.handle, C.c_void_p(output.data_ptr()),
+                                   C.c_void_p(token_ids.data_ptr()), int(token_ids.numel())))
+
+
+def forwardBatch(outputs, ids, lengths, weights: ModelWeights, ctx: Context | None = None) -> None:
+    """Embed a batch.  ids: device [batch, S] padded (S = row stride) or a
+    packed 1-D device tensor of sum(lengths) ids; lengths: host ints."""
+    lengths = np.ascontiguousarray(np.asarray(lengths, dtype=np.int32))
+    batch = int(lengths.shape[0])
+    if outputs.numel() != batch * weights.config.hidden_size:
+        raise ValueError("outputs must hold batch * hidden_size floats")
+    stride = int(ids.shape[1]) if ids.dim() == 2 else 0
+    check(lib().tzh_arctic_forward_batch(weights.handle, C.c_void_p(outputs.data_ptr()), C.c_void_p(ids.data_ptr()),
+                                         lengths.ctypes.data, batch, stride))

@@ -1,0 +1,692 @@
+// Arctic-embed-xs encoder forward on gfx950 (replaces arctic.zig:113-1013).
+//
+// Activations live in HBM as f16 between kernels; every reduction,
+// accumulation and normalisation is f32.  Sequences of a batch are packed
+// back to back (cu_seqlens) so padded positions cost nothing and each
+// sequence is forwarded at its true length, as the reference's per-sequence
+// forward does (arctic.zig:874-898, 959-1013).
+//
+// Per layer (arctic.zig:814-826):
+//   qkv  = h  @ Wqkv^T * s + b                    (one GEMM, N = 3*384)
+//   ctx  = attention(qkv)                         (K4)
+//   h1   = LN(h  + (ctx @ Wo^T * s + bo))          (GEMM + LN epilogue)
+//   f    = gelu(h1 @ W1^T * s + b1)               (GEMM + GELU epilogue)
+//   h    = LN(h1 + (f  @ W2^T * s + b2))           (GEMM + LN epilogue)
+#include "common.h"
+
+#include <algorithm>
+#include <cstring>
+#include <new>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "safetensors.h"
+
+int tzh_linear_w8_launch(hipStream_t st, const void *a, int32_t a_dtype, const int8_t *wq, const uint16_t *scale,
+                         const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k, int64_t n,
+                         int32_t epilogue, const void *residual, int32_t res_dtype, const float *gamma,
+                         const float *beta, float eps);
+int tzh_attention_launch(hipStream_t st, const _Float16 *qkv, _Float16 *out, const int *cu_seqlens,
+                         const int *order, int batch, int n_heads, int hidden);
+
+namespace {
+
+constexpr int H = 384;  // hidden size the kernels are specialised for
+
+// ---------------------------------------------------------------------------
+// kernels
+// ---------------------------------------------------------------------------
+
+// Pack ids of a (possibly padded) batch into [T] and record positions.
+__global__ void pack_ids_kernel(const uint32_t *__restrict__ ids, int64_t stride, const int *__restrict__ cu,
+                                uint32_t *__restrict__ tok_ids, int32_t *__restrict__ tok_pos, uint32_t vocab,
+                                int *__restrict__ bad) {
+    const int b = blockIdx.x;
+    const int start = cu[b], L = cu[b + 1] - start;
+    const uint32_t *src = stride ? ids + (int64_t)b * stride : ids + start;
+    for (int j = threadIdx.x; j < L; j += blockDim.x) {
+        uint32_t id = src[j];
+        if (id >= vocab) {  // out-of-range id: counted, clamped to keep the gather in bounds
+            atomicAdd(bad, 1);
+            id = vocab - 1;
+        }
+        tok_ids[start + j] = id;
+        tok_pos[start + j] = j;
+    }
+}
+
+struct TableRef {
+    const float *f32;
+    const int8_t *q8;
+    const uint16_t *scale;
+    __device__ __forceinline__ float get(int64_t row, int col) const {
+        if (f32) return f32[row * H + col];
+        return (float)q8[row * H + col] * f16_bits_to_f32(scale[row]);  // arctic.zig:490-508
+    }
+};
+
+// K2: x = (word[id] + pos[p]) + type[0], then LayerNorm (arctic.zig:543-585).
+// One wave per token, six columns per lane.
+__global__ void __launch_bounds__(256) embed_ln_kernel(const uint32_t *__restrict__ tok_ids,
+                                                       const int32_t *__restrict__ tok_pos, int64_t T,
+                                                       TableRef word, TableRef pos, TableRef type,
+                                                       const float *__restrict__ gamma,
+                                                       const float *__restrict__ beta, float eps,
+                                                       _Float16 *__restrict__ out) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= T) return;
+    const int64_t id = tok_ids[t];
+    const int64_t p = tok_pos[t];
+    float x[6];
+    float sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 6; q++) {
+        const int c = lane + 64 * q;
+        float v = word.get(id, c);
+        v = v + pos.get(p, c);
+        v = v + type.get(0, c);
+        x[q] = v;
+        sum += v;
+    }
+    const float mean = wave_sum(sum) / (float)H;
+    float vs = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 6; q++) {
+        const float d = x[q] - mean;
+        vs += d * d;
+    }
+    const float inv_std = 1.0f / sqrtf(wave_sum(vs) / (float)H + eps);
+#pragma unroll
+    for (int q = 0; q < 6; q++) {
+        const int c = lane + 64 * q;
+        out[t * H + c] = (_Float16)(((x[q] - mean) * inv_std) * gamma[c] + beta[c]);
+    }
+}
+
+// K5: CLS row of every sequence, L2-normalised (arctic.zig:893-897, 851-863).
+__global__ void __launch_bounds__(256) cls_l2_kernel(const _Float16 *__restrict__ hidden, const int *__restrict__ cu,
+                                                     int batch, float *__restrict__ out) {
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (b >= batch) return;
+    const _Float16 *row = hidden + (int64_t)cu[b] * H;
+    float v[6], ss = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 6; q++) {
+        v[q] = (float)row[lane + 64 * q];
+        ss += v[q] * v[q];
+    }
+    const float norm = sqrtf(wave_sum(ss));
+#pragma unroll
+    for (int q = 0; q < 6; q++) out[(int64_t)b * H + lane + 64 * q] = norm > 1e-12f ? v[q] / norm : v[q];
+}
+
+// Row-wise LayerNorm over the last dim, f32 in/out (layernorm.zig:26-117),
+// one wave per row.
+__global__ void __launch_bounds__(256) layernorm_rows_kernel(const float *x, const float *__restrict__ g,
+                                                             const float *__restrict__ bta, float *y,
+                                                             int64_t rows, int n, float eps) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float *xr = x + r * n;
+    float s = 0.0f;
+    for (int c = lane; c < n; c += 64) s += xr[c];
+    const float mean = wave_sum(s) / (float)n;
+    float vs = 0.0f;
+    for (int c = lane; c < n; c += 64) {
+        const float d = xr[c] - mean;
+        vs += d * d;
+    }
+    const float inv_std = 1.0f / sqrtf(wave_sum(vs) / (float)n + eps);
+    // all lanes have read their inputs before any write (wave_sum is a
+    // wave-wide exchange), so x == y is safe
+    for (int c = lane; c < n; c += 64) y[r * n + c] = ((xr[c] - mean) * inv_std) * g[c] + bta[c];
+}
+
+// GPU quantizer, bit-exact to quantize_arctic_xs.zig:152-173: one wave per
+// row; the max is order-independent and each code depends on its element only.
+__global__ void __launch_bounds__(256) quantize_rows_kernel(const float *__restrict__ w, int64_t rows, int64_t cols,
+                                                            int8_t *__restrict__ q, uint16_t *__restrict__ scale) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float *row = w + r * cols;
+    float mx = 0.0f;
+    for (int64_t c = lane; c < cols; c += 64) {
+        const float a = fabsf(row[c]);
+        mx = a > mx ? a : mx;
+    }
+    mx = wave_max(mx);
+    const float s32 = mx == 0.0f ? 1.0f : mx / 127.0f;
+    const _Float16 s16 = (_Float16)s32;  // v_cvt_f16_f32, round to nearest even
+    if (lane == 0) scale[r] = __builtin_bit_cast(uint16_t, s16);
+    const float inv = 1.0f / (float)s16;
+    for (int64_t c = lane; c < cols; c += 64) {
+        const float qf = roundf(row[c] * inv);
+        int qi = (int)qf;
+        qi = qi > 127 ? 127 : (qi < -127 ? -127 : qi);
+        q[r * cols + c] = (int8_t)qi;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// model state
+// ---------------------------------------------------------------------------
+struct DevTable {
+    float *f32 = nullptr;
+    int8_t *q8 = nullptr;
+    uint16_t *scale = nullptr;
+    TableRef ref() const { return TableRef{f32, q8, scale}; }
+};
+
+struct DevLinear {
+    int8_t *w = nullptr;
+    uint16_t *s = nullptr;
+    float *b = nullptr;
+};
+
+struct DevLayer {
+    DevLinear qkv, o, ffn1, ffn2;
+    float *ln1_g = nullptr, *ln1_b = nullptr, *ln2_g = nullptr, *ln2_b = nullptr;
+};
+
+}  // namespace
+
+struct tzh_model {
+    tzh_ctx *ctx = nullptr;
+    tzh_arctic_config cfg{};
+    std::vector<void *> allocs;  // weight allocations
+    DevTable word, pos, type;
+    float *emb_g = nullptr, *emb_b = nullptr;
+    std::vector<DevLayer> layers;
+    // workspace, grown on demand
+    int64_t cap_tokens = 0;
+    int cap_batch = 0;
+    _Float16 *h = nullptr, *h1 = nullptr, *qkv = nullptr, *attn = nullptr, *inter = nullptr;
+    uint32_t *tok_ids = nullptr;
+    int32_t *tok_pos = nullptr;
+    int *meta = nullptr;  // device: cu[batch+1] | order[batch]
+    int *bad_ids = nullptr;
+    int *host_meta = nullptr;  // pinned staging
+    hipEvent_t meta_done = nullptr;
+    int last_launches = 0;
+};
+
+namespace {
+
+int dev_alloc(tzh_model *m, void **p, size_t bytes) {
+    if (hipMalloc(p, bytes ? bytes : 16) != hipSuccess) {
+        (void)hipGetLastError();
+        return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "device allocation of %zu bytes failed", bytes);
+    }
+    m->allocs.push_back(*p);
+    return TZH_OK;
+}
+
+template <typename T>
+int upload(tzh_model *m, T **dst, const void *src, size_t count) {
+    TZH_TRY(dev_alloc(m, (void **)dst, count * sizeof(T)));
+    TZH_HIP(hipMemcpy(*dst, src, count * sizeof(T), hipMemcpyHostToDevice));
+    return TZH_OK;
+}
+
+int check_vec(const float *p, const char *what) {
+    return p ? TZH_OK : tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s", what);
+}
+
+int upload_table(tzh_model *m, const tzh_mat_view &v, int64_t rows, DevTable &t, const char *what) {
+    if (!v.data) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s", what);
+    if (v.rows != rows || v.cols != H)
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "%s has shape [%d,%d], expected [%lld,%d]", what, v.rows, v.cols,
+                        (long long)rows, H);
+    if (v.dtype == TZH_F32) return upload<float>(m, &t.f32, v.data, (size_t)rows * H);
+    if (v.dtype == TZH_I8) {
+        if (!v.scale) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s.scale", what);
+        TZH_TRY(upload<int8_t>(m, &t.q8, v.data, (size_t)rows * H));
+        return upload<uint16_t>(m, &t.scale, v.scale, (size_t)rows);
+    }
+    return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "Weight %s has unsupported dtype %d", what, v.dtype);
+}
+
+// Concatenate the row blocks of several [rows_i, cols] linears into one
+// int8 matrix (QKV fusion) with its scales and biases.
+int upload_linear(tzh_model *m, std::initializer_list<std::pair<const tzh_mat_view *, const float *>> parts,
+                  int cols, DevLinear &out, const char *what) {
+    int64_t rows = 0;
+    for (auto &pb : parts) {
+        const tzh_mat_view *v = pb.first;
+        if (!v->data) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s", what);
+        if (!pb.second) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s bias", what);
+        if (v->dtype == TZH_F32)
+            return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE,
+                            "%s is F32: this backend runs int8-weight (I8 + F16 scale) linears only", what);
+        if (v->dtype != TZH_I8) return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "Weight %s has unsupported dtype %d", what, v->dtype);
+        if (!v->scale) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s.scale", what);
+        if (v->cols != cols) return tzh_fail(TZH_ERR_INVALID_ARGS, "%s has %d columns, expected %d", what, v->cols, cols);
+        rows += v->rows;
+    }
+    std::vector<int8_t> w((size_t)(rows * cols));
+    std::vector<uint16_t> s((size_t)rows);
+    std::vector<float> b((size_t)rows);
+    int64_t r0 = 0;
+    for (auto &pb : parts) {
+        const tzh_mat_view *v = pb.first;
+        std::memcpy(w.data() + r0 * cols, v->data, (size_t)v->rows * cols);
+        std::memcpy(s.data() + r0, v->scale, (size_t)v->rows * 2);
+        std::memcpy(b.data() + r0, pb.second, (size_t)v->rows * 4);
+        r0 += v->rows;
+    }
+    TZH_TRY(upload<int8_t>(m, &out.w, w.data(), w.size()));
+    TZH_TRY(upload<uint16_t>(m, &out.s, s.data(), s.size()));
+    return upload<float>(m, &out.b, b.data(), b.size());
+}
+
+int check_config(const tzh_arctic_config &c) {
+    if (c.hidden_size != H || c.num_attention_heads != 12 || c.intermediate_size != 1536)
+        return tzh_fail(TZH_ERR_INVALID_ARGS,
+                        "kernels are specialised for hidden 384, 12 heads, intermediate 1536 (got %d, %d, %d)",
+                        c.hidden_size, c.num_attention_heads, c.intermediate_size);
+    if (c.num_hidden_layers < 1 || c.num_hidden_layers > 64) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad layer count");
+    if (c.max_position_embeddings < 1 || c.max_position_embeddings > 512)
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "max_position_embeddings must be in [1, 512]");
+    if (c.vocab_size < 1 || c.type_vocab_size < 1) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad vocab sizes");
+    return TZH_OK;
+}
+
+void free_workspace(tzh_model *m) {
+    void *bufs[] = {m->h, m->h1, m->qkv, m->attn, m->inter, m->tok_ids, m->tok_pos, m->meta};
+    for (void *p : bufs)
+        if (p) (void)hipFree(p);
+    m->h = m->h1 = m->qkv = m->attn = m->inter = nullptr;
+    m->tok_ids = nullptr;
+    m->tok_pos = nullptr;
+    m->meta = nullptr;
+    if (m->host_meta) (void)hipHostFree(m->host_meta);
+    m->host_meta = nullptr;
+    m->cap_tokens = 0;
+    m->cap_batch = 0;
+}
+
+int ensure_workspace(tzh_model *m, int64_t tokens, int batch) {
+    if (tokens <= m->cap_tokens && batch <= m->cap_batch) return TZH_OK;
+    TZH_HIP(hipStreamSynchronize(m->ctx->stream));
+    const int64_t T = std::max<int64_t>(tokens, m->cap_tokens);
+    const int B = std::max(batch, m->cap_batch);
+    free_workspace(m);
+    auto get = [&](void **p, size_t bytes) -> int {
+        if (hipMalloc(p, bytes ? bytes : 16) != hipSuccess) {
+            (void)hipGetLastError();
+            return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "workspace allocation of %zu bytes failed", bytes);
+        }
+        return TZH_OK;
+    };
+    TZH_TRY(get((void **)&m->h, (size_t)T * H * 2));
+    TZH_TRY(get((void **)&m->h1, (size_t)T * H * 2));
+    TZH_TRY(get((void **)&m->qkv, (size_t)T * 3 * H * 2));
+    TZH_TRY(get((void **)&m->attn, (size_t)T * H * 2));
+    TZH_TRY(get((void **)&m->inter, (size_t)T * 1536 * 2));
+    TZH_TRY(get((void **)&m->tok_ids, (size_t)T * 4));
+    TZH_TRY(get((void **)&m->tok_pos, (size_t)T * 4));
+    TZH_TRY(get((void **)&m->meta, (size_t)(2 * B + 1) * 4));
+    if (hipHostMalloc((void **)&m->host_meta, (size_t)(2 * B + 1) * 4, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        m->host_meta = nullptr;
+        return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "pinned staging allocation failed");
+    }
+    m->cap_tokens = T;
+    m->cap_batch = B;
+    return TZH_OK;
+}
+
+int model_new(tzh_ctx *ctx, const tzh_arctic_config &cfg, tzh_model **out) {
+    TZH_TRY(check_config(cfg));
+    tzh_model *m = new (std::nothrow) tzh_model();
+    if (!m) return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "model allocation failed");
+    m->ctx = ctx;
+    m->cfg = cfg;
+    m->layers.resize((size_t)cfg.num_hidden_layers);
+    if (hipEventCreateWithFlags(&m->meta_done, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        delete m;
+        return tzh_fail(TZH_ERR_DEVICE, "event creation failed");
+    }
+    void *bad = nullptr;
+    if (dev_alloc(m, &bad, 16) != TZH_OK || hipMemset(bad, 0, 16) != hipSuccess) {
+        (void)hipEventDestroy(m->meta_done);
+        for (void *p : m->allocs) (void)hipFree(p);
+        delete m;
+        return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "allocation failed");
+    }
+    m->bad_ids = (int *)bad;
+    *out = m;
+    return TZH_OK;
+}
+
+void model_delete(tzh_model *m) {
+    if (!m) return;
+    (void)hipSetDevice(m->ctx->device);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    free_workspace(m);
+    for (void *p : m->allocs) (void)hipFree(p);
+    if (m->meta_done) (void)hipEventDestroy(m->meta_done);
+    delete m;
+}
+
+int upload_weights(tzh_model *m, const tzh_arctic_weights *w) {
+    const tzh_arctic_config &c = m->cfg;
+    TZH_TRY(upload_table(m, w->word_embeddings, c.vocab_size, m->word, "embeddings.word_embeddings.weight"));
+    TZH_TRY(upload_table(m, w->position_embeddings, c.max_position_embeddings, m->pos,
+                         "embeddings.position_embeddings.weight"));
+    TZH_TRY(upload_table(m, w->token_type_embeddings, c.type_vocab_size, m->type,
+                         "embeddings.token_type_embeddings.weight"));
+    TZH_TRY(check_vec(w->layer_norm_gamma, "embeddings.LayerNorm.weight"));
+    TZH_TRY(check_vec(w->layer_norm_beta, "embeddings.LayerNorm.bias"));
+    TZH_TRY(upload<float>(m, &m->emb_g, w->layer_norm_gamma, H));
+    TZH_TRY(upload<float>(m, &m->emb_b, w->layer_norm_beta, H));
+    if (!w->layers) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: encoder layers");
+    for (int l = 0; l < c.num_hidden_layers; l++) {
+        const tzh_layer_weights &lw = w->layers[l];
+        DevLayer &d = m->layers[(size_t)l];
+        const tzh_attention_weights &a = lw.attention;
+        const tzh_ffn_weights &f = lw.ffn;
+        for (const tzh_mat_view *v : {&a.query_weight, &a.key_weight, &a.value_weight, &a.output_weight})
+            if (v->data && (v->rows != H || v->cols != H))
+                return tzh_fail(TZH_ERR_INVALID_ARGS, "layer %d attention weight shape [%d,%d]", l, v->rows, v->cols);
+        if (f.intermediate_weight.data && (f.intermediate_weight.rows != 1536 || f.intermediate_weight.cols != H))
+            return tzh_fail(TZH_ERR_INVALID_ARGS, "layer %d intermediate weight shape", l);
+        if (f.output_weight.data && (f.output_weight.rows != H || f.output_weight.cols != 1536))
+            return tzh_fail(TZH_ERR_INVALID_ARGS, "layer %d output weight shape", l);
+        TZH_TRY(upload_linear(m, {{&a.query_weight, a.query_bias}, {&a.key_weight, a.key_bias},
+                                  {&a.value_weight, a.value_bias}}, H, d.qkv, "attention.self.{query,key,value}.weight"));
+        TZH_TRY(upload_linear(m, {{&a.output_weight, a.output_bias}}, H, d.o, "attention.output.dense.weight"));
+        TZH_TRY(upload_linear(m, {{&f.intermediate_weight, f.intermediate_bias}}, H, d.ffn1, "intermediate.dense.weight"));
+        TZH_TRY(upload_linear(m, {{&f.output_weight, f.output_bias}}, 1536, d.ffn2, "output.dense.weight"));
+        TZH_TRY(check_vec(a.output_ln_gamma, "attention.output.LayerNorm.weight"));
+        TZH_TRY(check_vec(a.output_ln_beta, "attention.output.LayerNorm.bias"));
+        TZH_TRY(check_vec(f.output_ln_gamma, "output.LayerNorm.weight"));
+        TZH_TRY(check_vec(f.output_ln_beta, "output.LayerNorm.bias"));
+        TZH_TRY(upload<float>(m, &d.ln1_g, a.output_ln_gamma, H));
+        TZH_TRY(upload<float>(m, &d.ln1_b, a.output_ln_beta, H));
+        TZH_TRY(upload<float>(m, &d.ln2_g, f.output_ln_gamma, H));
+        TZH_TRY(upload<float>(m, &d.ln2_b, f.output_ln_beta, H));
+    }
+    return TZH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// safetensors -> host views (arctic.zig:113-166, 258-287)
+// ---------------------------------------------------------------------------
+struct HostStore {
+    StFile st;
+    std::vector<std::vector<uint8_t>> owned;  // aligned copies
+};
+
+const void *aligned_data(HostStore &hs, const StTensor &t) {
+    const uint8_t *p = hs.st.data(t);
+    const int es = st_dtype_size(t.dtype);
+    if (((uintptr_t)p % (uintptr_t)es) == 0) return p;  // safetensors.zig:147-161
+    hs.owned.emplace_back(p, p + (t.end - t.start));
+    return hs.owned.back().data();
+}
+
+int get_f32(HostStore &hs, const std::string &name, const float **out) {
+    const StTensor *t = hs.st.get(name);
+    if (!t) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s", name.c_str());
+    if (t->dtype != TZH_F32) return tzh_fail(TZH_ERR_WRONG_DTYPE, "Weight %s has wrong dtype, expected F32", name.c_str());
+    *out = (const float *)aligned_data(hs, *t);
+    return TZH_OK;
+}
+
+int get_f32_alt(HostStore &hs, const std::string &primary, const std::string &alt, const float **out) {
+    if (hs.st.get(primary)) return get_f32(hs, primary, out);  // arctic.zig:245-256
+    return get_f32(hs, alt, out);
+}
+
+int get_mat(HostStore &hs, const std::string &name, tzh_mat_view &v) {
+    const StTensor *t = hs.st.get(name);
+    if (!t) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s", name.c_str());
+    std::memset(&v, 0, sizeof v);
+    if (t->shape.size() != 2)
+        return tzh_fail(TZH_ERR_INVALID_FORMAT, "Weight %s must be 2-D", name.c_str());
+    v.rows = (int32_t)t->shape[0];
+    v.cols = (int32_t)t->shape[1];
+    if (t->dtype == TZH_F32) {
+        v.dtype = TZH_F32;
+        v.data = aligned_data(hs, *t);
+        return TZH_OK;
+    }
+    if (t->dtype == TZH_I8) {  // arctic.zig:273-281
+        v.dtype = TZH_I8;
+        v.data = aligned_data(hs, *t);
+        const std::string sname = name + ".scale";
+        const StTensor *s = hs.st.get(sname);
+        if (!s) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s", sname.c_str());
+        if (s->dtype != TZH_F16) return tzh_fail(TZH_ERR_WRONG_DTYPE, "Weight %s has wrong dtype, expected F16", sname.c_str());
+        if (s->numel() != v.rows) return tzh_fail(TZH_ERR_INVALID_FORMAT, "%s has %lld entries, expected %d", sname.c_str(), (long long)s->numel(), v.rows);
+        v.scale = (const uint16_t *)aligned_data(hs, *s);
+        return TZH_OK;
+    }
+    return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "Weight %s has unsupported dtype %s", name.c_str(), st_dtype_name(t->dtype));
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------
+extern "C" int tzh_arctic_upload(tzh_ctx *ctx, const tzh_arctic_weights *weights, tzh_model **out) {
+    tzh_clear_error();
+    TZH_TRY(tzh_ctx_enter(ctx));
+    if (!weights || !out) return tzh_fail(TZH_ERR_INVALID_ARGS, "null argument");
+    *out = nullptr;
+    tzh_model *m = nullptr;
+    TZH_TRY(model_new(ctx, weights->config, &m));
+    const int rc = upload_weights(m, weights);
+    if (rc != TZH_OK) {
+        const std::string msg = tzh_last_error();
+        model_delete(m);
+        return tzh_fail(rc, "%s", msg.c_str());
+    }
+    *out = m;
+    return TZH_OK;
+}
+
+extern "C" int tzh_arctic_load_safetensors(tzh_ctx *ctx, const char *path, const tzh_arctic_config *config,
+                                           tzh_model **out) {
+    tzh_clear_error();
+    TZH_TRY(tzh_ctx_enter(ctx));
+    if (!out || !config) return tzh_fail(TZH_ERR_INVALID_ARGS, "null argument");
+    *out = nullptr;
+    HostStore hs;
+    TZH_TRY(st_load(path, hs.st));
+    hs.owned.reserve(hs.st.tensors.size());
+    const bool bert = hs.st.get("bert.embeddings.word_embeddings.weight") != nullptr;  // arctic.zig:131
+    const std::string pre = bert ? "bert." : "";
+    tzh_arctic_weights w;
+    std::memset(&w, 0, sizeof w);
+    w.config = *config;
+    TZH_TRY(check_config(*config));
+    TZH_TRY(get_mat(hs, pre + "embeddings.word_embeddings.weight", w.word_embeddings));
+    TZH_TRY(get_mat(hs, pre + "embeddings.position_embeddings.weight", w.position_embeddings));
+    TZH_TRY(get_mat(hs, pre + "embeddings.token_type_embeddings.weight", w.token_type_embeddings));
+    TZH_TRY(get_f32_alt(hs, pre + "embeddings.LayerNorm.weight", pre + "embeddings.LayerNorm.gamma", &w.layer_norm_gamma));
+    TZH_TRY(get_f32_alt(hs, pre + "embeddings.LayerNorm.bias", pre + "embeddings.LayerNorm.beta", &w.layer_norm_beta));
+    std::vector<tzh_layer_weights> layers((size_t)config->num_hidden_layers);
+    for (int l = 0; l < config->num_hidden_layers; l++) {
+        const std::string b = pre + "encoder.layer." + std::to_string(l) + ".";  // arctic.zig:302
+        tzh_attention_weights &a = layers[(size_t)l].attention;
+        tzh_ffn_weights &f = layers[(size_t)l].ffn;
+        TZH_TRY(get_mat(hs, b + "attention.self.query.weight", a.query_weight));
+        TZH_TRY(get_f32(hs, b + "attention.self.query.bias", &a.query_bias));
+        TZH_TRY(get_mat(hs, b + "attention.self.key.weight", a.key_weight));
+        TZH_TRY(get_f32(hs, b + "attention.self.key.bias", &a.key_bias));
+        TZH_TRY(get_mat(hs, b + "attention.self.value.weight", a.value_weight));
+        TZH_TRY(get_f32(hs, b + "attention.self.value.bias", &a.value_bias));
+        TZH_TRY(get_mat(hs, b + "attention.output.dense.weight", a.output_weight));
+        TZH_TRY(get_f32(hs, b + "attention.output.dense.bias", &a.output_bias));
+        TZH_TRY(get_f32_alt(hs, b + "attention.output.LayerNorm.weight", b + "attention.output.LayerNorm.gamma", &a.output_ln_gamma));
+        TZH_TRY(get_f32_alt(hs, b + "attention.output.LayerNorm.bias", b + "attention.output.LayerNorm.beta", &a.output_ln_beta));
+        TZH_TRY(get_mat(hs, b + "intermediate.dense.weight", f.intermediate_weight));
+        TZH_TRY(get_f32(hs, b + "intermediate.dense.bias", &f.intermediate_bias));
+        TZH_TRY(get_mat(hs, b + "output.dense.weight", f.output_weight));
+        TZH_TRY(get_f32(hs, b + "output.dense.bias", &f.output_bias));
+        TZH_TRY(get_f32_alt(hs, b + "output.LayerNorm.weight", b + "output.LayerNorm.gamma", &f.output_ln_gamma));
+        TZH_TRY(get_f32_alt(hs, b + "output.LayerNorm.bias", b + "output.LayerNorm.beta", &f.output_ln_beta));
+    }
+    w.layers = layers.data();
+    return tzh_arctic_upload(ctx, &w, out);
+}
+
+extern "C" int tzh_arctic_free(tzh_model *model) {
+    model_delete(model);
+    return TZH_OK;
+}
+
+namespace {
+
+__global__ void f16_to_f32_kernel(const _Float16 *__restrict__ x, float *__restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = (float)x[i];
+}
+
+// Shared body of the batch entry points: embeddings, the first n_layers
+// encoder layers, then either CLS + L2 into `outputs` or the f32 hidden
+// state into `hidden_out`.
+int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t *ids, const int32_t *lengths,
+                int32_t batch, int64_t ids_stride, int32_t n_layers) {
+    tzh_clear_error();
+    if (!m) return tzh_fail(TZH_ERR_INVALID_ARGS, "null model");
+    TZH_TRY(tzh_ctx_enter(m->ctx));
+    if (batch == 0) return TZH_OK;  // arctic.zig:967
+    if (batch < 0 || !(outputs || hidden_out) || !ids || !lengths)
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "bad batch arguments");
+    if (n_layers < 0 || n_layers > m->cfg.num_hidden_layers)
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "n_layers %d out of range", n_layers);
+    if (ids_stride < 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "negative ids_stride");
+    int64_t T = 0;
+    for (int b = 0; b < batch; b++) {
+        if (lengths[b] < 1 || lengths[b] > m->cfg.max_position_embeddings)
+            return tzh_fail(TZH_ERR_INVALID_ARGS, "sequence %d has length %d (must be 1..%d)", b, lengths[b],
+                            m->cfg.max_position_embeddings);
+        if (ids_stride && lengths[b] > ids_stride)
+            return tzh_fail(TZH_ERR_INVALID_ARGS, "sequence %d length %d exceeds ids_stride %lld", b, lengths[b],
+                            (long long)ids_stride);
+        T += lengths[b];
+    }
+    if (T > ((int64_t)1 << 30)) return tzh_fail(TZH_ERR_TOO_LARGE, "batch of %lld tokens is too large", (long long)T);
+    TZH_TRY(ensure_workspace(m, T, batch));
+    hipStream_t st = m->ctx->stream;
+
+    // metadata: cu_seqlens and a longest-first order for attention
+    TZH_HIP(hipEventSynchronize(m->meta_done));  // previous copy out of the staging buffer finished
+    int *cu = m->host_meta, *order = m->host_meta + batch + 1;
+    cu[0] = 0;
+    for (int b = 0; b < batch; b++) cu[b + 1] = cu[b] + lengths[b];
+    std::iota(order, order + batch, 0);
+    std::stable_sort(order, order + batch, [&](int x, int y) { return lengths[x] > lengths[y]; });
+    TZH_HIP(hipMemcpyAsync(m->meta, m->host_meta, (size_t)(2 * batch + 1) * 4, hipMemcpyHostToDevice, st));
+    TZH_HIP(hipEventRecord(m->meta_done, st));
+    const int *d_cu = m->meta, *d_order = m->meta + batch + 1;
+
+    int launches = 0;
+    hipLaunchKernelGGL(pack_ids_kernel, dim3(batch), dim3(256), 0, st, ids, ids_stride, d_cu, m->tok_ids, m->tok_pos,
+                       (uint32_t)m->cfg.vocab_size, m->bad_ids);
+    TZH_LAUNCHED("pack_ids_kernel");
+    launches++;
+    hipLaunchKernelGGL(embed_ln_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, m->tok_ids, m->tok_pos, T,
+                       m->word.ref(), m->pos.ref(), m->type.ref(), m->emb_g, m->emb_b, m->cfg.layer_norm_eps, m->h);
+    TZH_LAUNCHED("embed_ln_kernel");
+    launches++;
+    const float eps = m->cfg.layer_norm_eps;
+    for (int32_t li = 0; li < n_layers; li++) {
+        const DevLayer &d = m->layers[(size_t)li];
+        TZH_TRY(tzh_linear_w8_launch(st, m->h, TZH_F16, d.qkv.w, d.qkv.s, d.qkv.b, m->qkv, TZH_F16, T, H, 3 * H,
+                                     TZH_EPI_BIAS, nullptr, TZH_F16, nullptr, nullptr, 0.0f));
+        TZH_TRY(tzh_attention_launch(st, m->qkv, m->attn, d_cu, d_order, batch, 12, H));
+        TZH_TRY(tzh_linear_w8_launch(st, m->attn, TZH_F16, d.o.w, d.o.s, d.o.b, m->h1, TZH_F16, T, H, H,
+                                     TZH_EPI_BIAS_RES_LN, m->h, TZH_F16, d.ln1_g, d.ln1_b, eps));
+        TZH_TRY(tzh_linear_w8_launch(st, m->h1, TZH_F16, d.ffn1.w, d.ffn1.s, d.ffn1.b, m->inter, TZH_F16, T, H, 1536,
+                                     TZH_EPI_BIAS_GELU, nullptr, TZH_F16, nullptr, nullptr, 0.0f));
+        TZH_TRY(tzh_linear_w8_launch(st, m->inter, TZH_F16, d.ffn2.w, d.ffn2.s, d.ffn2.b, m->h, TZH_F16, T, 1536, H,
+                                     TZH_EPI_BIAS_RES_LN, m->h1, TZH_F16, d.ln2_g, d.ln2_b, eps));
+        launches += 5;
+    }
+    if (outputs) {
+        hipLaunchKernelGGL(cls_l2_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, st, m->h, d_cu, batch,
+                           outputs);
+        TZH_LAUNCHED("cls_l2_kernel");
+        launches++;
+    }
+    if (hidden_out) {
+        const int64_t n = T * H;
+        hipLaunchKernelGGL(f16_to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m->h, hidden_out,
+                           n);
+        TZH_LAUNCHED("f16_to_f32_kernel");
+        launches++;
+    }
+    m->last_launches = launches;
+    return TZH_OK;
+}
+
+}  // namespace
+
+extern "C" int tzh_arctic_forward_batch(tzh_model *m, float *outputs, const uint32_t *ids, const int32_t *lengths,
+                                        int32_t batch, int64_t ids_stride) {
+    if (!outputs && batch > 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "null outputs");
+    return run_forward(m, outputs, nullptr, ids, lengths, batch, ids_stride,
+                       m ? m->cfg.num_hidden_layers : 0);
+}
+
+extern "C" int tzh_arctic_hidden(tzh_model *m, float *hidden, const uint32_t *ids, const int32_t *lengths,
+                                 int32_t batch, int64_t ids_stride, int32_t n_layers) {
+    if (!hidden && batch > 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "null hidden");
+    return run_forward(m, nullptr, hidden, ids, lengths, batch, ids_stride, n_layers);
+}
+
+extern "C" int tzh_arctic_forward(tzh_model *m, float *output, const uint32_t *token_ids, int64_t seq_len) {
+    if (seq_len <= 0 || seq_len > 512) return tzh_fail(TZH_ERR_INVALID_ARGS, "seq_len %lld out of range", (long long)seq_len);
+    const int32_t len = (int32_t)seq_len;
+    return tzh_arctic_forward_batch(m, output, token_ids, &len, 1, 0);
+}
+
+extern "C" int tzh_arctic_last_launch_count(tzh_model *m) { return m ? m->last_launches : 0; }
+
+// Number of out-of-range token ids seen (and clamped) since the model was
+// created; synchronises the model's stream.
+extern "C" int tzh_arctic_bad_id_count(tzh_model *m, int32_t *count) {
+    tzh_clear_error();
+    if (!m || !count) return tzh_fail(TZH_ERR_INVALID_ARGS, "null argument");
+    TZH_TRY(tzh_ctx_enter(m->ctx));
+    TZH_HIP(hipMemcpyAsync(count, m->bad_ids, 4, hipMemcpyDeviceToHost, m->ctx->stream));
+    TZH_HIP(hipStreamSynchronize(m->ctx->stream));
+    return TZH_OK;
+}
+
+extern "C" int tzh_layernorm_last_dim(tzh_ctx *ctx, const float *x, const float *gamma, const float *beta, float *y,
+                                      int64_t rows, int64_t n, float eps) {
+    tzh_clear_error();
+    TZH_TRY(tzh_ctx_enter(ctx));
+    if (rows < 0 || n <= 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad shape");
+    if (rows == 0) return TZH_OK;
+    if (!x || !gamma || !beta || !y) return tzh_fail(TZH_ERR_INVALID_ARGS, "null pointer");
+    hipLaunchKernelGGL(layernorm_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, ctx->stream, x, gamma,
+                       beta, y, rows, (int)n, eps);
+    TZH_LAUNCHED("layernorm_rows_kernel");
+    return TZH_OK;
+}
+
+extern "C" int tzh_quantize_rows(tzh_ctx *ctx, const float *w, int64_t rows, int64_t cols, int8_t *q,
+                                 uint16_t *scale) {
+    tzh_clear_error();
+    TZH_TRY(tzh_ctx_enter(ctx));
+    if (rows < 0 || cols < 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad shape");
+    if (rows == 0) return TZH_OK;
+    if (!w || !q || !scale) return tzh_fail(TZH_ERR_INVALID_ARGS, "null pointer");
+    hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, ctx->stream, w, rows,
+                       cols, q, scale);
+    TZH_LAUNCHED("quantize_rows_kernel");
+    return TZH_OK;
+}

@@ -1,0 +1,102 @@
+// Shared host/device definitions for libtenzor_hip (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/tenzor_hip.h"
+
+// ---------------------------------------------------------------------------
+// Error reporting: thread-local message, negative status codes.
+// ---------------------------------------------------------------------------
+int tzh_fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void tzh_clear_error();
+
+#define TZH_HIP(expr)                                                                    \
+    do {                                                                                 \
+        hipError_t e_ = (expr);                                                          \
+        if (e_ != hipSuccess)                                                            \
+            return tzh_fail(TZH_ERR_DEVICE, "%s failed: %s (%s:%d)", #expr,              \
+                            hipGetErrorString(e_), __FILE__, __LINE__);                  \
+    } while (0)
+
+#define TZH_TRY(expr)                                                                    \
+    do {                                                                                 \
+        int rc_ = (expr);                                                                \
+        if (rc_ != TZH_OK) return rc_;                                                   \
+    } while (0)
+
+// After a kernel launch: report launch-configuration errors immediately.
+#define TZH_LAUNCHED(name)                                                               \
+    do {                                                                                 \
+        hipError_t e_ = hipGetLastError();                                               \
+        if (e_ != hipSuccess)                                                            \
+            return tzh_fail(TZH_ERR_DEVICE, "launch of %s failed: %s", name,             \
+                            hipGetErrorString(e_));                                      \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// Context: one device, one stream.
+// ---------------------------------------------------------------------------
+struct tzh_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool own_stream = false;
+    int num_cus = 256;
+    // stream-ordered scratch used by eval for materialised reductions
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+};
+
+// Make ctx's device current for the calling thread.
+int tzh_ctx_enter(tzh_ctx *ctx);
+// Grow-only device scratch owned by the context (synchronises on growth).
+int tzh_ctx_scratch(tzh_ctx *ctx, size_t bytes, void **out);
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+#define TZH_WAVE 64
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// f32 -> f16 with round-to-nearest-even (v_cvt_f16_f32 honours the default RNE mode).
+__device__ __forceinline__ _Float16 to_f16(float x) { return (_Float16)x; }
+
+// f16 bits -> f32, exact.
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+    return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// Host-side f16 helpers (bit exact, RNE), used by the host quantizer and tests.
+uint16_t tzh_host_f32_to_f16(float x);
+float tzh_host_f16_to_f32(uint16_t h);
+
+// tanh-form GELU of arctic.zig:750-756 with the device tanhf.
+__device__ __forceinline__ float gelu_arctic(float x) {
+    const float sqrt_2_over_pi = 0.7978845608f;
+    const float coeff = 0.044715f;
+    float inner = sqrt_2_over_pi * (x + coeff * x * x * x);
+    return 0.5f * x * (1.0f + tanhf(inner));
+}

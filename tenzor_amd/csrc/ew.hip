@@ -1,0 +1,720 @@
+// K1: single-pass elementwise / broadcast / reduce chains for tzh_eval_into.
+//
+// Replaces executor.evalInto (executor.zig:49-196, 327-360), which
+// materialises one temporary per non-leaf child (executor.zig:551-578).
+// Here a post-order expression DAG becomes a small stack program that every
+// thread runs over VEC contiguous output elements, reading each leaf once
+// through its broadcast projection and writing the result once.  A reduce
+// node evaluates the chain below it inside the reduction (no temporary);
+// only a reduce that feeds further elementwise work is materialised.
+//
+// Op semantics follow simd.zig:107-315 (tanh = 2*sigmoid(2x)-1, gelu with
+// that tanh, relu = @max(x,0), round half away from zero) and
+// elementwise.zig:124-207 (supported op set).
+#include "common.h"
+
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+namespace {
+
+constexpr int kMaxNodes = 32;  // analyzer.zig:13 MAX_ELEMENTWISE_OPS
+constexpr int kMaxLeaves = 12;
+constexpr int kMaxDepth = 4;   // value stack slots per thread
+
+enum : int16_t { EK_LEAF = 0, EK_CONST = 1, EK_UNARY = 2, EK_BINARY = 3 };
+enum : int32_t { VEC_PER_ELEM = 0, VEC_CONTIG = 1, VEC_SPLAT = 2 };
+
+struct EwLeaf {
+    const void *ptr;
+    int64_t div;   // affine projection: off = (flat / div) % mod
+    int64_t mod;
+    int32_t general;  // 1: use strides[] with a full unflatten
+    int32_t vec;      // VEC_* for VEC consecutive outputs
+    int64_t strides[TZH_MAX_RANK];
+};
+
+struct EwNode {
+    int16_t kind;
+    int16_t op;
+    int16_t slot;
+    int16_t arg;
+    int32_t pad0, pad1;
+    double cval;
+};
+
+struct EwProgram {
+    int32_t n_nodes;
+    int32_t n_leaves;
+    int32_t ndim;
+    int32_t pad;
+    int64_t numel;
+    int64_t shape[TZH_MAX_RANK];
+    EwNode nodes[kMaxNodes];
+    EwLeaf leaves[kMaxLeaves];
+};
+
+static_assert(sizeof(EwProgram) < 3800, "kernel argument block too large");
+
+template <typename T, int V>
+struct Vec {
+    T v[V];
+};
+
+// ------------------------------------------------------------------------
+// scalar op semantics (simd.zig:107-315)
+// ------------------------------------------------------------------------
+__device__ __forceinline__ float dexp(float x) { return expf(x); }
+__device__ __forceinline__ double dexp(double x) { return exp(x); }
+
+template <typename T>
+__device__ __forceinline__ T sigm(T x) {
+    return T(1) / (T(1) + dexp(-x));
+}
+
+template <typename T>
+__device__ __forceinline__ T tanh_ref(T x) {
+    return T(2) * sigm<T>(T(2) * x) - T(1);
+}
+
+template <typename T>
+__device__ __forceinline__ T unary_op(int op, T x) {
+    switch (op) {
+    case TZH_OP_NEG: return -x;
+    case TZH_OP_ABS: return fabs(x);
+    case TZH_OP_EXP: return dexp(x);
+    case TZH_OP_LOG: return log(x);
+    case TZH_OP_SQRT: return sqrt(x);
+    case TZH_OP_RSQRT: return T(1) / sqrt(x);
+    case TZH_OP_SIN: return sin(x);
+    case TZH_OP_COS: return cos(x);
+    case TZH_OP_TANH: return tanh_ref<T>(x);
+    case TZH_OP_SIGMOID: return sigm<T>(x);
+    case TZH_OP_RELU: return fmax(x, T(0));
+    case TZH_OP_GELU: {
+        const T k0 = T(0.7978845608028654), k1 = T(0.044715);
+        T x3 = x * x * x;
+        T inner = k0 * (x + k1 * x3);
+        return T(0.5) * x * (T(1) + tanh_ref<T>(inner));
+    }
+    case TZH_OP_SILU: return x * sigm<T>(x);
+    case TZH_OP_SOFTPLUS: return log(T(1) + dexp(x));
+    case TZH_OP_FLOOR: return floor(x);
+    case TZH_OP_CEIL: return ceil(x);
+    case TZH_OP_ROUND: return round(x);
+    default: return x;
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ T binary_op(int op, T a, T b) {
+    switch (op) {
+    case TZH_OP_ADD: return a + b;
+    case TZH_OP_SUB: return a - b;
+    case TZH_OP_MUL: return a * b;
+    case TZH_OP_DIV: return a / b;
+    case TZH_OP_POW: return pow(a, b);
+    case TZH_OP_MAX: return fmax(a, b);
+    case TZH_OP_MIN: return fmin(a, b);
+    default: return a;
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ T red_ident(int op) {
+    switch (op) {
+    case TZH_OP_PROD: return T(1);
+    case TZH_OP_REDUCE_MAX: return -INFINITY;
+    case TZH_OP_REDUCE_MIN: return INFINITY;
+    default: return T(0);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ T red_apply(int op, T acc, T v) {
+    switch (op) {
+    case TZH_OP_PROD: return acc * v;
+    case TZH_OP_REDUCE_MAX: return fmax(acc, v);
+    case TZH_OP_REDUCE_MIN: return fmin(acc, v);
+    default: return acc + v;
+    }
+}
+
+// ------------------------------------------------------------------------
+// leaf loads
+// ------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ int64_t leaf_offset(const EwLeaf &lf, const EwProgram &p, int64_t flat) {
+    if (!lf.general) return (flat / lf.div) % lf.mod;
+    int64_t off = 0, rem = flat;
+    for (int d = p.ndim - 1; d >= 0; d--) {
+        const int64_t ix = rem % p.shape[d];
+        rem /= p.shape[d];
+        off += ix * lf.strides[d];
+    }
+    return off;
+}
+
+template <typename T, int V>
+__device__ __forceinline__ Vec<T, V> load_leaf(const EwLeaf &lf, const EwProgram &p, int64_t flat) {
+    Vec<T, V> r;
+    const T *base = (const T *)lf.ptr;
+    if (lf.vec == VEC_CONTIG) {
+        const int64_t off = (flat / lf.div) % lf.mod;
+        if constexpr (V * sizeof(T) == 16) {
+            const f32x4_t raw = *(const f32x4_t *)(base + off);
+            __builtin_memcpy(&r, &raw, 16);
+        } else {
+#pragma unroll
+            for (int e = 0; e < V; e++) r.v[e] = base[off + e];
+        }
+    } else if (lf.vec == VEC_SPLAT) {
+        const T x = base[leaf_offset<T>(lf, p, flat)];
+#pragma unroll
+        for (int e = 0; e < V; e++) r.v[e] = x;
+    } else {
+#pragma unroll
+        for (int e = 0; e < V; e++) r.v[e] = base[leaf_offset<T>(lf, p, flat + e)];
+    }
+    return r;
+}
+
+// value stack with a uniform stack pointer: slots live in registers and are
+// selected by scalar branches.
+template <typename T, int V>
+struct Stack {
+    Vec<T, V> s[kMaxDepth];
+    __device__ __forceinline__ Vec<T, V> get(int i) const {
+        switch (i) {
+        case 0: return s[0];
+        case 1: return s[1];
+        case 2: return s[2];
+        default: return s[3];
+        }
+    }
+    __device__ __forceinline__ void set(int i, const Vec<T, V> &x) {
+        switch (i) {
+        case 0: s[0] = x; break;
+        case 1: s[1] = x; break;
+        case 2: s[2] = x; break;
+        default: s[3] = x; break;
+        }
+    }
+};
+
+template <typename T, int V>
+__device__ __forceinline__ Vec<T, V> run_program(const EwProgram &p, int64_t flat) {
+    Stack<T, V> st;
+    for (int i = 0; i < p.n_nodes; i++) {
+        const EwNode &nd = p.nodes[i];
+        if (nd.kind == EK_LEAF) {
+            st.set(nd.slot, load_leaf<T, V>(p.leaves[nd.arg], p, flat));
+        } else if (nd.kind == EK_CONST) {
+            Vec<T, V> x;
+#pragma unroll
+            for (int e = 0; e < V; e++) x.v[e] = (T)nd.cval;
+            st.set(nd.slot, x);
+        } else if (nd.kind == EK_UNARY) {
+            Vec<T, V> x = st.get(nd.slot);
+#pragma unroll
+            for (int e = 0; e < V; e++) x.v[e] = unary_op<T>(nd.op, x.v[e]);
+            st.set(nd.slot, x);
+        } else {
+            Vec<T, V> a = st.get(nd.slot);
+            const Vec<T, V> b = st.get(nd.slot + 1);
+#pragma unroll
+            for (int e = 0; e < V; e++) a.v[e] = binary_op<T>(nd.op, a.v[e], b.v[e]);
+            st.set(nd.slot, a);
+        }
+    }
+    return st.get(0);
+}
+
+template <typename T, int V>
+__global__ void __launch_bounds__(256) ew_chain_kernel(const EwProgram p, T *__restrict__ out) {
+    const int64_t nvec = p.numel / V;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nvec; v += stride) {
+        const int64_t flat = v * V;
+        const Vec<T, V> r = run_program<T, V>(p, flat);
+        if constexpr (V * sizeof(T) == 16) {
+            f32x4_t raw;
+            __builtin_memcpy(&raw, &r, 16);
+            __builtin_nontemporal_store(raw, (f32x4_t *)(out + flat));
+        } else {
+#pragma unroll
+            for (int e = 0; e < V; e++) out[flat + e] = r.v[e];
+        }
+    }
+    // tail (numel % V elements), one element per thread of block 0
+    if (blockIdx.x == 0) {
+        const int64_t t = nvec * V + threadIdx.x;
+        // with V == 1 every leaf mode loads the single element at its
+        // affine or general offset, so the same program serves the tail
+        if (t < p.numel) out[t] = run_program<T, 1>(p, t).v[0];
+    }
+}
+
+// block-wide reduction of one value per thread (256 threads)
+template <typename T>
+__device__ __forceinline__ T block_reduce(int op, T v, T *smem) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = red_apply<T>(op, v, __shfl_xor(v, o, 64));
+    const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+    if (l == 0) smem[w] = v;
+    __syncthreads();
+    T r = red_ident<T>(op);
+    if (threadIdx.x == 0) {
+        for (int i = 0; i < (int)(blockDim.x / 64); i++) r = red_apply<T>(op, r, smem[i]);
+    }
+    __syncthreads();
+    return r;
+}
+
+// Reduce-all, stage 1: each block reduces a grid-stride share of the chain.
+template <typename T, int V>
+__global__ void __launch_bounds__(256) ew_reduce_all_kernel(const EwProgram p, int op,
+                                                            T *__restrict__ partials) {
+    __shared__ T smem[4];
+    T acc = red_ident<T>(op);
+    const int64_t nvec = p.numel / V;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nvec; v += stride) {
+        const Vec<T, V> r = run_program<T, V>(p, v * V);
+#pragma unroll
+        for (int e = 0; e < V; e++) acc = red_apply<T>(op, acc, r.v[e]);
+    }
+    if (blockIdx.x == 0) {
+        const int64_t t = nvec * V + threadIdx.x;
+        if (t < p.numel) acc = red_apply<T>(op, acc, run_program<T, 1>(p, t).v[0]);
+    }
+    const T r = block_reduce<T>(op, acc, smem);
+    if (threadIdx.x == 0) partials[blockIdx.x] = r;
+}
+
+// Reduce-all, stage 2: one block folds the partials; mean divides by n.
+template <typename T>
+__global__ void __launch_bounds__(256) ew_reduce_finish_kernel(const T *__restrict__ partials, int n,
+                                                               int op, int64_t count,
+                                                               T *__restrict__ out, int64_t out_numel) {
+    __shared__ T smem[4];
+    T acc = red_ident<T>(op);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) acc = red_apply<T>(op, acc, partials[i]);
+    T r = block_reduce<T>(op, acc, smem);
+    if (threadIdx.x == 0 && op == TZH_OP_MEAN) r = r / (T)count;
+    if (threadIdx.x == 0) smem[0] = r;
+    __syncthreads();
+    r = smem[0];
+    for (int64_t i = threadIdx.x; i < out_numel; i += blockDim.x) out[i] = r;
+}
+
+// Reduce over the last axis (inner == 1): one wave per output row.
+template <typename T>
+__global__ void __launch_bounds__(256) ew_reduce_rows_kernel(const EwProgram p, int op, int64_t outer,
+                                                             int64_t rsz, T *__restrict__ out) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
+    const int lane = threadIdx.x % 64;
+    if (row >= outer) return;
+    T acc = red_ident<T>(op);
+    for (int64_t r = lane; r < rsz; r += 64) acc = red_apply<T>(op, acc, run_program<T, 1>(p, row * rsz + r).v[0]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc = red_apply<T>(op, acc, __shfl_xor(acc, o, 64));
+    if (lane == 0) out[row] = (op == TZH_OP_MEAN) ? acc / (T)rsz : acc;
+}
+
+// Reduce over a middle/leading axis: one thread per (outer, inner) column.
+template <typename T>
+__global__ void __launch_bounds__(256) ew_reduce_cols_kernel(const EwProgram p, int op, int64_t outer,
+                                                             int64_t rsz, int64_t inner,
+                                                             T *__restrict__ out) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= outer * inner) return;
+    const int64_t o = idx / inner, i = idx % inner;
+    T acc = red_ident<T>(op);
+    for (int64_t r = 0; r < rsz; r++) acc = red_apply<T>(op, acc, run_program<T, 1>(p, (o * rsz + r) * inner + i).v[0]);
+    out[idx] = (op == TZH_OP_MEAN) ? acc / (T)rsz : acc;
+}
+
+// ------------------------------------------------------------------------
+// host planner
+// ------------------------------------------------------------------------
+bool unary_ok(int op) {
+    switch (op) {
+    case TZH_OP_NEG: case TZH_OP_ABS: case TZH_OP_EXP: case TZH_OP_LOG: case TZH_OP_SQRT:
+    case TZH_OP_RSQRT: case TZH_OP_SIN: case TZH_OP_COS: case TZH_OP_TANH: case TZH_OP_SIGMOID:
+    case TZH_OP_RELU: case TZH_OP_GELU: case TZH_OP_SILU: case TZH_OP_SOFTPLUS:
+    case TZH_OP_FLOOR: case TZH_OP_CEIL: case TZH_OP_ROUND:
+        return true;
+    default:
+        return false;
+    }
+}
+
+bool binary_ok(int op) {
+    switch (op) {
+    case TZH_OP_ADD: case TZH_OP_SUB: case TZH_OP_MUL: case TZH_OP_DIV: case TZH_OP_POW:
+    case TZH_OP_MAX: case TZH_OP_MIN:
+        return true;
+    default:
+        return false;
+    }
+}
+
+bool reduce_ok(int op) {
+    switch (op) {
+    case TZH_OP_SUM: case TZH_OP_MEAN: case TZH_OP_PROD: case TZH_OP_REDUCE_MAX:
+    case TZH_OP_REDUCE_MIN:
+        return true;
+    default:
+        return false;
+    }
+}
+
+int64_t numel_of(int32_t nd, const int64_t *s) {
+    int64_t n = 1;
+    for (int i = 0; i < nd; i++) n *= s[i];
+    return n;
+}
+
+struct Planner {
+    tzh_ctx *ctx;
+    const tzh_node *tape;
+    int32_t n_nodes;
+    const tzh_leaf *leaves;
+    int32_t n_leaves;
+    int32_t dtype;
+    size_t es;
+    std::vector<void *> temps;
+
+    ~Planner() {
+        if (!temps.empty()) {
+            hipStreamSynchronize(ctx->stream);
+            for (void *t : temps) hipFree(t);
+        }
+    }
+
+    int validate(int32_t idx) {
+        if (idx < 0 || idx >= n_nodes) return tzh_fail(TZH_ERR_INVALID_ARGS, "node index %d out of range", idx);
+        const tzh_node &n = tape[idx];
+        if (n.ndim < 0 || n.ndim > TZH_MAX_RANK) return tzh_fail(TZH_ERR_SHAPE, "node %d: rank %d", idx, n.ndim);
+        for (int i = 0; i < n.ndim; i++)
+            if (n.shape[i] < 0) return tzh_fail(TZH_ERR_SHAPE, "node %d: negative dim", idx);
+        switch (n.kind) {
+        case TZH_NODE_TENSOR: {
+            if (n.leaf < 0 || n.leaf >= n_leaves) return tzh_fail(TZH_ERR_INVALID_ARGS, "node %d: leaf %d out of range", idx, n.leaf);
+            const tzh_leaf &lf = leaves[n.leaf];
+            if (lf.ndim != n.ndim) return tzh_fail(TZH_ERR_SHAPE, "node %d: leaf rank mismatch", idx);
+            for (int i = 0; i < n.ndim; i++)
+                if (lf.shape[i] != n.shape[i]) return tzh_fail(TZH_ERR_SHAPE, "node %d: leaf shape mismatch", idx);
+            if (!lf.data && numel_of(lf.ndim, lf.shape) > 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "leaf %d: null data", n.leaf);
+            return TZH_OK;
+        }
+        case TZH_NODE_CONSTANT:
+            return TZH_OK;
+        case TZH_NODE_UNARY: {
+            if (!unary_ok(n.op)) return tzh_fail(TZH_ERR_UNSUPPORTED_OP, "Unsupported unary operation: tag %d", n.op);
+            if (n.lhs < 0 || n.lhs >= idx) return tzh_fail(TZH_ERR_INVALID_ARGS, "node %d: bad input index", idx);
+            const tzh_node &c = tape[n.lhs];
+            if (c.ndim != n.ndim) return tzh_fail(TZH_ERR_SHAPE, "node %d: unary shape mismatch", idx);
+            for (int i = 0; i < n.ndim; i++)
+                if (c.shape[i] != n.shape[i]) return tzh_fail(TZH_ERR_SHAPE, "node %d: unary shape mismatch", idx);
+            return validate(n.lhs);
+        }
+        case TZH_NODE_BINARY: {
+            if (!binary_ok(n.op)) return tzh_fail(TZH_ERR_UNSUPPORTED_OP, "Unsupported binary operation: tag %d", n.op);
+            if (n.lhs < 0 || n.lhs >= idx || n.rhs < 0 || n.rhs >= idx)
+                return tzh_fail(TZH_ERR_INVALID_ARGS, "node %d: bad operand index", idx);
+            const tzh_node &l = tape[n.lhs], &r = tape[n.rhs];
+            const int nd = l.ndim > r.ndim ? l.ndim : r.ndim;
+            if (n.ndim != nd) return tzh_fail(TZH_ERR_SHAPE, "Shapes not broadcast compatible (node %d)", idx);
+            for (int i = 0; i < nd; i++) {
+                const int li = i - (nd - l.ndim), ri = i - (nd - r.ndim);
+                const int64_t a = li >= 0 ? l.shape[li] : 1, b = ri >= 0 ? r.shape[ri] : 1;
+                if (a != b && a != 1 && b != 1) return tzh_fail(TZH_ERR_SHAPE, "Shapes not broadcast compatible (node %d)", idx);
+                if (n.shape[i] != (a > b ? a : b)) return tzh_fail(TZH_ERR_SHAPE, "node %d: wrong broadcast result shape", idx);
+            }
+            TZH_TRY(validate(n.lhs));
+            return validate(n.rhs);
+        }
+        case TZH_NODE_REDUCE: {
+            if (!reduce_ok(n.op)) return tzh_fail(TZH_ERR_UNSUPPORTED_OP, "Unsupported reduction: tag %d", n.op);
+            if (n.lhs < 0 || n.lhs >= idx) return tzh_fail(TZH_ERR_INVALID_ARGS, "node %d: bad input index", idx);
+            const tzh_node &c = tape[n.lhs];
+            if (n.axis < -1 || n.axis >= c.ndim) return tzh_fail(TZH_ERR_SHAPE, "node %d: axis %d out of range", idx, n.axis);
+            // shape.zig:279-320 ReduceShape
+            int64_t want[TZH_MAX_RANK];
+            int wn = 0;
+            if (n.axis < 0) {
+                if (n.keepdims) { wn = c.ndim; for (int i = 0; i < wn; i++) want[i] = 1; }
+            } else {
+                for (int i = 0; i < c.ndim; i++) {
+                    if (i == n.axis) { if (n.keepdims) want[wn++] = 1; }
+                    else want[wn++] = c.shape[i];
+                }
+            }
+            if (n.ndim != wn) return tzh_fail(TZH_ERR_SHAPE, "node %d: wrong reduce result rank", idx);
+            for (int i = 0; i < wn; i++)
+                if (n.shape[i] != want[i]) return tzh_fail(TZH_ERR_SHAPE, "node %d: wrong reduce result shape", idx);
+            return validate(n.lhs);
+        }
+        default:
+            return tzh_fail(TZH_ERR_UNSUPPORTED_OP, "node kind %d is not evaluated by this backend", n.kind);
+        }
+    }
+
+    // Nodes evaluated into a temporary before the program that reads them
+    // (reductions, and subtrees cut to fit the kernel's limits).
+    std::vector<char> cut;
+
+    bool is_leafish(int32_t idx) const {
+        const int k = tape[idx].kind;
+        return cut[(size_t)idx] || k == TZH_NODE_TENSOR || k == TZH_NODE_CONSTANT || k == TZH_NODE_REDUCE;
+    }
+    // value-stack depth to evaluate idx inline (Sethi-Ullman for a stack machine)
+    int depth(int32_t idx) const {
+        if (is_leafish(idx)) return 1;
+        const tzh_node &n = tape[idx];
+        if (n.kind == TZH_NODE_UNARY) return depth(n.lhs);
+        const int a = depth(n.lhs), b = depth(n.rhs) + 1;
+        return a > b ? a : b;
+    }
+    // program nodes and leaves to evaluate idx inline
+    int count(int32_t idx, int *leaves_out) const {
+        if (is_leafish(idx)) {
+            if (tape[idx].kind != TZH_NODE_CONSTANT) (*leaves_out)++;
+            return 1;
+        }
+        const tzh_node &n = tape[idx];
+        if (n.kind == TZH_NODE_UNARY) return 1 + count(n.lhs, leaves_out);
+        return 1 + count(n.lhs, leaves_out) + count(n.rhs, leaves_out);
+    }
+    bool fits(int32_t idx) const {
+        int nl = 0;
+        const int nn = count(idx, &nl);
+        return depth(idx) <= kMaxDepth && nn <= kMaxNodes && nl <= kMaxLeaves;
+    }
+    // Candidate cut points: elementwise nodes strictly below `root` and not
+    // already inside a cut subtree.  `rhs_only` restricts to right operands
+    // (the only place stack depth grows).
+    void candidates(int32_t idx, bool is_root, bool is_rhs, bool rhs_only, std::vector<int32_t> &out) const {
+        if (!is_root && is_leafish(idx)) return;
+        const tzh_node &n = tape[idx];
+        if (n.kind != TZH_NODE_UNARY && n.kind != TZH_NODE_BINARY) return;
+        if (!is_root && (!rhs_only || is_rhs)) out.push_back(idx);
+        candidates(n.lhs, false, false, rhs_only, out);
+        if (n.kind == TZH_NODE_BINARY) candidates(n.rhs, false, true, rhs_only, out);
+    }
+    // Cut subtrees below `root` until the inline program fits; each cut
+    // subtree is later compiled as a program of its own (and split again if
+    // it is still too large), so every program root is evaluated inline.
+    void choose_cuts(int32_t root) {
+        while (!fits(root)) {
+            const bool deep = depth(root) > kMaxDepth;
+            std::vector<int32_t> cand;
+            candidates(root, true, false, deep, cand);
+            if (cand.empty()) candidates(root, true, false, false, cand);
+            int32_t best = -1, best_score = -1;
+            bool best_fits = false;
+            for (int32_t c : cand) {
+                int nl = 0;
+                const int score = deep ? depth(c) : count(c, &nl);
+                const bool f = fits(c);
+                if ((f && !best_fits) || (f == best_fits && score > best_score)) {
+                    best = c;
+                    best_score = score;
+                    best_fits = f;
+                }
+            }
+            if (best < 0) break;  // nothing left to cut: root's own operands are leaves
+            cut[(size_t)best] = 1;
+        }
+    }
+
+    int add_leaf(EwProgram &p, const void *ptr, int32_t lnd, const int64_t *lshape, int vec, int *leaf_idx) {
+        if (p.n_leaves >= kMaxLeaves) return tzh_fail(TZH_ERR_INVALID_ARGS, "internal: too many leaves");
+        EwLeaf &lf = p.leaves[p.n_leaves];
+        std::memset(&lf, 0, sizeof lf);
+        lf.ptr = ptr;
+        // broadcast strides onto the program's output index space (strides.zig:92-121)
+        int64_t cs[TZH_MAX_RANK];
+        int64_t s = 1;
+        for (int i = lnd - 1; i >= 0; i--) { cs[i] = s; s *= lshape[i]; }
+        int first = -1, last = -1;
+        for (int i = 0; i < p.ndim; i++) {
+            const int si = i - (p.ndim - lnd);
+            lf.strides[i] = (si >= 0 && lshape[si] != 1) ? cs[si] : 0;
+            if (lf.strides[i] != 0) { if (first < 0) first = i; last = i; }
+        }
+        bool contiguous_run = true;
+        for (int i = first; first >= 0 && i <= last; i++)
+            if (lf.strides[i] == 0 && p.shape[i] != 1) contiguous_run = false;
+        if (first < 0) {  // scalar
+            lf.general = 0; lf.div = 1; lf.mod = 1;
+        } else if (contiguous_run) {
+            int64_t div = 1, mod = 1;
+            for (int i = last + 1; i < p.ndim; i++) div *= p.shape[i];
+            for (int i = first; i <= last; i++) mod *= p.shape[i];
+            lf.general = 0; lf.div = div; lf.mod = mod;
+        } else {
+            lf.general = 1; lf.div = 1; lf.mod = 1;
+        }
+        const bool aligned = ((uintptr_t)ptr % 16) == 0;
+        if (!lf.general && lf.div == 1 && lf.mod % vec == 0 && aligned) lf.vec = VEC_CONTIG;
+        else if (!lf.general && lf.div % vec == 0) lf.vec = VEC_SPLAT;
+        else lf.vec = VEC_PER_ELEM;
+        *leaf_idx = p.n_leaves++;
+        return TZH_OK;
+    }
+
+    int push(EwProgram &p, int16_t kind, int16_t op, int16_t slot, int16_t arg, double cval) {
+        if (p.n_nodes >= kMaxNodes) return tzh_fail(TZH_ERR_INVALID_ARGS, "internal: program too long");
+        EwNode &nd = p.nodes[p.n_nodes++];
+        nd.kind = kind; nd.op = op; nd.slot = slot; nd.arg = arg; nd.pad0 = nd.pad1 = 0; nd.cval = cval;
+        return TZH_OK;
+    }
+
+    // Materialise node idx into a fresh device temporary.
+    int materialise(int32_t idx, void **buf) {
+        const tzh_node &n = tape[idx];
+        const size_t bytes = (size_t)numel_of(n.ndim, n.shape) * es;
+        void *t = nullptr;
+        if (hipMalloc(&t, bytes ? bytes : es) != hipSuccess) {
+            (void)hipGetLastError();
+            return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "temporary of %zu bytes failed", bytes);
+        }
+        temps.push_back(t);
+        TZH_TRY(eval_into(idx, t));
+        *buf = t;
+        return TZH_OK;
+    }
+
+    int emit(EwProgram &p, int32_t idx, int sp, int vec, bool is_root) {
+        const tzh_node &n = tape[idx];
+        if (sp >= kMaxDepth) return tzh_fail(TZH_ERR_INVALID_ARGS, "internal: value stack overflow");
+        if (!is_root && (n.kind == TZH_NODE_REDUCE || cut[(size_t)idx])) {
+            void *buf = nullptr;
+            TZH_TRY(materialise(idx, &buf));
+            int li;
+            TZH_TRY(add_leaf(p, buf, n.ndim, n.shape, vec, &li));
+            return push(p, EK_LEAF, 0, (int16_t)sp, (int16_t)li, 0.0);
+        }
+        switch (n.kind) {
+        case TZH_NODE_TENSOR: {
+            int li;
+            TZH_TRY(add_leaf(p, leaves[n.leaf].data, n.ndim, n.shape, vec, &li));
+            return push(p, EK_LEAF, 0, (int16_t)sp, (int16_t)li, 0.0);
+        }
+        case TZH_NODE_CONSTANT:
+            return push(p, EK_CONST, 0, (int16_t)sp, 0, n.value);
+        case TZH_NODE_UNARY:
+            TZH_TRY(emit(p, n.lhs, sp, vec, false));
+            return push(p, EK_UNARY, (int16_t)n.op, (int16_t)sp, 0, 0.0);
+        case TZH_NODE_BINARY:
+            TZH_TRY(emit(p, n.lhs, sp, vec, false));
+            TZH_TRY(emit(p, n.rhs, sp + 1, vec, false));
+            return push(p, EK_BINARY, (int16_t)n.op, (int16_t)sp, 0, 0.0);
+        default:
+            return tzh_fail(TZH_ERR_UNSUPPORTED_OP, "node kind %d", n.kind);
+        }
+    }
+
+    int compile(int32_t idx, EwProgram &p, int vec) {
+        std::memset(&p, 0, sizeof p);
+        if (cut.size() != (size_t)n_nodes) cut.assign((size_t)n_nodes, 0);
+        const tzh_node &n = tape[idx];
+        p.ndim = n.ndim;
+        for (int i = 0; i < n.ndim; i++) p.shape[i] = n.shape[i];
+        p.numel = numel_of(n.ndim, n.shape);
+        // a cut node being materialised is this program's root: evaluate it inline
+        const char was_cut = cut[(size_t)idx];
+        cut[(size_t)idx] = 0;
+        choose_cuts(idx);
+        int rc = fits(idx) ? emit(p, idx, 0, vec, true)
+                           : tzh_fail(TZH_ERR_INVALID_ARGS, "internal: expression cannot be split to fit");
+        cut[(size_t)idx] = was_cut;
+        return rc;
+    }
+
+    int grid_for(int64_t work_items) const {
+        int64_t g = (work_items + 255) / 256;
+        const int64_t cap = (int64_t)ctx->num_cus * 16;
+        if (g > cap) g = cap;
+        if (g < 1) g = 1;
+        return (int)g;
+    }
+
+    template <typename T, int V>
+    int launch_chain(int32_t idx, T *out) {
+        EwProgram p;
+        TZH_TRY(compile(idx, p, V));
+        if (p.numel == 0) return TZH_OK;
+        const int g = grid_for(p.numel / V);
+        hipLaunchKernelGGL((ew_chain_kernel<T, V>), dim3(g), dim3(256), 0, ctx->stream, p, out);
+        TZH_LAUNCHED("ew_chain_kernel");
+        return TZH_OK;
+    }
+
+    template <typename T, int V>
+    int launch_reduce(int32_t idx, T *out) {
+        const tzh_node &n = tape[idx];
+        const tzh_node &c = tape[n.lhs];
+        EwProgram p;
+        const int64_t out_numel = numel_of(n.ndim, n.shape);
+        if (n.axis < 0) {
+            TZH_TRY(compile(n.lhs, p, V));
+            const int g = grid_for(p.numel / V);
+            void *partials = nullptr;
+            TZH_TRY(tzh_ctx_scratch(ctx, sizeof(T) * (size_t)g, &partials));
+            hipLaunchKernelGGL((ew_reduce_all_kernel<T, V>), dim3(g), dim3(256), 0, ctx->stream, p, n.op, (T *)partials);
+            TZH_LAUNCHED("ew_reduce_all_kernel");
+            hipLaunchKernelGGL((ew_reduce_finish_kernel<T>), dim3(1), dim3(256), 0, ctx->stream, (const T *)partials, g,
+                               n.op, p.numel, out, out_numel);
+            TZH_LAUNCHED("ew_reduce_finish_kernel");
+            return TZH_OK;
+        }
+        TZH_TRY(compile(n.lhs, p, 1));
+        int64_t outer = 1, inner = 1;
+        const int64_t rsz = c.shape[n.axis];
+        for (int i = 0; i < n.axis; i++) outer *= c.shape[i];
+        for (int i = n.axis + 1; i < c.ndim; i++) inner *= c.shape[i];
+        if (outer * inner == 0) return TZH_OK;
+        if (inner == 1) {
+            const int64_t blocks = (outer + 3) / 4;
+            hipLaunchKernelGGL((ew_reduce_rows_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, ctx->stream, p, n.op,
+                               outer, rsz, out);
+            TZH_LAUNCHED("ew_reduce_rows_kernel");
+        } else {
+            const int64_t blocks = (outer * inner + 255) / 256;
+            hipLaunchKernelGGL((ew_reduce_cols_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, ctx->stream, p, n.op,
+                               outer, rsz, inner, out);
+            TZH_LAUNCHED("ew_reduce_cols_kernel");
+        }
+        return TZH_OK;
+    }
+
+    int eval_into(int32_t idx, void *out) {
+        const tzh_node &n = tape[idx];
+        const bool is64 = dtype == TZH_F64;
+        if (n.kind == TZH_NODE_REDUCE)
+            return is64 ? launch_reduce<double, 2>(idx, (double *)out) : launch_reduce<float, 4>(idx, (float *)out);
+        return is64 ? launch_chain<double, 2>(idx, (double *)out) : launch_chain<float, 4>(idx, (float *)out);
+    }
+};
+
+}  // namespace
+
+extern "C" int tzh_eval_into(tzh_ctx *ctx, const tzh_node *tape, int32_t n_nodes, const tzh_leaf *leaves,
+                             int32_t n_leaves, int32_t dtype, void *out) {
+    tzh_clear_error();
+    TZH_TRY(tzh_ctx_enter(ctx));
+    if (!tape || n_nodes <= 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "empty expression");
+    if (n_leaves < 0 || (n_leaves > 0 && !leaves)) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad leaves");
+    if (dtype != TZH_F32 && dtype != TZH_F64)
+        return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "eval supports F32 and F64 element types (got %d)", dtype);
+    Planner pl{ctx, tape, n_nodes, leaves, n_leaves, dtype, dtype == TZH_F64 ? 8u : 4u, {}};
+    TZH_TRY(pl.validate(n_nodes - 1));
+    const tzh_node &root = tape[n_nodes - 1];
+    if (numel_of(root.ndim, root.shape) > 0 && !out) return tzh_fail(TZH_ERR_INVALID_ARGS, "null output");
+    return pl.eval_into(n_nodes - 1, out);
+}

@@ -1,0 +1,205 @@
+// TEST INFRASTRUCTURE ONLY: fiber scheduler and runtime-API stubs behind
+// tests/cpu_emu/hip/hip_runtime.h.  One OS thread runs every lane of a
+// block as a ucontext fiber; blocks run one after another.
+#include "hip/hip_runtime.h"
+
+#include <ucontext.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+#if defined(__has_feature)
+#if __has_feature(address_sanitizer)
+#define EMU_ASAN 1
+#include <sanitizer/common_interface_defs.h>
+#endif
+#endif
+
+namespace emu {
+
+dim3 g_threadIdx, g_blockIdx, g_blockDim, g_gridDim;
+
+namespace {
+enum State { RUN, AT_BLOCK, AT_WAVE, DONE };
+struct Fiber {
+    ucontext_t uc;
+    State st;
+};
+constexpr size_t kStack = 512 * 1024;
+constexpr size_t kSlot = 256;
+std::vector<Fiber> fibers;
+std::vector<char *> stacks;
+std::vector<unsigned char> slots;
+ucontext_t sched_uc;
+int cur = -1;
+void (*g_body)(void *) = nullptr;
+void *g_ctx = nullptr;
+const char *g_name = "";
+#ifdef EMU_ASAN
+const void *sched_bottom = nullptr;
+size_t sched_size = 0;
+#endif
+
+void to_sched(bool dying) {
+#ifdef EMU_ASAN
+    void *fake = nullptr;
+    __sanitizer_start_switch_fiber(dying ? nullptr : &fake, sched_bottom, sched_size);
+    swapcontext(&fibers[(size_t)cur].uc, &sched_uc);
+    __sanitizer_finish_switch_fiber(fake, nullptr, nullptr);
+#else
+    (void)dying;
+    swapcontext(&fibers[(size_t)cur].uc, &sched_uc);
+#endif
+}
+
+void fiber_entry(int) {
+#ifdef EMU_ASAN
+    __sanitizer_finish_switch_fiber(nullptr, &sched_bottom, &sched_size);
+#endif
+    g_body(g_ctx);
+    fibers[(size_t)cur].st = DONE;
+    to_sched(true);
+}
+
+void run_fiber(int i) {
+    cur = i;
+    g_threadIdx = dim3((unsigned)i % g_blockDim.x, 0, 0);
+#ifdef EMU_ASAN
+    void *fake = nullptr;
+    __sanitizer_start_switch_fiber(&fake, stacks[(size_t)i], kStack);
+    swapcontext(&sched_uc, &fibers[(size_t)i].uc);
+    __sanitizer_finish_switch_fiber(fake, &sched_bottom, &sched_size);
+#else
+    swapcontext(&sched_uc, &fibers[(size_t)i].uc);
+#endif
+}
+
+[[noreturn]] void deadlock(int n) {
+    std::fprintf(stderr, "EMU: kernel %s block (%u,%u,%u) cannot make progress (a barrier or wave operation "
+                         "that not every live lane reaches):\n", g_name, g_blockIdx.x, g_blockIdx.y, g_blockIdx.z);
+    for (int i = 0; i < n; i++)
+        std::fprintf(stderr, "  thread %d state %d\n", i, (int)fibers[(size_t)i].st);
+    std::abort();
+}
+}  // namespace
+
+void syncthreads() {
+    fibers[(size_t)cur].st = AT_BLOCK;
+    to_sched(false);
+}
+
+void wave_barrier() {
+    fibers[(size_t)cur].st = AT_WAVE;
+    to_sched(false);
+}
+
+int lane_id() { return cur % 64; }
+int wave_id() { return cur / 64; }
+void *wave_slot(int lane) { return &slots[((size_t)(cur / 64) * 64 + (size_t)lane) * kSlot]; }
+
+void launch(const char *name, dim3 grid, dim3 block, void (*body)(void *), void *ctx) {
+    if (block.y != 1 || block.z != 1 || block.x == 0 || block.x > 1024) {
+        std::fprintf(stderr, "EMU: unsupported block shape for %s\n", name);
+        std::abort();
+    }
+    const int n = (int)block.x;
+    if (grid.x == 0) {
+        std::fprintf(stderr, "EMU: kernel %s launched with an empty grid\n", name);
+        std::abort();
+    }
+    while ((int)stacks.size() < n) stacks.push_back((char *)std::malloc(kStack));
+    fibers.resize((size_t)n);
+    slots.assign((size_t)((n + 63) / 64) * 64 * kSlot, 0);
+    g_body = body;
+    g_ctx = ctx;
+    g_name = name;
+    g_blockDim = block;
+    g_gridDim = grid;
+    for (unsigned bz = 0; bz < grid.z; bz++)
+        for (unsigned by = 0; by < grid.y; by++)
+            for (unsigned bx = 0; bx < grid.x; bx++) {
+                g_blockIdx = dim3(bx, by, bz);
+                for (int i = 0; i < n; i++) {
+                    Fiber &f = fibers[(size_t)i];
+                    getcontext(&f.uc);
+                    f.uc.uc_stack.ss_sp = stacks[(size_t)i];
+                    f.uc.uc_stack.ss_size = kStack;
+                    f.uc.uc_link = nullptr;
+                    makecontext(&f.uc, (void (*)())fiber_entry, 1, i);
+                    f.st = RUN;
+                }
+                for (;;) {
+                    bool ran = false;
+                    for (int i = 0; i < n; i++)
+                        if (fibers[(size_t)i].st == RUN) {
+                            run_fiber(i);
+                            ran = true;
+                        }
+                    int live = 0, at_block = 0;
+                    for (int i = 0; i < n; i++) {
+                        live += fibers[(size_t)i].st != DONE;
+                        at_block += fibers[(size_t)i].st == AT_BLOCK;
+                    }
+                    if (live == 0) break;
+                    bool released = false;
+                    for (int w = 0; w < (n + 63) / 64; w++) {
+                        int wl = 0, wa = 0;
+                        for (int i = w * 64; i < n && i < (w + 1) * 64; i++) {
+                            wl += fibers[(size_t)i].st != DONE;
+                            wa += fibers[(size_t)i].st == AT_WAVE;
+                        }
+                        if (wl > 0 && wa == wl) {
+                            for (int i = w * 64; i < n && i < (w + 1) * 64; i++)
+                                if (fibers[(size_t)i].st == AT_WAVE) fibers[(size_t)i].st = RUN;
+                            released = true;
+                        }
+                    }
+                    if (!released && at_block == live) {
+                        for (int i = 0; i < n; i++)
+                            if (fibers[(size_t)i].st == AT_BLOCK) fibers[(size_t)i].st = RUN;
+                        released = true;
+                    }
+                    if (!ran && !released) deadlock(n);
+                }
+            }
+    cur = -1;
+}
+
+}  // namespace emu
+
+// ---------------------------------------------------------------------------
+// runtime stubs: "device" memory is host memory with exact-size allocations
+// (so AddressSanitizer's redzones sit right after every buffer)
+// ---------------------------------------------------------------------------
+struct emu_stream {};
+struct emu_event {};
+
+hipError_t hipGetDeviceCount(int *n) { *n = 1; return hipSuccess; }
+hipError_t hipSetDevice(int) { return hipSuccess; }
+hipError_t hipGetDeviceProperties(hipDeviceProp_t *p, int) {
+    std::memset(p, 0, sizeof *p);
+    std::strcpy(p->gcnArchName, "gfx950:sramecc+:xnack-");
+    p->multiProcessorCount = 4;
+    return hipSuccess;
+}
+hipError_t hipMalloc(void **p, size_t n) {
+    if (posix_memalign(p, 256, n ? n : 1)) return hipErrorOutOfMemory;
+    std::memset(*p, 0xA5, n);  // poison: kernels must not rely on zeroed memory
+    return hipSuccess;
+}
+hipError_t hipFree(void *p) { std::free(p); return hipSuccess; }
+hipError_t hipHostMalloc(void **p, size_t n, unsigned) { return hipMalloc(p, n); }
+hipError_t hipHostFree(void *p) { return hipFree(p); }
+hipError_t hipMemcpy(void *d, const void *s, size_t n, hipMemcpyKind) { std::memmove(d, s, n); return hipSuccess; }
+hipError_t hipMemcpyAsync(void *d, const void *s, size_t n, hipMemcpyKind k, hipStream_t) { return hipMemcpy(d, s, n, k); }
+hipError_t hipMemset(void *p, int v, size_t n) { std::memset(p, v, n); return hipSuccess; }
+hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
+hipError_t hipStreamCreateWithFlags(hipStream_t *s, unsigned) { *s = new emu_stream; return hipSuccess; }
+hipError_t hipStreamDestroy(hipStream_t s) { delete s; return hipSuccess; }
+hipError_t hipEventCreateWithFlags(hipEvent_t *e, unsigned) { *e = new emu_event; return hipSuccess; }
+hipError_t hipEventDestroy(hipEvent_t e) { delete e; return hipSuccess; }
+hipError_t hipEventRecord(hipEvent_t, hipStream_t) { return hipSuccess; }
+hipError_t hipEventSynchronize(hipEvent_t) { return hipSuccess; }
+hipError_t hipGetLastError() { return hipSuccess; }
+const char *hipGetErrorString(hipError_t) { return "emulated HIP error"; }

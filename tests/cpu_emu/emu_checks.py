@@ -1,0 +1,277 @@
+"""TEST INFRASTRUCTURE ONLY: run the GPU test scenarios against the CPU
+emulation build of libtenzor_hip (tests/cpu_emu), under AddressSanitizer.
+
+Every kernel runs with its real launch shape on the CPU; an out-of-bounds
+access aborts with an ASan report naming the kernel's source line, and a
+barrier that some lane can never reach aborts with the kernel named.  Results
+are also compared with the oracle, so kernel index logic is checked before
+anything runs on a GPU.
+
+Run (what tests/test_cpu_emulation.py does):
+    LD_PRELOAD=<libclang_rt.asan-x86_64.so> ASAN_OPTIONS=detect_leaks=0 \
+        python tests/cpu_emu/emu_checks.py [group ...]
+"""
+import ctypes as C
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+import oracle  # noqa: E402
+from tenzor_amd import _abi, synth  # noqa: E402
+from tenzor_amd.expr import BinaryExpr, ReduceExpr, ScalarExpr, Tensor, UnaryExpr, to_tape  # noqa: E402
+
+L = _abi.bind(C.CDLL(os.environ.get("TZH_EMU_LIB", os.path.join(HERE, "libtenzor_hip_emu.so"))))
+CTX = C.c_void_p()
+
+
+def check(rc):
+    if rc != 0:
+        raise RuntimeError(f"rc={rc}: {L.tzh_last_error().decode()}")
+
+
+def ulp(a, b):
+    ai = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    bi = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    ai = np.where(ai < 0, -(2 ** 31) - ai, ai)
+    bi = np.where(bi < 0, -(2 ** 31) - bi, bi)
+    return np.abs(ai - bi)
+
+
+class Host:
+    """Stand-in for a device tensor: a numpy array whose address is passed."""
+
+    def __init__(self, a):
+        self.a = np.ascontiguousarray(a)
+        self.shape = self.a.shape
+        self.dtype = type("D", (), {"is_floating_point": True, "__str__": lambda s: "torch." + str(self.a.dtype)})()
+
+    def is_contiguous(self):
+        return True
+
+    def data_ptr(self):
+        return self.a.ctypes.data
+
+
+def T(x, dt=np.float32):
+    return Tensor(Host(np.asarray(x, dt)))
+
+
+def eval_both(expr):
+    nodes, leaves = to_tape(expr)
+    dt = np.float64 if expr.dtype == "float64" else np.float32
+    out = np.empty(expr.shape, dt)
+    arr = (_abi.Leaf * max(1, len(leaves)))()
+    for i, t in enumerate(leaves):
+        arr[i].data = t.data.data_ptr()
+        arr[i].ndim = len(t.shape)
+        for j, d in enumerate(t.shape):
+            arr[i].shape[j] = d
+    tape = (_abi.Node * len(nodes))(*nodes)
+    check(L.tzh_eval_into(CTX, tape, len(nodes), arr, len(leaves), _abi.F64 if dt == np.float64 else _abi.F32,
+                          out.ctypes.data))
+    rc, ref = oracle.eval_tape(nodes, [t.data.a for t in leaves], dt)
+    assert rc == 0
+    return out, ref
+
+
+def group_eval():
+    assert eval_both(UnaryExpr("relu", T([-2, -1, 1, 2])))[0].tolist() == [0, 0, 1, 2]
+    assert eval_both(BinaryExpr("add", T([1, 2, 3, 4]), T([10, 20, 30, 40])))[0].tolist() == [11, 22, 33, 44]
+    e = UnaryExpr("relu", BinaryExpr("add", T([-1, 2, -3, 4]), T([1, 1, 1, 1])))
+    assert eval_both(e)[0].tolist() == [0, 3, 0, 5]
+    for op, axis, data, exp in [("sum", 1, [[1, 2, 3], [4, 5, 6]], [6, 15]), ("sum", 0, [[1, 2, 3], [4, 5, 6]], [5, 7, 9]),
+                                ("mean", 1, [[1, 2, 3], [4, 5, 6]], [2, 5]), ("reduce_max", 1, [[1, 5, 3], [4, 2, 6]], [5, 6])]:
+        out, _ = eval_both(ReduceExpr(op, T(data), (axis,)))
+        assert np.allclose(out, exp), (op, axis, out)
+    rng = np.random.default_rng(1)
+    x = rng.uniform(-4, 4, 203).astype(np.float32)
+    for op in ["neg", "abs", "relu", "floor", "ceil", "round", "exp", "sin", "tanh", "sigmoid", "gelu", "silu",
+               "softplus"]:
+        out, ref = eval_both(UnaryExpr(op, T(x)))
+        assert ((ulp(out, ref) <= 4) | (np.abs(out - ref) < 1e-6)).all(), op
+    xp = np.abs(x) + np.float32(1e-3)
+    for op in ["log", "sqrt", "rsqrt"]:
+        out, ref = eval_both(UnaryExpr(op, T(xp)))
+        assert ((ulp(out, ref) <= 4)).all(), op
+    a = rng.uniform(-3, 3, (7, 29)).astype(np.float32)
+    b = rng.uniform(-3, 3, (7, 29)).astype(np.float32)
+    for op in ["add", "sub", "mul", "div", "max", "min"]:
+        out, ref = eval_both(BinaryExpr(op, T(a), T(b)))
+        assert ulp(out, ref).max() == 0, op
+    for ls, rs in [((8, 12), (12,)), ((8, 12), (8, 1)), ((8, 12), ()), ((4, 1, 6), (3, 1)), ((2, 3, 4, 5), (3, 1, 5)),
+                   ((7,), (5, 1)), ((3, 5), (3, 5))]:
+        aa = rng.standard_normal(ls).astype(np.float32)
+        bb = rng.standard_normal(rs).astype(np.float32)
+        out, ref = eval_both(BinaryExpr("add", T(aa), T(bb)).mul(T(bb)).sub(T(aa)))
+        assert ulp(out, ref).max() == 0, (ls, rs)
+    xs = [T(rng.standard_normal((5, 9)).astype(np.float32)) for _ in range(8)]
+    e = xs[0]
+    for t in xs[1:]:
+        e = BinaryExpr("add", t, UnaryExpr("tanh", e))
+    out, ref = eval_both(e)
+    assert ((ulp(out, ref) <= 8) | (np.abs(out - ref) < 1e-6)).all()
+    xl = T(np.linspace(-1, 1, 97, dtype=np.float32))
+    e = xl
+    for _ in range(20):
+        e = e.mul(0.99).add(xl)
+    out, ref = eval_both(e)
+    assert ulp(out, ref).max() == 0
+    xr = rng.uniform(0.9, 1.1, (3, 10, 7)).astype(np.float32)
+    for op in ["sum", "mean", "prod", "reduce_max", "reduce_min"]:
+        for axes, keep in [((), False), ((), True), ((0,), False), ((1,), True), ((2,), False)]:
+            out, ref = eval_both(ReduceExpr(op, T(xr).mul(T(xr)), axes, keep))
+            assert np.allclose(out, ref, rtol=1e-4), (op, axes, keep)
+    xm = rng.standard_normal((6, 70)).astype(np.float32)
+    out, ref = eval_both(T(xm).sub(ReduceExpr("mean", T(xm), (1,), True)).exp())
+    assert np.allclose(out, ref, rtol=1e-5, atol=1e-6)
+    a64 = rng.standard_normal((5, 7))
+    b64 = rng.standard_normal((7,))
+    out, ref = eval_both(BinaryExpr("add", T(a64, np.float64), T(b64, np.float64)).exp().mul(T(a64, np.float64)))
+    assert np.allclose(out, ref, rtol=1e-14)
+    for n in (1, 3, 5, 255, 1027):
+        out, ref = eval_both(T(np.arange(n, dtype=np.float32)).add(1.0).exp())
+        assert (ulp(out, ref) <= 2).all()
+    out, _ = eval_both(ReduceExpr("sum", T(np.zeros(0, np.float32))))
+    assert float(out) == 0.0
+    A = rng.uniform(-1, 1, (16, 64)).astype(np.float32)
+    bb = rng.uniform(-1, 1, 64).astype(np.float32)
+    c = rng.uniform(-1, 1, (16, 64)).astype(np.float32)
+    out, _ = eval_both(BinaryExpr("add", T(A), T(bb)).mul(T(c)).exp())
+    assert ulp(out, oracle.chain_add_mul_exp(A, bb, c)).max() <= 2
+
+
+def problem(seed, m, k, n, scale=1.0):
+    rng = np.random.default_rng(seed)
+    a = (rng.standard_normal((m, k)) * scale).astype(np.float32)
+    q = rng.integers(-127, 128, size=(n, k)).astype(np.int8)
+    s = np.array([oracle.f32_to_f16(v) for v in rng.uniform(0.001, 0.02, n).astype(np.float32)], np.uint16)
+    bias = rng.uniform(-0.1, 0.1, n).astype(np.float32)
+    return a, q, s, bias
+
+
+def linear(a, q, s, bias, out_dt, epi, res=None, g=None, b=None):
+    m, k = a.shape
+    n = q.shape[0]
+    c = np.empty((m, n), out_dt)
+    adt = _abi.F16 if a.dtype == np.float16 else _abi.F32
+    cdt = _abi.F16 if out_dt == np.float16 else _abi.F32
+    ptr = lambda x: None if x is None else x.ctypes.data
+    check(L.tzh_linear_w8(CTX, a.ctypes.data, adt, q.ctypes.data, s.ctypes.data, ptr(bias), c.ctypes.data, cdt, m, k,
+                          n, epi, ptr(res), cdt, ptr(g), ptr(b), 1e-12))
+    return c.astype(np.float32)
+
+
+def group_gemm():
+    for m, k, n in [(1, 64, 128), (5, 384, 384), (133, 384, 1152), (70, 1536, 384)]:
+        a, q, s, bias = problem(m + n, m, k, n)
+        c = np.empty((m, n), np.float32)
+        check(L.tzh_matmul_w8a32(CTX, a.ctypes.data, q.ctypes.data, s.ctypes.data, bias.ctypes.data, c.ctypes.data, m,
+                                 k, n))
+        ref = oracle.matmul_w8a32(a, q, s, bias)
+        sf = s.view(np.float16).astype(np.float64)
+        bound = (np.abs(a) @ np.abs(q.astype(np.float64)).T) * sf * (2 ** -10 + k * 2 ** -23) + 1e-6
+        assert (np.abs(c - ref) <= bound).all(), (m, k, n)
+    a, q, s, bias = problem(5, 77, 384, 1152)
+    a16 = a.astype(np.float16)
+    c = linear(a16, q, s, bias, np.float16, _abi.EPI_BIAS)
+    ref = oracle.matmul_w8a32(a16.astype(np.float32), q, s, bias)
+    assert np.abs(c - ref).max() < 2e-2 * np.abs(ref).max()
+    a, q, s, bias = problem(6, 40, 384, 1536, 0.05)
+    c = linear(a, q, s, bias, np.float32, _abi.EPI_BIAS_GELU)
+    lin = oracle.matmul_w8a32(a, q, s, bias)
+    sf = s.view(np.float16).astype(np.float64)
+    bound = (np.abs(a) @ np.abs(q.astype(np.float64)).T) * sf * (2 ** -10 + 384 * 2 ** -23) * 1.13 + 1e-6
+    err = np.abs(c - oracle.gelu(lin))
+    assert (err <= bound).all(), float((err / bound).max())
+    for dt in (np.float32, np.float16):
+        a, q, s, bias = problem(7, 67, 1536, 384, 0.1)
+        rng = np.random.default_rng(8)
+        res = rng.standard_normal((67, 384)).astype(dt)
+        g = (1 + 0.1 * rng.standard_normal(384)).astype(np.float32)
+        b = (0.1 * rng.standard_normal(384)).astype(np.float32)
+        c = linear(a, q, s, bias, dt, _abi.EPI_BIAS_RES_LN, res, g, b)
+        ref = oracle.layernorm(res.astype(np.float32) + oracle.matmul_w8a32(a, q, s, bias), g, b, 1e-12)
+        assert np.abs(c - ref).max() < 2e-2, float(np.abs(c - ref).max())
+    w = (np.random.default_rng(12).standard_normal((64, 384)) * 0.02).astype(np.float32)
+    w[0] = 0
+    qg = np.empty((64, 384), np.int8)
+    sg = np.empty(64, np.uint16)
+    check(L.tzh_quantize_rows(CTX, w.ctypes.data, 64, 384, qg.ctypes.data, sg.ctypes.data))
+    qo, so = oracle.quantize_rows(w)
+    assert np.array_equal(qg, qo) and np.array_equal(sg, so)
+    x = np.random.default_rng(13).standard_normal((9, 384)).astype(np.float32)
+    gg = np.ones(384, np.float32)
+    bt = np.zeros(384, np.float32)
+    y = x.copy()
+    check(L.tzh_layernorm_last_dim(CTX, y.ctypes.data, gg.ctypes.data, bt.ctypes.data, y.ctypes.data, 9, 384, 1e-12))
+    assert np.allclose(y, oracle.layernorm(x, gg, bt, 1e-12), atol=1e-4)
+
+
+def group_attention():
+    H, D = 384, 32
+    for lengths in ([1], [2, 3], [15, 16, 17], [63, 64, 65], [100, 1, 130]):
+        rng = np.random.default_rng(sum(lengths))
+        Tn = sum(lengths)
+        qkv = (rng.standard_normal((Tn, 3 * H)) * 1.5).astype(np.float16)
+        cu = np.zeros(len(lengths) + 1, np.int32)
+        cu[1:] = np.cumsum(lengths)
+        out = np.zeros((Tn, H), np.float16)
+        check(L.tzh_attention_varlen(CTX, qkv.ctypes.data, out.ctypes.data, cu.ctypes.data, len(lengths), 12, H))
+        q32 = qkv.astype(np.float32)
+        for bi, Ln in enumerate(lengths):
+            s0 = cu[bi]
+            for h in (0, 7, 11):
+                ref = oracle.attention_head(q32[s0:s0 + Ln, h * D:(h + 1) * D], q32[s0:s0 + Ln, H + h * D:H + (h + 1) * D],
+                                            q32[s0:s0 + Ln, 2 * H + h * D:2 * H + (h + 1) * D])
+                got = out[s0:s0 + Ln, h * D:(h + 1) * D].astype(np.float32)
+                v = q32[s0:s0 + Ln, 2 * H + h * D:2 * H + (h + 1) * D]
+                assert (np.abs(got - ref) <= 2 ** -9 * np.abs(v).max() + 2 ** -10 * np.abs(ref)).all(), (lengths, bi, h)
+
+
+def group_arctic():
+    cfg = synth.Config()
+    w = synth.quantize(synth.make_arctic_f32(1234, cfg, ln_random=True))
+    hw = synth.HostWeights(w, cfg)
+    m = C.c_void_p()
+    check(L.tzh_arctic_upload(CTX, C.byref(hw.struct), C.byref(m)))
+    ids, lengths = synth.make_batch(21, 3, seq_len=40, min_len=5)
+    out = np.empty((3, 384), np.float32)
+    check(L.tzh_arctic_forward_batch(m, out.ctypes.data, ids.ctypes.data, lengths.ctypes.data, 3, 40))
+    ref = np.stack([oracle.arctic_forward(hw, ids[b, :Ln]) for b, Ln in enumerate(lengths)])
+    err = np.abs(out - ref).max()
+    print(f"  arctic emu vs oracle max-abs {err:.2e}", flush=True)
+    assert err < 1e-3
+    hid = np.empty((int(lengths.sum()), 384), np.float32)
+    check(L.tzh_arctic_hidden(m, hid.ctypes.data, ids.ctypes.data, lengths.ctypes.data, 3, 40, 1))
+    r1 = oracle.arctic_hidden(hw, ids[0, :lengths[0]], 1)
+    assert np.abs(hid[:lengths[0]] - r1).max() < 2e-2
+    flat, _ = synth.packed(ids, lengths)
+    out2 = np.empty((3, 384), np.float32)
+    check(L.tzh_arctic_forward_batch(m, out2.ctypes.data, flat.ctypes.data, lengths.ctypes.data, 3, 0))
+    assert np.array_equal(out, out2)
+    bad = ids.copy()
+    bad[1, 2] = 99999
+    check(L.tzh_arctic_forward_batch(m, out2.ctypes.data, bad.ctypes.data, lengths.ctypes.data, 3, 40))
+    n = C.c_int32()
+    check(L.tzh_arctic_bad_id_count(m, C.byref(n)))
+    assert n.value == 1
+    check(L.tzh_arctic_free(m))
+
+
+GROUPS = {"eval": group_eval, "gemm": group_gemm, "attention": group_attention, "arctic": group_arctic}
+
+if __name__ == "__main__":
+    check(L.tzh_init(0, None, C.byref(CTX)))
+    names = sys.argv[1:] or list(GROUPS)
+    for name in names:
+        t0 = time.time()
+        GROUPS[name]()
+        print(f"emu {name}: ok ({time.time() - t0:.1f}s)", flush=True)
+    check(L.tzh_destroy(CTX))
+    print("EMU CHECKS PASSED", flush=True)

@@ -1,0 +1,211 @@
+// TEST INFRASTRUCTURE ONLY: a CPU emulation of the subset of HIP that
+// libtenzor_hip's sources use, so the same kernel sources can be compiled
+// for the host (with AddressSanitizer) and every launch executed on the CPU
+// with its real grid/block shape.  Each lane is a fiber; wave-wide operations
+// (shuffles, MFMA) and __syncthreads are barriers over the wave / block.  A
+// barrier that can never complete (divergent __syncthreads, a lane that
+// never reaches a shuffle) aborts with the kernel and thread named, which is
+// how a GPU hang would show up here.
+//
+// MFMA operand/result layouts follow the CDNA register layouts the kernels
+// assume: v_mfma_f32_32x32x16_f16 (A: row = lane%32, k = 8*(lane/32)+i;
+// B: col = lane%32, same k; D element e of lane l: row 8*(e/4) + 4*(l/32) +
+// e%4, col l%32) and v_mfma_f32_16x16x32_f16 (A/B: row/col = lane%16,
+// k = 8*(lane/16)+i; D element e: row 4*(l/16)+e, col l%16).
+#pragma once
+
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+#include <cstring>
+
+#define __global__
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __launch_bounds__(...)
+#define __shared__ static
+
+struct dim3 {
+    unsigned x = 1, y = 1, z = 1;
+    dim3() = default;
+    dim3(unsigned a, unsigned b = 1, unsigned c = 1) : x(a), y(b), z(c) {}
+};
+
+struct uint4 {
+    unsigned x, y, z, w;
+};
+struct uint2 {
+    unsigned x, y;
+};
+inline uint4 make_uint4(unsigned a, unsigned b, unsigned c, unsigned d) { return uint4{a, b, c, d}; }
+
+namespace emu {
+extern dim3 g_threadIdx, g_blockIdx, g_blockDim, g_gridDim;
+void syncthreads();
+void wave_barrier();
+int lane_id();
+int wave_id();
+void *wave_slot(int lane);  // 256-byte exchange slot of `lane` in the caller's wave
+void launch(const char *name, dim3 grid, dim3 block, void (*body)(void *), void *ctx);
+}  // namespace emu
+
+#define threadIdx (emu::g_threadIdx)
+#define blockIdx (emu::g_blockIdx)
+#define blockDim (emu::g_blockDim)
+#define gridDim (emu::g_gridDim)
+
+inline void __syncthreads() { emu::syncthreads(); }
+
+template <typename T>
+inline T __shfl_xor(T v, int mask, int width = 64) {
+    static_assert(sizeof(T) <= 256, "slot too small");
+    const int lane = emu::lane_id();
+    std::memcpy(emu::wave_slot(lane), &v, sizeof(T));
+    emu::wave_barrier();
+    const int src = ((lane ^ mask) & (width - 1)) | (lane & ~(width - 1));
+    T r;
+    std::memcpy(&r, emu::wave_slot(src), sizeof(T));
+    emu::wave_barrier();
+    return r;
+}
+
+template <typename T>
+inline T atomicAdd(T *p, T v) {  // fibers are cooperative on one OS thread
+    T old = *p;
+    *p = old + v;
+    return old;
+}
+
+using std::max;
+using std::min;
+inline int min(int a, int b) { return a < b ? a : b; }
+inline int max(int a, int b) { return a > b ? a : b; }
+
+typedef _Float16 emu_half8 __attribute__((ext_vector_type(8)));
+typedef float emu_f32x16 __attribute__((ext_vector_type(16)));
+typedef float emu_f32x4 __attribute__((ext_vector_type(4)));
+
+namespace emu {
+struct MfmaIn {
+    emu_half8 a, b;
+};
+
+inline emu_f32x16 mfma_32x32x16(emu_half8 a, emu_half8 b, emu_f32x16 c) {
+    const int lane = lane_id();
+    MfmaIn in{a, b};
+    std::memcpy(wave_slot(lane), &in, sizeof in);
+    wave_barrier();
+    emu_f32x16 d = c;
+    for (int e = 0; e < 16; e++) {
+        const int row = 8 * (e / 4) + 4 * (lane / 32) + e % 4, col = lane % 32;
+        float acc = 0.0f;
+        for (int k = 0; k < 16; k++) {
+            MfmaIn ai, bi;
+            std::memcpy(&ai, wave_slot(row + 32 * (k / 8)), sizeof ai);
+            std::memcpy(&bi, wave_slot(col + 32 * (k / 8)), sizeof bi);
+            acc += (float)ai.a[k % 8] * (float)bi.b[k % 8];
+        }
+        d[e] += acc;
+    }
+    wave_barrier();
+    return d;
+}
+
+inline emu_f32x4 mfma_16x16x32(emu_half8 a, emu_half8 b, emu_f32x4 c) {
+    const int lane = lane_id();
+    MfmaIn in{a, b};
+    std::memcpy(wave_slot(lane), &in, sizeof in);
+    wave_barrier();
+    emu_f32x4 d = c;
+    for (int e = 0; e < 4; e++) {
+        const int row = 4 * (lane / 16) + e, col = lane % 16;
+        float acc = 0.0f;
+        for (int k = 0; k < 32; k++) {
+            MfmaIn ai, bi;
+            std::memcpy(&ai, wave_slot(row + 16 * (k / 8)), sizeof ai);
+            std::memcpy(&bi, wave_slot(col + 16 * (k / 8)), sizeof bi);
+            acc += (float)ai.a[k % 8] * (float)bi.b[k % 8];
+        }
+        d[e] += acc;
+    }
+    wave_barrier();
+    return d;
+}
+}  // namespace emu
+
+namespace emu {
+inline emu_f32x16 mfma_32x32x16_args(emu_half8 a, emu_half8 b, emu_f32x16 c, int, int, int) {
+    return mfma_32x32x16(a, b, c);
+}
+inline emu_f32x4 mfma_16x16x32_args(emu_half8 a, emu_half8 b, emu_f32x4 c, int, int, int) {
+    return mfma_16x16x32(a, b, c);
+}
+}  // namespace emu
+// variadic so that brace-initialised operands (which contain commas) pass through
+#define __builtin_amdgcn_mfma_f32_32x32x16_f16(...) emu::mfma_32x32x16_args(__VA_ARGS__)
+#define __builtin_amdgcn_mfma_f32_16x16x32_f16(...) emu::mfma_16x16x32_args(__VA_ARGS__)
+#define __builtin_amdgcn_exp2f(x) exp2f(x)
+
+// ---------------------------------------------------------------------------
+// runtime API subset
+// ---------------------------------------------------------------------------
+typedef int hipError_t;
+enum { hipSuccess = 0, hipErrorInvalidValue = 1, hipErrorOutOfMemory = 2, hipErrorNoDevice = 100 };
+typedef struct emu_stream *hipStream_t;
+typedef struct emu_event *hipEvent_t;
+enum hipMemcpyKind { hipMemcpyHostToHost, hipMemcpyHostToDevice, hipMemcpyDeviceToHost, hipMemcpyDeviceToDevice };
+#define hipEventDisableTiming 2u
+#define hipHostMallocDefault 0u
+#define hipStreamNonBlocking 1u
+
+struct hipDeviceProp_t {
+    char gcnArchName[256];
+    int multiProcessorCount;
+};
+
+hipError_t hipGetDeviceCount(int *n);
+hipError_t hipSetDevice(int d);
+hipError_t hipGetDeviceProperties(hipDeviceProp_t *p, int d);
+hipError_t hipMalloc(void **p, size_t n);
+hipError_t hipFree(void *p);
+hipError_t hipHostMalloc(void **p, size_t n, unsigned flags);
+hipError_t hipHostFree(void *p);
+hipError_t hipMemcpy(void *d, const void *s, size_t n, hipMemcpyKind k);
+hipError_t hipMemcpyAsync(void *d, const void *s, size_t n, hipMemcpyKind k, hipStream_t st);
+hipError_t hipMemset(void *p, int v, size_t n);
+hipError_t hipStreamSynchronize(hipStream_t s);
+hipError_t hipStreamCreateWithFlags(hipStream_t *s, unsigned f);
+hipError_t hipStreamDestroy(hipStream_t s);
+hipError_t hipEventCreateWithFlags(hipEvent_t *e, unsigned f);
+hipError_t hipEventDestroy(hipEvent_t e);
+hipError_t hipEventRecord(hipEvent_t e, hipStream_t s);
+hipError_t hipEventSynchronize(hipEvent_t e);
+hipError_t hipGetLastError();
+const char *hipGetErrorString(hipError_t e);
+
+// hipLaunchKernelGGL(kernel, grid, block, shmem, stream, args...): every lane
+// runs `kernel(args...)` in its own fiber.
+#include <tuple>
+#include <utility>
+namespace emu {
+template <typename F, typename Tup>
+struct LaunchCtx {
+    F f;
+    Tup args;
+};
+template <typename F, typename Tup>
+void launch_body(void *p) {
+    auto *c = static_cast<LaunchCtx<F, Tup> *>(p);
+    std::apply(c->f, c->args);
+}
+template <typename F, typename... A>
+void launch_kernel(const char *name, F f, dim3 g, dim3 b, A &&...args) {
+    using Tup = std::tuple<std::decay_t<A>...>;
+    LaunchCtx<F, Tup> ctx{f, Tup(std::forward<A>(args)...)};
+    launch(name, g, b, &launch_body<F, Tup>, &ctx);
+}
+}  // namespace emu
+
+#define hipLaunchKernelGGL(kernel, grid, block, shmem, stream, ...) \
+    emu::launch_kernel(#kernel, (kernel), dim3(grid), dim3(block), __VA_ARGS__)

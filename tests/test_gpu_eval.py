@@ -1,0 +1,244 @@
+"""GPU parity of tzh_eval_into (K1 chain / reduce kernels) against the oracle
+executor (executor.zig:29-360 restated in oracle.c), plus the reference's
+own known-answer tests (executor.zig:605-740, reduce.zig:241-350)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tenzor_amd import TzhError, _abi
+from tenzor_amd.expr import BinaryExpr, ReduceExpr, ScalarExpr, Tensor, UnaryExpr, eval, evalInto, to_tape
+from tests.conftest import ulp_diff
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def T(x, dtype=torch.float32):
+    return Tensor(torch.as_tensor(np.asarray(x), dtype=dtype).to(DEV).contiguous())
+
+
+def run_both(expr, ctx):
+    """(gpu result, oracle result) as numpy arrays."""
+    out = eval(expr, ctx).cpu().numpy()
+    nodes, leaves = to_tape(expr)
+    rc, ref = oracle.eval_tape(nodes, [l.data.cpu().numpy() for l in leaves],
+                               np.float64 if expr.dtype == "float64" else np.float32)
+    assert rc == 0
+    return out, ref
+
+
+# ---------------------------------------------------------------- known answers
+def test_eval_unary_relu(ctx):  # executor.zig:616-631
+    out = eval(UnaryExpr("relu", T([-2, -1, 1, 2])), ctx).cpu().numpy()
+    np.testing.assert_allclose(out, [0, 0, 1, 2], atol=1e-6)
+
+
+def test_eval_binary_add(ctx):  # executor.zig:633-650
+    out = eval(BinaryExpr("add", T([1, 2, 3, 4]), T([10, 20, 30, 40])), ctx).cpu().numpy()
+    assert out.tolist() == [11, 22, 33, 44]
+
+
+def test_eval_chained_expression(ctx):  # executor.zig:652-673
+    e = UnaryExpr("relu", BinaryExpr("add", T([-1, 2, -3, 4]), T([1, 1, 1, 1])))
+    assert eval(e, ctx).cpu().numpy().tolist() == [0, 3, 0, 5]
+
+
+def test_eval_reduce_sum(ctx):  # executor.zig:694-706
+    out = eval(ReduceExpr("sum", T([1, 2, 3, 4])), ctx).cpu().numpy()
+    assert out.shape == () and abs(float(out) - 10) < 1e-6
+
+
+@pytest.mark.parametrize("op,axis,data,expected", [
+    ("sum", 1, [[1, 2, 3], [4, 5, 6]], [6, 15]),       # reduce.zig:292-301
+    ("sum", 0, [[1, 2, 3], [4, 5, 6]], [5, 7, 9]),     # reduce.zig:303-313
+    ("mean", 1, [[1, 2, 3], [4, 5, 6]], [2, 5]),       # reduce.zig:315-323
+    ("reduce_max", 1, [[1, 5, 3], [4, 2, 6]], [5, 6]), # reduce.zig:325-333
+])
+def test_eval_reduce_axis_known(ctx, op, axis, data, expected):
+    out = eval(ReduceExpr(op, T(data), (axis,)), ctx).cpu().numpy()
+    np.testing.assert_allclose(out, expected, atol=1e-6)
+
+
+def test_eval_reduce_empty(ctx):  # reduce.zig:345-349
+    e = torch.empty(0, device=DEV)
+    assert float(eval(ReduceExpr("sum", Tensor(e)), ctx).cpu()) == 0.0
+    assert float(eval(ReduceExpr("prod", Tensor(e)), ctx).cpu()) == 1.0
+
+
+def test_elementwise_known(ctx):  # elementwise.zig:363-372, 437-447
+    out = eval(UnaryExpr("exp", T([0.0, 1.0])), ctx).cpu().numpy()
+    assert abs(out[0] - 1.0) < 1e-6 and abs(out[1] - 2.71828) < 1e-4
+    s = eval(UnaryExpr("sigmoid", T([-100.0, 0.0, 100.0, 1.0])), ctx).cpu().numpy()
+    np.testing.assert_allclose(s[:3], [0, 0.5, 1], atol=1e-6)
+    assert abs(s[3] - 0.7310586) < 1e-5
+
+
+# ---------------------------------------------------------------- oracle parity
+EXACT_UNARY = ["neg", "abs", "relu", "floor", "ceil", "round", "sqrt", "rsqrt"]
+TRANSC_UNARY = ["exp", "log", "sin", "cos", "tanh", "sigmoid", "gelu", "silu", "softplus"]
+
+
+@pytest.mark.parametrize("op", EXACT_UNARY + TRANSC_UNARY)
+def test_unary_ops_vs_oracle(ctx, op):
+    rng = np.random.default_rng(1)
+    x = rng.uniform(-4, 4, size=5003).astype(np.float32)
+    if op in ("log", "sqrt", "rsqrt"):
+        x = np.abs(x) + np.float32(1e-3)
+    if op == "round":
+        x = np.concatenate([x, np.array([0.5, -0.5, 1.5, -2.5, 2.5], np.float32)])
+    out, ref = run_both(UnaryExpr(op, T(x)), ctx)
+    d = ulp_diff(out, ref)
+    # correctly rounded ops must match bit for bit; transcendental ones within
+    # the device library's error (a few ulp, or tiny absolute near zero)
+    if op in EXACT_UNARY:
+        assert d.max() == 0, (op, d.max())
+    else:
+        close = (d <= 4) | (np.abs(out - ref) <= 1e-7)
+        assert close.all(), (op, int(d.max()))
+
+
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "max", "min", "pow"])
+def test_binary_ops_vs_oracle(ctx, op):
+    rng = np.random.default_rng(2)
+    a = rng.uniform(-3, 3, size=(37, 129)).astype(np.float32)
+    b = rng.uniform(-3, 3, size=(37, 129)).astype(np.float32)
+    if op == "pow":
+        a = np.abs(a) + np.float32(0.1)
+    out, ref = run_both(BinaryExpr(op, T(a), T(b)), ctx)
+    d = ulp_diff(out, ref)
+    if op == "pow":
+        assert ((d <= 4) | (np.abs(out - ref) <= 1e-7)).all()
+    else:
+        assert d.max() == 0, op
+
+
+@pytest.mark.parametrize("lshape,rshape", [
+    ((64, 128), (128,)),       # row vector (config 2 pattern)
+    ((64, 128), (64, 1)),      # column vector
+    ((64, 128), ()),           # scalar leaf
+    ((4, 1, 6), (3, 1)),       # both sides broadcast -> [4,3,6]
+    ((2, 3, 4, 5), (3, 1, 5)), # non-contiguous broadcast run (general path)
+    ((7,), (5, 1)),            # outer product shape
+    ((3, 5), (3, 5)),
+])
+def test_broadcast_vs_oracle(ctx, lshape, rshape):
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal(lshape).astype(np.float32)
+    b = rng.standard_normal(rshape).astype(np.float32)
+    e = BinaryExpr("add", T(a), T(b)).mul(T(b)).sub(T(a))
+    out, ref = run_both(e, ctx)
+    assert out.shape == np.broadcast_shapes(lshape, rshape)
+    assert ulp_diff(out, ref).max() == 0
+
+
+def test_scalar_constants(ctx):
+    x = np.linspace(-2, 2, 1001, dtype=np.float32)
+    e = T(x).mul(2.5).add(ScalarExpr(-1.0)).maximum(0.0)
+    out, ref = run_both(e, ctx)
+    assert ulp_diff(out, ref).max() == 0
+
+
+def test_deep_tree_materialises_and_matches(ctx):
+    """Right-deep nesting needs more stack than the kernel has: the planner
+    evaluates subtrees first; results must not change."""
+    rng = np.random.default_rng(4)
+    xs = [T(rng.standard_normal((33, 65)).astype(np.float32)) for _ in range(8)]
+    e = xs[0]
+    for x in xs[1:]:
+        e = BinaryExpr("add", x, UnaryExpr("tanh", e))  # right operand grows
+    out, ref = run_both(e, ctx)
+    assert ((ulp_diff(out, ref) <= 8) | (np.abs(out - ref) < 1e-6)).all()
+
+
+def test_long_chain_over_32_nodes(ctx):
+    x = T(np.linspace(-1, 1, 4097, dtype=np.float32))
+    e = x
+    for i in range(20):
+        e = e.mul(0.99).add(x)
+    out, ref = run_both(e, ctx)
+    assert ulp_diff(out, ref).max() == 0
+
+
+@pytest.mark.parametrize("op", ["sum", "mean", "prod", "reduce_max", "reduce_min"])
+@pytest.mark.parametrize("axes,keep", [((), False), ((), True), ((0,), False), ((1,), True), ((2,), False)])
+def test_reduce_vs_oracle(ctx, op, axes, keep):
+    rng = np.random.default_rng(5)
+    x = rng.uniform(0.9, 1.1, size=(6, 50, 33)).astype(np.float32)
+    e = ReduceExpr(op, T(x).mul(T(x)), axes, keep)  # chain fused into the reduction
+    out, ref = run_both(e, ctx)
+    assert out.shape == ref.shape
+    np.testing.assert_allclose(out, ref, rtol=2e-5 if op != "prod" else 2e-4)
+
+
+def test_reduce_feeds_chain(ctx):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((40, 300)).astype(np.float32)
+    e = T(x).sub(ReduceExpr("mean", T(x), (1,), True)).exp()  # materialised reduce -> leaf
+    out, ref = run_both(e, ctx)
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_f64_chain(ctx):
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((17, 31))
+    b = rng.standard_normal((31,))
+    e = BinaryExpr("add", T(a, torch.float64), T(b, torch.float64)).exp().mul(T(a, torch.float64))
+    out, ref = run_both(e, ctx)
+    np.testing.assert_allclose(out, ref, rtol=1e-14, atol=1e-15)
+
+
+def test_tail_and_empty(ctx):
+    for n in (1, 3, 5, 255, 1027):
+        x = np.arange(n, dtype=np.float32)
+        out, ref = run_both(T(x).add(1.0).exp(), ctx)
+        assert ((ulp_diff(out, ref) <= 2)).all()
+    z = torch.empty(0, 4, device=DEV)
+    assert eval(Tensor(z).add(1.0), ctx).numel() == 0
+
+
+def test_errors_mirror_compile_errors(ctx):
+    with pytest.raises(ValueError):
+        BinaryExpr("add", T(np.zeros((2, 3))), T(np.zeros((4,))))
+    with pytest.raises(TypeError):
+        BinaryExpr("add", T(np.zeros(3)), T(np.zeros(3), torch.float64))
+    # an op the CPU executor rejects at comptime (elementwise.zig:143) is rejected here too
+    with pytest.raises(TzhError) as ei:
+        eval(UnaryExpr("exp2", T(np.zeros(3))), ctx)
+    assert ei.value.code == _abi.ERR_UNSUPPORTED_OP
+    with pytest.raises(TzhError) as ei:
+        eval(ReduceExpr("variance", T(np.zeros(3))), ctx)
+    assert ei.value.code == _abi.ERR_UNSUPPORTED_OP
+
+
+def test_config2_chain_medium(ctx):
+    """exp((A + b) * c) at 2048 x 4096 against the three-pass oracle."""
+    g = torch.Generator(device=DEV).manual_seed(11)
+    A = torch.rand(2048, 4096, device=DEV, generator=g) * 2 - 1
+    b = torch.rand(4096, device=DEV, generator=g) * 2 - 1
+    c = torch.rand(2048, 4096, device=DEV, generator=g) * 2 - 1
+    out = torch.empty_like(A)
+    evalInto(BinaryExpr("add", Tensor(A), Tensor(b)).mul(Tensor(c)).exp(), out, ctx)
+    ref = oracle.chain_add_mul_exp(A.cpu().numpy(), b.cpu().numpy(), c.cpu().numpy())
+    d = ulp_diff(out.cpu().numpy(), ref)
+    assert d.max() <= 2, int(d.max())
+
+
+def test_config2_chain_full_size(ctx):
+    """BASELINE config 2 at its full 16384 x 16384 size."""
+    n = 16384
+    g = torch.Generator(device=DEV).manual_seed(12)
+    A = torch.rand(n, n, device=DEV, generator=g) * 2 - 1
+    b = torch.rand(n, device=DEV, generator=g) * 2 - 1
+    c = torch.rand(n, n, device=DEV, generator=g) * 2 - 1
+    out = torch.empty_like(A)
+    evalInto(BinaryExpr("add", Tensor(A), Tensor(b)).mul(Tensor(c)).exp(), out, ctx)
+    torch.cuda.synchronize()
+    # exact property over every element: out > 0 and finite (|(a+b)c| <= 2)
+    assert bool(torch.isfinite(out).all()) and float(out.min()) > 0
+    # oracle parity on a row band (rows are independent)
+    rows = slice(8000, 8256)
+    ref = oracle.chain_add_mul_exp(A[rows].cpu().numpy(), b.cpu().numpy(), c[rows].cpu().numpy())
+    assert ulp_diff(out[rows].cpu().numpy(), ref).max() <= 2
+    del A, c, out
