@@ -94,9 +94,10 @@ void orc_quantize_rows(const float *w, int64_t rows, int64_t cols, int8_t *q, ui
         float inv_s = 1.0f / orc_f16_to_f32(s_f16); /* :165 */
         for (int64_t c = 0; c < cols; c++) {        /* :166-172 */
             float qf = roundf(row[c] * inv_s);        /* @round: half away from zero */
-            int32_t qi = (int32_t)qf;
-            if (qi > 127) qi = 127;
-            if (qi < -127) qi = -127;
+            /* @intFromFloat then clamp; a zero f16 scale (max_abs < ~3.8e-6)
+             * makes qf +-inf or NaN, where the reference is undefined (a
+             * safety panic): saturate to +-127, NaN (0 * inf) to 0 */
+            int32_t qi = isnan(qf) ? 0 : qf >= 127.0f ? 127 : qf <= -127.0f ? -127 : (int32_t)qf;
             q[r * cols + c] = (int8_t)qi;
         }
     }

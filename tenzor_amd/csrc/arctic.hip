@@ -166,8 +166,8 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const float *__restr
     const float inv = 1.0f / (float)s16;
     for (int64_t c = lane; c < cols; c += 64) {
         const float qf = roundf(row[c] * inv);
-        int qi = (int)qf;
-        qi = qi > 127 ? 127 : (qi < -127 ? -127 : qi);
+        // same saturation as the host quantizer for a zero f16 scale
+        const int qi = isnan(qf) ? 0 : qf >= 127.0f ? 127 : qf <= -127.0f ? -127 : (int)qf;
         q[r * cols + c] = (int8_t)qi;
     }
 }

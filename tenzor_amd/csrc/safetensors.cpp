@@ -293,8 +293,9 @@ extern "C" int tzh_quantize_rows_host(const float *w, int64_t rows, int64_t cols
         const float inv = 1.0f / tzh_host_f16_to_f32(s16);
         for (int64_t c = 0; c < cols; c++) {
             const float qf = std::round(row[c] * inv);  // @round: half away from zero
-            int32_t qi = (int32_t)qf;
-            qi = qi > 127 ? 127 : (qi < -127 ? -127 : qi);
+            // clamp before converting: a zero f16 scale gives +-inf / NaN here
+            // (undefined in the reference); saturate to +-127 and map NaN to 0
+            const int32_t qi = std::isnan(qf) ? 0 : qf >= 127.0f ? 127 : qf <= -127.0f ? -127 : (int32_t)qf;
             q[r * cols + c] = (int8_t)qi;
         }
     }

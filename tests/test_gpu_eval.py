@@ -91,12 +91,14 @@ def test_unary_ops_vs_oracle(ctx, op):
     out, ref = run_both(UnaryExpr(op, T(x)), ctx)
     d = ulp_diff(out, ref)
     # correctly rounded ops must match bit for bit; transcendental ones within
-    # the device library's error (a few ulp, or tiny absolute near zero)
+    # the device library's error: a few ulp, or an absolute error of a few
+    # ulp of the O(1) intermediate where the reference formula cancels
+    # (tanh = 2*sigmoid(2x)-1 near 0, softplus = log(1+exp(x)) for x << 0)
     if op in EXACT_UNARY:
         assert d.max() == 0, (op, d.max())
     else:
-        close = (d <= 4) | (np.abs(out - ref) <= 1e-7)
-        assert close.all(), (op, int(d.max()))
+        close = (d <= 4) | (np.abs(out - ref) <= 4 * 2.0 ** -23)
+        assert close.all(), (op, int(d.max()), float(np.abs(out - ref).max()))
 
 
 @pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "max", "min", "pow"])
