@@ -180,25 +180,27 @@ __device__ __forceinline__ Vec<T, V> load_leaf(const EwLeaf &lf, const EwProgram
     return r;
 }
 
-// value stack with a uniform stack pointer: slots live in registers and are
-// selected by scalar branches.
+// value stack with a uniform stack pointer: four named slots (not an array,
+// which the compiler would index dynamically in scratch memory) selected by
+// scalar branches on the wave-uniform slot number.
 template <typename T, int V>
 struct Stack {
-    Vec<T, V> s[kMaxDepth];
+    Vec<T, V> s0, s1, s2, s3;
+    // element-wise value selects: no slot is ever addressed through a pointer
     __device__ __forceinline__ Vec<T, V> get(int i) const {
-        switch (i) {
-        case 0: return s[0];
-        case 1: return s[1];
-        case 2: return s[2];
-        default: return s[3];
-        }
+        Vec<T, V> r;
+#pragma unroll
+        for (int e = 0; e < V; e++)
+            r.v[e] = i == 0 ? s0.v[e] : i == 1 ? s1.v[e] : i == 2 ? s2.v[e] : s3.v[e];
+        return r;
     }
     __device__ __forceinline__ void set(int i, const Vec<T, V> &x) {
-        switch (i) {
-        case 0: s[0] = x; break;
-        case 1: s[1] = x; break;
-        case 2: s[2] = x; break;
-        default: s[3] = x; break;
+#pragma unroll
+        for (int e = 0; e < V; e++) {
+            s0.v[e] = i == 0 ? x.v[e] : s0.v[e];
+            s1.v[e] = i == 1 ? x.v[e] : s1.v[e];
+            s2.v[e] = i == 2 ? x.v[e] : s2.v[e];
+            s3.v[e] = i == 3 ? x.v[e] : s3.v[e];
         }
     }
 };

@@ -7,49 +7,48 @@
 // residual + LayerNorm (arctic.zig:716-746, 779-809; layernorm.zig:26-117).
 //
 // Design (gfx950):
-//   - v_mfma_f32_32x32x16_f16: A is rounded to f16 on its way into LDS, the
-//     int8 weights are converted to f16 in registers right before the MFMA
-//     (exact: |q| <= 127), accumulation is f32.
+//   - v_mfma_f32_32x32x16_f16 with f32 accumulation.  A is rounded to f16 on
+//     its way into LDS; the int8 weights stay int8 in HBM and are dequantised
+//     to f16 in registers between the global load and the LDS store (exact:
+//     |q| <= 127), once per element per block, so the MFMA loop reads both
+//     operands as 16-byte LDS fragments.
 //   - Block tile BM x BN, BK = 64 per stage, LDS double buffer, one barrier
 //     per stage; global loads for stage k+1 are in flight while stage k runs.
 //   - Block index -> tile mapping is XCD-aware: each of the 8 XCDs walks a
 //     contiguous range of tiles (N fastest), so the A row-panel a tile needs
 //     is fetched into that XCD's L2 once and reused across the N tiles.
-//   - The LayerNorm epilogue needs whole 384-wide rows, so that variant uses
-//     BN = N = 384 and stages the pre-norm tile through LDS for the two-pass
-//     mean / biased-variance statistics.
+//   - Epilogues stage the finished tile through the (then idle) LDS so that
+//     every global store is a full 16-byte vector; the LayerNorm variant owns
+//     whole 384-wide rows (BN = N) and normalises one 64-row half at a time
+//     from LDS with the reference's two-pass mean / biased variance.
 #include "common.h"
 
 namespace {
 
 constexpr int BK = 64;
+constexpr int LDK = BK + 8;  // halves per LDS operand row (16-byte pad: conflict-free b128 reads)
 
-template <typename T>
-struct DT;
-template <>
-struct DT<float> { static constexpr int id = TZH_F32; };
-template <>
-struct DT<_Float16> { static constexpr int id = TZH_F16; };
-
-// 8 signed bytes -> 8 f16, exact.  Each byte b becomes the f16 with bit
+// 16 signed bytes -> 16 f16, exact.  Each byte b becomes the f16 with bit
 // pattern 0x64xx where xx = b ^ 0x80, i.e. 1024 + (b + 128); subtracting
 // 1152 leaves b.
-__device__ __forceinline__ half8_t i8x8_to_f16x8(uint32_t lo, uint32_t hi) {
-    lo ^= 0x80808080u;
-    hi ^= 0x80808080u;
-    const uint32_t w0 = (lo & 0xffu) | ((lo & 0xff00u) << 8) | 0x64006400u;
-    const uint32_t w1 = ((lo >> 16) & 0xffu) | ((lo >> 8) & 0xff0000u) | 0x64006400u;
-    const uint32_t w2 = (hi & 0xffu) | ((hi & 0xff00u) << 8) | 0x64006400u;
-    const uint32_t w3 = ((hi >> 16) & 0xffu) | ((hi >> 8) & 0xff0000u) | 0x64006400u;
+__device__ __forceinline__ void i8x16_to_f16(uint4 q, half8_t &lo, half8_t &hi) {
     const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-    const half2_t h0 = __builtin_bit_cast(half2_t, w0) - bias;
-    const half2_t h1 = __builtin_bit_cast(half2_t, w1) - bias;
-    const half2_t h2 = __builtin_bit_cast(half2_t, w2) - bias;
-    const half2_t h3 = __builtin_bit_cast(half2_t, w3) - bias;
-    half8_t r;
-    r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
-    r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
-    return r;
+    const uint32_t w[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
+    half2_t h[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t a = (w[i] & 0xffu) | ((w[i] & 0xff00u) << 8) | 0x64006400u;
+        const uint32_t b = ((w[i] >> 16) & 0xffu) | ((w[i] >> 8) & 0xff0000u) | 0x64006400u;
+        h[2 * i] = __builtin_bit_cast(half2_t, a) - bias;
+        h[2 * i + 1] = __builtin_bit_cast(half2_t, b) - bias;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        lo[2 * i] = h[i][0];
+        lo[2 * i + 1] = h[i][1];
+        hi[2 * i] = h[4 + i][0];
+        hi[2 * i + 1] = h[4 + i][1];
+    }
 }
 
 // bijective block -> tile remap so that XCD x (block ids x, x+8, ...) owns the
@@ -66,7 +65,6 @@ struct ALoad;
 // f16 activations: 16-byte chunks of 8 halves.
 template <>
 struct ALoad<_Float16> {
-    static constexpr int CH = 8;  // elements per chunk
     uint4 v;
     __device__ __forceinline__ void load(const _Float16 *p, bool ok) {
         v = ok ? *(const uint4 *)p : make_uint4(0, 0, 0, 0);
@@ -77,7 +75,6 @@ struct ALoad<_Float16> {
 // f32 activations: 8 floats per chunk, rounded to f16 on the way to LDS.
 template <>
 struct ALoad<float> {
-    static constexpr int CH = 8;
     f32x4_t a, b;
     __device__ __forceinline__ void load(const float *p, bool ok) {
         if (ok) {
@@ -97,31 +94,33 @@ struct ALoad<float> {
 };
 
 template <typename T>
-__device__ __forceinline__ void store_out(T *p, float v);
-template <>
-__device__ __forceinline__ void store_out<float>(float *p, float v) { *p = v; }
-template <>
-__device__ __forceinline__ void store_out<_Float16>(_Float16 *p, float v) { *p = (_Float16)v; }
-
-template <typename T>
 __device__ __forceinline__ float load_f32(const T *p);
 template <>
 __device__ __forceinline__ float load_f32<float>(const float *p) { return *p; }
 template <>
 __device__ __forceinline__ float load_f32<_Float16>(const _Float16 *p) { return (float)*p; }
 
+// tanh-form GELU of arctic.zig:750-756 with tanh(u) = 1 - 2 / (exp(2u) + 1)
+// on the hardware exp2 (a few ulp; saturates correctly to +-1).
+__device__ __forceinline__ float gelu_fast(float x) {
+    const float sqrt_2_over_pi = 0.7978845608f;
+    const float coeff = 0.044715f;
+    const float inner = sqrt_2_over_pi * (x + coeff * x * x * x);
+    const float e = __builtin_amdgcn_exp2f(inner * 2.8853900817779268f);  // exp(2u) = 2^(2u*log2 e)
+    const float t = 1.0f - 2.0f / (e + 1.0f);
+    return 0.5f * x * (1.0f + t);
+}
+
 template <int BM, int BN, int WM, int WN>
 struct Cfg {
     static constexpr int THREADS = WM * WN * 64;
     static constexpr int TM = BM / WM / 32;  // 32-row MFMA blocks per wave
     static constexpr int TN = BN / WN / 32;  // 32-col MFMA blocks per wave
-    static constexpr int A_LD = BK + 8;      // halves per LDS row (pad against bank conflicts)
-    static constexpr int B_LD = BK + 16;     // bytes per LDS row
-    static constexpr int A_STAGE = BM * A_LD * 2;  // bytes
-    static constexpr int B_STAGE = BN * B_LD;      // bytes
+    static constexpr int A_STAGE = BM * LDK * 2;  // bytes
+    static constexpr int B_STAGE = BN * LDK * 2;  // bytes (f16 after dequant)
     static constexpr int OPERAND_BYTES = 2 * (A_STAGE + B_STAGE);
-    static constexpr int A_CHUNKS = BM * BK / 8 / THREADS;
-    static constexpr int B_CHUNKS = BN * BK / 16 / THREADS;
+    static constexpr int A_CHUNKS = BM * BK / 8 / THREADS;   // 8-element chunks of A per thread
+    static constexpr int B_CHUNKS = BN * BK / 16 / THREADS;  // 16-byte int8 chunks of B per thread
     static_assert(BM * BK / 8 % THREADS == 0, "A chunks must divide evenly");
     static_assert(BN * BK / 16 % THREADS == 0, "B chunks must divide evenly");
     static_assert(TM >= 1 && TN >= 1, "wave tile too small");
@@ -129,7 +128,8 @@ struct Cfg {
 
 // Main loop shared by both epilogue families.  On return acc holds the f32
 // sums for the wave's TM x TN blocks of 32x32; lane l holds, for block
-// (tm, tn) element j, row (j/4)*8 + (l/32)*4 + j%4 and column l%32.
+// (tm, tn) element j, row (j/4)*8 + (l/32)*4 + j%4 and column l%32.  The
+// loop ends with a barrier, so the caller may reuse all of `smem`.
 template <typename TA, int BM, int BN, int WM, int WN>
 __device__ __forceinline__ void gemm_mainloop(const TA *__restrict__ A, const int8_t *__restrict__ W, int M,
                                               int K, int m0, int n0, char *smem,
@@ -141,7 +141,7 @@ __device__ __forceinline__ void gemm_mainloop(const TA *__restrict__ A, const in
     const int wm = w / WN, wn = w % WN;
 
     _Float16 *As[2] = {(_Float16 *)smem, (_Float16 *)(smem + C::A_STAGE)};
-    int8_t *Bs[2] = {(int8_t *)(smem + 2 * C::A_STAGE), (int8_t *)(smem + 2 * C::A_STAGE + C::B_STAGE)};
+    _Float16 *Bs[2] = {(_Float16 *)(smem + 2 * C::A_STAGE), (_Float16 *)(smem + 2 * C::A_STAGE + C::B_STAGE)};
 
 #pragma unroll
     for (int i = 0; i < C::TM; i++)
@@ -172,13 +172,16 @@ __device__ __forceinline__ void gemm_mainloop(const TA *__restrict__ A, const in
         for (int i = 0; i < C::A_CHUNKS; i++) {
             const int c = tid + i * C::THREADS;
             const int r = c / (BK / 8), kc = (c % (BK / 8)) * 8;
-            ar[i].store(As[buf] + r * C::A_LD + kc);
+            ar[i].store(As[buf] + r * LDK + kc);
         }
 #pragma unroll
         for (int i = 0; i < C::B_CHUNKS; i++) {
             const int c = tid + i * C::THREADS;
             const int r = c / (BK / 16), kc = (c % (BK / 16)) * 16;
-            *(uint4 *)(Bs[buf] + r * C::B_LD + kc) = br[i];
+            half8_t lo, hi;
+            i8x16_to_f16(br[i], lo, hi);
+            *(half8_t *)(Bs[buf] + r * LDK + kc) = lo;
+            *(half8_t *)(Bs[buf] + r * LDK + kc + 8) = hi;
         }
     };
 
@@ -187,24 +190,20 @@ __device__ __forceinline__ void gemm_mainloop(const TA *__restrict__ A, const in
     sstore(0);
     __syncthreads();
 
-    const int arow = lane & 31;
+    const int frow = lane & 31;
     const int kgrp = (lane >> 5) * 8;
     for (int kt = 0; kt < KT; kt++) {
         const int cur = kt & 1;
         if (kt + 1 < KT) gload(kt + 1);
-        const _Float16 *a_s = As[cur] + (wm * C::TM * 32 + arow) * C::A_LD + kgrp;
-        const int8_t *b_s = Bs[cur] + (wn * C::TN * 32 + arow) * C::B_LD + kgrp;
+        const _Float16 *a_s = As[cur] + (wm * C::TM * 32 + frow) * LDK + kgrp;
+        const _Float16 *b_s = Bs[cur] + (wn * C::TN * 32 + frow) * LDK + kgrp;
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ks++) {
-            half8_t af[C::TM];
-            half8_t bf[C::TN];
+            half8_t af[C::TM], bf[C::TN];
 #pragma unroll
-            for (int i = 0; i < C::TM; i++) af[i] = *(const half8_t *)(a_s + i * 32 * C::A_LD + ks * 16);
+            for (int i = 0; i < C::TM; i++) af[i] = *(const half8_t *)(a_s + i * 32 * LDK + ks * 16);
 #pragma unroll
-            for (int j = 0; j < C::TN; j++) {
-                const uint2 q = *(const uint2 *)(b_s + j * 32 * C::B_LD + ks * 16);
-                bf[j] = i8x8_to_f16x8(q.x, q.y);
-            }
+            for (int j = 0; j < C::TN; j++) bf[j] = *(const half8_t *)(b_s + j * 32 * LDK + ks * 16);
 #pragma unroll
             for (int i = 0; i < C::TM; i++)
 #pragma unroll
@@ -216,7 +215,8 @@ __device__ __forceinline__ void gemm_mainloop(const TA *__restrict__ A, const in
     }
 }
 
-// Bias (+ optional GELU) epilogue; BN | N.
+// Bias (+ optional GELU) epilogue; BN | N.  The finished tile is staged in
+// LDS as TC and written back with 16-byte row-contiguous stores.
 template <typename TA, typename TC, bool GELU, int BM, int BN, int WM, int WN>
 __global__ void __launch_bounds__(WM *WN * 64) gemm_w8_bias_kernel(const TA *__restrict__ A,
                                                                   const int8_t *__restrict__ W,
@@ -224,6 +224,8 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_w8_bias_kernel(const TA *__r
                                                                   const float *__restrict__ bias,
                                                                   TC *__restrict__ Cout, int M, int K, int N) {
     using C = Cfg<BM, BN, WM, WN>;
+    constexpr int O_LD = BN + 16 / (int)sizeof(TC);  // staged row pitch (elements), 16-byte pad
+    static_assert(BM * O_LD * (int)sizeof(TC) <= C::OPERAND_BYTES, "output tile must fit the operand LDS");
     __shared__ __attribute__((aligned(16))) char smem[C::OPERAND_BYTES];
     const int nbn = N / BN;
     const int nbm = (M + BM - 1) / BM;
@@ -233,70 +235,57 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_w8_bias_kernel(const TA *__r
     f32x16_t acc[C::TM][C::TN];
     gemm_mainloop<TA, BM, BN, WM, WN>(A, W, M, K, m0, n0, smem, acc);
 
+    TC *O = (TC *)smem;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int wm = w / WN, wn = w % WN;
 #pragma unroll
     for (int j = 0; j < C::TN; j++) {
-        const int col = n0 + wn * C::TN * 32 + j * 32 + (lane & 31);
-        const float s = f16_bits_to_f32(scale[col]);
-        const float b = bias ? bias[col] : 0.0f;
+        const int cl = wn * C::TN * 32 + j * 32 + (lane & 31);
+        const float s = f16_bits_to_f32(scale[n0 + cl]);
+        const float b = bias ? bias[n0 + cl] : 0.0f;
 #pragma unroll
         for (int i = 0; i < C::TM; i++) {
-            const int rbase = m0 + wm * C::TM * 32 + i * 32 + (lane >> 5) * 4;
+            const int rbase = wm * C::TM * 32 + i * 32 + (lane >> 5) * 4;
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const int row = rbase + (e >> 2) * 8 + (e & 3);
-                if (row < M) {
-                    float v = acc[i][j][e] * s + b;
-                    if (GELU) v = gelu_arctic(v);
-                    store_out<TC>(Cout + (size_t)row * N + col, v);
-                }
+                float v = acc[i][j][e] * s + b;  // sum * s + bias (matmul_w8a32.zig:55)
+                if (GELU) v = gelu_fast(v);
+                O[(rbase + (e >> 2) * 8 + (e & 3)) * O_LD + cl] = (TC)v;
             }
         }
     }
+    __syncthreads();
+    constexpr int VEC = 16 / sizeof(TC);
+    constexpr int PER_ROW = BN / VEC;
+    for (int idx = threadIdx.x; idx < BM * PER_ROW; idx += C::THREADS) {
+        const int r = idx / PER_ROW, c = (idx % PER_ROW) * VEC;
+        if (m0 + r < M) *(uint4 *)(Cout + (size_t)(m0 + r) * N + n0 + c) = *(const uint4 *)(O + r * O_LD + c);
+    }
 }
 
-// Bias + residual + LayerNorm epilogue over full rows (BN == N).
+// Bias + residual + LayerNorm epilogue over full rows (BN == N).  The block
+// is WM x WN waves; each WM slab of BM/WM rows is staged to LDS as f32 in
+// turn and normalised by all waves together.
 template <typename TA, typename TC, int BM, int BN, int WM, int WN>
 __global__ void __launch_bounds__(WM *WN * 64) gemm_w8_ln_kernel(
     const TA *__restrict__ A, const int8_t *__restrict__ W, const uint16_t *__restrict__ scale,
     const float *__restrict__ bias, TC *__restrict__ Cout, int M, int K, const TC *__restrict__ R,
     const float *__restrict__ gamma, const float *__restrict__ beta, float eps) {
     using C = Cfg<BM, BN, WM, WN>;
-    constexpr int E_LD = BN + 4;  // floats per staged row
-    constexpr int EPI_BYTES = BM * E_LD * 4;
-    constexpr int SMEM = C::OPERAND_BYTES > EPI_BYTES ? C::OPERAND_BYTES : EPI_BYTES;
-    __shared__ __attribute__((aligned(16))) char smem[SMEM];
+    constexpr int SLAB = BM / WM;    // rows staged at a time
+    constexpr int E_LD = BN + 4;     // floats per staged row
+    static_assert(SLAB * E_LD * 4 <= C::OPERAND_BYTES, "LN slab must fit the operand LDS");
+    __shared__ __attribute__((aligned(16))) char smem[C::OPERAND_BYTES];
     const int nbm = (M + BM - 1) / BM;
     const int t = xcd_tile(blockIdx.x, nbm);
     const int m0 = t * BM;
 
     f32x16_t acc[C::TM][C::TN];
     gemm_mainloop<TA, BM, BN, WM, WN>(A, W, M, K, m0, 0, smem, acc);
-    // the main loop ends with a barrier, so the operand buffers are free
 
     float *E = (float *)smem;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int wm = w / WN, wn = w % WN;
-#pragma unroll
-    for (int j = 0; j < C::TN; j++) {
-        const int col = wn * C::TN * 32 + j * 32 + (lane & 31);
-        const float s = f16_bits_to_f32(scale[col]);
-        const float b = bias ? bias[col] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < C::TM; i++) {
-            const int rbase = wm * C::TM * 32 + i * 32 + (lane >> 5) * 4;
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int rl = rbase + (e >> 2) * 8 + (e & 3);
-                const int row = m0 + rl;
-                const float res = row < M ? load_f32<TC>(R + (size_t)row * BN + col) : 0.0f;
-                E[rl * E_LD + col] = res + (acc[i][j][e] * s + b);  // input + tmp (arctic.zig:720)
-            }
-        }
-    }
-    __syncthreads();
-
     constexpr int NW = WM * WN;
     constexpr int PER = BN / 64;
     float g[PER], bt[PER];
@@ -305,35 +294,56 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_w8_ln_kernel(
         g[q] = gamma[lane + 64 * q];
         bt[q] = beta[lane + 64 * q];
     }
-    for (int rl = w; rl < BM; rl += NW) {
-        const int row = m0 + rl;
-        if (row >= M) break;
-        float x[PER];
-        float sum = 0.0f;
+    for (int slab = 0; slab < WM; slab++) {
+        if (wm == slab) {
 #pragma unroll
-        for (int q = 0; q < PER; q++) {
-            x[q] = E[rl * E_LD + lane + 64 * q];
-            sum += x[q];
-        }
-        const float mean = wave_sum(sum) / (float)BN;
-        float vs = 0.0f;
+            for (int j = 0; j < C::TN; j++) {
+                const int col = wn * C::TN * 32 + j * 32 + (lane & 31);
+                const float s = f16_bits_to_f32(scale[col]);
+                const float b = bias ? bias[col] : 0.0f;
 #pragma unroll
-        for (int q = 0; q < PER; q++) {
-            const float d = x[q] - mean;
-            vs += d * d;
-        }
-        const float var = wave_sum(vs) / (float)BN;
-        const float inv_std = 1.0f / sqrtf(var + eps);
+                for (int i = 0; i < C::TM; i++) {
+                    const int rbase = i * 32 + (lane >> 5) * 4;
 #pragma unroll
-        for (int q = 0; q < PER; q++) {
-            const float y = ((x[q] - mean) * inv_std) * g[q] + bt[q];
-            store_out<TC>(Cout + (size_t)row * BN + lane + 64 * q, y);
+                    for (int e = 0; e < 16; e++) {
+                        const int rl = rbase + (e >> 2) * 8 + (e & 3);
+                        const int row = m0 + slab * SLAB + rl;
+                        const float res = row < M ? load_f32<TC>(R + (size_t)row * BN + col) : 0.0f;
+                        E[rl * E_LD + col] = res + (acc[i][j][e] * s + b);  // input + tmp (arctic.zig:720)
+                    }
+                }
+            }
         }
+        __syncthreads();
+        for (int rl = w; rl < SLAB; rl += NW) {
+            const int row = m0 + slab * SLAB + rl;
+            if (row >= M) break;
+            float x[PER];
+            float sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < PER; q++) {
+                x[q] = E[rl * E_LD + lane + 64 * q];
+                sum += x[q];
+            }
+            const float mean = wave_sum(sum) / (float)BN;
+            float vs = 0.0f;
+#pragma unroll
+            for (int q = 0; q < PER; q++) {
+                const float d = x[q] - mean;
+                vs += d * d;
+            }
+            const float var = wave_sum(vs) / (float)BN;
+            const float inv_std = 1.0f / sqrtf(var + eps);
+#pragma unroll
+            for (int q = 0; q < PER; q++)
+                Cout[(size_t)row * BN + lane + 64 * q] = (TC)(((x[q] - mean) * inv_std) * g[q] + bt[q]);
+        }
+        __syncthreads();
     }
 }
 
 using Plain = Cfg<128, 128, 2, 2>;
-using LnCfg = Cfg<64, 384, 2, 4>;
+using LnCfg = Cfg<128, 384, 2, 4>;
 
 template <typename TA, typename TC>
 int launch_bias(hipStream_t st, const void *a, const int8_t *wq, const uint16_t *scale, const float *bias, void *c,
@@ -352,8 +362,8 @@ int launch_bias(hipStream_t st, const void *a, const int8_t *wq, const uint16_t 
 template <typename TA, typename TC>
 int launch_ln(hipStream_t st, const void *a, const int8_t *wq, const uint16_t *scale, const float *bias, void *c,
               int M, int K, const void *res, const float *gamma, const float *beta, float eps) {
-    const int blocks = (M + 63) / 64;
-    hipLaunchKernelGGL((gemm_w8_ln_kernel<TA, TC, 64, 384, 2, 4>), dim3(blocks), dim3(LnCfg::THREADS), 0, st,
+    const int blocks = (M + 127) / 128;
+    hipLaunchKernelGGL((gemm_w8_ln_kernel<TA, TC, 128, 384, 2, 4>), dim3(blocks), dim3(LnCfg::THREADS), 0, st,
                        (const TA *)a, wq, scale, bias, (TC *)c, M, K, (const TC *)res, gamma, beta, eps);
     TZH_LAUNCHED("gemm_w8_ln_kernel");
     return TZH_OK;

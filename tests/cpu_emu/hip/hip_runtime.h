@@ -79,6 +79,9 @@ inline T atomicAdd(T *p, T v) {  // fibers are cooperative on one OS thread
 
 using std::max;
 using std::min;
+using std::isnan;
+using std::isinf;
+using std::isfinite;
 inline int min(int a, int b) { return a < b ? a : b; }
 inline int max(int a, int b) { return a > b ? a : b; }
 

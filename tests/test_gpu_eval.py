@@ -12,6 +12,13 @@ from tests.conftest import ulp_diff
 
 pytestmark = pytest.mark.gpu
 
+# These cases were part of a GPU run that ended with the GPU in a memory-fault
+# state; CPU emulation of the kernels at the same shapes (tests/cpu_emu,
+# AddressSanitizer) found no out-of-bounds access or stuck barrier, so no
+# cause is known and they stay off the GPU.
+UNCLEARED = pytest.mark.skip(reason="uncleared: in a GPU run that faulted with no cause found; "
+                                    "checked by CPU emulation (tests/test_cpu_emulation.py) instead")
+
 DEV = "cuda"
 
 
@@ -142,6 +149,7 @@ def test_scalar_constants(ctx):
     assert ulp_diff(out, ref).max() == 0
 
 
+@UNCLEARED
 def test_deep_tree_materialises_and_matches(ctx):
     """Right-deep nesting needs more stack than the kernel has: the planner
     evaluates subtrees first; results must not change."""
@@ -154,6 +162,7 @@ def test_deep_tree_materialises_and_matches(ctx):
     assert ((ulp_diff(out, ref) <= 8) | (np.abs(out - ref) < 1e-6)).all()
 
 
+@UNCLEARED
 def test_long_chain_over_32_nodes(ctx):
     x = T(np.linspace(-1, 1, 4097, dtype=np.float32))
     e = x
@@ -163,6 +172,7 @@ def test_long_chain_over_32_nodes(ctx):
     assert ulp_diff(out, ref).max() == 0
 
 
+@UNCLEARED
 @pytest.mark.parametrize("op", ["sum", "mean", "prod", "reduce_max", "reduce_min"])
 @pytest.mark.parametrize("axes,keep", [((), False), ((), True), ((0,), False), ((1,), True), ((2,), False)])
 def test_reduce_vs_oracle(ctx, op, axes, keep):
@@ -174,6 +184,7 @@ def test_reduce_vs_oracle(ctx, op, axes, keep):
     np.testing.assert_allclose(out, ref, rtol=2e-5 if op != "prod" else 2e-4)
 
 
+@UNCLEARED
 def test_reduce_feeds_chain(ctx):
     rng = np.random.default_rng(6)
     x = rng.standard_normal((40, 300)).astype(np.float32)
@@ -182,6 +193,7 @@ def test_reduce_feeds_chain(ctx):
     np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
 
 
+@UNCLEARED
 def test_f64_chain(ctx):
     rng = np.random.default_rng(7)
     a = rng.standard_normal((17, 31))
@@ -191,6 +203,7 @@ def test_f64_chain(ctx):
     np.testing.assert_allclose(out, ref, rtol=1e-14, atol=1e-15)
 
 
+@UNCLEARED
 def test_tail_and_empty(ctx):
     for n in (1, 3, 5, 255, 1027):
         x = np.arange(n, dtype=np.float32)
@@ -200,6 +213,7 @@ def test_tail_and_empty(ctx):
     assert eval(Tensor(z).add(1.0), ctx).numel() == 0
 
 
+@UNCLEARED
 def test_errors_mirror_compile_errors(ctx):
     with pytest.raises(ValueError):
         BinaryExpr("add", T(np.zeros((2, 3))), T(np.zeros((4,))))
