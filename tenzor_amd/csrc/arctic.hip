@@ -23,10 +23,10 @@
 
 #include "safetensors.h"
 
-int tzh_linear_w8_launch(hipStream_t st, const void *a, int32_t a_dtype, const int8_t *wq, const uint16_t *scale,
-                         const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k, int64_t n,
-                         int32_t epilogue, const void *residual, int32_t res_dtype, const float *gamma,
-                         const float *beta, float eps);
+int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc,
+                            const uint16_t *scale, const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k,
+                            int64_t n, int32_t epilogue, const void *res, const float *gamma, const float *beta,
+                            float eps);
 int tzh_attention_launch(hipStream_t st, const _Float16 *qkv, _Float16 *out, const int *cu_seqlens,
                          const int *order, int batch, int n_heads, int hidden);
 
@@ -182,8 +182,10 @@ struct DevTable {
     TableRef ref() const { return TableRef{f32, q8, scale}; }
 };
 
+// int8 codes are kept widened to f16 (exact) on the device: the MFMA consumes
+// f16 and the weights are a tiny share of the traffic.
 struct DevLinear {
-    int8_t *w = nullptr;
+    _Float16 *w = nullptr;
     uint16_t *s = nullptr;
     float *b = nullptr;
 };
@@ -268,18 +270,21 @@ int upload_linear(tzh_model *m, std::initializer_list<std::pair<const tzh_mat_vi
         if (v->cols != cols) return tzh_fail(TZH_ERR_INVALID_ARGS, "%s has %d columns, expected %d", what, v->cols, cols);
         rows += v->rows;
     }
-    std::vector<int8_t> w((size_t)(rows * cols));
+    std::vector<uint16_t> w((size_t)(rows * cols));  // f16 bits of the int8 codes
     std::vector<uint16_t> s((size_t)rows);
     std::vector<float> b((size_t)rows);
+    uint16_t code16[256];
+    for (int c = 0; c < 256; c++) code16[c] = tzh_host_f32_to_f16((float)(int8_t)c);
     int64_t r0 = 0;
     for (auto &pb : parts) {
         const tzh_mat_view *v = pb.first;
-        std::memcpy(w.data() + r0 * cols, v->data, (size_t)v->rows * cols);
+        const int8_t *q = (const int8_t *)v->data;
+        for (size_t i = 0; i < (size_t)v->rows * cols; i++) w[(size_t)r0 * cols + i] = code16[(uint8_t)q[i]];
         std::memcpy(s.data() + r0, v->scale, (size_t)v->rows * 2);
         std::memcpy(b.data() + r0, pb.second, (size_t)v->rows * 4);
         r0 += v->rows;
     }
-    TZH_TRY(upload<int8_t>(m, &out.w, w.data(), w.size()));
+    TZH_TRY(upload<_Float16>(m, &out.w, w.data(), w.size()));
     TZH_TRY(upload<uint16_t>(m, &out.s, s.data(), s.size()));
     return upload<float>(m, &out.b, b.data(), b.size());
 }
@@ -603,15 +608,16 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
     const float eps = m->cfg.layer_norm_eps;
     for (int32_t li = 0; li < n_layers; li++) {
         const DevLayer &d = m->layers[(size_t)li];
-        TZH_TRY(tzh_linear_w8_launch(st, m->h, TZH_F16, d.qkv.w, d.qkv.s, d.qkv.b, m->qkv, TZH_F16, T, H, 3 * H,
-                                     TZH_EPI_BIAS, nullptr, TZH_F16, nullptr, nullptr, 0.0f));
+        const int cus = m->ctx->num_cus;
+        TZH_TRY(tzh_linear_codes_launch(st, cus, m->h, d.qkv.w, d.qkv.s, d.qkv.b, m->qkv, TZH_F16, T, H, 3 * H,
+                                        TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f));
         TZH_TRY(tzh_attention_launch(st, m->qkv, m->attn, d_cu, d_order, batch, 12, H));
-        TZH_TRY(tzh_linear_w8_launch(st, m->attn, TZH_F16, d.o.w, d.o.s, d.o.b, m->h1, TZH_F16, T, H, H,
-                                     TZH_EPI_BIAS_RES_LN, m->h, TZH_F16, d.ln1_g, d.ln1_b, eps));
-        TZH_TRY(tzh_linear_w8_launch(st, m->h1, TZH_F16, d.ffn1.w, d.ffn1.s, d.ffn1.b, m->inter, TZH_F16, T, H, 1536,
-                                     TZH_EPI_BIAS_GELU, nullptr, TZH_F16, nullptr, nullptr, 0.0f));
-        TZH_TRY(tzh_linear_w8_launch(st, m->inter, TZH_F16, d.ffn2.w, d.ffn2.s, d.ffn2.b, m->h, TZH_F16, T, 1536, H,
-                                     TZH_EPI_BIAS_RES_LN, m->h1, TZH_F16, d.ln2_g, d.ln2_b, eps));
+        TZH_TRY(tzh_linear_codes_launch(st, cus, m->attn, d.o.w, d.o.s, d.o.b, m->h1, TZH_F16, T, H, H,
+                                        TZH_EPI_BIAS_RES_LN, m->h, d.ln1_g, d.ln1_b, eps));
+        TZH_TRY(tzh_linear_codes_launch(st, cus, m->h1, d.ffn1.w, d.ffn1.s, d.ffn1.b, m->inter, TZH_F16, T, H, 1536,
+                                        TZH_EPI_BIAS_GELU, nullptr, nullptr, nullptr, 0.0f));
+        TZH_TRY(tzh_linear_codes_launch(st, cus, m->inter, d.ffn2.w, d.ffn2.s, d.ffn2.b, m->h, TZH_F16, T, 1536, H,
+                                        TZH_EPI_BIAS_RES_LN, m->h1, d.ln2_g, d.ln2_b, eps));
         launches += 5;
     }
     if (outputs) {

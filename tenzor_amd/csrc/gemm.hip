@@ -406,12 +406,33 @@ int tzh_linear_w8_launch(hipStream_t st, const void *a, int32_t a_dtype, const i
     return tzh_fail(TZH_ERR_INVALID_ARGS, "unknown epilogue %d", epilogue);
 }
 
+int tzh_widen_codes_launch(hipStream_t st, const int8_t *q, _Float16 *out, int64_t n);
+int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc,
+                            const uint16_t *scale, const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k,
+                            int64_t n, int32_t epilogue, const void *res, const float *gamma, const float *beta,
+                            float eps);
+
 extern "C" int tzh_linear_w8(tzh_ctx *ctx, const void *a, int32_t a_dtype, const int8_t *wq, const uint16_t *scale,
                              const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k, int64_t n,
                              int32_t epilogue, const void *residual, int32_t res_dtype, const float *gamma,
                              const float *beta, float eps) {
     tzh_clear_error();
     TZH_TRY(tzh_ctx_enter(ctx));
+    // f16 activations at the shapes the pipelined kernel covers: widen the
+    // codes once into the context scratch and run the model's kernel
+    auto al16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    const bool pipe_shape =
+        k > 0 && k % 64 == 0 && k <= 65536 && m > 0 && m <= ((int64_t)1 << 30) &&
+        (((epilogue == TZH_EPI_BIAS || epilogue == TZH_EPI_BIAS_GELU) && n > 0 && n % 128 == 0 && n <= 1536) ||
+         (epilogue == TZH_EPI_BIAS_RES_LN && n == 384 && residual && gamma && beta && res_dtype == c_dtype));
+    if (a_dtype == TZH_F16 && (c_dtype == TZH_F16 || c_dtype == TZH_F32) && pipe_shape && a && wq && scale && c &&
+        al16(a) && al16(c) && (!residual || al16(residual))) {
+        void *codes = nullptr;
+        TZH_TRY(tzh_ctx_scratch(ctx, (size_t)(n * k * 2), &codes));
+        TZH_TRY(tzh_widen_codes_launch(ctx->stream, wq, (_Float16 *)codes, n * k));
+        return tzh_linear_codes_launch(ctx->stream, ctx->num_cus, (const _Float16 *)a, (const _Float16 *)codes, scale,
+                                       bias, c, c_dtype, m, k, n, epilogue, residual, gamma, beta, eps);
+    }
     return tzh_linear_w8_launch(ctx->stream, a, a_dtype, wq, scale, bias, c, c_dtype, m, k, n, epilogue, residual,
                                 res_dtype, gamma, beta, eps);
 }

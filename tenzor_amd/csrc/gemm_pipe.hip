@@ -1,0 +1,472 @@
+// K3 fast path: f16 activations x int8-valued weight codes on MFMA, with the
+// operand tiles streamed HBM/L2 -> LDS by the gfx950 direct-to-LDS loads
+// (global_load_lds_dwordx4) through an NS-deep ring of stage buffers.
+//
+//   C[t, n] = epi( (sum_k X[t,k] * Wc[n,k]) * f32(scale[n]) + bias[n] )
+//
+// Wc holds the int8 codes widened to f16 (exact: |q| <= 127), so the sums are
+// those of matmulTransposeB_f32_i8_rowScale_bias (matmul_w8a32.zig:14-57) on
+// f16-rounded activations.  Epilogues: bias, bias + GELU (arctic.zig:771-776),
+// bias + residual + LayerNorm over the full 384-wide row (arctic.zig:716-746,
+// layernorm.zig:26-117, two-pass mean / biased variance).
+//
+// Design:
+//   - The MFMA computes C^T tiles (weights as the A operand, tokens as B):
+//     each lane then owns four consecutive output columns of one token, so
+//     stores are 8-byte (f16) / 16-byte (f32) vectors straight from the
+//     accumulators, and a token's LayerNorm statistics reduce in registers,
+//     across the two half-waves, then across the waves of the row in LDS.
+//   - Persistent blocks (one per CU): the (row panel, column tile) work units
+//     are split into contiguous per-block ranges and the stage ring runs
+//     across unit boundaries, so the next unit's tiles are already in flight
+//     while a unit's epilogue runs.
+//   - Each stage buffer is its own __shared__ array: the compiler can then
+//     tell a read of stage s from the in-flight loads of stages s+1.. and
+//     does not drain the ring before every LDS read.  Stage completion is
+//     tracked with explicit vmcnt waits (in-order counter; every vector
+//     memory op issued after a stage's loads is counted as still pending).
+//   - Rows of each tile are 16-byte-chunk XOR-swizzled so the eight rows an
+//     MFMA fragment read touches per 128-byte LDS window hit eight different
+//     chunks (bank-conflict free ds_read_b128).
+#include <type_traits>
+
+#include "common.h"
+
+namespace {
+
+#ifndef TZH_EMULATION
+// global_load_lds_dwordx4: lane l's 16 bytes at sbase + voff[l] land in LDS
+// at lds_base + 16*l.  Written as asm so that the compiler does not treat
+// the ring's loads as pending LDS writes (it would wait for all of them
+// before every LDS read); completion is tracked with explicit vmcnt waits.
+// M0 is set here and used by nothing else in these kernels.
+__device__ __forceinline__ void dma16(const char *sbase, uint32_t voff, char *lds_base) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds_base;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(voff), "s"(sbase)
+                 : "memory", "m0");
+}
+
+// Workgroup barrier for LDS traffic.  The caller has waited for its own LDS
+// ops (lgkmcnt); the memory clobber keeps the compiler from moving LDS
+// accesses across it, and no fence means no wait for the ring's loads.
+__device__ __forceinline__ void lds_barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+#endif
+
+// Tile of rows x BK halves (k contiguous) as laid out in LDS.
+template <int BK>
+struct TileFmt {
+    static constexpr int CPR = BK / 8;            // 16-byte chunks per row
+    static constexpr int ROW_BYTES = BK * 2;
+    static constexpr int RPI = 64 / CPR;          // rows per DMA instruction (64 lanes x 16 B)
+    static constexpr int RPW = 128 / ROW_BYTES;   // rows sharing one 128-byte window
+    __device__ static __forceinline__ int swz(int r) { return (r / RPW) & (CPR - 1); }
+};
+
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_>
+struct PipeCfg {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, NS = NS_;
+    static constexpr int NW = WM * WN, THREADS = NW * 64;
+    static constexpr int TMF = BM / WM / 32;  // token fragments per wave
+    static constexpr int TNF = BN / WN / 32;  // weight fragments per wave
+    using F = TileFmt<BK>;
+    static constexpr int X_BYTES = BM * BK * 2, W_BYTES = BN * BK * 2, STAGE = X_BYTES + W_BYTES;
+    static constexpr int XG = BM / F::RPI, WG = BN / F::RPI;  // DMA instructions per tile
+    static constexpr int LX = XG / NW, LW = WG / NW, L = LX + LW;
+    static_assert(XG % NW == 0 && WG % NW == 0, "DMA groups must split evenly over the waves");
+    static_assert(TMF >= 1 && TNF >= 1, "wave tile too small");
+    static_assert(NS >= 2 && NS <= 4, "2..4 stages");
+    // LDS of one block (stage ring + parameter table + LayerNorm statistics)
+    // and how many such blocks a CU's 160 KiB holds
+    static constexpr int lds_bytes(bool ln) {
+        return NS * STAGE + (ln ? 4 * BN * 4 + 2 * BM * WN * 4 : 2 * 1536 * 4);
+    }
+    static constexpr int blocks_per_cu(bool ln) {
+        return 163840 / lds_bytes(ln) > 2 ? 2 : 163840 / lds_bytes(ln);
+    }
+};
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding; expcnt left at its maximum).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+// Wait until at most L*A vector memory ops are outstanding, A chosen at run
+// time from {0..AMAX} (the largest A <= ahead).  Loads complete in issue
+// order, so this guarantees every load issued before the last L*A has
+// landed; other ops in flight (epilogue stores) only make it stricter.
+template <int AMAX, int L>
+__device__ __forceinline__ void wait_stage(int ahead) {
+    if constexpr (AMAX == 0) {
+        wait_vm_lgkm0<0>();
+    } else {
+        if (ahead >= AMAX)
+            wait_vm_lgkm0<L * AMAX>();
+        else
+            wait_stage<AMAX - 1, L>(ahead);
+    }
+}
+
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt, expcnt not waited for
+    lds_barrier_only();
+}
+
+__device__ __forceinline__ float gelu_fast(float x) {
+    // tanh-form GELU (arctic.zig:750-756), tanh(u) = 1 - 2 / (exp(2u) + 1)
+    const float inner = 0.7978845608f * (x + 0.044715f * x * x * x);
+    const float e = __builtin_amdgcn_exp2f(inner * 2.8853900817779268f);
+    return 0.5f * x * (2.0f - 2.0f / (e + 1.0f));
+}
+
+template <typename TC>
+__device__ __forceinline__ void store4(TC *p, float a, float b, float c, float d);
+template <>
+__device__ __forceinline__ void store4<_Float16>(_Float16 *p, float a, float b, float c, float d) {
+    half4_t h = {(_Float16)a, (_Float16)b, (_Float16)c, (_Float16)d};
+    *(half4_t *)p = h;
+}
+template <>
+__device__ __forceinline__ void store4<float>(float *p, float a, float b, float c, float d) {
+    *(f32x4_t *)p = f32x4_t{a, b, c, d};
+}
+
+enum { EPI_BIAS = 0, EPI_GELU = 1, EPI_LN = 2 };
+
+template <int EPI, typename TC, typename P>
+__global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
+    const _Float16 *__restrict__ X, const _Float16 *__restrict__ Wc, const uint16_t *__restrict__ scale,
+    const float *__restrict__ bias, TC *__restrict__ C, int M, int K, int N, int units, const TC *__restrict__ R,
+    const float *__restrict__ gamma, const float *__restrict__ beta, float eps) {
+    using F = typename P::F;
+    constexpr int BM = P::BM, BN = P::BN, BK = P::BK, NS = P::NS, TMF = P::TMF, TNF = P::TNF;
+    constexpr int ROWB = F::ROW_BYTES;
+    constexpr bool LN = EPI == EPI_LN;
+    static_assert(!LN || P::WN * TNF * 32 == BN, "LayerNorm tiles cover whole rows");
+    constexpr int NPAR = LN ? 4 : 2;                        // per-column parameters kept in LDS
+    constexpr int MAXN = LN ? BN : 1536;
+
+    __shared__ __attribute__((aligned(16))) char st0[P::STAGE];
+    __shared__ __attribute__((aligned(16))) char st1[P::STAGE];
+    __shared__ __attribute__((aligned(16))) char st2[NS > 2 ? P::STAGE : 16];
+    __shared__ __attribute__((aligned(16))) char st3[NS > 3 ? P::STAGE : 16];
+    __shared__ __attribute__((aligned(16))) float par[NPAR][MAXN];
+    __shared__ float stat0[LN ? BM * P::WN : 1], stat1[LN ? BM * P::WN : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int wm = w / P::WN, wn = w % P::WN;
+    const int KT = K / BK;
+    const int nbn = N / BN;
+    const int u0 = (int)((int64_t)blockIdx.x * units / gridDim.x);
+    const int u1 = (int)((int64_t)(blockIdx.x + 1) * units / gridDim.x);
+    const int S = (u1 - u0) * KT;
+
+    // per-column parameters -> LDS (visible after the first stage barrier)
+    for (int i = tid; i < N; i += P::THREADS) {
+        par[0][i] = f16_bits_to_f32(scale[i]);
+        par[1][i] = bias ? bias[i] : 0.0f;
+        if constexpr (LN) {
+            par[2][i] = gamma[i];
+            par[3][i] = beta[i];
+        }
+    }
+
+    // --- DMA issue state -------------------------------------------------
+    // Each lane fetches one 16-byte chunk per DMA instruction: source address
+    // = wave-uniform row base (scalar) + a small per-lane byte offset.
+    const int wu = __builtin_amdgcn_readfirstlane(w);                // wave index, uniform
+    const int r_in = lane / F::CPR;                                  // row inside a DMA group
+    const int chunk = (lane % F::CPR) ^ F::swz(r_in);                // logical 16-byte chunk it fetches
+    const uint32_t w_loff = (uint32_t)(r_in * K + chunk * 8) * 2u;   // bytes, same for every unit
+    const char *const Xb = (const char *)X;
+    const char *const Wb = (const char *)Wc;
+    int iu = u0, ikt = 0;                                            // next stage to issue
+    int x_row0[P::LX];                                               // uniform first row of each X group
+    uint32_t x_loff[P::LX];                                          // per-lane byte offset (row clamp)
+    const char *w_unit = nullptr;                                    // uniform: first W row of the wave
+    auto set_unit = [&](int u) __attribute__((always_inline)) {
+        const int m0 = LN ? u * BM : (u / nbn) * BM;
+        const int n0 = LN ? 0 : (u % nbn) * BN;
+#pragma unroll
+        for (int i = 0; i < P::LX; i++) {
+            int r0 = m0 + (wu * P::LX + i) * F::RPI;
+            r0 = r0 < M ? r0 : M - 1;
+            const int r = r0 + r_in < M ? r0 + r_in : M - 1;
+            x_row0[i] = r0;
+            x_loff[i] = (uint32_t)((r - r0) * K + chunk * 8) * 2u;
+        }
+        w_unit = Wb + (size_t)(n0 + wu * P::LW * F::RPI) * K * 2;
+    };
+    auto issue = [&](char *buf) __attribute__((always_inline)) {
+        const size_t k0b = (size_t)ikt * BK * 2;
+#pragma unroll
+        for (int i = 0; i < P::LX; i++)
+            dma16(Xb + ((size_t)x_row0[i] * K * 2 + k0b), x_loff[i], buf + (wu * P::LX + i) * F::RPI * ROWB);
+#pragma unroll
+        for (int i = 0; i < P::LW; i++)
+            dma16(w_unit + ((size_t)i * F::RPI * K * 2 + k0b), w_loff,
+                  buf + P::X_BYTES + (wu * P::LW + i) * F::RPI * ROWB);
+        if (++ikt == KT) {
+            ikt = 0;
+            if (++iu < u1) set_unit(iu);
+        }
+    };
+
+    // --- fragment read offsets -------------------------------------------
+    const int l31 = lane & 31, half = lane >> 5;
+    const int fx = F::swz(l31);
+    int xoff[BK / 16], woff[BK / 16];
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ks++) {
+        const int pc = ((2 * ks + half) ^ fx) << 4;
+        xoff[ks] = (wm * TMF * 32 + l31) * ROWB + pc;
+        woff[ks] = P::X_BYTES + (wn * TNF * 32 + l31) * ROWB + pc;
+    }
+
+    f32x16_t acc[TNF][TMF];
+#pragma unroll
+    for (int a = 0; a < TNF; a++)
+#pragma unroll
+        for (int b = 0; b < TMF; b++) acc[a][b] = f32x16_t{};
+
+    auto compute = [&](const char *buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ks++) {
+            half8_t xf[TMF], wf[TNF];
+#pragma unroll
+            for (int b = 0; b < TMF; b++) xf[b] = *(const half8_t *)(buf + xoff[ks] + b * 32 * ROWB);
+#pragma unroll
+            for (int a = 0; a < TNF; a++) wf[a] = *(const half8_t *)(buf + woff[ks] + a * 32 * ROWB);
+#pragma unroll
+            for (int a = 0; a < TNF; a++)
+#pragma unroll
+                for (int b = 0; b < TMF; b++)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[a], xf[b], acc[a][b], 0, 0, 0);
+        }
+    };
+
+    using RV = std::conditional_t<std::is_same<TC, float>::value, f32x4_t, half4_t>;
+
+    auto epilogue = [&](int u) __attribute__((always_inline)) {
+        const int m0 = LN ? u * BM : (u / nbn) * BM;
+        const int n0 = LN ? 0 : (u % nbn) * BN;
+        if constexpr (!LN) {
+#pragma unroll
+            for (int b = 0; b < TMF; b++) {
+                const int t = m0 + wm * TMF * 32 + b * 32 + l31;
+#pragma unroll
+                for (int a = 0; a < TNF; a++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const int n = n0 + wn * TNF * 32 + a * 32 + 8 * g + 4 * half;
+                        const f32x4_t s = *(const f32x4_t *)&par[0][n];
+                        const f32x4_t bb = *(const f32x4_t *)&par[1][n];
+                        float v[4];
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            v[q] = acc[a][b][4 * g + q] * s[q] + bb[q];  // sum * s + bias (matmul_w8a32.zig:55)
+                            if (EPI == EPI_GELU) v[q] = gelu_fast(v[q]);
+                        }
+                        if (t < M) store4<TC>(C + (size_t)t * N + n, v[0], v[1], v[2], v[3]);
+                    }
+            }
+        } else {
+            RV res[TMF][TNF][4];
+#pragma unroll
+            for (int b = 0; b < TMF; b++) {
+                int t = m0 + wm * TMF * 32 + b * 32 + l31;
+                t = t < M ? t : M - 1;
+#pragma unroll
+                for (int a = 0; a < TNF; a++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++)
+                        res[b][a][g] = *(const RV *)(R + (size_t)t * BN + wn * TNF * 32 + a * 32 + 8 * g + 4 * half);
+            }
+            float part[TMF];
+#pragma unroll
+            for (int b = 0; b < TMF; b++) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int a = 0; a < TNF; a++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const int n = wn * TNF * 32 + a * 32 + 8 * g + 4 * half;
+                        const f32x4_t s = *(const f32x4_t *)&par[0][n];
+                        const f32x4_t bb = *(const f32x4_t *)&par[1][n];
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            // input + (sum * s + bias)  (arctic.zig:720)
+                            const float v = (float)res[b][a][g][q] + (acc[a][b][4 * g + q] * s[q] + bb[q]);
+                            acc[a][b][4 * g + q] = v;
+                            sum += v;
+                        }
+                    }
+                part[b] = sum + __shfl_xor(sum, 32, 64);
+            }
+            if (half == 0)
+#pragma unroll
+                for (int b = 0; b < TMF; b++) stat0[(wm * TMF * 32 + b * 32 + l31) * P::WN + wn] = part[b];
+            lds_barrier();
+            float mean[TMF];
+#pragma unroll
+            for (int b = 0; b < TMF; b++) {
+                const float *sp = &stat0[(wm * TMF * 32 + b * 32 + l31) * P::WN];
+                float tot = 0.0f;
+#pragma unroll
+                for (int j = 0; j < P::WN; j++) tot += sp[j];
+                mean[b] = tot / (float)BN;
+                float sq = 0.0f;
+#pragma unroll
+                for (int a = 0; a < TNF; a++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const float d = acc[a][b][e] - mean[b];
+                        sq += d * d;
+                    }
+                part[b] = sq + __shfl_xor(sq, 32, 64);
+            }
+            if (half == 0)
+#pragma unroll
+                for (int b = 0; b < TMF; b++) stat1[(wm * TMF * 32 + b * 32 + l31) * P::WN + wn] = part[b];
+            lds_barrier();
+#pragma unroll
+            for (int b = 0; b < TMF; b++) {
+                const float *sp = &stat1[(wm * TMF * 32 + b * 32 + l31) * P::WN];
+                float tot = 0.0f;
+#pragma unroll
+                for (int j = 0; j < P::WN; j++) tot += sp[j];
+                const float inv_std = 1.0f / sqrtf(tot / (float)BN + eps);
+                const int t = m0 + wm * TMF * 32 + b * 32 + l31;
+#pragma unroll
+                for (int a = 0; a < TNF; a++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const int n = wn * TNF * 32 + a * 32 + 8 * g + 4 * half;
+                        const f32x4_t gg = *(const f32x4_t *)&par[2][n];
+                        const f32x4_t bt = *(const f32x4_t *)&par[3][n];
+                        float y[4];
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+                            y[q] = ((acc[a][b][4 * g + q] - mean[b]) * inv_std) * gg[q] + bt[q];
+                        if (t < M) store4<TC>(C + (size_t)t * BN + n, y[0], y[1], y[2], y[3]);
+                    }
+            }
+        }
+#pragma unroll
+        for (int a = 0; a < TNF; a++)
+#pragma unroll
+            for (int b = 0; b < TMF; b++) acc[a][b] = f32x16_t{};
+    };
+
+    if (S == 0) return;
+    set_unit(u0);
+    char *const bufs[4] = {st0, st1, st2, st3};
+    // prologue: stages 0 .. NS-2
+#pragma unroll
+    for (int j = 0; j < NS - 1; j++)
+        if (j < S) issue(bufs[j]);
+
+    auto step = [&](auto jc, int s) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        wait_stage<NS - 2, P::L>(min(NS - 2, S - 1 - s));  // own loads of stage s landed, own LDS reads done
+        lds_barrier_only();  // every wave's loads of stage s landed; stage s-1 fully read
+        const int kt = s % KT;
+        if (s + NS - 1 < S) issue(bufs[(j + NS - 1) % NS]);
+        compute(bufs[j]);
+        if (kt == KT - 1) epilogue(u0 + s / KT);
+    };
+    for (int s = 0; s < S; s += NS) {
+        step(std::integral_constant<int, 0>{}, s);
+        if (s + 1 < S) step(std::integral_constant<int, 1>{}, s + 1);
+        if constexpr (NS > 2)
+            if (s + 2 < S) step(std::integral_constant<int, 2>{}, s + 2);
+        if constexpr (NS > 3)
+            if (s + 3 < S) step(std::integral_constant<int, 3>{}, s + 3);
+    }
+}
+
+using BiasCfg = PipeCfg<128, 128, 64, 2, 2, 4>;
+using LnCfg = PipeCfg<128, 384, 32, 2, 4, 4>;
+
+template <int EPI, typename TC, typename P>
+int launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc, const uint16_t *scale,
+           const float *bias, TC *c, int M, int K, int N, const TC *res, const float *gamma, const float *beta,
+           float eps) {
+    const int nbm = (M + P::BM - 1) / P::BM;
+    const int units = EPI == EPI_LN ? nbm : nbm * (N / P::BN);
+    const int slots = num_cus * P::blocks_per_cu(EPI == EPI_LN);
+    const int grid = units < slots ? units : slots;
+    hipLaunchKernelGGL((linear_pipe_kernel<EPI, TC, P>), dim3(grid), dim3(P::THREADS), 0, st, x, wc, scale, bias, c,
+                       M, K, N, units, res, gamma, beta, eps);
+    TZH_LAUNCHED("linear_pipe_kernel");
+    return TZH_OK;
+}
+
+__global__ void widen_codes_kernel(const int8_t *__restrict__ q, _Float16 *__restrict__ out, int64_t n) {
+    const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (i + 8 <= n) {
+        const uint2 v = *(const uint2 *)(q + i);
+        half8_t h;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            h[j] = (_Float16)(float)(int8_t)(v.x >> (8 * j));
+            h[4 + j] = (_Float16)(float)(int8_t)(v.y >> (8 * j));
+        }
+        *(half8_t *)(out + i) = h;
+    } else {
+        for (int64_t j = i; j < n; j++) out[j] = (_Float16)(float)q[j];
+    }
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+// int8 codes -> f16 codes (exact), n elements.
+int tzh_widen_codes_launch(hipStream_t st, const int8_t *q, _Float16 *out, int64_t n) {
+    if (n <= 0) return TZH_OK;
+    const int64_t threads = (n + 7) / 8;
+    hipLaunchKernelGGL(widen_codes_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, q, out, n);
+    TZH_LAUNCHED("widen_codes_kernel");
+    return TZH_OK;
+}
+
+// f16 activations x f16 weight codes; output and residual both F16 or both F32.
+int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc,
+                            const uint16_t *scale, const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k,
+                            int64_t n, int32_t epilogue, const void *res, const float *gamma, const float *beta,
+                            float eps) {
+    if (m < 0 || k <= 0 || n <= 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad GEMM shape");
+    if (m == 0) return TZH_OK;  // matmul_w8a32.zig:24
+    if (m > (int64_t)1 << 30 || k > 65536) return tzh_fail(TZH_ERR_TOO_LARGE, "GEMM shape too large");
+    if (k % 64) return tzh_fail(TZH_ERR_INVALID_ARGS, "k=%lld must be a multiple of 64", (long long)k);
+    if (!x || !wc || !scale || !c) return tzh_fail(TZH_ERR_INVALID_ARGS, "null operand");
+    if (!aligned16(x) || !aligned16(wc) || !aligned16(c) || (res && !aligned16(res)))
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "operands must be 16-byte aligned");
+    if (c_dtype != TZH_F16 && c_dtype != TZH_F32) return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "output must be F16 or F32");
+    const int M = (int)m, K = (int)k, N = (int)n;
+    const bool c16 = c_dtype == TZH_F16;
+    if (epilogue == TZH_EPI_BIAS || epilogue == TZH_EPI_BIAS_GELU) {
+        if (N % BiasCfg::BN || N > 1536)
+            return tzh_fail(TZH_ERR_INVALID_ARGS, "n=%d must be a multiple of %d and at most 1536", N, BiasCfg::BN);
+        if (epilogue == TZH_EPI_BIAS)
+            return c16 ? launch<EPI_BIAS, _Float16, BiasCfg>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K, N,
+                                                             nullptr, nullptr, nullptr, 0.0f)
+                       : launch<EPI_BIAS, float, BiasCfg>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, N,
+                                                          nullptr, nullptr, nullptr, 0.0f);
+        return c16 ? launch<EPI_GELU, _Float16, BiasCfg>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K, N,
+                                                         nullptr, nullptr, nullptr, 0.0f)
+                   : launch<EPI_GELU, float, BiasCfg>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, N, nullptr,
+                                                      nullptr, nullptr, 0.0f);
+    }
+    if (epilogue == TZH_EPI_BIAS_RES_LN) {
+        if (N != LnCfg::BN) return tzh_fail(TZH_ERR_INVALID_ARGS, "LayerNorm epilogue needs n == 384 (got %d)", N);
+        if (!res || !gamma || !beta) return tzh_fail(TZH_ERR_INVALID_ARGS, "null residual/gamma/beta");
+        return c16 ? launch<EPI_LN, _Float16, LnCfg>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K, N,
+                                                     (const _Float16 *)res, gamma, beta, eps)
+                   : launch<EPI_LN, float, LnCfg>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, N,
+                                                  (const float *)res, gamma, beta, eps);
+    }
+    return tzh_fail(TZH_ERR_INVALID_ARGS, "unknown epilogue %d", epilogue);
+}

@@ -7,6 +7,7 @@
 
 #include <cstdio>
 #include <cstdlib>
+#include <deque>
 #include <vector>
 
 #if defined(__has_feature)
@@ -31,6 +32,11 @@ constexpr size_t kSlot = 256;
 std::vector<Fiber> fibers;
 std::vector<char *> stacks;
 std::vector<unsigned char> slots;
+struct PendingDma {
+    char *dst;
+    unsigned char data[16];
+};
+std::vector<std::deque<PendingDma>> dma_q;  // per lane of the running block
 ucontext_t sched_uc;
 int cur = -1;
 void (*g_body)(void *) = nullptr;
@@ -94,6 +100,21 @@ void wave_barrier() {
     to_sched(false);
 }
 
+void dma16(const void *src, void *lds_dst) {
+    PendingDma p;
+    p.dst = (char *)lds_dst;
+    std::memcpy(p.data, src, 16);  // the global read (bounds-checked here)
+    dma_q[(size_t)cur].push_back(p);
+}
+
+void waitcnt_vm(int n) {
+    std::deque<PendingDma> &q = dma_q[(size_t)cur];
+    while ((int)q.size() > n) {
+        std::memcpy(q.front().dst, q.front().data, 16);  // the LDS write (bounds-checked here)
+        q.pop_front();
+    }
+}
+
 int lane_id() { return cur % 64; }
 int wave_id() { return cur / 64; }
 void *wave_slot(int lane) { return &slots[((size_t)(cur / 64) * 64 + (size_t)lane) * kSlot]; }
@@ -110,6 +131,7 @@ void launch(const char *name, dim3 grid, dim3 block, void (*body)(void *), void 
     }
     while ((int)stacks.size() < n) stacks.push_back((char *)std::malloc(kStack));
     fibers.resize((size_t)n);
+    dma_q.assign((size_t)n, {});
     slots.assign((size_t)((n + 63) / 64) * 64 * kSlot, 0);
     g_body = body;
     g_ctx = ctx;
@@ -162,6 +184,12 @@ void launch(const char *name, dim3 grid, dim3 block, void (*body)(void *), void 
                     }
                     if (!ran && !released) deadlock(n);
                 }
+                for (int i = 0; i < n; i++)
+                    if (!dma_q[(size_t)i].empty()) {
+                        std::fprintf(stderr, "EMU: kernel %s thread %d exited with %zu direct-to-LDS loads never "
+                                             "waited for\n", name, i, dma_q[(size_t)i].size());
+                        std::abort();
+                    }
             }
     cur = -1;
 }

@@ -198,6 +198,29 @@ def group_gemm():
         c = linear(a, q, s, bias, dt, _abi.EPI_BIAS_RES_LN, res, g, b)
         ref = oracle.layernorm(res.astype(np.float32) + oracle.matmul_w8a32(a, q, s, bias), g, b, 1e-12)
         assert np.abs(c - ref).max() < 2e-2, float(np.abs(c - ref).max())
+    # f16 activations: the pipelined direct-to-LDS kernel (several units per
+    # persistent block: the emulated device has 4 CUs)
+    for m, k, n, epi, odt in [(1, 64, 128, _abi.EPI_BIAS, np.float16), (333, 384, 1152, _abi.EPI_BIAS, np.float16),
+                              (200, 384, 1536, _abi.EPI_BIAS_GELU, np.float16), (129, 64, 256, _abi.EPI_BIAS, np.float32),
+                              (130, 1536, 384, _abi.EPI_BIAS_RES_LN, np.float16),
+                              (61, 384, 384, _abi.EPI_BIAS_RES_LN, np.float32)]:
+        a, q, s, bias = problem(m + k + n, m, k, n, 0.1 if epi == _abi.EPI_BIAS_GELU else 1.0)
+        a16 = a.astype(np.float16)
+        lin = oracle.matmul_w8a32(a16.astype(np.float32), q, s, bias)
+        if epi == _abi.EPI_BIAS_RES_LN:
+            rng = np.random.default_rng(m)
+            res = rng.standard_normal((m, n)).astype(odt)
+            g = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+            b = (0.1 * rng.standard_normal(n)).astype(np.float32)
+            c = linear(a16, q, s, bias, odt, epi, res, g, b)
+            ref = oracle.layernorm(res.astype(np.float32) + lin, g, b, 1e-12)
+            tol = 2e-2
+        else:
+            c = linear(a16, q, s, bias, odt, epi)
+            ref = oracle.gelu(lin) if epi == _abi.EPI_BIAS_GELU else lin
+            tol = 2e-3 * max(1.0, float(np.abs(ref).max()))
+        err = float(np.abs(c - ref).max())
+        assert err < tol, (m, k, n, epi, err)
     w = (np.random.default_rng(12).standard_normal((64, 384)) * 0.02).astype(np.float32)
     w[0] = 0
     qg = np.empty((64, 384), np.int8)

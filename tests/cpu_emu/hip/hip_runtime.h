@@ -48,7 +48,21 @@ int lane_id();
 int wave_id();
 void *wave_slot(int lane);  // 256-byte exchange slot of `lane` in the caller's wave
 void launch(const char *name, dim3 grid, dim3 block, void (*body)(void *), void *ctx);
+// direct-to-LDS loads: queued per lane at issue, written to LDS when a
+// vmcnt wait of that lane retires them (oldest first), so a stage read
+// before its wait sees stale data and fails the parity checks
+void dma16(const void *src, void *lds_dst);
+void waitcnt_vm(int n);
 }  // namespace emu
+
+// the hooks gemm_pipe.hip takes from its target: DMA issue and LDS barrier
+#define TZH_EMULATION 1
+inline void dma16(const char *sbase, uint32_t voff, char *lds_base) {
+    emu::dma16(sbase + voff, lds_base + 16 * emu::lane_id());
+}
+inline void lds_barrier_only() { emu::syncthreads(); }
+#define __builtin_amdgcn_s_waitcnt(imm) emu::waitcnt_vm(((imm)&15) | ((((imm) >> 14) & 3) << 4))
+#define __builtin_amdgcn_readfirstlane(x) (x)
 
 #define threadIdx (emu::g_threadIdx)
 #define blockIdx (emu::g_blockIdx)
