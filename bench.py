@@ -6,8 +6,8 @@
 Prints one JSON line.  A step is one forward of the whole batch with the
 padded token ids already resident in HBM; `value` counts real (unpadded)
 tokens.  `roofline` describes the dominant kernel (by total time in the
-forward), timed alone with HIP events on the stream the forward uses, at the
-same shape; `cpu_baseline` times the C restatement of the reference's
+forward), timed inside the forward with HIP events recorded around every
+launch on the forward's own stream; `cpu_baseline` times the C restatement of the reference's
 batch-parallel CPU forward (forwardBatchParallel) on a sample of the same
 batch on the host cores.
 """
@@ -30,32 +30,34 @@ SEED_WEIGHTS, SEED_BATCH = 1, 5
 BATCH, SEQ = 256, 512
 
 
-def gemm_shapes(T):
-    """(name, K, N, epilogue, flops, algorithmic HBM bytes) per layer of the
-    forward, at f16 activation boundaries (A read once, C written once,
-    int8 weights + f16 scales + f32 bias read once, residual read once)."""
-    out = []
-    for name, K, N, epi, res in (("qkv", 384, 1152, 0, False), ("attn_out_ln", 384, 384, 2, True),
-                                 ("ffn1_gelu", 384, 1536, 1, False), ("ffn2_ln", 1536, 384, 2, True)):
-        flops = 2.0 * T * K * N
+KERNELS = {
+    "qkv": "linear_pipe_kernel bias, 384 -> 1152",
+    "attention": "attn_varlen_kernel",
+    "attn_out_ln": "linear_pipe_kernel bias+residual+LayerNorm, 384 -> 384",
+    "ffn1_gelu": "linear_pipe_kernel bias+GELU, 384 -> 1536",
+    "ffn2_ln": "linear_pipe_kernel bias+residual+LayerNorm, 1536 -> 384",
+    "embed_ln": "embed_ln_kernel", "pack_ids": "pack_ids_kernel", "cls_l2": "cls_l2_kernel",
+}
+
+
+def stage_work(T, lengths):
+    """Algorithmic (flops, HBM bytes) of one launch of each forward stage at
+    f16 activation boundaries: each activation read once and written once,
+    int8 weights + f16 scales + f32 biases read once, residual read once."""
+    H, I = 384, 1536
+    w = {}
+    for name, K, N, res in (("qkv", H, 3 * H, False), ("attn_out_ln", H, H, True),
+                            ("ffn1_gelu", H, I, False), ("ffn2_ln", I, H, True)):
         byts = T * K * 2 + T * N * 2 + (T * N * 2 if res else 0) + N * K + N * (2 + 4) + (2 * N * 4 if res else 0)
-        out.append((name, K, N, epi, flops, byts))
-    return out
-
-
-def time_kernel(fn, iters=20, warmup=3):
-    import torch
-
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(iters):
-        fn()
-    e.record()
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) / iters * 1e-3  # seconds
+        w[name] = (2.0 * T * K * N, float(byts))
+    L2 = float((lengths.astype(np.float64) ** 2).sum())
+    # per head QK^T and PV: 2 * L^2 * 32 flops each; 12 heads
+    w["attention"] = (4.0 * L2 * H, float(T * 3 * H * 2 + T * H * 2))
+    # word/position/type rows (f32) gathered per token, LN, f16 out
+    w["embed_ln"] = (0.0, float(T * H * 4 * 3 + T * H * 2))
+    w["pack_ids"] = (0.0, float(T * 4 * 3))
+    w["cls_l2"] = (0.0, float(len(lengths) * H * (2 + 4)))
+    return w
 
 
 def main():
@@ -71,12 +73,10 @@ def main():
               "sequences and multi-GPU runs are not part of this build", file=sys.stderr)
         sys.exit(2)
 
-    import ctypes as C
-
     import torch
 
     import tenzor_amd
-    from tenzor_amd import _abi, check, lib, synth
+    from tenzor_amd import synth
     from tenzor_amd.arctic import ModelWeights, forwardBatch
 
     assert torch.cuda.is_available(), "bench.py needs the GPU"
@@ -103,30 +103,35 @@ def main():
     value = real_tokens * args.steps / elapsed
     assert torch.isfinite(out).all()
 
-    # per-GEMM standalone timing at the forward's shapes (same kernels, same stream)
+    # per-kernel durations inside the forward: HIP events around every launch
+    # on the forward's own stream (tzh_arctic_set_timing)
+    model.set_timing(True)
+    per_stage = {}
+    n_timed = 3
+    for _ in range(n_timed):
+        forwardBatch(out, d_ids, lengths, model)
+        for name, us in model.launch_times():
+            per_stage.setdefault(name, []).append(us)
+    model.set_timing(False)
     T = real_tokens
-    gemms = []
-    X = torch.randn(T, 1536, device="cuda").half()
-    R = torch.randn(T, 384, device="cuda").half()
-    Y = torch.empty(T, 1536, device="cuda", dtype=torch.half)
-    G, Bt = torch.ones(384, device="cuda"), torch.zeros(384, device="cuda")
-    for name, K, N, epi, flops, byts in gemm_shapes(T):
-        W = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda")
-        S = torch.full((N,), int(np.float16(0.01).view(np.int16)), dtype=torch.int16, device="cuda")
-        B = torch.zeros(N, device="cuda")
-        fn = lambda: check(lib().tzh_linear_w8(ctx.handle, X.data_ptr(), _abi.F16, W.data_ptr(), S.data_ptr(),
-                                               B.data_ptr(), Y.data_ptr(), _abi.F16, T, K, N, epi,
-                                               R.data_ptr() if epi == 2 else None, _abi.F16, G.data_ptr(),
-                                               Bt.data_ptr(), 1e-12))
-        t = time_kernel(fn)
-        roof_t = max(flops / (F16_PEAK_TFLOPS * 1e12), byts / (HBM_PEAK_GBS * 1e9))
-        gemms.append(dict(name=name, seconds=t, flops=flops, bytes=byts, roof_t=roof_t,
-                          bound="mfma" if flops / (F16_PEAK_TFLOPS * 1e12) > byts / (HBM_PEAK_GBS * 1e9) else "hbm"))
-    dom = max(gemms, key=lambda g: g["seconds"])
+    work = stage_work(T, lengths)
+    stages = {}
+    for name, v in per_stage.items():
+        launches_per_fwd = len(v) // n_timed
+        avg_us = sum(v) / len(v)
+        flops, byts = work.get(name, (0.0, 0.0))
+        roof_us = max(flops / (F16_PEAK_TFLOPS * 1e12), byts / (HBM_PEAK_GBS * 1e9)) * 1e6
+        stages[name] = dict(avg_us=avg_us, launches=launches_per_fwd, total_us=avg_us * launches_per_fwd,
+                            flops=flops, bytes=byts, roof_us=roof_us,
+                            bound="mfma" if flops / (F16_PEAK_TFLOPS * 1e12) > byts / (HBM_PEAK_GBS * 1e9) else "hbm")
+    dom_name = max(stages, key=lambda k: stages[k]["total_us"])
+    dom = stages[dom_name]
+    secs = dom["avg_us"] * 1e-6
     if dom["bound"] == "hbm":
-        achieved, peak, unit = dom["bytes"] / dom["seconds"] / 1e9, HBM_PEAK_GBS, "GB/s"
+        achieved, peak, unit = dom["bytes"] / secs / 1e9, HBM_PEAK_GBS, "GB/s"
     else:
-        achieved, peak, unit = dom["flops"] / dom["seconds"] / 1e12, F16_PEAK_TFLOPS, "TFLOP/s"
+        achieved, peak, unit = dom["flops"] / secs / 1e12, F16_PEAK_TFLOPS, "TFLOP/s"
+    fwd_roof_us = sum(st["roof_us"] * st["launches"] for st in stages.values())
 
     line = {
         "metric": "tokens/sec int8 arctic-embed-xs b256 s512, 1 GPU; % of HBM/MFMA roofline",
@@ -152,17 +157,19 @@ def main():
             "parallelism": "single GPU",
         },
         "roofline": {
-            "kernel": f"gemm_w8 {dom['name']} (T={T}, K,N from the layer)",
+            "kernel": f"{dom_name} ({KERNELS[dom_name]}, T={T})",
             "bound": dom["bound"],
             "achieved": round(achieved, 2),
             "peak": peak,
             "unit": unit,
             "frac": round(achieved / peak, 4),
             "traffic": None,
-            "avg_us": round(dom["seconds"] * 1e6, 2),
+            "avg_us": round(dom["avg_us"], 2),
+            "algorithmic_bytes": int(dom["bytes"]),
+            "algorithmic_flops": int(dom["flops"]),
         },
-        "forward_roofline_frac": round(6 * sum(g["roof_t"] for g in gemms) / (ms_per_step * 1e-3), 4),
-        "gemm_us": {g["name"]: round(g["seconds"] * 1e6, 1) for g in gemms},
+        "forward_roofline_frac": round(fwd_roof_us / (ms_per_step * 1e3), 4),
+        "stage_us": {k: round(v["avg_us"], 1) for k, v in stages.items()},
         "padded_equivalent_tokens_per_s": round(BATCH * SEQ * args.steps / elapsed, 1),
     }
 

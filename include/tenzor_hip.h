@@ -144,7 +144,7 @@ int tzh_eval_into(tzh_ctx *ctx, const tzh_node *tape, int32_t n_nodes,
 /* c[i,j] = (sum_k a[i,k]*f32(wq[j,k])) * f32(scale[j]) + bias[j]
  * Replaces matmulTransposeB_f32_i8_rowScale_bias (matmul_w8a32.zig:14-57).
  * a f32 [m,k], wq i8 [n,k] row-major, scale f16 bits [n], bias f32 [n] (may be
- * NULL = zeros), c f32 [m,n]; all device pointers.  k must be a multiple of 32. */
+ * NULL = zeros), c f32 [m,n]; all device pointers.  k must be a multiple of 64. */
 int tzh_matmul_w8a32(tzh_ctx *ctx, const float *a, const int8_t *wq, const uint16_t *scale,
                      const float *bias, float *c, int64_t m, int64_t k, int64_t n);
 
@@ -301,6 +301,20 @@ int tzh_arctic_bad_id_count(tzh_model *model, int32_t *count);
 /* Last-batch timing hook: number of kernel launches the previous
  * tzh_arctic_forward_batch enqueued (for launch-overhead accounting). */
 int tzh_arctic_last_launch_count(tzh_model *model);
+
+/* Launch tracing (no counterpart in the reference, whose CPU path has no
+ * kernels to time): with timing enabled, every later forward records a HIP
+ * event on the model's stream before its first and after each of its
+ * kernel launches. */
+int tzh_arctic_set_timing(tzh_model *model, int32_t enable);
+
+/* Per-launch durations of the most recent timed forward, in launch order:
+ * us[i] (microseconds between the events around launch i) and names[i]
+ * (static stage names: "pack_ids", "embed_ln", "qkv", "attention",
+ * "attn_out_ln", "ffn1_gelu", "ffn2_ln", "cls_l2", "hidden_f32"), at most
+ * `capacity` entries; *count = number of launches (0 if the last forward was
+ * not timed).  Waits for that forward to finish.  Either array may be NULL. */
+int tzh_arctic_launch_times(tzh_model *model, float *us, const char **names, int32_t capacity, int32_t *count);
 
 #ifdef __cplusplus
 }

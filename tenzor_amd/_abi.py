@@ -139,6 +139,8 @@ PROTOTYPES = {
     "tzh_attention_varlen": (C.c_int, [vp, vp, vp, vp, i32, i32, i32]),
     "tzh_arctic_bad_id_count": (C.c_int, [vp, C.POINTER(i32)]),
     "tzh_arctic_last_launch_count": (C.c_int, [vp]),
+    "tzh_arctic_set_timing": (C.c_int, [vp, i32]),
+    "tzh_arctic_launch_times": (C.c_int, [vp, C.POINTER(f32), C.POINTER(C.c_char_p), i32, C.POINTER(i32)]),
 }
 
 

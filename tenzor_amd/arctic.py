@@ -50,6 +50,20 @@ class ModelWeights:
     def last_launch_count(self) -> int:
         return lib().tzh_arctic_last_launch_count(self.handle)
 
+    def set_timing(self, enable: bool) -> None:
+        """Record a HIP event around every kernel launch of later forwards."""
+        check(lib().tzh_arctic_set_timing(self.handle, 1 if enable else 0))
+
+    def launch_times(self) -> list:
+        """[(stage name, microseconds)] of the most recent timed forward, in
+        launch order (waits for it to finish)."""
+        n = C.c_int32()
+        check(lib().tzh_arctic_launch_times(self.handle, None, None, 0, C.byref(n)))
+        us = (C.c_float * max(1, n.value))()
+        names = (C.c_char_p * max(1, n.value))()
+        check(lib().tzh_arctic_launch_times(self.handle, us, names, n.value, C.byref(n)))
+        return [(names[i].decode(), float(us[i])) for i in range(n.value)]
+
     def deinit(self) -> None:
         if self.handle:
             lib().tzh_arctic_free(self.handle)

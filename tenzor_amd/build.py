@@ -22,6 +22,9 @@ SOURCES = ["runtime.cpp", "safetensors.cpp", "ew.hip", "gemm.hip", "gemm_pipe.hi
 # -ffp-contract=off: every multiply and add rounds separately unless a kernel
 # asks for an FMA explicitly (bit-exact elementwise chains).
 # -packed-fp32-ops off: no v_pk_*_f32 in generated code.
+# -amdgpu-mfma-vgpr-form: MFMA accumulators live in ordinary VGPRs; with the
+# accumulation-register form the compiler copied every accumulator between
+# the two register files around each pipeline stage of the GEMM.
 HIPFLAGS = [
     "--offload-arch=gfx950",
     "-O3",
@@ -29,6 +32,7 @@ HIPFLAGS = [
     "-fPIC",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall",
     "-Wno-unused-result",
     "-Wno-unused-function",

@@ -215,6 +215,12 @@ struct tzh_model {
     int *host_meta = nullptr;  // pinned staging
     hipEvent_t meta_done = nullptr;
     int last_launches = 0;
+    // launch timing (tzh_arctic_set_timing): events[0] before the first
+    // launch, events[i+1] after launch i, names[i] = its stage name
+    bool timing = false;
+    std::vector<hipEvent_t> events;
+    std::vector<const char *> names;
+    int timed = 0;
 };
 
 namespace {
@@ -377,6 +383,7 @@ void model_delete(tzh_model *m) {
     free_workspace(m);
     for (void *p : m->allocs) (void)hipFree(p);
     if (m->meta_done) (void)hipEventDestroy(m->meta_done);
+    for (hipEvent_t e : m->events) (void)hipEventDestroy(e);
     delete m;
 }
 
@@ -597,42 +604,70 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
     const int *d_cu = m->meta, *d_order = m->meta + batch + 1;
 
     int launches = 0;
+    // with timing on, an event after every launch (and one before the first)
+    auto mark = [&](const char *name) -> int {
+        if (m->timing) {
+            if ((size_t)launches + 1 >= m->events.size()) {
+                hipEvent_t e;
+                TZH_HIP(hipEventCreate(&e));
+                m->events.push_back(e);
+            }
+            m->names.resize((size_t)launches + 1);
+            m->names[(size_t)launches] = name;
+            TZH_HIP(hipEventRecord(m->events[(size_t)launches + 1], st));
+        }
+        launches++;
+        return TZH_OK;
+    };
+    if (m->timing) {
+        if (m->events.empty()) {
+            hipEvent_t e;
+            TZH_HIP(hipEventCreate(&e));
+            m->events.push_back(e);
+        }
+        TZH_HIP(hipEventRecord(m->events[0], st));
+    }
     hipLaunchKernelGGL(pack_ids_kernel, dim3(batch), dim3(256), 0, st, ids, ids_stride, d_cu, m->tok_ids, m->tok_pos,
                        (uint32_t)m->cfg.vocab_size, m->bad_ids);
     TZH_LAUNCHED("pack_ids_kernel");
-    launches++;
+    TZH_TRY(mark("pack_ids"));
     hipLaunchKernelGGL(embed_ln_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, m->tok_ids, m->tok_pos, T,
                        m->word.ref(), m->pos.ref(), m->type.ref(), m->emb_g, m->emb_b, m->cfg.layer_norm_eps, m->h);
     TZH_LAUNCHED("embed_ln_kernel");
-    launches++;
+    TZH_TRY(mark("embed_ln"));
     const float eps = m->cfg.layer_norm_eps;
     for (int32_t li = 0; li < n_layers; li++) {
         const DevLayer &d = m->layers[(size_t)li];
         const int cus = m->ctx->num_cus;
         TZH_TRY(tzh_linear_codes_launch(st, cus, m->h, d.qkv.w, d.qkv.s, d.qkv.b, m->qkv, TZH_F16, T, H, 3 * H,
                                         TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f));
+        TZH_TRY(mark("qkv"));
         TZH_TRY(tzh_attention_launch(st, m->qkv, m->attn, d_cu, d_order, batch, 12, H));
+        TZH_TRY(mark("attention"));
         TZH_TRY(tzh_linear_codes_launch(st, cus, m->attn, d.o.w, d.o.s, d.o.b, m->h1, TZH_F16, T, H, H,
                                         TZH_EPI_BIAS_RES_LN, m->h, d.ln1_g, d.ln1_b, eps));
+        TZH_TRY(mark("attn_out_ln"));
         TZH_TRY(tzh_linear_codes_launch(st, cus, m->h1, d.ffn1.w, d.ffn1.s, d.ffn1.b, m->inter, TZH_F16, T, H, 1536,
                                         TZH_EPI_BIAS_GELU, nullptr, nullptr, nullptr, 0.0f));
+        TZH_TRY(mark("ffn1_gelu"));
         TZH_TRY(tzh_linear_codes_launch(st, cus, m->inter, d.ffn2.w, d.ffn2.s, d.ffn2.b, m->h, TZH_F16, T, 1536, H,
                                         TZH_EPI_BIAS_RES_LN, m->h1, d.ln2_g, d.ln2_b, eps));
-        launches += 5;
+        TZH_TRY(mark("ffn2_ln"));
     }
     if (outputs) {
         hipLaunchKernelGGL(cls_l2_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, st, m->h, d_cu, batch,
                            outputs);
         TZH_LAUNCHED("cls_l2_kernel");
-        launches++;
+        TZH_TRY(mark("cls_l2"));
     }
     if (hidden_out) {
         const int64_t n = T * H;
         hipLaunchKernelGGL(f16_to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m->h, hidden_out,
                            n);
         TZH_LAUNCHED("f16_to_f32_kernel");
-        launches++;
+        TZH_TRY(mark("hidden_f32"));
     }
+    m->timed = m->timing ? launches : 0;
     m->last_launches = launches;
     return TZH_OK;
 }
@@ -659,6 +694,31 @@ extern "C" int tzh_arctic_forward(tzh_model *m, float *output, const uint32_t *t
 }
 
 extern "C" int tzh_arctic_last_launch_count(tzh_model *m) { return m ? m->last_launches : 0; }
+
+extern "C" int tzh_arctic_set_timing(tzh_model *m, int32_t enable) {
+    tzh_clear_error();
+    if (!m) return tzh_fail(TZH_ERR_INVALID_ARGS, "null model");
+    m->timing = enable != 0;
+    m->timed = 0;
+    return TZH_OK;
+}
+
+extern "C" int tzh_arctic_launch_times(tzh_model *m, float *us, const char **names, int32_t capacity,
+                                       int32_t *count) {
+    tzh_clear_error();
+    if (!m || !count) return tzh_fail(TZH_ERR_INVALID_ARGS, "null argument");
+    TZH_TRY(tzh_ctx_enter(m->ctx));
+    *count = m->timed;
+    if (m->timed == 0) return TZH_OK;
+    TZH_HIP(hipEventSynchronize(m->events[(size_t)m->timed]));
+    for (int i = 0; i < m->timed && i < capacity; i++) {
+        float ms = 0.0f;
+        TZH_HIP(hipEventElapsedTime(&ms, m->events[(size_t)i], m->events[(size_t)i + 1]));
+        if (us) us[i] = ms * 1000.0f;
+        if (names) names[i] = m->names[(size_t)i];
+    }
+    return TZH_OK;
+}
 
 // Number of out-of-range token ids seen (and clamped) since the model was
 // created; synchronises the model's stream.

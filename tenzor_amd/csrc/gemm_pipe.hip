@@ -25,9 +25,9 @@
 //     does not drain the ring before every LDS read.  Stage completion is
 //     tracked with explicit vmcnt waits (in-order counter; every vector
 //     memory op issued after a stage's loads is counted as still pending).
-//   - Rows of each tile are 16-byte-chunk XOR-swizzled so the eight rows an
-//     MFMA fragment read touches per 128-byte LDS window hit eight different
-//     chunks (bank-conflict free ds_read_b128).
+//   - Rows of each tile are 16-byte-chunk XOR-swizzled so that the sixteen
+//     rows one ds_read_b128 cycle serves (16 lanes x 16 B = the 256 bytes of
+//     the 64 LDS banks) land on sixteen different bank slots.
 #include <type_traits>
 
 #include "common.h"
@@ -58,8 +58,11 @@ struct TileFmt {
     static constexpr int CPR = BK / 8;            // 16-byte chunks per row
     static constexpr int ROW_BYTES = BK * 2;
     static constexpr int RPI = 64 / CPR;          // rows per DMA instruction (64 lanes x 16 B)
-    static constexpr int RPW = 128 / ROW_BYTES;   // rows sharing one 128-byte window
+    static constexpr int RPW = 256 / ROW_BYTES;   // rows sharing one 256-byte bank window
     __device__ static __forceinline__ int swz(int r) { return (r / RPW) & (CPR - 1); }
+    // the swizzle of a DMA group's rows depends on the group index only
+    // through its parity (BK = 64: 8-row groups, 2 rows per window)
+    static constexpr bool PARITY = (RPI / RPW) % CPR != 0;
 };
 
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_>
@@ -177,8 +180,11 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     // = wave-uniform row base (scalar) + a small per-lane byte offset.
     const int wu = __builtin_amdgcn_readfirstlane(w);                // wave index, uniform
     const int r_in = lane / F::CPR;                                  // row inside a DMA group
-    const int chunk = (lane % F::CPR) ^ F::swz(r_in);                // logical 16-byte chunk it fetches
-    const uint32_t w_loff = (uint32_t)(r_in * K + chunk * 8) * 2u;   // bytes, same for every unit
+    // logical 16-byte chunk this lane fetches in an even / odd DMA group
+    const int chunk_e = (lane % F::CPR) ^ F::swz(r_in);
+    const int chunk_o = (lane % F::CPR) ^ F::swz(F::RPI + r_in);
+    const uint32_t w_loff_e = (uint32_t)(r_in * K + chunk_e * 8) * 2u;  // bytes, same for every unit
+    const uint32_t w_loff_o = (uint32_t)(r_in * K + chunk_o * 8) * 2u;
     const char *const Xb = (const char *)X;
     const char *const Wb = (const char *)Wc;
     int iu = u0, ikt = 0;                                            // next stage to issue
@@ -194,6 +200,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
             r0 = r0 < M ? r0 : M - 1;
             const int r = r0 + r_in < M ? r0 + r_in : M - 1;
             x_row0[i] = r0;
+            const int chunk = (F::PARITY && ((wu * P::LX + i) & 1)) ? chunk_o : chunk_e;
             x_loff[i] = (uint32_t)((r - r0) * K + chunk * 8) * 2u;
         }
         w_unit = Wb + (size_t)(n0 + wu * P::LW * F::RPI) * K * 2;
@@ -205,7 +212,8 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
             dma16(Xb + ((size_t)x_row0[i] * K * 2 + k0b), x_loff[i], buf + (wu * P::LX + i) * F::RPI * ROWB);
 #pragma unroll
         for (int i = 0; i < P::LW; i++)
-            dma16(w_unit + ((size_t)i * F::RPI * K * 2 + k0b), w_loff,
+            dma16(w_unit + ((size_t)i * F::RPI * K * 2 + k0b),
+                  (F::PARITY && ((wu * P::LW + i) & 1)) ? w_loff_o : w_loff_e,
                   buf + P::X_BYTES + (wu * P::LW + i) * F::RPI * ROWB);
         if (++ikt == KT) {
             ikt = 0;
@@ -386,8 +394,13 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     }
 }
 
-using BiasCfg = PipeCfg<128, 128, 64, 2, 2, 4>;
+// Tile shapes (tokens x output columns x k per stage, waves, stages), chosen
+// by measurement on MI355X at the Arctic shapes (T = 67590 tokens):
+// 128 x 384 tiles halve the L2 -> LDS operand traffic of 128 x 128 ones.
+using BiasCfg = PipeCfg<128, 384, 64, 2, 4, 2>;      // n a multiple of 384
+using BiasCfgNarrow = PipeCfg<128, 128, 64, 2, 2, 4>;  // other multiples of 128
 using LnCfg = PipeCfg<128, 384, 32, 2, 4, 4>;
+
 
 template <int EPI, typename TC, typename P>
 int launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc, const uint16_t *scale,
@@ -401,6 +414,15 @@ int launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc, c
                        M, K, N, units, res, gamma, beta, eps);
     TZH_LAUNCHED("linear_pipe_kernel");
     return TZH_OK;
+}
+
+template <int EPI, typename TC>
+int launch_bias(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc, const uint16_t *scale,
+                const float *bias, TC *c, int M, int K, int N) {
+    if (N % BiasCfg::BN == 0)
+        return launch<EPI, TC, BiasCfg>(st, num_cus, x, wc, scale, bias, c, M, K, N, nullptr, nullptr, nullptr, 0.f);
+    return launch<EPI, TC, BiasCfgNarrow>(st, num_cus, x, wc, scale, bias, c, M, K, N, nullptr, nullptr, nullptr,
+                                          0.f);
 }
 
 __global__ void widen_codes_kernel(const int8_t *__restrict__ q, _Float16 *__restrict__ out, int64_t n) {
@@ -448,17 +470,14 @@ int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, cons
     const int M = (int)m, K = (int)k, N = (int)n;
     const bool c16 = c_dtype == TZH_F16;
     if (epilogue == TZH_EPI_BIAS || epilogue == TZH_EPI_BIAS_GELU) {
-        if (N % BiasCfg::BN || N > 1536)
-            return tzh_fail(TZH_ERR_INVALID_ARGS, "n=%d must be a multiple of %d and at most 1536", N, BiasCfg::BN);
+        if (N % BiasCfgNarrow::BN || N > 1536)
+            return tzh_fail(TZH_ERR_INVALID_ARGS, "n=%d must be a multiple of %d and at most 1536", N,
+                            BiasCfgNarrow::BN);
         if (epilogue == TZH_EPI_BIAS)
-            return c16 ? launch<EPI_BIAS, _Float16, BiasCfg>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K, N,
-                                                             nullptr, nullptr, nullptr, 0.0f)
-                       : launch<EPI_BIAS, float, BiasCfg>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, N,
-                                                          nullptr, nullptr, nullptr, 0.0f);
-        return c16 ? launch<EPI_GELU, _Float16, BiasCfg>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K, N,
-                                                         nullptr, nullptr, nullptr, 0.0f)
-                   : launch<EPI_GELU, float, BiasCfg>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, N, nullptr,
-                                                      nullptr, nullptr, 0.0f);
+            return c16 ? launch_bias<EPI_BIAS, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K, N)
+                       : launch_bias<EPI_BIAS, float>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, N);
+        return c16 ? launch_bias<EPI_GELU, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K, N)
+                   : launch_bias<EPI_GELU, float>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, N);
     }
     if (epilogue == TZH_EPI_BIAS_RES_LN) {
         if (N != LnCfg::BN) return tzh_fail(TZH_ERR_INVALID_ARGS, "LayerNorm epilogue needs n == 384 (got %d)", N);

@@ -195,6 +195,8 @@ hipError_t hipStreamSynchronize(hipStream_t s);
 hipError_t hipStreamCreateWithFlags(hipStream_t *s, unsigned f);
 hipError_t hipStreamDestroy(hipStream_t s);
 hipError_t hipEventCreateWithFlags(hipEvent_t *e, unsigned f);
+hipError_t hipEventCreate(hipEvent_t *e);
+hipError_t hipEventElapsedTime(float *ms, hipEvent_t a, hipEvent_t b);
 hipError_t hipEventDestroy(hipEvent_t e);
 hipError_t hipEventRecord(hipEvent_t e, hipStream_t s);
 hipError_t hipEventSynchronize(hipEvent_t e);
