@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libtenzor_hip.so"
-SOURCES = ["runtime.cpp", "safetensors.cpp", "ew.hip", "gemm.hip", "gemm_pipe.hip", "attention.hip", "arctic.hip"]
+SOURCES = ["runtime.cpp", "safetensors.cpp", "ew.hip", "gemm.hip", "gemm_pipe.hip", "ew_jit.cpp", "attention.hip", "arctic.hip"]
 
 # -ffp-contract=off: every multiply and add rounds separately unless a kernel
 # asks for an FMA explicitly (bit-exact elementwise chains).
@@ -63,7 +63,8 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
+           "-L/opt/rocm/lib", "-lhiprtc"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

@@ -48,15 +48,30 @@ struct tzh_ctx {
     hipStream_t stream = nullptr;
     bool own_stream = false;
     int num_cus = 256;
+    // elementwise chains through the interpreter kernel instead of generated
+    // kernels (environment TZH_EW_INTERPRETER=1 at tzh_init)
+    bool ew_interpreter = false;
     // stream-ordered scratch used by eval for materialised reductions
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
+    // ring of kernel-program slots (device + pinned host staging)
+    static constexpr int kProgSlots = 32;
+    static constexpr size_t kProgSlotBytes = 4096;
+    void *prog_dev = nullptr;
+    void *prog_host = nullptr;
+    hipEvent_t prog_ev[kProgSlots] = {};
+    int prog_next = 0;
 };
 
 // Make ctx's device current for the calling thread.
 int tzh_ctx_enter(tzh_ctx *ctx);
 // Grow-only device scratch owned by the context (synchronises on growth).
 int tzh_ctx_scratch(tzh_ctx *ctx, size_t bytes, void **out);
+// Stream-ordered upload of a small kernel descriptor (<= kProgSlotBytes):
+// copies `bytes` from src into the next device slot of the context's ring
+// and returns its device address, valid for kernels enqueued next on the
+// context's stream.
+int tzh_ctx_upload_program(tzh_ctx *ctx, const void *src, size_t bytes, const void **dev_out);
 
 // ---------------------------------------------------------------------------
 // Device helpers

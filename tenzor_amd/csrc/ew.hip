@@ -11,141 +11,65 @@
 // Op semantics follow simd.zig:107-315 (tanh = 2*sigmoid(2x)-1, gelu with
 // that tanh, relu = @max(x,0), round half away from zero) and
 // elementwise.zig:124-207 (supported op set).
-#include "common.h"
+#include "ew_program.h"
 
 #include <cmath>
 #include <cstring>
 #include <vector>
 
+namespace tzh_ew {
+
+FastDiv make_fastdiv(uint64_t d) {
+    FastDiv f{};
+    if (d == 0 || d > 0xffffffffull) return FastDiv{0, 0, 0, 0};  // unused: 64-bit path
+    int l = 0;
+    while ((1ull << l) < d) l++;
+    f.d = (uint32_t)d;
+    f.m = (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+    f.s1 = l > 0 ? 1 : 0;
+    f.s2 = l > 0 ? (uint32_t)(l - 1) : 0;
+    return f;
+}
+
+}  // namespace tzh_ew
+
 namespace {
 
-constexpr int kMaxNodes = 32;  // analyzer.zig:13 MAX_ELEMENTWISE_OPS
-constexpr int kMaxLeaves = 12;
-constexpr int kMaxDepth = 4;   // value stack slots per thread
+using namespace tzh_ew;
 
-enum : int16_t { EK_LEAF = 0, EK_CONST = 1, EK_UNARY = 2, EK_BINARY = 3 };
-enum : int32_t { VEC_PER_ELEM = 0, VEC_CONTIG = 1, VEC_SPLAT = 2 };
-
-struct EwLeaf {
-    const void *ptr;
-    int64_t div;   // affine projection: off = (flat / div) % mod
-    int64_t mod;
-    int32_t general;  // 1: use strides[] with a full unflatten
-    int32_t vec;      // VEC_* for VEC consecutive outputs
-    int64_t strides[TZH_MAX_RANK];
-};
-
-struct EwNode {
-    int16_t kind;
-    int16_t op;
-    int16_t slot;
-    int16_t arg;
-    int32_t pad0, pad1;
-    double cval;
-};
-
-struct EwProgram {
-    int32_t n_nodes;
-    int32_t n_leaves;
-    int32_t ndim;
-    int32_t pad;
-    int64_t numel;
-    int64_t shape[TZH_MAX_RANK];
-    EwNode nodes[kMaxNodes];
-    EwLeaf leaves[kMaxLeaves];
-};
-
-static_assert(sizeof(EwProgram) < 3800, "kernel argument block too large");
+// Chains run as generated kernels (ew_jit.cpp) unless the context asks for
+// the interpreter; the CPU emulation build has no run-time compiler.
+#ifdef TZH_EMULATION
+constexpr bool kHaveJit = false;
+#else
+constexpr bool kHaveJit = true;
+#endif
 
 template <typename T, int V>
 struct Vec {
     T v[V];
 };
 
-// ------------------------------------------------------------------------
-// scalar op semantics (simd.zig:107-315)
-// ------------------------------------------------------------------------
-__device__ __forceinline__ float dexp(float x) { return expf(x); }
-__device__ __forceinline__ double dexp(double x) { return exp(x); }
-
-template <typename T>
-__device__ __forceinline__ T sigm(T x) {
-    return T(1) / (T(1) + dexp(-x));
-}
-
-template <typename T>
-__device__ __forceinline__ T tanh_ref(T x) {
-    return T(2) * sigm<T>(T(2) * x) - T(1);
-}
-
-template <typename T>
-__device__ __forceinline__ T unary_op(int op, T x) {
-    switch (op) {
-    case TZH_OP_NEG: return -x;
-    case TZH_OP_ABS: return fabs(x);
-    case TZH_OP_EXP: return dexp(x);
-    case TZH_OP_LOG: return log(x);
-    case TZH_OP_SQRT: return sqrt(x);
-    case TZH_OP_RSQRT: return T(1) / sqrt(x);
-    case TZH_OP_SIN: return sin(x);
-    case TZH_OP_COS: return cos(x);
-    case TZH_OP_TANH: return tanh_ref<T>(x);
-    case TZH_OP_SIGMOID: return sigm<T>(x);
-    case TZH_OP_RELU: return fmax(x, T(0));
-    case TZH_OP_GELU: {
-        const T k0 = T(0.7978845608028654), k1 = T(0.044715);
-        T x3 = x * x * x;
-        T inner = k0 * (x + k1 * x3);
-        return T(0.5) * x * (T(1) + tanh_ref<T>(inner));
-    }
-    case TZH_OP_SILU: return x * sigm<T>(x);
-    case TZH_OP_SOFTPLUS: return log(T(1) + dexp(x));
-    case TZH_OP_FLOOR: return floor(x);
-    case TZH_OP_CEIL: return ceil(x);
-    case TZH_OP_ROUND: return round(x);
-    default: return x;
-    }
-}
-
-template <typename T>
-__device__ __forceinline__ T binary_op(int op, T a, T b) {
-    switch (op) {
-    case TZH_OP_ADD: return a + b;
-    case TZH_OP_SUB: return a - b;
-    case TZH_OP_MUL: return a * b;
-    case TZH_OP_DIV: return a / b;
-    case TZH_OP_POW: return pow(a, b);
-    case TZH_OP_MAX: return fmax(a, b);
-    case TZH_OP_MIN: return fmin(a, b);
-    default: return a;
-    }
-}
-
-template <typename T>
-__device__ __forceinline__ T red_ident(int op) {
-    switch (op) {
-    case TZH_OP_PROD: return T(1);
-    case TZH_OP_REDUCE_MAX: return -INFINITY;
-    case TZH_OP_REDUCE_MIN: return INFINITY;
-    default: return T(0);
-    }
-}
-
-template <typename T>
-__device__ __forceinline__ T red_apply(int op, T acc, T v) {
-    switch (op) {
-    case TZH_OP_PROD: return acc * v;
-    case TZH_OP_REDUCE_MAX: return fmax(acc, v);
-    case TZH_OP_REDUCE_MIN: return fmin(acc, v);
-    default: return acc + v;
-    }
-}
-
+// scalar op semantics (simd.zig:107-315): ew_shared.inc
 // ------------------------------------------------------------------------
 // leaf loads
 // ------------------------------------------------------------------------
 template <typename T>
 __device__ __forceinline__ int64_t leaf_offset(const EwLeaf &lf, const EwProgram &p, int64_t flat) {
+    if (p.small) {
+        const uint32_t f = (uint32_t)flat;
+        if (!lf.general) {
+            const uint32_t q = lf.div == 1 ? f : fast_div(lf.fdiv, f);
+            return lf.mod > (int64_t)0xffffffff ? q : q - fast_div(lf.fmod, q) * lf.fmod.d;
+        }
+        uint32_t off = 0, rem = f;
+        for (int d = p.ndim - 1; d >= 0; d--) {
+            const uint32_t q = fast_div(p.fshape[d], rem);
+            off += (rem - q * p.fshape[d].d) * (uint32_t)lf.strides[d];
+            rem = q;
+        }
+        return off;
+    }
     if (!lf.general) return (flat / lf.div) % lf.mod;
     int64_t off = 0, rem = flat;
     for (int d = p.ndim - 1; d >= 0; d--) {
@@ -161,7 +85,7 @@ __device__ __forceinline__ Vec<T, V> load_leaf(const EwLeaf &lf, const EwProgram
     Vec<T, V> r;
     const T *base = (const T *)lf.ptr;
     if (lf.vec == VEC_CONTIG) {
-        const int64_t off = (flat / lf.div) % lf.mod;
+        const int64_t off = leaf_offset<T>(lf, p, flat);
         if constexpr (V * sizeof(T) == 16) {
             const f32x4_t raw = *(const f32x4_t *)(base + off);
             __builtin_memcpy(&r, &raw, 16);
@@ -561,10 +485,15 @@ struct Planner {
         } else {
             lf.general = 1; lf.div = 1; lf.mod = 1;
         }
+        lf.fdiv = make_fastdiv((uint64_t)lf.div);
+        lf.fmod = make_fastdiv((uint64_t)lf.mod);
+        // (flat / div) < numel <= mod: the modulo never wraps, skip it
+        const bool wraps = lf.mod < p.numel;
         const bool aligned = ((uintptr_t)ptr % 16) == 0;
-        if (!lf.general && lf.div == 1 && lf.mod % vec == 0 && aligned) lf.vec = VEC_CONTIG;
+        if (!lf.general && lf.div == 1 && (!wraps || lf.mod % vec == 0) && aligned) lf.vec = VEC_CONTIG;
         else if (!lf.general && lf.div % vec == 0) lf.vec = VEC_SPLAT;
         else lf.vec = VEC_PER_ELEM;
+        if (!wraps) lf.mod = INT64_MAX;
         *leaf_idx = p.n_leaves++;
         return TZH_OK;
     }
@@ -628,6 +557,8 @@ struct Planner {
         p.ndim = n.ndim;
         for (int i = 0; i < n.ndim; i++) p.shape[i] = n.shape[i];
         p.numel = numel_of(n.ndim, n.shape);
+        p.small = p.numel < ((int64_t)1 << 32) ? 1 : 0;
+        for (int i = 0; i < n.ndim; i++) p.fshape[i] = make_fastdiv((uint64_t)n.shape[i]);
         // a cut node being materialised is this program's root: evaluate it inline
         const char was_cut = cut[(size_t)idx];
         cut[(size_t)idx] = 0;
@@ -652,6 +583,9 @@ struct Planner {
         TZH_TRY(compile(idx, p, V));
         if (p.numel == 0) return TZH_OK;
         const int g = grid_for(p.numel / V);
+        if constexpr (kHaveJit) {
+            if (!ctx->ew_interpreter) return jit_chain_launch(ctx, p, sizeof(T) == 8, V, g, out);
+        }
         hipLaunchKernelGGL((ew_chain_kernel<T, V>), dim3(g), dim3(256), 0, ctx->stream, p, out);
         TZH_LAUNCHED("ew_chain_kernel");
         return TZH_OK;

@@ -1,0 +1,254 @@
+// Generated single-pass chain kernels (K1 fast path).
+//
+// The reference fuses an elementwise chain at compile time into one loop
+// (codegen.zig:15-205 FusedElementwiseKernel: the ops of the chain applied
+// in post-order per element, patterns.zig:43-63).  Here the same happens at
+// run time: a chain program (ew_program.h) is turned into straight-line HIP
+// source - every leaf loaded up front through its broadcast projection with
+// the projection kind baked in, every op inlined with its tag as a
+// constant - compiled once per program shape with hipRTC for the device's
+// architecture, and cached.  Pointers, shapes, divisors and constant values
+// stay run-time kernel arguments (the EwProgram struct itself), so programs
+// that differ only in those share one kernel.
+//
+// The op semantics and the program layout are the exact text the
+// interpreter kernels are compiled from (ew_shared.inc, stringified below).
+#include <hip/hiprtc.h>
+
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "ew_program.h"
+
+namespace tzh_ew {
+namespace {
+
+#define TZH_EW_SHARED(...) #__VA_ARGS__
+const char kSharedSrc[] =
+#include "ew_shared.inc"
+    ;
+#undef TZH_EW_SHARED
+
+#define TZH_JIT_OPS(X)                                                                                    \
+    X(TZH_OP_NEG) X(TZH_OP_ABS) X(TZH_OP_EXP) X(TZH_OP_LOG) X(TZH_OP_SQRT) X(TZH_OP_RSQRT) X(TZH_OP_SIN)   \
+    X(TZH_OP_COS) X(TZH_OP_TANH) X(TZH_OP_SIGMOID) X(TZH_OP_RELU) X(TZH_OP_GELU) X(TZH_OP_SILU)           \
+    X(TZH_OP_SOFTPLUS) X(TZH_OP_FLOOR) X(TZH_OP_CEIL) X(TZH_OP_ROUND) X(TZH_OP_ADD) X(TZH_OP_SUB)         \
+    X(TZH_OP_MUL) X(TZH_OP_DIV) X(TZH_OP_POW) X(TZH_OP_MAX) X(TZH_OP_MIN) X(TZH_OP_PROD)                  \
+    X(TZH_OP_REDUCE_MAX) X(TZH_OP_REDUCE_MIN)
+
+std::string prelude() {
+    std::string s = "typedef float tzh_f32x4 __attribute__((ext_vector_type(4)));\n"
+                    "typedef double tzh_f64x2 __attribute__((ext_vector_type(2)));\n"
+                    "enum {";
+#define TZH_JIT_ENUM(name) s += std::string(#name) + " = " + std::to_string((int)name) + ", ";
+    TZH_JIT_OPS(TZH_JIT_ENUM)
+#undef TZH_JIT_ENUM
+    s += "};\n";
+    s += kSharedSrc;
+    s += "\n";
+    return s;
+}
+
+// Offset expression of leaf j for the flat output index held in `var`.
+std::string offset_fn(const EwProgram &p, int j) {
+    const EwLeaf &lf = p.leaves[j];
+    const std::string L = "p.leaves[" + std::to_string(j) + "]";
+    std::string b = "__device__ __forceinline__ long long off" + std::to_string(j) +
+                    "(const EwProgram &p, long long flat) {\n";
+    if (p.small) {
+        b += "    unsigned f = (unsigned)flat;\n";
+        if (!lf.general) {
+            if (lf.div != 1) b += "    f = fast_div(" + L + ".fdiv, f);\n";
+            if (lf.mod <= (long long)0xffffffff) b += "    f = f - fast_div(" + L + ".fmod, f) * " + L + ".fmod.d;\n";
+            b += "    return f;\n";
+        } else {
+            b += "    unsigned off = 0, rem = f, q;\n";
+            for (int d = p.ndim - 1; d >= 0; d--) {
+                const std::string D = std::to_string(d);
+                b += "    q = fast_div(p.fshape[" + D + "], rem);\n";
+                if (lf.strides[d] != 0)
+                    b += "    off += (rem - q * p.fshape[" + D + "].d) * (unsigned)" + L + ".strides[" + D + "];\n";
+                b += "    rem = q;\n";
+            }
+            b += "    return off;\n";
+        }
+    } else {
+        if (!lf.general) {
+            b += "    return (flat / " + L + ".div) % " + L + ".mod;\n";
+        } else {
+            b += "    long long off = 0, rem = flat;\n";
+            for (int d = p.ndim - 1; d >= 0; d--) {
+                const std::string D = std::to_string(d);
+                if (lf.strides[d] != 0) b += "    off += (rem % p.shape[" + D + "]) * " + L + ".strides[" + D + "];\n";
+                b += "    rem /= p.shape[" + D + "];\n";
+            }
+            b += "    return off;\n";
+        }
+    }
+    b += "}\n";
+    return b;
+}
+
+// Body computing r[0..W) for outputs flat .. flat+W-1.
+std::string body(const EwProgram &p, const char *T, int W, bool vec16) {
+    std::string b;
+    const std::string WS = std::to_string(W);
+    for (int j = 0; j < p.n_leaves; j++) {
+        const std::string J = std::to_string(j);
+        const std::string ptr = "((const " + std::string(T) + " *)p.leaves[" + J + "].ptr)";
+        b += "        " + std::string(T) + " L" + J + "[" + WS + "];\n";
+        const int mode = W == 1 ? VEC_PER_ELEM : p.leaves[j].vec;
+        if (mode == VEC_CONTIG && vec16) {
+            const std::string VT = std::string(T) == "float" ? "tzh_f32x4" : "tzh_f64x2";
+            b += "        { const " + VT + " raw = *(const " + VT + " *)(" + ptr + " + off" + J + "(p, flat));\n";
+            for (int e = 0; e < W; e++) b += "          L" + J + "[" + std::to_string(e) + "] = raw[" + std::to_string(e) + "];\n";
+            b += "        }\n";
+        } else if (mode == VEC_CONTIG) {
+            b += "        { const long long o = off" + J + "(p, flat);\n";
+            for (int e = 0; e < W; e++)
+                b += "          L" + J + "[" + std::to_string(e) + "] = " + ptr + "[o + " + std::to_string(e) + "];\n";
+            b += "        }\n";
+        } else if (mode == VEC_SPLAT) {
+            b += "        { const " + std::string(T) + " x = " + ptr + "[off" + J + "(p, flat)];\n";
+            for (int e = 0; e < W; e++) b += "          L" + J + "[" + std::to_string(e) + "] = x;\n";
+            b += "        }\n";
+        } else {
+            for (int e = 0; e < W; e++)
+                b += "        L" + J + "[" + std::to_string(e) + "] = " + ptr + "[off" + J + "(p, flat + " +
+                     std::to_string(e) + ")];\n";
+        }
+    }
+    // the stack program run symbolically: slot -> expression name
+    for (int e = 0; e < W; e++) {
+        const std::string E = std::to_string(e);
+        std::string slot[kMaxDepth + 1];
+        for (int i = 0; i < p.n_nodes; i++) {
+            const EwNode &nd = p.nodes[i];
+            const std::string v = "v" + std::to_string(i) + "_" + E;
+            const std::string I = std::to_string(i);
+            switch (nd.kind) {
+            case EK_LEAF:
+                slot[nd.slot] = "L" + std::to_string(nd.arg) + "[" + E + "]";
+                break;
+            case EK_CONST:
+                b += "        const " + std::string(T) + " " + v + " = (" + T + ")p.nodes[" + I + "].cval;\n";
+                slot[nd.slot] = v;
+                break;
+            case EK_UNARY:
+                b += "        const " + std::string(T) + " " + v + " = unary_op<" + T + ">(" + std::to_string(nd.op) +
+                     ", " + slot[nd.slot] + ");\n";
+                slot[nd.slot] = v;
+                break;
+            default:
+                b += "        const " + std::string(T) + " " + v + " = binary_op<" + T + ">(" + std::to_string(nd.op) +
+                     ", " + slot[nd.slot] + ", " + slot[nd.slot + 1] + ");\n";
+                slot[nd.slot] = v;
+                break;
+            }
+        }
+        b += "        r[" + E + "] = " + slot[0] + ";\n";
+    }
+    return b;
+}
+
+std::string chain_source(const EwProgram &p, bool f64, int V) {
+    const char *T = f64 ? "double" : "float";
+    const bool vec16 = V * (f64 ? 8 : 4) == 16;
+    std::string s = prelude();
+    for (int j = 0; j < p.n_leaves; j++) s += offset_fn(p, j);
+    const std::string VS = std::to_string(V);
+    s += "extern \"C\" __global__ void __launch_bounds__(256) tzh_chain(const EwProgram p, " + std::string(T) +
+         " *__restrict__ out) {\n";
+    s += "    const long long nvec = p.numel / " + VS + ";\n";
+    s += "    const long long stride = (long long)gridDim.x * blockDim.x;\n";
+    s += "    for (long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x; v < nvec; v += stride) {\n";
+    s += "        const long long flat = v * " + VS + ";\n";
+    s += "        " + std::string(T) + " r[" + VS + "];\n";
+    s += body(p, T, V, vec16);
+    if (vec16) {
+        const std::string VT = f64 ? "tzh_f64x2" : "tzh_f32x4";
+        s += "        " + VT + " o;\n";
+        for (int e = 0; e < V; e++) s += "        o[" + std::to_string(e) + "] = r[" + std::to_string(e) + "];\n";
+        s += "        __builtin_nontemporal_store(o, (" + VT + " *)(out + flat));\n";
+    } else {
+        for (int e = 0; e < V; e++) s += "        out[flat + " + std::to_string(e) + "] = r[" + std::to_string(e) + "];\n";
+    }
+    s += "    }\n";
+    // tail (numel % V elements): one element per thread of block 0
+    s += "    if (blockIdx.x == 0) {\n";
+    s += "        const long long flat = nvec * " + VS + " + threadIdx.x;\n";
+    s += "        if (flat < p.numel) {\n";
+    s += "        " + std::string(T) + " r[1];\n";
+    s += body(p, T, 1, false);
+    s += "        out[flat] = r[0];\n";
+    s += "        }\n    }\n}\n";
+    return s;
+}
+
+struct Compiled {
+    hipModule_t module;
+    hipFunction_t fn;
+};
+
+std::mutex g_mu;
+std::unordered_map<std::string, Compiled> g_cache;  // key: device id + source
+
+int compile(int device, const std::string &src, Compiled *out) {
+    hipDeviceProp_t prop;
+    TZH_HIP(hipGetDeviceProperties(&prop, device));
+    std::string arch = prop.gcnArchName;
+    arch = arch.substr(0, arch.find(':'));
+    hiprtcProgram prog;
+    if (hiprtcCreateProgram(&prog, src.c_str(), "tzh_chain.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+        return tzh_fail(TZH_ERR_DEVICE, "hiprtcCreateProgram failed");
+    const std::string arch_opt = "--offload-arch=" + arch;
+    // same floating-point contract as the library build: no contraction, no
+    // packed f32 instructions
+    const char *opts[] = {arch_opt.c_str(), "-O3", "-std=c++17", "-ffp-contract=off",
+                          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+    const hiprtcResult rc = hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof opts[0]), opts);
+    if (rc != HIPRTC_SUCCESS) {
+        size_t n = 0;
+        hiprtcGetProgramLogSize(prog, &n);
+        std::string log(n + 1, '\0');
+        hiprtcGetProgramLog(prog, &log[0]);
+        hiprtcDestroyProgram(&prog);
+        return tzh_fail(TZH_ERR_DEVICE, "chain kernel compilation failed (%s): %.1500s", hiprtcGetErrorString(rc),
+                        log.c_str());
+    }
+    size_t n = 0;
+    hiprtcGetCodeSize(prog, &n);
+    std::vector<char> code(n);
+    hiprtcGetCode(prog, code.data());
+    hiprtcDestroyProgram(&prog);
+    TZH_HIP(hipModuleLoadData(&out->module, code.data()));
+    TZH_HIP(hipModuleGetFunction(&out->fn, out->module, "tzh_chain"));
+    return TZH_OK;
+}
+
+}  // namespace
+
+int jit_chain_launch(tzh_ctx *ctx, const EwProgram &p, bool f64, int V, int grid, void *out) {
+    const std::string src = chain_source(p, f64, V);
+    const std::string key = std::to_string(ctx->device) + "\n" + src;
+    Compiled k{};
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        auto it = g_cache.find(key);
+        if (it == g_cache.end()) {
+            TZH_TRY(compile(ctx->device, src, &k));
+            g_cache.emplace(key, k);
+        } else {
+            k = it->second;
+        }
+    }
+    EwProgram arg = p;
+    void *args[] = {&arg, &out};
+    TZH_HIP(hipModuleLaunchKernel(k.fn, (unsigned)grid, 1, 1, 256, 1, 1, 0, ctx->stream, args, nullptr));
+    return TZH_OK;
+}
+
+}  // namespace tzh_ew

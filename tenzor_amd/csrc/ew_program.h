@@ -1,0 +1,33 @@
+// Programs of the elementwise engine (K1): the descriptor the interpreter
+// kernels in ew.hip execute and the chain-kernel generator (ew_jit.cpp)
+// specialises into straight-line code.
+#pragma once
+
+#include "common.h"
+
+namespace tzh_ew {
+
+constexpr int kMaxNodes = 32;  // analyzer.zig:13 MAX_ELEMENTWISE_OPS
+constexpr int kMaxLeaves = 12;
+constexpr int kMaxDepth = 4;   // value stack slots per thread
+
+enum : int16_t { EK_LEAF = 0, EK_CONST = 1, EK_UNARY = 2, EK_BINARY = 3 };
+enum : int32_t { VEC_PER_ELEM = 0, VEC_CONTIG = 1, VEC_SPLAT = 2 };
+
+#define TZH_EW_SHARED(...) __VA_ARGS__
+#include "ew_shared.inc"
+#undef TZH_EW_SHARED
+
+static_assert(TZH_MAX_RANK == 8 && kMaxNodes == 32 && kMaxLeaves == 12,
+              "array bounds in ew_shared.inc are written as literals");
+static_assert(sizeof(EwProgram) < 3800, "kernel argument block too large");
+
+FastDiv make_fastdiv(uint64_t d);
+
+// Launch the generated single-pass kernel for chain program p (no reduce
+// node) writing p.numel elements of type f64 ? double : float to out, with
+// V outputs per thread and `grid` blocks of 256 threads; kernels are
+// compiled on first use of a program shape and cached per device.
+int jit_chain_launch(tzh_ctx *ctx, const EwProgram &p, bool f64, int V, int grid, void *out);
+
+}  // namespace tzh_ew

@@ -1,6 +1,7 @@
 // Context, memory and error plumbing of the C-ABI (include/tenzor_hip.h).
 #include "common.h"
 
+#include <cstdlib>
 #include <cstring>
 #include <new>
 
@@ -68,6 +69,8 @@ extern "C" int tzh_init(int device, void *stream, tzh_ctx **out) {
     if (!ctx) return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "context allocation failed");
     ctx->device = device;
     ctx->num_cus = prop.multiProcessorCount;
+    const char *interp = std::getenv("TZH_EW_INTERPRETER");
+    ctx->ew_interpreter = interp && interp[0] == '1';
     // NULL is the device's default stream, as in every HIP/CUDA library API,
     // so callers on the default stream need no extra synchronisation.
     ctx->stream = (hipStream_t)stream;
@@ -76,10 +79,45 @@ extern "C" int tzh_init(int device, void *stream, tzh_ctx **out) {
     return TZH_OK;
 }
 
+int tzh_ctx_upload_program(tzh_ctx *ctx, const void *src, size_t bytes, const void **dev_out) {
+    if (bytes > tzh_ctx::kProgSlotBytes) return tzh_fail(TZH_ERR_INVALID_ARGS, "internal: program of %zu bytes", bytes);
+    if (!ctx->prog_dev) {
+        const size_t total = (size_t)tzh_ctx::kProgSlots * tzh_ctx::kProgSlotBytes;
+        if (hipMalloc(&ctx->prog_dev, total) != hipSuccess) {
+            (void)hipGetLastError();
+            ctx->prog_dev = nullptr;
+            return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "program ring allocation failed");
+        }
+        if (hipHostMalloc(&ctx->prog_host, total, hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            ctx->prog_host = nullptr;
+            return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "program staging allocation failed");
+        }
+        for (int i = 0; i < tzh_ctx::kProgSlots; i++)
+            TZH_HIP(hipEventCreateWithFlags(&ctx->prog_ev[i], hipEventDisableTiming));
+    }
+    const int k = ctx->prog_next;
+    ctx->prog_next = (k + 1) % tzh_ctx::kProgSlots;
+    // the previous copy out of this staging slot has finished (events start
+    // out complete, so the first round does not wait)
+    TZH_HIP(hipEventSynchronize(ctx->prog_ev[k]));
+    char *host = (char *)ctx->prog_host + (size_t)k * tzh_ctx::kProgSlotBytes;
+    char *dev = (char *)ctx->prog_dev + (size_t)k * tzh_ctx::kProgSlotBytes;
+    std::memcpy(host, src, bytes);
+    TZH_HIP(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    TZH_HIP(hipEventRecord(ctx->prog_ev[k], ctx->stream));
+    *dev_out = dev;
+    return TZH_OK;
+}
+
 extern "C" int tzh_destroy(tzh_ctx *ctx) {
     if (!ctx) return TZH_OK;
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
+    for (hipEvent_t e : ctx->prog_ev)
+        if (e) hipEventDestroy(e);
+    if (ctx->prog_dev) hipFree(ctx->prog_dev);
+    if (ctx->prog_host) hipHostFree(ctx->prog_host);
     if (ctx->scratch) hipFree(ctx->scratch);
     if (ctx->own_stream) hipStreamDestroy(ctx->stream);
     delete ctx;

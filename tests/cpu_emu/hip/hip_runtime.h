@@ -96,6 +96,7 @@ using std::min;
 using std::isnan;
 using std::isinf;
 using std::isfinite;
+inline unsigned __umulhi(unsigned a, unsigned b) { return (unsigned)(((unsigned long long)a * b) >> 32); }
 inline int min(int a, int b) { return a < b ? a : b; }
 inline int max(int a, int b) { return a > b ? a : b; }
 
