@@ -258,9 +258,10 @@ typedef struct {
 
 typedef struct tzh_model tzh_model;
 
-/* Upload host weights to HBM (int8 linears stay int8; f32 linears are kept
- * f32 in HBM and rounded to f16 per tile on load).  The model is bound to
- * ctx's device and stream. */
+/* Upload host weights to HBM.  The encoder linears must be I8 + F16 scale
+ * (an F32 linear is rejected with TZH_ERR_UNSUPPORTED_DTYPE); their codes
+ * are kept on the device widened to f16 (exact).  Embedding tables may be
+ * F32 or I8.  The model is bound to ctx's device and stream. */
 int tzh_arctic_upload(tzh_ctx *ctx, const tzh_arctic_weights *weights, tzh_model **out);
 
 /* ModelWeights.fromSafeTensors (arctic.zig:113-166): "bert." prefix

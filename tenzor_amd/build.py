@@ -74,6 +74,23 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     return LIB
 
 
+def build_host_tests(verbose: bool = False) -> Path:
+    """Compile the C++ host-API parity test (tests/cpp/test_host_api.cpp)
+    against the built library and the CPU oracle (its checker)."""
+    root = Path(__file__).resolve().parent.parent
+    src = root / "tests" / "cpp" / "test_host_api.cpp"
+    exe = root / "tests" / "cpp" / "test_host_api"
+    cmd = ["g++", "-std=c++17", "-O2", "-Wall", str(src), "-o", str(exe),
+           f"-L{root / 'tenzor_amd'}", "-ltenzor_hip", f"-L{root / 'oracle'}", "-loracle",
+           "-Wl,-rpath,$ORIGIN/../../tenzor_amd:$ORIGIN/../../oracle"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"host test build failed:\n{res.stderr}")
+    if verbose:
+        print(f"built {exe}")
+    return exe
+
+
 if __name__ == "__main__":
     build(verbose=True)
     sys.exit(0)

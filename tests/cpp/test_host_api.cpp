@@ -1,0 +1,240 @@
+// GPU parity of the C++ host API (tenzor_amd/host/tenzor.hpp), written as
+// the reference writes its tests: the executor known answers
+// (executor.zig:605-740), broadcasting and scalars (elementwise.zig:339-460),
+// reductions (reduce.zig:241-350), config-2 chains against the oracle, and
+// the Arctic integration flow (arctic_integration_test.zig: safetensors +
+// token file -> embeddings) against expected embeddings computed by the
+// oracle.  Test infrastructure: links the CPU oracle as the checker.
+//
+//   test_host_api [fixture_dir]     (fixture_dir: model.safetensors, ids.bin,
+//                                    lengths.bin, expected.bin)
+#include <cmath>
+#include <cstdio>
+#include <fstream>
+#include <functional>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "../../oracle/oracle.h"
+#include "../../tenzor_amd/host/tenzor.hpp"
+
+using namespace tenzor;
+
+static int g_failed = 0;
+
+#define EXPECT(cond)                                                                                 \
+    do {                                                                                             \
+        if (!(cond)) throw std::runtime_error(std::string("expectation failed: ") + #cond + " line " + \
+                                              std::to_string(__LINE__));                             \
+    } while (0)
+
+static void run(const char *name, const std::function<void()> &fn) {
+    try {
+        fn();
+        std::printf("PASS %s\n", name);
+    } catch (const std::exception &e) {
+        std::printf("FAIL %s: %s\n", name, e.what());
+        g_failed++;
+    }
+    std::fflush(stdout);
+}
+
+static int64_t ulp_diff(float a, float b) {
+    int32_t ia, ib;
+    std::memcpy(&ia, &a, 4);
+    std::memcpy(&ib, &b, 4);
+    int64_t x = ia < 0 ? (int64_t)INT32_MIN - ia : ia;
+    int64_t y = ib < 0 ? (int64_t)INT32_MIN - ib : ib;
+    return x > y ? x - y : y - x;
+}
+
+template <typename T>
+static std::vector<T> read_file(const std::string &path) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) throw std::runtime_error("cannot open " + path);
+    f.seekg(0, std::ios::end);
+    const size_t n = (size_t)f.tellg() / sizeof(T);
+    f.seekg(0);
+    std::vector<T> v(n);
+    f.read((char *)v.data(), (std::streamsize)(n * sizeof(T)));
+    return v;
+}
+
+int main(int argc, char **argv) {
+    Context ctx(0);
+
+    run("eval tensor passthrough", [&] {  // executor.zig:605-614
+        using Vec = Tensor<float, 4>;
+        auto input = Vec::fromSlice(ctx, {1, 2, 3, 4});
+        auto result = eval(ctx, input);
+        EXPECT(result.slice(ctx) == input.slice(ctx));
+    });
+
+    run("eval unary relu", [&] {  // executor.zig:616-631
+        using Vec = Tensor<float, 4>;
+        auto input = Vec::fromSlice(ctx, {-2, -1, 1, 2});
+        auto expr = UnaryExpr<OpTag::relu, Vec>::init(input);
+        auto result = eval(ctx, expr).slice(ctx);
+        const float expected[] = {0, 0, 1, 2};
+        for (int i = 0; i < 4; i++) EXPECT(std::fabs(result[i] - expected[i]) <= 1e-6f);
+    });
+
+    run("eval binary add", [&] {  // executor.zig:633-650
+        using Vec = Tensor<float, 4>;
+        auto a = Vec::fromSlice(ctx, {1, 2, 3, 4});
+        auto b = Vec::fromSlice(ctx, {10, 20, 30, 40});
+        auto expr = BinaryExpr<OpTag::add, Vec, Vec>::init(a, b);
+        EXPECT((eval(ctx, expr).slice(ctx) == std::vector<float>{11, 22, 33, 44}));
+    });
+
+    run("eval chained expression", [&] {  // executor.zig:652-673
+        using Vec = Tensor<float, 4>;
+        auto a = Vec::fromSlice(ctx, {-1, 2, -3, 4});
+        auto b = Vec::fromSlice(ctx, {1, 1, 1, 1});
+        using AddExpr = BinaryExpr<OpTag::add, Vec, Vec>;
+        auto relu_expr = UnaryExpr<OpTag::relu, AddExpr>::init(AddExpr::init(a, b));
+        EXPECT((eval(ctx, relu_expr).slice(ctx) == std::vector<float>{0, 3, 0, 5}));
+    });
+
+    run("eval reduce sum", [&] {  // executor.zig:694-706
+        using Vec = Tensor<float, 4>;
+        auto input = Vec::fromSlice(ctx, {1, 2, 3, 4});
+        auto s = eval(ctx, ReduceExpr<OpTag::sum, Vec>::init(input)).slice(ctx);
+        EXPECT(s.size() == 1 && s[0] == 10.0f);
+    });
+
+    run("reduce along an axis", [&] {  // reduce.zig:283-300
+        using Mat = Tensor<float, 2, 3>;
+        auto m = Mat::fromSlice(ctx, {1, 2, 3, 4, 5, 6});
+        EXPECT((eval(ctx, ReduceExpr<OpTag::sum, Mat, 1>::init(m)).slice(ctx) == std::vector<float>{6, 15}));
+        EXPECT((eval(ctx, ReduceExpr<OpTag::sum, Mat, 0>::init(m)).slice(ctx) == std::vector<float>{5, 7, 9}));
+        EXPECT((eval(ctx, ReduceExpr<OpTag::mean, Mat, 1, true>::init(m)).slice(ctx) == std::vector<float>{2, 5}));
+        EXPECT((eval(ctx, ReduceExpr<OpTag::reduce_max, Mat, 0>::init(m)).slice(ctx) ==
+                std::vector<float>{4, 5, 6}));
+    });
+
+    run("broadcast row and column", [&] {  // strides.zig:92-121 stride-0 rule
+        using Mat = Tensor<float, 2, 3>;
+        using Row = Tensor<float, 3>;
+        using Col = Tensor<float, 2, 1>;
+        auto m = Mat::fromSlice(ctx, {1, 2, 3, 4, 5, 6});
+        auto r = Row::fromSlice(ctx, {10, 20, 30});
+        auto c = Col::fromSlice(ctx, {100, 200});
+        auto e = m.add(r).add(c);
+        static_assert(decltype(e)::shape[0] == 2 && decltype(e)::shape[1] == 3, "broadcast shape");
+        EXPECT((eval(ctx, e).slice(ctx) == std::vector<float>{111, 122, 133, 214, 225, 236}));
+    });
+
+    run("scalar operands", [&] {  // ScalarExpr, expr.zig:1010-1063
+        using Vec = Tensor<float, 5>;
+        auto x = Vec::fromSlice(ctx, {-2, -0.5f, 0, 0.5f, 2});
+        auto r = eval(ctx, x.mul(2.5).add(-1.0).maximum(0.0)).slice(ctx);
+        const float expected[] = {0, 0, 0, 0.25f, 4.0f};
+        for (int i = 0; i < 5; i++) EXPECT(r[i] == expected[i]);
+    });
+
+    run("config-2 chain exp((A + b) * c) vs oracle", [&] {
+        constexpr int64_t R = 512, C = 4096;
+        using Mat = Tensor<float, R, C>;
+        using Row = Tensor<float, C>;
+        std::mt19937 gen(11);
+        std::uniform_real_distribution<float> u(-1.0f, 1.0f);
+        std::vector<float> ha(R * C), hb(C), hc(R * C), ref(R * C), t1(R * C), t2(R * C);
+        for (auto &v : ha) v = u(gen);
+        for (auto &v : hb) v = u(gen);
+        for (auto &v : hc) v = u(gen);
+        auto a = Mat::fromSlice(ctx, ha);
+        auto b = Row::fromSlice(ctx, hb);
+        auto c = Mat::fromSlice(ctx, hc);
+        auto out = eval(ctx, BinaryExpr<OpTag::add, Mat, Row>::init(a, b).mul(c).exp()).slice(ctx);
+        orc_chain_add_mul_exp(ha.data(), hb.data(), hc.data(), ref.data(), R, C, t1.data(), t2.data());
+        int64_t worst = 0;
+        for (size_t i = 0; i < out.size(); i++) worst = std::max(worst, ulp_diff(out[i], ref[i]));
+        EXPECT(worst <= 2);
+    });
+
+    run("f64 chain vs oracle executor", [&] {
+        using Mat = Tensor<double, 17, 31>;
+        using Row = Tensor<double, 31>;
+        std::mt19937 gen(7);
+        std::normal_distribution<double> n01;
+        std::vector<double> ha(17 * 31), hb(31);
+        for (auto &v : ha) v = n01(gen);
+        for (auto &v : hb) v = n01(gen);
+        auto a = Mat::fromSlice(ctx, ha);
+        auto b = Row::fromSlice(ctx, hb);
+        auto e = BinaryExpr<OpTag::add, Mat, Row>::init(a, b).exp().mul(a);
+        auto got = eval(ctx, e).slice(ctx);
+        // the oracle evaluates the same tape over host copies of the leaves
+        Tape tape;
+        e.emit(tape);
+        std::vector<tzh_leaf> host = tape.leaves;
+        host[0].data = ha.data();
+        host[1].data = hb.data();
+        std::vector<double> ref(got.size());
+        EXPECT(orc_eval(tape.nodes.data(), (int32_t)tape.nodes.size(), host.data(), (int32_t)host.size(), TZH_F64,
+                        ref.data()) == 0);
+        for (size_t i = 0; i < got.size(); i++) EXPECT(std::fabs(got[i] - ref[i]) <= 1e-14 * std::fabs(ref[i]) + 1e-15);
+    });
+
+    run("errors carry the reference's error names", [&] {
+        using Vec = Tensor<float, 4>;
+        auto x = Vec::fromSlice(ctx, {1, 2, 3, 4});
+        try {
+            evalInto(ctx, x.exp(), (float *)nullptr);
+            EXPECT(false);
+        } catch (const Error &e) {
+            EXPECT(e.code == TZH_ERR_INVALID_ARGS);
+        }
+        try {
+            (void)arctic::ModelWeights::fromSafeTensors(ctx, "/nonexistent/model.safetensors");
+            EXPECT(false);
+        } catch (const Error &e) {
+            EXPECT(e.code == TZH_ERR_IO);
+        }
+    });
+
+    if (argc > 1) {
+        const std::string dir = argv[1];
+        run("arctic integration: safetensors + tokens -> embeddings", [&] {  // arctic_integration_test.zig
+            auto weights = arctic::ModelWeights::fromSafeTensors(ctx, dir + "/model.safetensors");
+            const auto ids = read_file<uint32_t>(dir + "/ids.bin");
+            const auto lengths = read_file<int32_t>(dir + "/lengths.bin");
+            const auto expected = read_file<float>(dir + "/expected.bin");
+            const size_t batch = lengths.size();
+            EXPECT(expected.size() == batch * 384);
+            void *d_ids = nullptr, *d_out = nullptr;
+            check(tzh_malloc(ctx.handle(), ids.size() * 4, &d_ids));
+            check(tzh_malloc(ctx.handle(), expected.size() * 4, &d_out));
+            check(tzh_memcpy_h2d(ctx.handle(), d_ids, ids.data(), ids.size() * 4));
+            arctic::forwardBatch((float *)d_out, (const uint32_t *)d_ids, lengths, 0, weights);
+            std::vector<float> got(expected.size());
+            check(tzh_memcpy_d2h(ctx.handle(), got.data(), d_out, got.size() * 4));
+            // single-sequence entry point on the first sequence
+            std::vector<float> one(384);
+            arctic::forward((float *)d_out, (const uint32_t *)d_ids, lengths[0], weights);
+            check(tzh_memcpy_d2h(ctx.handle(), one.data(), d_out, 384 * 4));
+            tzh_free(ctx.handle(), d_ids);
+            tzh_free(ctx.handle(), d_out);
+            double max_abs = 0, min_cos = 1;
+            for (size_t b = 0; b < batch; b++) {
+                double dot = 0, ng = 0, nr = 0;
+                for (int j = 0; j < 384; j++) {
+                    const double g = got[b * 384 + j], r = expected[b * 384 + j];
+                    max_abs = std::max(max_abs, std::fabs(g - r));
+                    dot += g * r;
+                    ng += g * g;
+                    nr += r * r;
+                }
+                min_cos = std::min(min_cos, dot / std::sqrt(ng * nr));
+            }
+            std::printf("  arctic: %zu sequences, max-abs %.3g, min cosine %.7f\n", batch, max_abs, min_cos);
+            EXPECT(max_abs <= 1e-3 && min_cos >= 0.9999);
+            for (int j = 0; j < 384; j++) EXPECT(one[j] == got[j]);  // same kernels, same sums
+        });
+    }
+
+    std::printf(g_failed ? "FAILED %d\n" : "ALL PASSED\n", g_failed);
+    return g_failed ? 1 : 0;
+}

@@ -1,0 +1,55 @@
+"""Every kernel of libtenzor_hip run on the CPU (tests/cpu_emu): each lane a
+fiber, wave operations and MFMA in software, AddressSanitizer on every
+buffer and LDS array, barrier deadlock detection, direct-to-LDS loads as
+deferred writes retired only by the issuing lane's vmcnt wait.  The
+scenarios are the GPU tests' (emu_checks.py) and the C++ host API test;
+results are compared with the oracle.  This is how index arithmetic,
+launch shapes and synchronisation are checked before anything runs on a
+GPU, and it covers the GPU cases that are kept off the GPU."""
+import os
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+EMU = os.path.join(ROOT, "tests", "cpu_emu")
+CLANG = "/opt/rocm/llvm/bin/clang++"
+
+
+def _asan_runtime():
+    res = subprocess.run([CLANG, "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    return res.stdout.strip()
+
+
+@pytest.fixture(scope="module")
+def emu_env():
+    if not os.path.exists(CLANG):
+        pytest.skip("ROCm clang not available")
+    res = subprocess.run(["make", "-s", "-j8", "-C", EMU], capture_output=True, text=True, timeout=900)
+    assert res.returncode == 0, res.stderr[-3000:]
+    env = dict(os.environ)
+    env["LD_PRELOAD"] = _asan_runtime()
+    env["ASAN_OPTIONS"] = "detect_leaks=0"
+    return env
+
+
+@pytest.mark.parametrize("group", ["eval", "attention", "gemm"])
+def test_kernels_under_emulation(emu_env, group):
+    res = subprocess.run(["python", os.path.join(EMU, "emu_checks.py"), group], capture_output=True, text=True,
+                         env=emu_env, timeout=900, cwd=ROOT)
+    assert res.returncode == 0, (res.stdout + res.stderr)[-4000:]
+    assert "EMU CHECKS PASSED" in res.stdout
+
+
+def test_cpp_host_api_under_emulation(emu_env, tmp_path):
+    exe = str(tmp_path / "test_host_api_emu")
+    asan = emu_env["LD_PRELOAD"]
+    build = subprocess.run(
+        ["g++", "-std=c++17", "-O1", os.path.join(ROOT, "tests", "cpp", "test_host_api.cpp"), "-o", exe,
+         f"-L{EMU}", "-ltenzor_hip_emu", f"-L{os.path.join(ROOT, 'oracle')}", "-loracle", asan,
+         f"-Wl,-rpath,{EMU}:{os.path.join(ROOT, 'oracle')}:{os.path.dirname(asan)}"],
+        capture_output=True, text=True, timeout=300)
+    assert build.returncode == 0, build.stderr[-3000:]
+    res = subprocess.run([exe], capture_output=True, text=True, env=emu_env, timeout=900)
+    assert res.returncode == 0, (res.stdout + res.stderr)[-4000:]
+    assert "ALL PASSED" in res.stdout
