@@ -50,6 +50,10 @@ __device__ __forceinline__ void dma16(const char *sbase, uint32_t voff, char *ld
 // ops (lgkmcnt); the memory clobber keeps the compiler from moving LDS
 // accesses across it, and no fence means no wait for the ring's loads.
 __device__ __forceinline__ void lds_barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+// Marks a vector store the stage waits count (the CPU emulation keeps its
+// own in-order record of vector memory ops; on the GPU vmcnt does).
+__device__ __forceinline__ void vmem_store_issued() {}
 #endif
 
 // Tile of rows x BK halves (k contiguous) as laid out in LDS.
@@ -95,19 +99,29 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
-// Wait until at most L*A vector memory ops are outstanding, A chosen at run
-// time from {0..AMAX} (the largest A <= ahead).  Loads complete in issue
-// order, so this guarantees every load issued before the last L*A has
-// landed; other ops in flight (epilogue stores) only make it stricter.
-template <int AMAX, int L>
-__device__ __forceinline__ void wait_stage(int ahead) {
+// Wait until at most L*A + E vector memory ops are outstanding, A chosen at
+// run time from {0..AMAX} (the largest A <= ahead) and E from {0, EXTRA}.
+// On gfx9 every vector memory op (loads, stores, direct-to-LDS loads)
+// retires from vmcnt in issue order, so when at least L*A + E ops were
+// issued after a stage's loads, this guarantees that stage has landed.  E
+// counts the epilogue stores issued after them: without it the ring would
+// wait for those stores too.
+template <int AMAX, int L, int EXTRA>
+__device__ __forceinline__ void wait_stage(int ahead, bool extra) {
     if constexpr (AMAX == 0) {
-        wait_vm_lgkm0<0>();
-    } else {
-        if (ahead >= AMAX)
-            wait_vm_lgkm0<L * AMAX>();
+        if (extra)
+            wait_vm_lgkm0<EXTRA>();
         else
-            wait_stage<AMAX - 1, L>(ahead);
+            wait_vm_lgkm0<0>();
+    } else {
+        if (ahead >= AMAX) {
+            if (extra)
+                wait_vm_lgkm0<L * AMAX + EXTRA>();
+            else
+                wait_vm_lgkm0<L * AMAX>();
+        } else {
+            wait_stage<AMAX - 1, L, EXTRA>(ahead, extra);
+        }
     }
 }
 
@@ -276,7 +290,10 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                             v[q] = acc[a][b][4 * g + q] * s[q] + bb[q];  // sum * s + bias (matmul_w8a32.zig:55)
                             if (EPI == EPI_GELU) v[q] = gelu_fast(v[q]);
                         }
-                        if (t < M) store4<TC>(C + (size_t)t * N + n, v[0], v[1], v[2], v[3]);
+                        if (t < M) {
+                            store4<TC>(C + (size_t)t * N + n, v[0], v[1], v[2], v[3]);
+                            vmem_store_issued();
+                        }
                     }
             }
         } else {
@@ -357,7 +374,10 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 #pragma unroll
                         for (int q = 0; q < 4; q++)
                             y[q] = ((acc[a][b][4 * g + q] - mean[b]) * inv_std) * gg[q] + bt[q];
-                        if (t < M) store4<TC>(C + (size_t)t * BN + n, y[0], y[1], y[2], y[3]);
+                        if (t < M) {
+                            store4<TC>(C + (size_t)t * BN + n, y[0], y[1], y[2], y[3]);
+                            vmem_store_issued();
+                        }
                     }
             }
         }
@@ -375,14 +395,28 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     for (int j = 0; j < NS - 1; j++)
         if (j < S) issue(bufs[j]);
 
+    // The stores of the most recent epilogue (one vector store per lane per
+    // (token fragment, weight fragment, 4-column group)) were issued after
+    // the loads of stages up to last_epi + NS - 1; they are all issued
+    // exactly when the unit lies inside M (no lane of any store is masked
+    // off), and only then are they counted.
+    constexpr int EPI_STORES = TMF * TNF * 4;
+    int last_epi = -NS;
+    bool last_full = false;
     auto step = [&](auto jc, int s) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
-        wait_stage<NS - 2, P::L>(min(NS - 2, S - 1 - s));  // own loads of stage s landed, own LDS reads done
+        // own loads of stage s landed, own LDS reads done
+        wait_stage<NS - 2, P::L, EPI_STORES>(min(NS - 2, S - 1 - s), last_full && last_epi >= s - NS + 1);
         lds_barrier_only();  // every wave's loads of stage s landed; stage s-1 fully read
         const int kt = s % KT;
         if (s + NS - 1 < S) issue(bufs[(j + NS - 1) % NS]);
         compute(bufs[j]);
-        if (kt == KT - 1) epilogue(u0 + s / KT);
+        if (kt == KT - 1) {
+            const int u = u0 + s / KT;
+            epilogue(u);
+            last_epi = s;
+            last_full = (LN ? u * BM : (u / nbn) * BM) + BM <= M;
+        }
     };
     for (int s = 0; s < S; s += NS) {
         step(std::integral_constant<int, 0>{}, s);

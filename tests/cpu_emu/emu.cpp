@@ -33,7 +33,7 @@ std::vector<Fiber> fibers;
 std::vector<char *> stacks;
 std::vector<unsigned char> slots;
 struct PendingDma {
-    char *dst;
+    char *dst;  // nullptr: a store marker (retires with no LDS effect)
     unsigned char data[16];
 };
 std::vector<std::deque<PendingDma>> dma_q;  // per lane of the running block
@@ -107,10 +107,16 @@ void dma16(const void *src, void *lds_dst) {
     dma_q[(size_t)cur].push_back(p);
 }
 
+void vmem_marker() {
+    PendingDma p;
+    p.dst = nullptr;
+    dma_q[(size_t)cur].push_back(p);
+}
+
 void waitcnt_vm(int n) {
     std::deque<PendingDma> &q = dma_q[(size_t)cur];
     while ((int)q.size() > n) {
-        std::memcpy(q.front().dst, q.front().data, 16);  // the LDS write (bounds-checked here)
+        if (q.front().dst) std::memcpy(q.front().dst, q.front().data, 16);  // the LDS write (bounds-checked here)
         q.pop_front();
     }
 }
@@ -183,6 +189,13 @@ void launch(const char *name, dim3 grid, dim3 block, void (*body)(void *), void 
                         released = true;
                     }
                     if (!ran && !released) deadlock(n);
+                }
+                for (int i = 0; i < n; i++) {
+                    // trailing store markers may stay pending at exit; loads may not
+                    while (!dma_q[(size_t)i].empty() && !dma_q[(size_t)i].back().dst) dma_q[(size_t)i].pop_back();
+                    bool loads_pending = false;
+                    for (const PendingDma &d : dma_q[(size_t)i]) loads_pending |= d.dst != nullptr;
+                    if (!loads_pending) dma_q[(size_t)i].clear();
                 }
                 for (int i = 0; i < n; i++)
                     if (!dma_q[(size_t)i].empty()) {

@@ -53,6 +53,7 @@ void launch(const char *name, dim3 grid, dim3 block, void (*body)(void *), void 
 // before its wait sees stale data and fails the parity checks
 void dma16(const void *src, void *lds_dst);
 void waitcnt_vm(int n);
+void vmem_marker();  // a vector memory op with no LDS effect (a store), in issue order
 }  // namespace emu
 
 // the hooks gemm_pipe.hip takes from its target: DMA issue and LDS barrier
@@ -61,6 +62,7 @@ inline void dma16(const char *sbase, uint32_t voff, char *lds_base) {
     emu::dma16(sbase + voff, lds_base + 16 * emu::lane_id());
 }
 inline void lds_barrier_only() { emu::syncthreads(); }
+inline void vmem_store_issued() { emu::vmem_marker(); }
 #define __builtin_amdgcn_s_waitcnt(imm) emu::waitcnt_vm(((imm)&15) | ((((imm) >> 14) & 3) << 4))
 #define __builtin_amdgcn_readfirstlane(x) (x)
 
