@@ -13,9 +13,11 @@
 // Design:
 //   - The MFMA computes C^T tiles (weights as the A operand, tokens as B):
 //     each lane then owns four consecutive output columns of one token, so
-//     stores are 8-byte (f16) / 16-byte (f32) vectors straight from the
-//     accumulators, and a token's LayerNorm statistics reduce in registers,
-//     across the two half-waves, then across the waves of the row in LDS.
+//     a token's LayerNorm statistics reduce in registers, across the two
+//     half-waves, then across the waves of the row in LDS.  f16 results
+//     are turned into whole 64-byte row pieces through a wave-private LDS
+//     tile before they are stored; f32 ones are stored as 16-byte vectors
+//     straight from the accumulators.
 //   - Persistent blocks (one per CU): the (row panel, column tile) work units
 //     are split into contiguous per-block ranges and the stage ring runs
 //     across unit boundaries, so the next unit's tiles are already in flight
@@ -54,7 +56,66 @@ __device__ __forceinline__ void lds_barrier_only() { asm volatile("s_barrier" ::
 // Marks a vector store the stage waits count (the CPU emulation keeps its
 // own in-order record of vector memory ops; on the GPU vmcnt does).
 __device__ __forceinline__ void vmem_store_issued() {}
+
+// v_permlane32_swap_b32: lanes 32..63 of `lo` trade values with lanes 0..31
+// of `hi` (lanes 0..31 of `lo` and 32..63 of `hi` keep theirs).
+__device__ __forceinline__ void lane_swap32(uint32_t &lo, uint32_t &hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
+    lo = r[0];
+    hi = r[1];
+}
+
+// Orders a wave's LDS writes before its later LDS reads of what other lanes
+// of the same wave wrote.  The LDS performs one wave's operations in issue
+// order, so only the compiler has to be kept from reordering them.
+__device__ __forceinline__ void wave_lds_order() { asm volatile("" ::: "memory"); }
 #endif
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Stores one 32-token x 32-column f16 fragment given in the MFMA D layout
+// (this lane: token lane%32; element 4g+q is column 8g + 4*(lane/32) + q)
+// as whole 64-byte row pieces.  Output rows are 16-byte chunks spread over
+// 32 rows per store instruction otherwise, which costs the L2 one request
+// per 16 bytes; here a swap between the half-waves gives each lane two
+// complete 16-byte column chunks of its token, a wave-private 2 KiB LDS tile
+// (chunks XOR-swizzled by row/4: conflict-free both ways) transposes them,
+// and each store instruction writes sixteen full 64-byte rows.
+//   ws: the wave's staging tile; dst: &C[t0][c0]; ld: row pitch (elements);
+//   rows: how many of the 32 tokens lie inside the matrix.
+// Issues two store instructions per lane (fewer where rows < 32).
+__device__ __forceinline__ void store_frag_f16(char *ws, const float (&v)[16], _Float16 *dst, int ld, int rows) {
+    const int lane = threadIdx.x & 63, l31 = lane & 31, half = lane >> 5;
+    uint32_t pk[4][2];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const half2_t h0 = {(_Float16)v[4 * g], (_Float16)v[4 * g + 1]};
+        const half2_t h1 = {(_Float16)v[4 * g + 2], (_Float16)v[4 * g + 3]};
+        pk[g][0] = __builtin_bit_cast(uint32_t, h0);
+        pk[g][1] = __builtin_bit_cast(uint32_t, h1);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        // lower half-wave keeps group 2k and receives the upper one's;
+        // upper half-wave keeps group 2k+1 and receives the lower one's
+        uint32_t x0 = pk[2 * k][0], x1 = pk[2 * k][1], y0 = pk[2 * k + 1][0], y1 = pk[2 * k + 1][1];
+        lane_swap32(x0, y0);
+        lane_swap32(x1, y1);
+        const int c = 2 * k + half;  // columns 8c .. 8c+7
+        *(u32x4_t *)(ws + l31 * 64 + ((c ^ ((l31 >> 2) & 3)) << 4)) = u32x4_t{x0, x1, y0, y1};
+    }
+    wave_lds_order();
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int q = i * 64 + lane, row = q >> 2, c = q & 3;
+        const u32x4_t d = *(const u32x4_t *)(ws + row * 64 + ((c ^ ((row >> 2) & 3)) << 4));
+        if (row < rows) {
+            *(u32x4_t *)(dst + (size_t)row * ld + c * 8) = d;
+            vmem_store_issued();
+        }
+    }
+    wave_lds_order();
+}
 
 // Tile of rows x BK halves (k contiguous) as laid out in LDS.
 template <int BK>
@@ -82,10 +143,11 @@ struct PipeCfg {
     static_assert(XG % NW == 0 && WG % NW == 0, "DMA groups must split evenly over the waves");
     static_assert(TMF >= 1 && TNF >= 1, "wave tile too small");
     static_assert(NS >= 2 && NS <= 4, "2..4 stages");
-    // LDS of one block (stage ring + parameter table + LayerNorm statistics)
-    // and how many such blocks a CU's 160 KiB holds
+    // LDS of one block (stage ring + parameter table + LayerNorm statistics
+    // + per-wave output staging tiles) and how many such blocks a CU's
+    // 160 KiB holds
     static constexpr int lds_bytes(bool ln) {
-        return NS * STAGE + (ln ? 4 * BN * 4 + 2 * BM * WN * 4 : 2 * 1536 * 4);
+        return NS * STAGE + (ln ? 4 * BN * 4 + 2 * BM * WN * 4 : 2 * 1536 * 4) + NW * 2048;
     }
     static constexpr int blocks_per_cu(bool ln) {
         return 163840 / lds_bytes(ln) > 2 ? 2 : 163840 / lds_bytes(ln);
@@ -131,10 +193,14 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 __device__ __forceinline__ float gelu_fast(float x) {
-    // tanh-form GELU (arctic.zig:750-756), tanh(u) = 1 - 2 / (exp(2u) + 1)
-    const float inner = 0.7978845608f * (x + 0.044715f * x * x * x);
-    const float e = __builtin_amdgcn_exp2f(inner * 2.8853900817779268f);
-    return 0.5f * x * (2.0f - 2.0f / (e + 1.0f));
+    // tanh-form GELU (arctic.zig:750-756): 0.5 x (1 + tanh(u)) = x / (1 + exp(-2u))
+    // with u = sqrt(2/pi) (x + 0.044715 x^3); exp and 1/d by v_exp_f32 and
+    // v_rcp_f32 (about 1 ulp each, far below the f16 rounding of the result).
+    // x -> -inf: exp -> +inf, 1/d -> 0, result -0; x -> +inf: result x.
+    constexpr float c0 = -2.0f * 0.7978845608f * 1.4426950408889634f;  // -2 sqrt(2/pi) log2(e)
+    constexpr float c1 = c0 * 0.044715f;
+    const float e = __builtin_amdgcn_exp2f(x * __builtin_fmaf(x * x, c1, c0));
+    return x * __builtin_amdgcn_rcpf(e + 1.0f);
 }
 
 template <typename TC>
@@ -170,6 +236,8 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     __shared__ __attribute__((aligned(16))) char st3[NS > 3 ? P::STAGE : 16];
     __shared__ __attribute__((aligned(16))) float par[NPAR][MAXN];
     __shared__ float stat0[LN ? BM * P::WN : 1], stat1[LN ? BM * P::WN : 1];
+    constexpr bool STAGED = std::is_same<TC, _Float16>::value;  // f16 output goes through LDS
+    __shared__ __attribute__((aligned(16))) char epi_ws[STAGED ? P::NW * 2048 : 16];
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wm = w / P::WN, wn = w % P::WN;
@@ -289,12 +357,25 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                         for (int q = 0; q < 4; q++) {
                             v[q] = acc[a][b][4 * g + q] * s[q] + bb[q];  // sum * s + bias (matmul_w8a32.zig:55)
                             if (EPI == EPI_GELU) v[q] = gelu_fast(v[q]);
+                            if constexpr (STAGED) acc[a][b][4 * g + q] = v[q];
                         }
-                        if (t < M) {
-                            store4<TC>(C + (size_t)t * N + n, v[0], v[1], v[2], v[3]);
-                            vmem_store_issued();
-                        }
+                        if constexpr (!STAGED)
+                            if (t < M) {
+                                store4<TC>(C + (size_t)t * N + n, v[0], v[1], v[2], v[3]);
+                                vmem_store_issued();
+                            }
                     }
+                if constexpr (STAGED) {
+                    const int t0 = m0 + wm * TMF * 32 + b * 32;
+#pragma unroll
+                    for (int a = 0; a < TNF; a++) {
+                        float v[16];
+#pragma unroll
+                        for (int e = 0; e < 16; e++) v[e] = acc[a][b][e];
+                        store_frag_f16(epi_ws + w * 2048, v, (_Float16 *)C + (size_t)t0 * N + n0 + wn * TNF * 32 + a * 32,
+                                       N, M - t0);
+                    }
+                }
             }
         } else {
             RV res[TMF][TNF][4];
@@ -372,13 +453,27 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                         const f32x4_t bt = *(const f32x4_t *)&par[3][n];
                         float y[4];
 #pragma unroll
-                        for (int q = 0; q < 4; q++)
+                        for (int q = 0; q < 4; q++) {
                             y[q] = ((acc[a][b][4 * g + q] - mean[b]) * inv_std) * gg[q] + bt[q];
-                        if (t < M) {
-                            store4<TC>(C + (size_t)t * BN + n, y[0], y[1], y[2], y[3]);
-                            vmem_store_issued();
+                            if constexpr (STAGED) acc[a][b][4 * g + q] = y[q];
                         }
+                        if constexpr (!STAGED)
+                            if (t < M) {
+                                store4<TC>(C + (size_t)t * BN + n, y[0], y[1], y[2], y[3]);
+                                vmem_store_issued();
+                            }
                     }
+                if constexpr (STAGED) {
+                    const int t0 = m0 + wm * TMF * 32 + b * 32;
+#pragma unroll
+                    for (int a = 0; a < TNF; a++) {
+                        float v[16];
+#pragma unroll
+                        for (int e = 0; e < 16; e++) v[e] = acc[a][b][e];
+                        store_frag_f16(epi_ws + w * 2048, v, (_Float16 *)C + (size_t)t0 * BN + wn * TNF * 32 + a * 32,
+                                       BN, M - t0);
+                    }
+                }
             }
         }
 #pragma unroll
@@ -395,12 +490,13 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     for (int j = 0; j < NS - 1; j++)
         if (j < S) issue(bufs[j]);
 
-    // The stores of the most recent epilogue (one vector store per lane per
-    // (token fragment, weight fragment, 4-column group)) were issued after
-    // the loads of stages up to last_epi + NS - 1; they are all issued
-    // exactly when the unit lies inside M (no lane of any store is masked
-    // off), and only then are they counted.
-    constexpr int EPI_STORES = TMF * TNF * 4;
+    // The stores of the most recent epilogue (per lane and (token fragment,
+    // weight fragment): two 16-byte stores of staged f16 rows, or one store
+    // per 4-column group of f32) were issued after the loads of stages up to
+    // last_epi + NS - 1; they are all issued exactly when the unit lies
+    // inside M (no lane of any store is masked off), and only then are they
+    // counted.
+    constexpr int EPI_STORES = TMF * TNF * (STAGED ? 2 : 4);
     int last_epi = -NS;
     bool last_full = false;
     auto step = [&](auto jc, int s) __attribute__((always_inline)) {

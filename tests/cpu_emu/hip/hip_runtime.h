@@ -63,6 +63,21 @@ inline void dma16(const char *sbase, uint32_t voff, char *lds_base) {
 }
 inline void lds_barrier_only() { emu::syncthreads(); }
 inline void vmem_store_issued() { emu::vmem_marker(); }
+// v_permlane32_swap_b32: lanes 32..63 of `lo` <-> lanes 0..31 of `hi`
+inline void lane_swap32(uint32_t &lo, uint32_t &hi) {
+    const int lane = emu::lane_id();
+    const uint32_t mine[2] = {lo, hi};
+    std::memcpy(emu::wave_slot(lane), mine, sizeof mine);
+    emu::wave_barrier();
+    uint32_t other[2];
+    std::memcpy(other, emu::wave_slot(lane ^ 32), sizeof other);
+    emu::wave_barrier();
+    if (lane < 32)
+        hi = other[0];  // the upper partner's lo
+    else
+        lo = other[1];  // the lower partner's hi
+}
+inline void wave_lds_order() { emu::wave_barrier(); }
 #define __builtin_amdgcn_s_waitcnt(imm) emu::waitcnt_vm(((imm)&15) | ((((imm) >> 14) & 3) << 4))
 #define __builtin_amdgcn_readfirstlane(x) (x)
 
@@ -166,6 +181,7 @@ inline emu_f32x4 mfma_16x16x32_args(emu_half8 a, emu_half8 b, emu_f32x4 c, int, 
 #define __builtin_amdgcn_mfma_f32_32x32x16_f16(...) emu::mfma_32x32x16_args(__VA_ARGS__)
 #define __builtin_amdgcn_mfma_f32_16x16x32_f16(...) emu::mfma_16x16x32_args(__VA_ARGS__)
 #define __builtin_amdgcn_exp2f(x) exp2f(x)
+#define __builtin_amdgcn_rcpf(x) (1.0f / (x))
 
 // ---------------------------------------------------------------------------
 // runtime API subset
