@@ -9,10 +9,15 @@
 // Design (gfx950): one workgroup per (sequence, head); its K and V^T
 // (L <= 512 keys) are staged in LDS once and every wave walks 16-query
 // tiles over them.  S^T = K Q^T and O^T = V^T P^T use
-// v_mfma_f32_16x16x32_f16 so that each lane owns one query: row max and row
-// sum are in-lane over 16 scores plus two cross-lane steps.  Softmax is the
-// online (running max / rescale) form in the exp2 domain; the division by
-// the row sum happens once at the end.
+// v_mfma_f32_16x16x32_f16 so that each lane owns one query.  The loop is
+// VALU-bound (one exp per score against 128 MFMA flops), so per score it
+// spends one FMA (scale and running max folded into the exp2 argument), one
+// exp2, half a max3 and half a packed convert: the row max crosses the four
+// lane rows with permlane swaps, keys past the end are masked only in the
+// last 64-key block, and the row sum is a third MFMA against a ones operand
+// (it sums the same f16 probabilities the P V product uses).  Softmax is the
+// online (running max / rescale) form; the division by the row sum happens
+// once at the end.
 #include "common.h"
 
 #include <vector>
@@ -21,8 +26,17 @@ namespace {
 
 constexpr int kHeadDim = 32;
 constexpr int kMaxKeys = 512;
-constexpr int K_LD = kHeadDim + 8;     // halves per K row in LDS
-constexpr int V_LD = kMaxKeys + 8;     // halves per V^T row in LDS
+constexpr int K_LD = kHeadDim + 8;     // halves per K row in LDS (80 B: conflict-free 16-byte reads)
+constexpr int V_LD = kMaxKeys + 8;     // halves per V^T row in LDS (1040 B: likewise)
+
+// Where key j sits in a V^T row.  Within each 32-key group, the keys the
+// PV operand of lane row g takes ({4g..4g+3} and {16+4g..16+4g+3}, the
+// order the S^T accumulators hold them in) are stored at 8g..8g+7, so one
+// 16-byte read fetches them.
+__device__ __forceinline__ int vt_pos(int key) {
+    const int j = key & 31;
+    return (key & ~31) + 8 * ((j & 15) >> 2) + 4 * (j >> 4) + (j & 3);
+}
 
 __global__ void __launch_bounds__(256) attn_varlen_kernel(const _Float16 *__restrict__ qkv, int ld,
                                                           _Float16 *__restrict__ out, int ld_out,
@@ -45,6 +59,7 @@ __global__ void __launch_bounds__(256) attn_varlen_kernel(const _Float16 *__rest
     const _Float16 *kbase = qbase + hidden;
     const _Float16 *vbase = qbase + 2 * hidden;
 
+    // keys L..Lp-1 are zero-filled: their probabilities are 0 and 0 * V must stay 0
     for (int idx = tid; idx < Lp * 4; idx += 256) {
         const int key = idx >> 2, c = (idx & 3) * 8;
         half8_t kv = {}, vv = {};
@@ -53,19 +68,21 @@ __global__ void __launch_bounds__(256) attn_varlen_kernel(const _Float16 *__rest
             vv = *(const half8_t *)(vbase + (size_t)key * ld + c);
         }
         *(half8_t *)(Ks + key * K_LD + c) = kv;
+        const int p = vt_pos(key);
 #pragma unroll
-        for (int i = 0; i < 8; i++) Vt[(c + i) * V_LD + key] = vv[i];
+        for (int i = 0; i < 8; i++) Vt[(c + i) * V_LD + p] = vv[i];
     }
     __syncthreads();
 
-    const int g = lane >> 4;   // lane group: k-slots 8g..8g+7, C rows 4g..4g+3
+    const int g = lane >> 4;   // lane row: k-slots 8g..8g+7, C rows 4g..4g+3
     const int ql = lane & 15;  // query (C column) owned by this lane
+    const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
     for (int q0 = w * 16; q0 < L; q0 += 64) {
         const int qrow = q0 + ql;
         half8_t qf = {};
         if (qrow < L) qf = *(const half8_t *)(qbase + (size_t)qrow * ld + g * 8);
-        float m = -INFINITY, l = 0.0f;
-        f32x4_t o0 = {0, 0, 0, 0}, o1 = {0, 0, 0, 0};
+        float m = -INFINITY;  // running max of the raw scores
+        f32x4_t o0 = {0, 0, 0, 0}, o1 = {0, 0, 0, 0}, lsum = {0, 0, 0, 0};
         for (int kb0 = 0; kb0 < Lp; kb0 += 64) {
             f32x4_t s[4];
 #pragma unroll
@@ -73,32 +90,29 @@ __global__ void __launch_bounds__(256) attn_varlen_kernel(const _Float16 *__rest
                 const half8_t kf = *(const half8_t *)(Ks + (kb0 + 16 * t + ql) * K_LD + g * 8);
                 s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf, f32x4_t{0, 0, 0, 0}, 0, 0, 0);
             }
-            float mx = -INFINITY;
+            if (kb0 + 64 > L) {  // the block holding the sequence end (wave-uniform)
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (kb0 + 16 * t + 4 * g + i >= L) s[t][i] = -INFINITY;
+            }
+            float mx = s[0][0];
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int key = kb0 + 16 * t + 4 * g + i;
-                    const float x = key < L ? s[t][i] * scale_log2 : -INFINITY;
-                    s[t][i] = x;
-                    mx = fmaxf(mx, x);
-                }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float m_new = fmaxf(m, mx);  // finite: every 64-key block holds a valid key
-            const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-            float ps = 0.0f;
+                for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[t][i]);
+            // finite: every 64-key block below Lp holds a key < L
+            const float m_new = fmaxf(m, max_over_rows(mx));
+            const float mc = m_new * scale_log2;
+            const float alpha = __builtin_amdgcn_exp2f((m - m_new) * scale_log2);  // 0 on the first block
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float p = __builtin_amdgcn_exp2f(s[t][i] - m_new);
-                    s[t][i] = p;
-                    ps += p;
-                }
-            l = l * alpha + ps;
+                for (int i = 0; i < 4; i++) s[t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][i], scale_log2, -mc));
             o0 *= alpha;
             o1 *= alpha;
+            lsum *= alpha;
 #pragma unroll
             for (int st = 0; st < 2; st++) {
                 half8_t pf;
@@ -107,26 +121,17 @@ __global__ void __launch_bounds__(256) attn_varlen_kernel(const _Float16 *__rest
                     pf[i] = (_Float16)s[2 * st][i];
                     pf[4 + i] = (_Float16)s[2 * st + 1][i];
                 }
-                const int kA = kb0 + 32 * st + 4 * g;
-                const _Float16 *v0 = Vt + ql * V_LD;
-                const _Float16 *v1 = Vt + (16 + ql) * V_LD;
-                const half4_t a0 = *(const half4_t *)(v0 + kA), a1 = *(const half4_t *)(v0 + kA + 16);
-                const half4_t b0 = *(const half4_t *)(v1 + kA), b1 = *(const half4_t *)(v1 + kA + 16);
-                half8_t va, vb;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    va[i] = a0[i]; va[4 + i] = a1[i];
-                    vb[i] = b0[i]; vb[4 + i] = b1[i];
-                }
+                const int kv = kb0 + 32 * st + 8 * g;
+                const half8_t va = *(const half8_t *)(Vt + ql * V_LD + kv);
+                const half8_t vb = *(const half8_t *)(Vt + (16 + ql) * V_LD + kv);
                 o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf, o0, 0, 0, 0);
                 o1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vb, pf, o1, 0, 0, 0);
+                lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lsum, 0, 0, 0);
             }
             m = m_new;
         }
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
         if (qrow < L) {
-            const float inv = 1.0f / l;
+            const float inv = 1.0f / lsum[0];  // every row of the ones product holds the row sum
             _Float16 *dst = out + (size_t)(start + qrow) * ld_out + h * kHeadDim + 4 * g;
             half4_t r0, r1;
 #pragma unroll

@@ -96,6 +96,36 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+#ifndef TZH_EMULATION
+// v_permlane32_swap_b32: lanes 32..63 of `lo` trade values with lanes 0..31
+// of `hi` (lanes 0..31 of `lo` and 32..63 of `hi` keep theirs).
+__device__ __forceinline__ void lane_swap32(uint32_t &lo, uint32_t &hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
+    lo = r[0];
+    hi = r[1];
+}
+
+// v_permlane16_swap_b32: lanes 16..31 and 48..63 of `a` trade values with
+// lanes 0..15 and 32..47 of `b` (lane i of one 16-lane row with lane i of
+// the row below it).
+__device__ __forceinline__ void lane_swap16(uint32_t &a, uint32_t &b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+    a = r[0];
+    b = r[1];
+}
+#endif
+
+// Maximum over the four lanes l % 16 + 16j (j = 0..3), left in all four:
+// two row swaps instead of LDS-routed shuffles.
+__device__ __forceinline__ float max_over_rows(float x) {
+    uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+    lane_swap16(a, b);
+    x = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    a = b = __builtin_bit_cast(uint32_t, x);
+    lane_swap32(a, b);
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
 // f32 -> f16 with round-to-nearest-even (v_cvt_f16_f32 honours the default RNE mode).
 __device__ __forceinline__ _Float16 to_f16(float x) { return (_Float16)x; }
 

@@ -57,14 +57,6 @@ __device__ __forceinline__ void lds_barrier_only() { asm volatile("s_barrier" ::
 // own in-order record of vector memory ops; on the GPU vmcnt does).
 __device__ __forceinline__ void vmem_store_issued() {}
 
-// v_permlane32_swap_b32: lanes 32..63 of `lo` trade values with lanes 0..31
-// of `hi` (lanes 0..31 of `lo` and 32..63 of `hi` keep theirs).
-__device__ __forceinline__ void lane_swap32(uint32_t &lo, uint32_t &hi) {
-    const auto r = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
-    lo = r[0];
-    hi = r[1];
-}
-
 // Orders a wave's LDS writes before its later LDS reads of what other lanes
 // of the same wave wrote.  The LDS performs one wave's operations in issue
 // order, so only the compiler has to be kept from reordering them.
@@ -529,7 +521,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 // 128 x 384 tiles halve the L2 -> LDS operand traffic of 128 x 128 ones.
 using BiasCfg = PipeCfg<128, 384, 64, 2, 4, 2>;      // n a multiple of 384
 using BiasCfgNarrow = PipeCfg<128, 128, 64, 2, 2, 4>;  // other multiples of 128
-using LnCfg = PipeCfg<128, 384, 32, 2, 4, 4>;
+using LnCfg = PipeCfg<128, 384, 64, 2, 4, 2>;
 
 
 template <int EPI, typename TC, typename P>

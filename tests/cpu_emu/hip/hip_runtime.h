@@ -77,6 +77,20 @@ inline void lane_swap32(uint32_t &lo, uint32_t &hi) {
     else
         lo = other[1];  // the lower partner's hi
 }
+// v_permlane16_swap_b32: odd 16-lane rows of `a` <-> even rows of `b`
+inline void lane_swap16(uint32_t &a, uint32_t &b) {
+    const int lane = emu::lane_id();
+    const uint32_t mine[2] = {a, b};
+    std::memcpy(emu::wave_slot(lane), mine, sizeof mine);
+    emu::wave_barrier();
+    uint32_t other[2];
+    std::memcpy(other, emu::wave_slot(lane ^ 16), sizeof other);
+    emu::wave_barrier();
+    if (lane & 16)
+        a = other[1];  // the even-row partner's b
+    else
+        b = other[0];  // the odd-row partner's a
+}
 inline void wave_lds_order() { emu::wave_barrier(); }
 #define __builtin_amdgcn_s_waitcnt(imm) emu::waitcnt_vm(((imm)&15) | ((((imm) >> 14) & 3) << 4))
 #define __builtin_amdgcn_readfirstlane(x) (x)
