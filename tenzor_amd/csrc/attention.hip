@@ -29,14 +29,10 @@ constexpr int kMaxKeys = 512;
 constexpr int K_LD = kHeadDim + 8;     // halves per K row in LDS (80 B: conflict-free 16-byte reads)
 constexpr int V_LD = kMaxKeys + 8;     // halves per V^T row in LDS (1040 B: likewise)
 
-// Where key j sits in a V^T row.  Within each 32-key group, the keys the
-// PV operand of lane row g takes ({4g..4g+3} and {16+4g..16+4g+3}, the
-// order the S^T accumulators hold them in) are stored at 8g..8g+7, so one
-// 16-byte read fetches them.
-__device__ __forceinline__ int vt_pos(int key) {
-    const int j = key & 31;
-    return (key & ~31) + 8 * ((j & 15) >> 2) + 4 * (j >> 4) + (j & 3);
-}
+// V^T row layout: within each 32-key group, the keys the PV operand of lane
+// row g takes ({4g..4g+3} and {16+4g..16+4g+3}, the order the S^T
+// accumulators hold them in) are stored at 8g..8g+7, so one 16-byte read
+// fetches them: key j of a group sits at 8 * ((j % 16) / 4) + 4 * (j / 16) + j % 4.
 
 __global__ void __launch_bounds__(256) attn_varlen_kernel(const _Float16 *__restrict__ qkv, int ld,
                                                           _Float16 *__restrict__ out, int ld_out,
@@ -62,85 +58,129 @@ __global__ void __launch_bounds__(256) attn_varlen_kernel(const _Float16 *__rest
     // keys L..Lp-1 are zero-filled: their probabilities are 0 and 0 * V must stay 0
     for (int idx = tid; idx < Lp * 4; idx += 256) {
         const int key = idx >> 2, c = (idx & 3) * 8;
-        half8_t kv = {}, vv = {};
-        if (key < L) {
-            kv = *(const half8_t *)(kbase + (size_t)key * ld + c);
-            vv = *(const half8_t *)(vbase + (size_t)key * ld + c);
-        }
+        half8_t kv = {};
+        if (key < L) kv = *(const half8_t *)(kbase + (size_t)key * ld + c);
         *(half8_t *)(Ks + key * K_LD + c) = kv;
-        const int p = vt_pos(key);
+    }
+    // V^T: each lane loads an 8-key x 8-dim block (the keys one PV operand
+    // read takes), transposes it in registers and writes eight 16-byte rows
+    // (lanes 0..15 of a write cover sixteen distinct bank slots).
+    {
+        const int gq = lane & 3, kg = (lane >> 2) & 3, c = lane >> 4;
+        for (int kb = 128 * w; kb < Lp; kb += 512) {
+            const int k0 = kb + 32 * kg + 4 * gq;  // keys k0 + {0..3} and k0 + 16 + {0..3}
+            half8_t v[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) Vt[(c + i) * V_LD + p] = vv[i];
+            for (int r = 0; r < 8; r++) {
+                const int key = k0 + (r & 3) + 16 * (r >> 2);
+                v[r] = half8_t{};
+                if (key < L) v[r] = *(const half8_t *)(vbase + (size_t)key * ld + 8 * c);
+            }
+#pragma unroll
+            for (int d = 0; d < 8; d++) {
+                half8_t col;
+#pragma unroll
+                for (int r = 0; r < 8; r++) col[r] = v[r][d];
+                *(half8_t *)(Vt + (8 * c + d) * V_LD + kb + 32 * kg + 8 * gq) = col;
+            }
+        }
     }
     __syncthreads();
 
     const int g = lane >> 4;   // lane row: k-slots 8g..8g+7, C rows 4g..4g+3
-    const int ql = lane & 15;  // query (C column) owned by this lane
+    const int ql = lane & 15;  // query (C column) owned by this lane in each tile
     const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
-    for (int q0 = w * 16; q0 < L; q0 += 64) {
-        const int qrow = q0 + ql;
-        half8_t qf = {};
-        if (qrow < L) qf = *(const half8_t *)(qbase + (size_t)qrow * ld + g * 8);
-        float m = -INFINITY;  // running max of the raw scores
-        f32x4_t o0 = {0, 0, 0, 0}, o1 = {0, 0, 0, 0}, lsum = {0, 0, 0, 0};
+    // Each wave carries QT 16-query tiles at once: they share every K and V
+    // fragment read, and their softmax chains are independent work for the
+    // scheduler to interleave.
+    constexpr int QT = 2;
+    for (int q0 = w * 16 * QT; q0 < L; q0 += 64 * QT) {
+        half8_t qf[QT];
+        float m[QT];  // running max of the raw scores
+        f32x4_t o0[QT], o1[QT], lsum[QT];
+#pragma unroll
+        for (int j = 0; j < QT; j++) {
+            const int qrow = q0 + 16 * j + ql;
+            qf[j] = half8_t{};
+            if (qrow < L) qf[j] = *(const half8_t *)(qbase + (size_t)qrow * ld + g * 8);
+            m[j] = -INFINITY;
+            o0[j] = o1[j] = lsum[j] = f32x4_t{0, 0, 0, 0};
+        }
         for (int kb0 = 0; kb0 < Lp; kb0 += 64) {
-            f32x4_t s[4];
+            f32x4_t s[QT][4];
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const half8_t kf = *(const half8_t *)(Ks + (kb0 + 16 * t + ql) * K_LD + g * 8);
-                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf, f32x4_t{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < QT; j++)
+                    s[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[j], f32x4_t{0, 0, 0, 0}, 0, 0, 0);
             }
             if (kb0 + 64 > L) {  // the block holding the sequence end (wave-uniform)
+                const int rem = L - kb0 - 4 * g;  // element (t, i) is key kb0 + 4g + 16t + i
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const bool past = 16 * t + i >= rem;
+#pragma unroll
+                        for (int j = 0; j < QT; j++) s[j][t][i] = past ? -INFINITY : s[j][t][i];
+                    }
+            }
+#pragma unroll
+            for (int j = 0; j < QT; j++) {
+                float mx = s[j][0][0];
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[j][t][i]);
+                // finite: every 64-key block below Lp holds a key < L
+                const float m_new = fmaxf(m[j], max_over_rows(mx));
+                const float mc = m_new * scale_log2;
+                const float alpha = __builtin_amdgcn_exp2f((m[j] - m_new) * scale_log2);  // 0 on the first block
 #pragma unroll
                 for (int t = 0; t < 4; t++)
 #pragma unroll
                     for (int i = 0; i < 4; i++)
-                        if (kb0 + 16 * t + 4 * g + i >= L) s[t][i] = -INFINITY;
+                        s[j][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][t][i], scale_log2, -mc));
+                o0[j] *= alpha;
+                o1[j] *= alpha;
+                lsum[j] *= alpha;
+                m[j] = m_new;
             }
-            float mx = s[0][0];
-#pragma unroll
-            for (int t = 0; t < 4; t++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[t][i]);
-            // finite: every 64-key block below Lp holds a key < L
-            const float m_new = fmaxf(m, max_over_rows(mx));
-            const float mc = m_new * scale_log2;
-            const float alpha = __builtin_amdgcn_exp2f((m - m_new) * scale_log2);  // 0 on the first block
-#pragma unroll
-            for (int t = 0; t < 4; t++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) s[t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][i], scale_log2, -mc));
-            o0 *= alpha;
-            o1 *= alpha;
-            lsum *= alpha;
 #pragma unroll
             for (int st = 0; st < 2; st++) {
-                half8_t pf;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    pf[i] = (_Float16)s[2 * st][i];
-                    pf[4 + i] = (_Float16)s[2 * st + 1][i];
-                }
                 const int kv = kb0 + 32 * st + 8 * g;
                 const half8_t va = *(const half8_t *)(Vt + ql * V_LD + kv);
                 const half8_t vb = *(const half8_t *)(Vt + (16 + ql) * V_LD + kv);
-                o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf, o0, 0, 0, 0);
-                o1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vb, pf, o1, 0, 0, 0);
-                lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lsum, 0, 0, 0);
-            }
-            m = m_new;
-        }
-        if (qrow < L) {
-            const float inv = 1.0f / lsum[0];  // every row of the ones product holds the row sum
-            _Float16 *dst = out + (size_t)(start + qrow) * ld_out + h * kHeadDim + 4 * g;
-            half4_t r0, r1;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                r0[i] = (_Float16)(o0[i] * inv);
-                r1[i] = (_Float16)(o1[i] * inv);
+                for (int j = 0; j < QT; j++) {
+                    half8_t pf;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        pf[i] = (_Float16)s[j][2 * st][i];
+                        pf[4 + i] = (_Float16)s[j][2 * st + 1][i];
+                    }
+                    o0[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf, o0[j], 0, 0, 0);
+                    o1[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vb, pf, o1[j], 0, 0, 0);
+                    lsum[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lsum[j], 0, 0, 0);
+                }
             }
-            *(half4_t *)dst = r0;
-            *(half4_t *)(dst + 16) = r1;
+        }
+#pragma unroll
+        for (int j = 0; j < QT; j++) {
+            const int qrow = q0 + 16 * j + ql;
+            if (qrow < L) {
+                const float inv = 1.0f / lsum[j][0];  // every row of the ones product holds the row sum
+                _Float16 *dst = out + (size_t)(start + qrow) * ld_out + h * kHeadDim + 4 * g;
+                half4_t r0, r1;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    r0[i] = (_Float16)(o0[j][i] * inv);
+                    r1[i] = (_Float16)(o1[j][i] * inv);
+                }
+                *(half4_t *)dst = r0;
+                *(half4_t *)(dst + 16) = r1;
+            }
         }
     }
 }

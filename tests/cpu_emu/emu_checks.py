@@ -238,7 +238,7 @@ def group_gemm():
 
 def group_attention():
     H, D = 384, 32
-    for lengths in ([1], [2, 3], [15, 16, 17], [63, 64, 65], [100, 1, 130]):
+    for lengths in ([1], [2, 3], [15, 16, 17], [63, 64, 65], [100, 1, 130], [512]):
         rng = np.random.default_rng(sum(lengths))
         Tn = sum(lengths)
         qkv = (rng.standard_normal((Tn, 3 * H)) * 1.5).astype(np.float16)
