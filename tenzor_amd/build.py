@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -47,12 +48,34 @@ def hipcc() -> str:
     return exe
 
 
+def scratch_spills(remarks: str) -> list[tuple[str, int]]:
+    """(kernel, bytes per lane) for every kernel the compiler's
+    kernel-resource-usage remarks report with a non-zero scratch size."""
+    out, name = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and name and int(m.group(1)) > 0:
+            out.append((name, int(m.group(1))))
+    return out
+
+
 def _compile(src: str) -> Path:
     obj = BUILD / (Path(src).stem + ".o")
-    cmd = [hipcc(), "-x", "hip", *HIPFLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [hipcc(), "-x", "hip", *HIPFLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src), "-o",
+           str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile of {src} failed:\n{res.stderr}")
+    # The pipelined GEMM tracks its direct-to-LDS loads with explicit vmcnt
+    # counts; compiler spill traffic would be vector memory ops it does not
+    # plan for, so no kernel may spill to scratch.
+    spills = scratch_spills(res.stderr)
+    if spills:
+        raise RuntimeError(f"{src}: kernels spill to scratch: {spills}")
     return obj
 
 

@@ -28,13 +28,16 @@ constexpr int kHeadDim = 32;
 constexpr int kMaxKeys = 512;
 constexpr int K_LD = kHeadDim + 8;     // halves per K row in LDS (80 B: conflict-free 16-byte reads)
 constexpr int V_LD = kMaxKeys + 8;     // halves per V^T row in LDS (1040 B: likewise)
+constexpr int kWaves = 8;              // waves per workgroup (2 workgroups per CU by LDS)
+constexpr int kQueryTiles = 2;         // 16-query tiles a wave carries at once
 
 // V^T row layout: within each 32-key group, the keys the PV operand of lane
 // row g takes ({4g..4g+3} and {16+4g..16+4g+3}, the order the S^T
 // accumulators hold them in) are stored at 8g..8g+7, so one 16-byte read
 // fetches them: key j of a group sits at 8 * ((j % 16) / 4) + 4 * (j / 16) + j % 4.
 
-__global__ void __launch_bounds__(256) attn_varlen_kernel(const _Float16 *__restrict__ qkv, int ld,
+template <int NW, int QT>
+__global__ void __launch_bounds__(NW * 64) attn_varlen_kernel(const _Float16 *__restrict__ qkv, int ld,
                                                           _Float16 *__restrict__ out, int ld_out,
                                                           const int *__restrict__ cu_seqlens,
                                                           const int *__restrict__ order, int n_heads,
@@ -56,7 +59,7 @@ __global__ void __launch_bounds__(256) attn_varlen_kernel(const _Float16 *__rest
     const _Float16 *vbase = qbase + 2 * hidden;
 
     // keys L..Lp-1 are zero-filled: their probabilities are 0 and 0 * V must stay 0
-    for (int idx = tid; idx < Lp * 4; idx += 256) {
+    for (int idx = tid; idx < Lp * 4; idx += NW * 64) {
         const int key = idx >> 2, c = (idx & 3) * 8;
         half8_t kv = {};
         if (key < L) kv = *(const half8_t *)(kbase + (size_t)key * ld + c);
@@ -67,7 +70,7 @@ __global__ void __launch_bounds__(256) attn_varlen_kernel(const _Float16 *__rest
     // (lanes 0..15 of a write cover sixteen distinct bank slots).
     {
         const int gq = lane & 3, kg = (lane >> 2) & 3, c = lane >> 4;
-        for (int kb = 128 * w; kb < Lp; kb += 512) {
+        for (int kb = 128 * w; kb < Lp; kb += 128 * NW) {
             const int k0 = kb + 32 * kg + 4 * gq;  // keys k0 + {0..3} and k0 + 16 + {0..3}
             half8_t v[8];
 #pragma unroll
@@ -93,8 +96,7 @@ __global__ void __launch_bounds__(256) attn_varlen_kernel(const _Float16 *__rest
     // Each wave carries QT 16-query tiles at once: they share every K and V
     // fragment read, and their softmax chains are independent work for the
     // scheduler to interleave.
-    constexpr int QT = 2;
-    for (int q0 = w * 16 * QT; q0 < L; q0 += 64 * QT) {
+    for (int q0 = w * 16 * QT; q0 < L; q0 += NW * 16 * QT) {
         half8_t qf[QT];
         float m[QT];  // running max of the raw scores
         f32x4_t o0[QT], o1[QT], lsum[QT];
@@ -197,8 +199,8 @@ int tzh_attention_launch(hipStream_t st, const _Float16 *qkv, _Float16 *out, con
     if (batch <= 0) return TZH_OK;
     const float scale = 1.0f / sqrtf((float)kHeadDim);  // arctic.zig:649
     const float scale_log2 = scale * 1.4426950408889634f;
-    hipLaunchKernelGGL(attn_varlen_kernel, dim3(batch * n_heads), dim3(256), 0, st, qkv, 3 * hidden, out, hidden,
-                       cu_seqlens, order, n_heads, hidden, scale_log2);
+    hipLaunchKernelGGL((attn_varlen_kernel<kWaves, kQueryTiles>), dim3(batch * n_heads), dim3(kWaves * 64), 0, st, qkv,
+                       3 * hidden, out, hidden, cu_seqlens, order, n_heads, hidden, scale_log2);
     TZH_LAUNCHED("attn_varlen_kernel");
     return TZH_OK;
 }

@@ -370,23 +370,20 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                 }
             }
         } else {
-            RV res[TMF][TNF][4];
-#pragma unroll
-            for (int b = 0; b < TMF; b++) {
-                int t = m0 + wm * TMF * 32 + b * 32 + l31;
-                t = t < M ? t : M - 1;
-#pragma unroll
-                for (int a = 0; a < TNF; a++)
-#pragma unroll
-                    for (int g = 0; g < 4; g++)
-                        res[b][a][g] = *(const RV *)(R + (size_t)t * BN + wn * TNF * 32 + a * 32 + 8 * g + 4 * half);
-            }
             float part[TMF];
 #pragma unroll
             for (int b = 0; b < TMF; b++) {
+                // the residual is loaded one weight fragment at a time so that
+                // the live registers stay within budget (no scratch spills)
+                int t = m0 + wm * TMF * 32 + b * 32 + l31;
+                t = t < M ? t : M - 1;
                 float sum = 0.0f;
 #pragma unroll
-                for (int a = 0; a < TNF; a++)
+                for (int a = 0; a < TNF; a++) {
+                    RV res[4];
+#pragma unroll
+                    for (int g = 0; g < 4; g++)
+                        res[g] = *(const RV *)(R + (size_t)t * BN + wn * TNF * 32 + a * 32 + 8 * g + 4 * half);
 #pragma unroll
                     for (int g = 0; g < 4; g++) {
                         const int n = wn * TNF * 32 + a * 32 + 8 * g + 4 * half;
@@ -395,11 +392,12 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 #pragma unroll
                         for (int q = 0; q < 4; q++) {
                             // input + (sum * s + bias)  (arctic.zig:720)
-                            const float v = (float)res[b][a][g][q] + (acc[a][b][4 * g + q] * s[q] + bb[q]);
+                            const float v = (float)res[g][q] + (acc[a][b][4 * g + q] * s[q] + bb[q]);
                             acc[a][b][4 * g + q] = v;
                             sum += v;
                         }
                     }
+                }
                 part[b] = sum + __shfl_xor(sum, 32, 64);
             }
             if (half == 0)

@@ -151,3 +151,16 @@ def test_synthetic_batches_follow_the_config():
     assert flat.size == lengths.sum() and offs[-1] + lengths[-1] == flat.size
     w = synth.quantize(synth.make_arctic_f32(1, synth.Config(num_hidden_layers=1)))
     assert sum(1 for k, v in w.items() if v.dtype == np.int8) == 6
+
+
+def test_build_rejects_scratch_spills():
+    # the build refuses kernels that spill to scratch (their vector memory
+    # traffic would not be in the pipelined GEMM's vmcnt plan)
+    from tenzor_amd.build import scratch_spills
+    remarks = "\n".join([
+        "a.hip:1:1: remark: Function Name: k_ok [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:1:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:9:1: remark: Function Name: k_spill [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:9:1: remark:     ScratchSize [bytes/lane]: 40 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert scratch_spills(remarks) == [("k_spill", 40)]
