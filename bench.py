@@ -28,6 +28,7 @@ HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 F16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 SEED_WEIGHTS, SEED_BATCH = 1, 5
 BATCH, SEQ = 256, 512
+TRAFFIC_PROFILE = "arctic_b256_stage_profile.md"
 
 
 KERNELS = {
@@ -138,6 +139,15 @@ def main():
     else:
         achieved, peak, unit = dom["flops"] / secs / 1e12, F16_PEAK_TFLOPS, "TFLOP/s"
     fwd_roof_us = sum(st["roof_us"] * st["launches"] for st in stages.values())
+    # HBM bytes per launch of that stage, measured by rocprofv3 FETCH_SIZE and
+    # WRITE_SIZE passes over the same workload (calibrated against a known
+    # copy; see profile_summary.py) and committed with the profile
+    from tenzor_amd.profile_summary import load_traffic
+
+    measured = load_traffic(os.path.join(ROOT, "profiles", TRAFFIC_PROFILE)).get("stages", {}).get(dom_name, {})
+    traffic = None
+    if measured.get("read_bytes") is not None and measured.get("write_bytes") is not None:
+        traffic = measured["read_bytes"] + measured["write_bytes"]
 
     line = {
         "metric": "tokens/sec int8 arctic-embed-xs b256 s512, 1 GPU; % of HBM/MFMA roofline",
@@ -169,7 +179,8 @@ def main():
             "peak": peak,
             "unit": unit,
             "frac": round(achieved / peak, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": f"profiles/{TRAFFIC_PROFILE}" if traffic is not None else None,
             "avg_us": round(dom["avg_us"], 2),
             "algorithmic_bytes": int(dom["bytes"]),
             "algorithmic_flops": int(dom["flops"]),

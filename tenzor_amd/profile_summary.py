@@ -1,0 +1,217 @@
+"""Per-stage figures of the Arctic forward from rocprofv3 output.
+
+Two subcommands:
+
+    python -m tenzor_amd.profile_summary run
+        One forward of the bench workload (config 5) plus one elementwise
+        multiply that reads and writes CAL_BYTES, for `rocprofv3
+        --kernel-trace` or `--pmc FETCH_SIZE` / `--pmc WRITE_SIZE` to
+        observe (the program goes right after `--`).
+
+    python -m tenzor_amd.profile_summary summarize [--trace DIR] [--fetch DIR] [--write DIR]
+        Reads the CSV output of those runs and prints a markdown summary with
+        one row per forward stage, ending in a fenced JSON block that
+        bench.py reads for `roofline.traffic`.
+
+Dispatches are mapped to forward stages by kernel and launch order: both
+LayerNorm GEMMs are one kernel instantiation; the one launched after
+attention is attn_out_ln and the one after ffn1_gelu is ffn2_ln.
+
+FETCH_SIZE and WRITE_SIZE (KiB per dispatch, summed over the L2 channels)
+are scaled by what they read for the calibration multiply, whose true traffic
+is CAL_BYTES read and CAL_BYTES written.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import json
+import os
+import sys
+
+CAL_BYTES = 1 << 30
+STAGES = ("pack_ids", "embed_ln", "qkv", "attention", "attn_out_ln", "ffn1_gelu", "ffn2_ln", "cls_l2")
+
+
+def stage_of(kernel: str, prev: str | None) -> str | None:
+    """Forward stage of a dispatch of `kernel`, given the previous stage."""
+    if "pack_ids_kernel" in kernel:
+        return "pack_ids"
+    if "embed_ln_kernel" in kernel:
+        return "embed_ln"
+    if "attn_varlen_kernel" in kernel:
+        return "attention"
+    if "cls_l2_kernel" in kernel:
+        return "cls_l2"
+    if "linear_pipe_kernelILi0E" in kernel:
+        return "qkv"
+    if "linear_pipe_kernelILi1E" in kernel:
+        return "ffn1_gelu"
+    if "linear_pipe_kernelILi2E" in kernel:
+        return "attn_out_ln" if prev == "attention" else "ffn2_ln" if prev == "ffn1_gelu" else None
+    return None
+
+
+def _rows(directory: str, suffix: str) -> list[dict]:
+    files = sorted(glob.glob(os.path.join(directory, "**", f"*{suffix}"), recursive=True))
+    if not files:
+        raise FileNotFoundError(f"no *{suffix} under {directory}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
+def trace_stats(directory: str) -> dict:
+    """{stage: (dispatches, average microseconds)} from a kernel trace."""
+    rows = sorted(_rows(directory, "kernel_trace.csv"), key=lambda r: int(r["Dispatch_Id"]))
+    acc, prev = {}, None
+    for r in rows:
+        st = stage_of(r["Kernel_Name"], prev)
+        if st is None:
+            continue
+        prev = st
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
+        acc.setdefault(st, []).append(us)
+    return {k: (len(v), sum(v) / len(v)) for k, v in acc.items()}
+
+
+def counter_stats(directory: str, counter: str) -> tuple[dict, float]:
+    """({stage: average counter value per dispatch}, the calibration multiply's value)."""
+    per_dispatch = {}
+    for r in _rows(directory, "counter_collection.csv"):
+        if r["Counter_Name"] != counter:
+            continue
+        d = int(r["Dispatch_Id"])
+        name, v = per_dispatch.get(d, (r["Kernel_Name"], 0.0))
+        per_dispatch[d] = (name, v + float(r["Counter_Value"]))
+    acc, prev, cal = {}, None, 0.0
+    for d in sorted(per_dispatch):
+        name, v = per_dispatch[d]
+        if "elementwise_kernel" in name:  # the calibration multiply (and torch's fills)
+            cal = max(cal, v)
+        st = stage_of(name, prev)
+        if st is None:
+            continue
+        prev = st
+        acc.setdefault(st, []).append(v)
+    return {k: sum(v) / len(v) for k, v in acc.items()}, cal
+
+
+COMMANDS = """Commands (on one MI355X; rocprofv3 runs from /tmp with TMPDIR=/tmp and
+PYTHONPATH=<repo>, the program right after `--`):
+
+    rocprofv3 --kernel-trace --stats --output-format csv -d <out>/trace -o fwd -- \\
+        python3 <repo>/bench.py --steps 5 --warmup 2 --no-cpu-baseline
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/fetch -o f -- \\
+        python3 <repo>/tenzor_amd/profile_summary.py run
+    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/write -o w -- \\
+        python3 <repo>/tenzor_amd/profile_summary.py run
+    python3 <repo>/tenzor_amd/profile_summary.py summarize \\
+        --trace <out>/trace --fetch <out>/fetch --write <out>/write
+"""
+
+
+def kernel_stats_table(directory: str, top: int = 10) -> list[str]:
+    """rocprofv3's --stats kernel summary as a markdown table."""
+    rows = _rows(directory, "kernel_stats.csv")
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    out = ["| kernel | calls | avg us | total ms | % |", "|---|---:|---:|---:|---:|"]
+    for r in rows[:top]:
+        out.append(f"| `{r['Name'][:96]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                   f"{float(r['TotalDurationNs']) / 1e6:.2f} | {float(r['Percentage']):.1f} |")
+    return out
+
+
+def summarize(trace: str | None, fetch: str | None, write: str | None) -> str:
+    out = ["# Per-stage profile: int8 Arctic-embed-xs forward, batch 256 x seq 512", "", COMMANDS]
+    data: dict = {"stages": {}}
+    times = trace_stats(trace) if trace else {}
+    f_stats, f_cal = counter_stats(fetch, "FETCH_SIZE") if fetch else ({}, 0.0)
+    w_stats, w_cal = counter_stats(write, "WRITE_SIZE") if write else ({}, 0.0)
+    cal_kib = CAL_BYTES / 1024.0
+    f_scale = cal_kib / f_cal if f_cal else None
+    w_scale = cal_kib / w_cal if w_cal else None
+    if fetch or write:
+        out.append(f"Calibration: an elementwise multiply over {CAL_BYTES} bytes read FETCH_SIZE {f_cal:.0f} KiB "
+                   f"(scale {f_scale if f_scale is None else round(f_scale, 4)}) and WRITE_SIZE {w_cal:.0f} KiB "
+                   f"(scale {w_scale if w_scale is None else round(w_scale, 4)}); per-stage bytes below are "
+                   "counter x scale.")
+        out.append("")
+    out.append("| stage | dispatches | avg us | HBM read MB | HBM write MB |")
+    out.append("|---|---:|---:|---:|---:|")
+    for st in STAGES:
+        n, us = times.get(st, (0, float("nan")))
+        rd = f_stats[st] * 1024 * f_scale if st in f_stats and f_scale else None
+        wr = w_stats[st] * 1024 * w_scale if st in w_stats and w_scale else None
+        data["stages"][st] = {"dispatches": n, "avg_us": None if n == 0 else round(us, 2),
+                              "read_bytes": None if rd is None else int(rd),
+                              "write_bytes": None if wr is None else int(wr)}
+        out.append(f"| {st} | {n} | {us:.1f} | {'' if rd is None else f'{rd / 1e6:.1f}'} | "
+                   f"{'' if wr is None else f'{wr / 1e6:.1f}'} |")
+    data["calibration"] = {"bytes": CAL_BYTES, "fetch_kib": f_cal, "write_kib": w_cal}
+    if trace:
+        out += ["", "The two LayerNorm GEMMs are one kernel instantiation; the rows above separate",
+                "them by launch order. rocprofv3's own kernel summary of the trace run (5 timed",
+                "forwards + 2 warmup + 3 with per-launch events):", ""]
+        out += kernel_stats_table(trace)
+    out += ["", "```json", json.dumps(data, indent=1), "```", ""]
+    return "\n".join(out)
+
+
+def load_traffic(path: str) -> dict:
+    """The JSON block of a summary written by `summarize` ({} if absent)."""
+    try:
+        text = open(path).read()
+    except OSError:
+        return {}
+    start = text.find("```json")
+    if start < 0:
+        return {}
+    end = text.find("```", start + 7)
+    return json.loads(text[start + 7:end])
+
+
+def run() -> None:
+    import numpy as np
+    import torch
+
+    import tenzor_amd
+    from tenzor_amd import synth
+    from tenzor_amd.arctic import ModelWeights, forwardBatch
+
+    cfg = synth.Config()
+    ctx = tenzor_amd.Context(0)
+    model = ModelWeights.fromHost(ctx, synth.quantize(synth.make_arctic_f32(1, cfg)), cfg)
+    ids, lengths = synth.make_batch(5, 256, 512)
+    d_ids = torch.from_numpy(ids.view(np.int32)).cuda()
+    out = torch.empty((256, cfg.hidden_size), device="cuda")
+    forwardBatch(out, d_ids, lengths, model)
+    torch.cuda.synchronize()
+    src = torch.ones(CAL_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.mul(src, 2.0, out=dst)  # reads and writes CAL_BYTES
+    torch.cuda.synchronize()
+    print("forward and calibration multiply done", flush=True)
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    sub.add_parser("run")
+    s = sub.add_parser("summarize")
+    s.add_argument("--trace")
+    s.add_argument("--fetch")
+    s.add_argument("--write")
+    a = ap.parse_args(argv)
+    if a.cmd == "run":
+        run()
+    else:
+        sys.stdout.write(summarize(a.trace, a.fetch, a.write))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
