@@ -19,9 +19,10 @@
 //     tile before they are stored; f32 ones are stored as 16-byte vectors
 //     straight from the accumulators.
 //   - Persistent blocks (one per CU): the (row panel, column tile) work units
-//     are split into contiguous per-block ranges and the stage ring runs
-//     across unit boundaries, so the next unit's tiles are already in flight
-//     while a unit's epilogue runs.
+//     are dealt out XCD by XCD so that the column tiles of a row panel run
+//     together on one XCD and share its L2, and the stage ring runs across
+//     unit boundaries, so the next unit's tiles are already in flight while
+//     a unit's epilogue runs.
 //   - Each stage buffer is its own __shared__ array: the compiler can then
 //     tell a read of stage s from the in-flight loads of stages s+1.. and
 //     does not drain the ring before every LDS read.  Stage completion is
@@ -35,6 +36,8 @@
 #include "common.h"
 
 namespace {
+
+constexpr int kXcds = 8;  // MI355X: 8 XCDs of 32 CUs
 
 #ifndef TZH_EMULATION
 // global_load_lds_dwordx4: lane l's 16 bytes at sbase + voff[l] land in LDS
@@ -212,7 +215,7 @@ enum { EPI_BIAS = 0, EPI_GELU = 1, EPI_LN = 2 };
 template <int EPI, typename TC, typename P>
 __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     const _Float16 *__restrict__ X, const _Float16 *__restrict__ Wc, const uint16_t *__restrict__ scale,
-    const float *__restrict__ bias, TC *__restrict__ C, int M, int K, int N, int units, const TC *__restrict__ R,
+    const float *__restrict__ bias, TC *__restrict__ C, int M, int K, int N, const TC *__restrict__ R,
     const float *__restrict__ gamma, const float *__restrict__ beta, float eps) {
     using F = typename P::F;
     constexpr int BM = P::BM, BN = P::BN, BK = P::BK, NS = P::NS, TMF = P::TMF, TNF = P::TNF;
@@ -234,10 +237,24 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wm = w / P::WN, wn = w % P::WN;
     const int KT = K / BK;
-    const int nbn = N / BN;
-    const int u0 = (int)((int64_t)blockIdx.x * units / gridDim.x);
-    const int u1 = (int)((int64_t)(blockIdx.x + 1) * units / gridDim.x);
-    const int S = (u1 - u0) * KT;
+    const int nbn = N / BN;  // column tiles per row panel (1 with the LayerNorm epilogue)
+    // Work units are (row panel, column tile) pairs.  Workgroups go to the
+    // XCDs round-robin (block b on XCD b % 8) and each XCD has its own L2.
+    // Panel p belongs to XCD p % 8, and an XCD's units, column tile fastest,
+    // are dealt to its blocks one per block per round: the column tiles of a
+    // panel run at the same time on one XCD, so its activations come from
+    // HBM once and from L2 for the other tiles.  Unit i of this block is
+    // j = slot + i * spx of its XCD.
+    const int nxcd = gridDim.x % kXcds == 0 ? kXcds : 1;
+    const int xcd = blockIdx.x % nxcd, spx = gridDim.x / nxcd, slot = blockIdx.x / nxcd;
+    const int panels = (M + BM - 1) / BM;
+    const int xunits = (panels - xcd + nxcd - 1) / nxcd * nbn;  // units of this XCD
+    const int count = slot < xunits ? (xunits - slot + spx - 1) / spx : 0;
+    const int S = count * KT;
+    auto unit_m0 = [&](int i) __attribute__((always_inline)) {
+        return ((slot + i * spx) / nbn * nxcd + xcd) * BM;
+    };
+    auto unit_n0 = [&](int i) __attribute__((always_inline)) { return (slot + i * spx) % nbn * BN; };
 
     // per-column parameters -> LDS (visible after the first stage barrier)
     for (int i = tid; i < N; i += P::THREADS) {
@@ -261,13 +278,12 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     const uint32_t w_loff_o = (uint32_t)(r_in * K + chunk_o * 8) * 2u;
     const char *const Xb = (const char *)X;
     const char *const Wb = (const char *)Wc;
-    int iu = u0, ikt = 0;                                            // next stage to issue
+    int iu = 0, ikt = 0;                                             // next stage to issue
     int x_row0[P::LX];                                               // uniform first row of each X group
     uint32_t x_loff[P::LX];                                          // per-lane byte offset (row clamp)
     const char *w_unit = nullptr;                                    // uniform: first W row of the wave
-    auto set_unit = [&](int u) __attribute__((always_inline)) {
-        const int m0 = LN ? u * BM : (u / nbn) * BM;
-        const int n0 = LN ? 0 : (u % nbn) * BN;
+    auto set_unit = [&](int i) __attribute__((always_inline)) {
+        const int m0 = unit_m0(i), n0 = unit_n0(i);
 #pragma unroll
         for (int i = 0; i < P::LX; i++) {
             int r0 = m0 + (wu * P::LX + i) * F::RPI;
@@ -291,7 +307,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                   buf + P::X_BYTES + (wu * P::LW + i) * F::RPI * ROWB);
         if (++ikt == KT) {
             ikt = 0;
-            if (++iu < u1) set_unit(iu);
+            if (++iu < count) set_unit(iu);
         }
     };
 
@@ -330,9 +346,8 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 
     using RV = std::conditional_t<std::is_same<TC, float>::value, f32x4_t, half4_t>;
 
-    auto epilogue = [&](int u) __attribute__((always_inline)) {
-        const int m0 = LN ? u * BM : (u / nbn) * BM;
-        const int n0 = LN ? 0 : (u % nbn) * BN;
+    auto epilogue = [&](int i) __attribute__((always_inline)) {
+        const int m0 = unit_m0(i), n0 = unit_n0(i);
         if constexpr (!LN) {
 #pragma unroll
             for (int b = 0; b < TMF; b++) {
@@ -473,7 +488,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     };
 
     if (S == 0) return;
-    set_unit(u0);
+    set_unit(0);
     char *const bufs[4] = {st0, st1, st2, st3};
     // prologue: stages 0 .. NS-2
 #pragma unroll
@@ -498,10 +513,10 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
         if (s + NS - 1 < S) issue(bufs[(j + NS - 1) % NS]);
         compute(bufs[j]);
         if (kt == KT - 1) {
-            const int u = u0 + s / KT;
-            epilogue(u);
+            const int i = s / KT;
+            epilogue(i);
             last_epi = s;
-            last_full = (LN ? u * BM : (u / nbn) * BM) + BM <= M;
+            last_full = unit_m0(i) + BM <= M;
         }
     };
     for (int s = 0; s < S; s += NS) {
@@ -529,9 +544,12 @@ int launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc, c
     const int nbm = (M + P::BM - 1) / P::BM;
     const int units = EPI == EPI_LN ? nbm : nbm * (N / P::BN);
     const int slots = num_cus * P::blocks_per_cu(EPI == EPI_LN);
-    const int grid = units < slots ? units : slots;
+    // persistent blocks; a multiple of the XCD count when there are enough
+    // units (blocks without a unit return at once)
+    const int rounded = (units + kXcds - 1) / kXcds * kXcds;
+    const int grid = rounded < slots ? rounded : slots;
     hipLaunchKernelGGL((linear_pipe_kernel<EPI, TC, P>), dim3(grid), dim3(P::THREADS), 0, st, x, wc, scale, bias, c,
-                       M, K, N, units, res, gamma, beta, eps);
+                       M, K, N, res, gamma, beta, eps);
     TZH_LAUNCHED("linear_pipe_kernel");
     return TZH_OK;
 }

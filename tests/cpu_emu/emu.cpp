@@ -221,7 +221,8 @@ hipError_t hipSetDevice(int) { return hipSuccess; }
 hipError_t hipGetDeviceProperties(hipDeviceProp_t *p, int) {
     std::memset(p, 0, sizeof *p);
     std::strcpy(p->gcnArchName, "gfx950:sramecc+:xnack-");
-    p->multiProcessorCount = 4;
+    const char *cus = getenv("TZH_EMU_CUS");
+    p->multiProcessorCount = cus ? atoi(cus) : 16;
     return hipSuccess;
 }
 hipError_t hipMalloc(void **p, size_t n) {

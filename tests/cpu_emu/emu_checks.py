@@ -199,7 +199,7 @@ def group_gemm():
         ref = oracle.layernorm(res.astype(np.float32) + oracle.matmul_w8a32(a, q, s, bias), g, b, 1e-12)
         assert np.abs(c - ref).max() < 2e-2, float(np.abs(c - ref).max())
     # f16 activations: the pipelined direct-to-LDS kernel (several units per
-    # persistent block: the emulated device has 4 CUs)
+    # persistent block: the emulated device has 16 CUs, two per XCD)
     for m, k, n, epi, odt in [(1, 64, 128, _abi.EPI_BIAS, np.float16), (333, 384, 1152, _abi.EPI_BIAS, np.float16),
                               (200, 384, 1536, _abi.EPI_BIAS_GELU, np.float16), (129, 64, 256, _abi.EPI_BIAS, np.float32),
                               (130, 1536, 384, _abi.EPI_BIAS_RES_LN, np.float16),
