@@ -30,6 +30,7 @@ constexpr int K_LD = kHeadDim + 8;     // halves per K row in LDS (80 B: conflic
 constexpr int V_LD = kMaxKeys + 8;     // halves per V^T row in LDS (1040 B: likewise)
 constexpr int kWaves = 8;              // waves per workgroup (2 workgroups per CU by LDS)
 constexpr int kQueryTiles = 2;         // 16-query tiles a wave carries at once
+constexpr float kLazyLog2 = 8.0f;      // softmax reference-point slack (exp2 units)
 
 // V^T row layout: within each 32-key group, the keys the PV operand of lane
 // row g takes ({4g..4g+3} and {16+4g..16+4g+3}, the order the S^T
@@ -40,13 +41,27 @@ template <int NW, int QT>
 __global__ void __launch_bounds__(NW * 64) attn_varlen_kernel(const _Float16 *__restrict__ qkv, int ld,
                                                           _Float16 *__restrict__ out, int ld_out,
                                                           const int *__restrict__ cu_seqlens,
-                                                          const int *__restrict__ order, int n_heads,
+                                                          const int *__restrict__ order, int batch, int n_heads,
                                                           int hidden, float scale_log2) {
     __shared__ __attribute__((aligned(16))) _Float16 Ks[kMaxKeys * K_LD];
     __shared__ __attribute__((aligned(16))) _Float16 Vt[kHeadDim * V_LD];
 
-    const int item = blockIdx.x / n_heads;
-    const int h = blockIdx.x % n_heads;
+    // Workgroups go to the XCDs round-robin (block b on XCD b % 8), each XCD
+    // with its own L2.  Heads 2k and 2k+1 of a sequence share every 128-byte
+    // line of its Q/K/V rows (64 bytes each), so they get blocks b and b + 8:
+    // same XCD, dispatched together, each line read from HBM once.  With an
+    // odd head count blocks map to (sequence, head) in order.
+    int item, h;
+    if (n_heads % 2 == 0) {
+        const int pairs = n_heads / 2;
+        const int hp = (int)(blockIdx.x / 16) * 8 + (int)(blockIdx.x % 8);  // (sequence, head pair)
+        item = hp / pairs;
+        h = 2 * (hp % pairs) + (int)(blockIdx.x / 8) % 2;
+    } else {
+        item = blockIdx.x / n_heads;
+        h = blockIdx.x % n_heads;
+    }
+    if (item >= batch) return;  // padding blocks of the pair layout (whole workgroup)
     const int b = order ? order[item] : item;
     const int start = cu_seqlens[b];
     // the host validates lengths; the clamp keeps every LDS index in bounds regardless
@@ -136,18 +151,27 @@ __global__ void __launch_bounds__(NW * 64) attn_varlen_kernel(const _Float16 *__
 #pragma unroll
                     for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[j][t][i]);
                 // finite: every 64-key block below Lp holds a key < L
-                const float m_new = fmaxf(m[j], max_over_rows(mx));
-                const float mc = m_new * scale_log2;
-                const float alpha = __builtin_amdgcn_exp2f((m[j] - m_new) * scale_log2);  // 0 on the first block
+                mx = max_over_rows(mx);
+                // Lazy rescaling: the reference point m only moves (and the
+                // accumulators are rescaled) when some lane's block max
+                // exceeds it by more than kLazyLog2 in the exp2 domain, so the
+                // probabilities stay <= 2^kLazyLog2 (f16 and f32 hold them
+                // exactly as well as values <= 1) and most blocks skip the
+                // rescale.  The first block always moves m off -inf.
+                if (wave_any((mx - m[j]) * scale_log2 > kLazyLog2)) {
+                    const float m_new = fmaxf(m[j], mx);
+                    const float alpha = __builtin_amdgcn_exp2f((m[j] - m_new) * scale_log2);  // 0 on the first block
+                    o0[j] *= alpha;
+                    o1[j] *= alpha;
+                    lsum[j] *= alpha;
+                    m[j] = m_new;
+                }
+                const float mc = m[j] * scale_log2;
 #pragma unroll
                 for (int t = 0; t < 4; t++)
 #pragma unroll
                     for (int i = 0; i < 4; i++)
                         s[j][t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][t][i], scale_log2, -mc));
-                o0[j] *= alpha;
-                o1[j] *= alpha;
-                lsum[j] *= alpha;
-                m[j] = m_new;
             }
 #pragma unroll
             for (int st = 0; st < 2; st++) {
@@ -199,8 +223,10 @@ int tzh_attention_launch(hipStream_t st, const _Float16 *qkv, _Float16 *out, con
     if (batch <= 0) return TZH_OK;
     const float scale = 1.0f / sqrtf((float)kHeadDim);  // arctic.zig:649
     const float scale_log2 = scale * 1.4426950408889634f;
-    hipLaunchKernelGGL((attn_varlen_kernel<kWaves, kQueryTiles>), dim3(batch * n_heads), dim3(kWaves * 64), 0, st, qkv,
-                       3 * hidden, out, hidden, cu_seqlens, order, n_heads, hidden, scale_log2);
+    // head-pair layout: 16 blocks per 8 (sequence, head pair)s
+    const int64_t blocks = n_heads % 2 == 0 ? ((int64_t)batch * (n_heads / 2) + 7) / 8 * 16 : (int64_t)batch * n_heads;
+    hipLaunchKernelGGL((attn_varlen_kernel<kWaves, kQueryTiles>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, st,
+                       qkv, 3 * hidden, out, hidden, cu_seqlens, order, batch, n_heads, hidden, scale_log2);
     TZH_LAUNCHED("attn_varlen_kernel");
     return TZH_OK;
 }

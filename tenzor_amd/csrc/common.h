@@ -105,6 +105,9 @@ __device__ __forceinline__ void lane_swap32(uint32_t &lo, uint32_t &hi) {
     hi = r[1];
 }
 
+// True when `p` holds in any active lane of the wave.
+__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
 // v_permlane16_swap_b32: lanes 16..31 and 48..63 of `a` trade values with
 // lanes 0..15 and 32..47 of `b` (lane i of one 16-lane row with lane i of
 // the row below it).

@@ -238,10 +238,17 @@ def group_gemm():
 
 def group_attention():
     H, D = 384, 32
-    for lengths in ([1], [2, 3], [15, 16, 17], [63, 64, 65], [100, 1, 130], [512]):
+    for lengths in ([1], [2, 3], [15, 16, 17], [63, 64, 65], [100, 1, 130], [512], [300, 0]):
+        # [300, 0]: key norms growing along the sequence (the row max moves
+        # up block after block: lazy rescaling both skipped and taken)
+        grow = lengths[-1] == 0
+        lengths = [x for x in lengths if x]
         rng = np.random.default_rng(sum(lengths))
         Tn = sum(lengths)
-        qkv = (rng.standard_normal((Tn, 3 * H)) * 1.5).astype(np.float16)
+        qkv = (rng.standard_normal((Tn, 3 * H)) * 1.5).astype(np.float32)
+        if grow:
+            qkv[:, H:2 * H] *= (0.2 + np.arange(Tn) / 30.0)[:, None]
+        qkv = qkv.astype(np.float16)
         cu = np.zeros(len(lengths) + 1, np.int32)
         cu[1:] = np.cumsum(lengths)
         out = np.zeros((Tn, H), np.float16)

@@ -92,6 +92,15 @@ inline void lane_swap16(uint32_t &a, uint32_t &b) {
         b = other[0];  // the odd-row partner's a
 }
 inline void wave_lds_order() { emu::wave_barrier(); }
+inline bool wave_any(bool p) {  // every lane of the emulated wave is active
+    const int lane = emu::lane_id();
+    *(unsigned char *)emu::wave_slot(lane) = p ? 1 : 0;
+    emu::wave_barrier();
+    bool any = false;
+    for (int l = 0; l < 64; l++) any = any || *(unsigned char *)emu::wave_slot(l);
+    emu::wave_barrier();
+    return any;
+}
 #define __builtin_amdgcn_s_waitcnt(imm) emu::waitcnt_vm(((imm)&15) | ((((imm) >> 14) & 3) << 4))
 #define __builtin_amdgcn_readfirstlane(x) (x)
 

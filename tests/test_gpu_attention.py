@@ -64,6 +64,25 @@ def test_attention_sharp_softmax(ctx):
         assert (np.abs(out[:, h * D:(h + 1) * D] - ref) <= tol).all()
 
 
+def test_attention_growing_scores(ctx):
+    """Key norms that grow along the sequence push the row max up block after
+    block, by less than and by more than the softmax's lazy-rescale slack."""
+    rng = np.random.default_rng(9)
+    L = 512
+    qkv = rng.standard_normal((L, 3 * H)).astype(np.float32)
+    qkv[:, H:2 * H] *= (0.2 + np.arange(L) / 48.0)[:, None]
+    qkv = qkv.astype(np.float16)
+    out, _ = run(ctx, qkv, [L])
+    q32 = qkv.astype(np.float32)
+    for h in (0, 6, 11):
+        q = q32[:, h * D:(h + 1) * D]
+        k = q32[:, H + h * D:H + (h + 1) * D]
+        v = q32[:, 2 * H + h * D:2 * H + (h + 1) * D]
+        ref = oracle.attention_head(q, k, v)
+        tol = 2.0 ** -9 * np.abs(v).max() + 2.0 ** -10 * np.abs(ref) + 1e-3
+        assert (np.abs(out[:, h * D:(h + 1) * D] - ref) <= tol).all()
+
+
 def test_sequences_are_independent(ctx):
     """Packing order must not change any sequence's result (bit-exact)."""
     rng = np.random.default_rng(6)
