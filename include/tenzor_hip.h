@@ -258,10 +258,14 @@ typedef struct {
 
 typedef struct tzh_model tzh_model;
 
-/* Upload host weights to HBM.  The encoder linears must be I8 + F16 scale
- * (an F32 linear is rejected with TZH_ERR_UNSUPPORTED_DTYPE); their codes
- * are kept on the device widened to f16 (exact).  Embedding tables may be
- * F32 or I8.  The model is bound to ctx's device and stream. */
+/* Upload host weights to HBM (MatWeight, arctic.zig:55-58; ModelWeights,
+ * arctic.zig:100).  Encoder linears are I8 + F16 scale (MatWeight.q8) or
+ * F32 (MatWeight.f32); other
+ * dtypes give TZH_ERR_UNSUPPORTED_DTYPE.  On the device both become f16
+ * codes with an f16 row scale: int8 codes widened exactly, f32 rows as
+ * W * 2^k with scale 2^-k (only the f16 rounding of W * 2^k is inexact).
+ * Embedding tables may be F32 or I8.  The model is bound to ctx's device
+ * and stream. */
 int tzh_arctic_upload(tzh_ctx *ctx, const tzh_arctic_weights *weights, tzh_model **out);
 
 /* ModelWeights.fromSafeTensors (arctic.zig:113-166): "bert." prefix

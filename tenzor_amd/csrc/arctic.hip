@@ -15,6 +15,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <new>
 #include <numeric>
@@ -182,8 +183,11 @@ struct DevTable {
     TableRef ref() const { return TableRef{f32, q8, scale}; }
 };
 
-// int8 codes are kept widened to f16 (exact) on the device: the MFMA consumes
-// f16 and the weights are a tiny share of the traffic.
+// Weight codes in f16 with a per-row f16 scale: C = (X . codes) * scale + b.
+// int8 codes are widened exactly (|q| <= 127).  f32 weights (the reference's
+// f32 model, MatWeight.f32) become codes W * 2^k with a power-of-two scale
+// 2^-k per row, so the scaling itself is exact and only the f16 rounding of
+// W * 2^k remains.
 struct DevLinear {
     _Float16 *w = nullptr;
     uint16_t *s = nullptr;
@@ -259,8 +263,25 @@ int upload_table(tzh_model *m, const tzh_mat_view &v, int64_t rows, DevTable &t,
     return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "Weight %s has unsupported dtype %d", what, v.dtype);
 }
 
+// f32 row -> f16 codes W * 2^k and the f16 bits of the scale 2^-k.  k puts
+// the row's largest magnitude in [2^13, 2^14), clamped to [-15, 24] so that
+// 2^-k is an exact f16 (normal or subnormal); an all-zero row gets k = 0.
+uint16_t f32_row_codes(const float *w, int cols, uint16_t *codes) {
+    float mx = 0.0f;
+    for (int i = 0; i < cols; i++) mx = std::max(mx, std::fabs(w[i]));
+    int k = 0;
+    if (mx > 0.0f && std::isfinite(mx)) {
+        int e;
+        std::frexp(mx, &e);  // mx in [2^(e-1), 2^e)
+        k = std::min(24, std::max(-15, 14 - e));
+    }
+    for (int i = 0; i < cols; i++) codes[i] = tzh_host_f32_to_f16(std::ldexp(w[i], k));
+    return tzh_host_f32_to_f16(std::ldexp(1.0f, -k));
+}
+
 // Concatenate the row blocks of several [rows_i, cols] linears into one
-// int8 matrix (QKV fusion) with its scales and biases.
+// code matrix (QKV fusion) with its scales and biases.  Each block is int8
+// (I8 + F16 scale, the quantized model) or F32 (the f32 model).
 int upload_linear(tzh_model *m, std::initializer_list<std::pair<const tzh_mat_view *, const float *>> parts,
                   int cols, DevLinear &out, const char *what) {
     int64_t rows = 0;
@@ -268,15 +289,13 @@ int upload_linear(tzh_model *m, std::initializer_list<std::pair<const tzh_mat_vi
         const tzh_mat_view *v = pb.first;
         if (!v->data) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s", what);
         if (!pb.second) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s bias", what);
-        if (v->dtype == TZH_F32)
-            return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE,
-                            "%s is F32: this backend runs int8-weight (I8 + F16 scale) linears only", what);
-        if (v->dtype != TZH_I8) return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "Weight %s has unsupported dtype %d", what, v->dtype);
-        if (!v->scale) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s.scale", what);
+        if (v->dtype != TZH_I8 && v->dtype != TZH_F32)
+            return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "Weight %s has unsupported dtype %d", what, v->dtype);
+        if (v->dtype == TZH_I8 && !v->scale) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s.scale", what);
         if (v->cols != cols) return tzh_fail(TZH_ERR_INVALID_ARGS, "%s has %d columns, expected %d", what, v->cols, cols);
         rows += v->rows;
     }
-    std::vector<uint16_t> w((size_t)(rows * cols));  // f16 bits of the int8 codes
+    std::vector<uint16_t> w((size_t)(rows * cols));  // f16 bits of the codes
     std::vector<uint16_t> s((size_t)rows);
     std::vector<float> b((size_t)rows);
     uint16_t code16[256];
@@ -284,9 +303,15 @@ int upload_linear(tzh_model *m, std::initializer_list<std::pair<const tzh_mat_vi
     int64_t r0 = 0;
     for (auto &pb : parts) {
         const tzh_mat_view *v = pb.first;
-        const int8_t *q = (const int8_t *)v->data;
-        for (size_t i = 0; i < (size_t)v->rows * cols; i++) w[(size_t)r0 * cols + i] = code16[(uint8_t)q[i]];
-        std::memcpy(s.data() + r0, v->scale, (size_t)v->rows * 2);
+        if (v->dtype == TZH_I8) {
+            const int8_t *q = (const int8_t *)v->data;
+            for (size_t i = 0; i < (size_t)v->rows * cols; i++) w[(size_t)r0 * cols + i] = code16[(uint8_t)q[i]];
+            std::memcpy(s.data() + r0, v->scale, (size_t)v->rows * 2);
+        } else {
+            const float *f = (const float *)v->data;
+            for (int r = 0; r < v->rows; r++)
+                s[(size_t)(r0 + r)] = f32_row_codes(f + (size_t)r * cols, cols, &w[(size_t)(r0 + r) * cols]);
+        }
         std::memcpy(b.data() + r0, pb.second, (size_t)v->rows * 4);
         r0 += v->rows;
     }

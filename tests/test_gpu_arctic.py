@@ -232,8 +232,22 @@ def test_safetensors_loader_variants(ctx, weights, tmp_path):
     assert ei.value.code == _abi.ERR_UNSUPPORTED_DTYPE
 
 
-def test_f32_linears_are_rejected_loudly(ctx):
-    w = synth.make_arctic_f32(3, CFG)
-    with pytest.raises(TzhError) as ei:
-        ModelWeights.fromHost(ctx, w, CFG)
-    assert ei.value.code == _abi.ERR_UNSUPPORTED_DTYPE
+def test_f32_model_config1(ctx):
+    """Config 1: the f32 model (MatWeight.f32 linears and tables), batch 1 x
+    seq 128, and a ragged batch, against the oracle's f32 forward.  The
+    linears run as f16 codes W * 2^k with an exact power-of-two row scale."""
+    w = synth.make_arctic_f32(3, CFG, ln_random=True)
+    m = ModelWeights.fromHost(ctx, w, CFG)
+    try:
+        hw = synth.HostWeights(w, CFG)
+        ids, lengths = synth.make_batch(31, 1, seq_len=128, fixed=True)
+        got = gpu_embed(m, ids, lengths)
+        assert_embedding_parity(got, oracle.arctic_forward(hw, ids[0, :128])[None])
+        ids, lengths = synth.make_batch(32, 6, seq_len=300)
+        got = gpu_embed(m, ids, lengths)
+        ref = np.stack([oracle.arctic_forward(hw, ids[b, :lengths[b]]) for b in range(6)])
+        assert_embedding_parity(got, ref)
+    finally:
+        m.deinit()
+
+
