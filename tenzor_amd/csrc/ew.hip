@@ -569,9 +569,13 @@ struct Planner {
         return rc;
     }
 
+    // One work item per thread: measured on MI355X (config 2, 2^26 vectors)
+    // a grid that covers every item once streams at 6.1 TB/s, while
+    // grid-stride loops over 16 to 512 blocks per CU reached 4.5 to 5.4.
+    // The cap only keeps the block count bounded for very large tensors.
     int grid_for(int64_t work_items) const {
         int64_t g = (work_items + 255) / 256;
-        const int64_t cap = (int64_t)ctx->num_cus * 16;
+        const int64_t cap = (int64_t)ctx->num_cus * 4096;
         if (g > cap) g = cap;
         if (g < 1) g = 1;
         return (int)g;

@@ -92,46 +92,54 @@ std::string offset_fn(const EwProgram &p, int j) {
     return b;
 }
 
-// Body computing r[0..W) for outputs flat .. flat+W-1.
-std::string body(const EwProgram &p, const char *T, int W, bool vec16) {
+// Leaf loads for outputs flat .. flat+W-1 into L<j><sfx>[W].  `flat` is the
+// name of the index expression in the generated code.
+std::string loads(const EwProgram &p, const char *T, int W, bool vec16, const std::string &sfx,
+                  const std::string &flat) {
     std::string b;
     const std::string WS = std::to_string(W);
     for (int j = 0; j < p.n_leaves; j++) {
-        const std::string J = std::to_string(j);
+        const std::string J = std::to_string(j), LJ = "L" + J + sfx;
         const std::string ptr = "((const " + std::string(T) + " *)p.leaves[" + J + "].ptr)";
-        b += "        " + std::string(T) + " L" + J + "[" + WS + "];\n";
+        b += "        " + std::string(T) + " " + LJ + "[" + WS + "];\n";
         const int mode = W == 1 ? VEC_PER_ELEM : p.leaves[j].vec;
         if (mode == VEC_CONTIG && vec16) {
             const std::string VT = std::string(T) == "float" ? "tzh_f32x4" : "tzh_f64x2";
-            b += "        { const " + VT + " raw = *(const " + VT + " *)(" + ptr + " + off" + J + "(p, flat));\n";
-            for (int e = 0; e < W; e++) b += "          L" + J + "[" + std::to_string(e) + "] = raw[" + std::to_string(e) + "];\n";
+            b += "        { const " + VT + " raw = *(const " + VT + " *)(" + ptr + " + off" + J + "(p, " + flat + "));\n";
+            for (int e = 0; e < W; e++) b += "          " + LJ + "[" + std::to_string(e) + "] = raw[" + std::to_string(e) + "];\n";
             b += "        }\n";
         } else if (mode == VEC_CONTIG) {
-            b += "        { const long long o = off" + J + "(p, flat);\n";
+            b += "        { const long long o = off" + J + "(p, " + flat + ");\n";
             for (int e = 0; e < W; e++)
-                b += "          L" + J + "[" + std::to_string(e) + "] = " + ptr + "[o + " + std::to_string(e) + "];\n";
+                b += "          " + LJ + "[" + std::to_string(e) + "] = " + ptr + "[o + " + std::to_string(e) + "];\n";
             b += "        }\n";
         } else if (mode == VEC_SPLAT) {
-            b += "        { const " + std::string(T) + " x = " + ptr + "[off" + J + "(p, flat)];\n";
-            for (int e = 0; e < W; e++) b += "          L" + J + "[" + std::to_string(e) + "] = x;\n";
+            b += "        { const " + std::string(T) + " x = " + ptr + "[off" + J + "(p, " + flat + ")];\n";
+            for (int e = 0; e < W; e++) b += "          " + LJ + "[" + std::to_string(e) + "] = x;\n";
             b += "        }\n";
         } else {
             for (int e = 0; e < W; e++)
-                b += "        L" + J + "[" + std::to_string(e) + "] = " + ptr + "[off" + J + "(p, flat + " +
+                b += "        " + LJ + "[" + std::to_string(e) + "] = " + ptr + "[off" + J + "(p, " + flat + " + " +
                      std::to_string(e) + ")];\n";
         }
     }
-    // the stack program run symbolically: slot -> expression name
+    return b;
+}
+
+// The stack program run symbolically (slot -> expression name) on the
+// loaded leaves: r<sfx>[0..W).
+std::string compute(const EwProgram &p, const char *T, int W, const std::string &sfx) {
+    std::string b;
     for (int e = 0; e < W; e++) {
         const std::string E = std::to_string(e);
         std::string slot[kMaxDepth + 1];
         for (int i = 0; i < p.n_nodes; i++) {
             const EwNode &nd = p.nodes[i];
-            const std::string v = "v" + std::to_string(i) + "_" + E;
+            const std::string v = "v" + std::to_string(i) + "_" + E + sfx;
             const std::string I = std::to_string(i);
             switch (nd.kind) {
             case EK_LEAF:
-                slot[nd.slot] = "L" + std::to_string(nd.arg) + "[" + E + "]";
+                slot[nd.slot] = "L" + std::to_string(nd.arg) + sfx + "[" + E + "]";
                 break;
             case EK_CONST:
                 b += "        const " + std::string(T) + " " + v + " = (" + T + ")p.nodes[" + I + "].cval;\n";
@@ -149,10 +157,32 @@ std::string body(const EwProgram &p, const char *T, int W, bool vec16) {
                 break;
             }
         }
-        b += "        r[" + E + "] = " + slot[0] + ";\n";
+        b += "        r" + sfx + "[" + E + "] = " + slot[0] + ";\n";
     }
     return b;
 }
+
+// Store of r<sfx>[0..W) at out + flat (16-byte nontemporal when whole).
+std::string store(const char *T, int W, bool vec16, bool f64, const std::string &sfx, const std::string &flat) {
+    std::string b;
+    if (vec16) {
+        const std::string VT = f64 ? "tzh_f64x2" : "tzh_f32x4";
+        b += "        { " + VT + " o;\n";
+        for (int e = 0; e < W; e++) b += "          o[" + std::to_string(e) + "] = r" + sfx + "[" + std::to_string(e) + "];\n";
+        b += "          __builtin_nontemporal_store(o, (" + VT + " *)(out + " + flat + ")); }\n";
+    } else {
+        for (int e = 0; e < W; e++)
+            b += "        out[" + flat + " + " + std::to_string(e) + "] = r" + sfx + "[" + std::to_string(e) + "];\n";
+    }
+    return b;
+}
+
+// Grid-stride kernel over numel / V vectors of V outputs.  Each thread
+// takes kUnroll vectors (one grid stride apart) per trip: all their leaf
+// loads are issued before any arithmetic, which doubles the bytes in flight
+// per thread.  Leftover vectors run one per trip; the numel % V tail
+// elements run one per thread of block 0.
+constexpr int kUnroll = 2;
 
 std::string chain_source(const EwProgram &p, bool f64, int V) {
     const char *T = f64 ? "double" : "float";
@@ -164,25 +194,35 @@ std::string chain_source(const EwProgram &p, bool f64, int V) {
          " *__restrict__ out) {\n";
     s += "    const long long nvec = p.numel / " + VS + ";\n";
     s += "    const long long stride = (long long)gridDim.x * blockDim.x;\n";
-    s += "    for (long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x; v < nvec; v += stride) {\n";
-    s += "        const long long flat = v * " + VS + ";\n";
-    s += "        " + std::string(T) + " r[" + VS + "];\n";
-    s += body(p, T, V, vec16);
-    if (vec16) {
-        const std::string VT = f64 ? "tzh_f64x2" : "tzh_f32x4";
-        s += "        " + VT + " o;\n";
-        for (int e = 0; e < V; e++) s += "        o[" + std::to_string(e) + "] = r[" + std::to_string(e) + "];\n";
-        s += "        __builtin_nontemporal_store(o, (" + VT + " *)(out + flat));\n";
-    } else {
-        for (int e = 0; e < V; e++) s += "        out[flat + " + std::to_string(e) + "] = r[" + std::to_string(e) + "];\n";
+    s += "    long long v = (long long)blockIdx.x * blockDim.x + threadIdx.x;\n";
+    s += "    for (; v + " + std::to_string(kUnroll - 1) + " * stride < nvec; v += " + std::to_string(kUnroll) +
+         " * stride) {\n";
+    for (int u = 0; u < kUnroll; u++) {
+        const std::string U = "_" + std::to_string(u);
+        s += "        const long long flat" + U + " = (v + " + std::to_string(u) + " * stride) * " + VS + ";\n";
+        s += loads(p, T, V, vec16, U, "flat" + U);
     }
+    for (int u = 0; u < kUnroll; u++) {
+        const std::string U = "_" + std::to_string(u);
+        s += "        " + std::string(T) + " r" + U + "[" + VS + "];\n";
+        s += compute(p, T, V, U);
+        s += store(T, V, vec16, f64, U, "flat" + U);
+    }
+    s += "    }\n";
+    s += "    for (; v < nvec; v += stride) {\n";
+    s += "        const long long flat = v * " + VS + ";\n";
+    s += loads(p, T, V, vec16, "", "flat");
+    s += "        " + std::string(T) + " r[" + VS + "];\n";
+    s += compute(p, T, V, "");
+    s += store(T, V, vec16, f64, "", "flat");
     s += "    }\n";
     // tail (numel % V elements): one element per thread of block 0
     s += "    if (blockIdx.x == 0) {\n";
     s += "        const long long flat = nvec * " + VS + " + threadIdx.x;\n";
     s += "        if (flat < p.numel) {\n";
+    s += loads(p, T, 1, false, "", "flat");
     s += "        " + std::string(T) + " r[1];\n";
-    s += body(p, T, 1, false);
+    s += compute(p, T, 1, "");
     s += "        out[flat] = r[0];\n";
     s += "        }\n    }\n}\n";
     return s;
