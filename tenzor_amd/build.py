@@ -41,6 +41,12 @@ HIPFLAGS = [
 ]
 
 
+# Per-source additions.  attention.hip: its scores are finite or -inf by
+# construction, and with NaNs honoured every fmaxf of an MFMA or permlane
+# result gets an extra quieting v_max per operand.
+EXTRA_FLAGS = {"attention.hip": ["-fno-honor-nans"]}
+
+
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(exe):
@@ -65,8 +71,8 @@ def scratch_spills(remarks: str) -> list[tuple[str, int]]:
 
 def _compile(src: str) -> Path:
     obj = BUILD / (Path(src).stem + ".o")
-    cmd = [hipcc(), "-x", "hip", *HIPFLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src), "-o",
-           str(obj)]
+    cmd = [hipcc(), "-x", "hip", *HIPFLAGS, *EXTRA_FLAGS.get(src, []), "-Rpass-analysis=kernel-resource-usage", "-c",
+           str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile of {src} failed:\n{res.stderr}")
