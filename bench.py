@@ -34,9 +34,11 @@ TRAFFIC_PROFILE = "arctic_b256_stage_profile.md"
 KERNELS = {
     "qkv": "linear_pipe_kernel bias, 384 -> 1152",
     "attention": "attn_varlen_kernel",
-    "attn_out_ln": "linear_pipe_kernel bias+residual+LayerNorm, 384 -> 384",
+    "attn_out_ln": "linear_pipe_kernel bias+residual+LayerNorm, 384 -> 384, + split last round "
+                   "(linear_pipe_kernel residual pieces, ln_rows_kernel)",
     "ffn1_gelu": "linear_pipe_kernel bias+GELU, 384 -> 1536",
-    "ffn2_ln": "linear_pipe_kernel bias+residual+LayerNorm, 1536 -> 384",
+    "ffn2_ln": "linear_pipe_kernel bias+residual+LayerNorm, 1536 -> 384, + split last round "
+               "(linear_pipe_kernel residual pieces, ln_rows_kernel)",
     "embed_ln": "embed_ln_kernel", "pack_ids": "pack_ids_kernel", "cls_l2": "cls_l2_kernel",
 }
 

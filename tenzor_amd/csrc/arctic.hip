@@ -27,7 +27,7 @@
 int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc,
                             const uint16_t *scale, const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k,
                             int64_t n, int32_t epilogue, const void *res, const float *gamma, const float *beta,
-                            float eps);
+                            float eps, float *ln_ws, int64_t ln_ws_rows);
 int tzh_attention_launch(hipStream_t st, const _Float16 *qkv, _Float16 *out, const int *cu_seqlens,
                          const int *order, int batch, int n_heads, int hidden);
 
@@ -212,6 +212,8 @@ struct tzh_model {
     int64_t cap_tokens = 0;
     int cap_batch = 0;
     _Float16 *h = nullptr, *h1 = nullptr, *qkv = nullptr, *attn = nullptr, *inter = nullptr;
+    float *ln_ws = nullptr;  // f32 rows of a split LayerNorm GEMM round
+    int64_t ln_ws_rows = 0;
     uint32_t *tok_ids = nullptr;
     int32_t *tok_pos = nullptr;
     int *meta = nullptr;  // device: cu[batch+1] | order[batch]
@@ -333,10 +335,12 @@ int check_config(const tzh_arctic_config &c) {
 }
 
 void free_workspace(tzh_model *m) {
-    void *bufs[] = {m->h, m->h1, m->qkv, m->attn, m->inter, m->tok_ids, m->tok_pos, m->meta};
+    void *bufs[] = {m->h, m->h1, m->qkv, m->attn, m->inter, m->ln_ws, m->tok_ids, m->tok_pos, m->meta};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     m->h = m->h1 = m->qkv = m->attn = m->inter = nullptr;
+    m->ln_ws = nullptr;
+    m->ln_ws_rows = 0;
     m->tok_ids = nullptr;
     m->tok_pos = nullptr;
     m->meta = nullptr;
@@ -364,6 +368,9 @@ int ensure_workspace(tzh_model *m, int64_t tokens, int batch) {
     TZH_TRY(get((void **)&m->qkv, (size_t)T * 3 * H * 2));
     TZH_TRY(get((void **)&m->attn, (size_t)T * H * 2));
     TZH_TRY(get((void **)&m->inter, (size_t)T * 1536 * 2));
+    // a split partial round is at most a third of the CUs' 128-row tiles
+    m->ln_ws_rows = std::min<int64_t>((T + 127) / 128, m->ctx->num_cus / 3 + 1) * 128;
+    TZH_TRY(get((void **)&m->ln_ws, (size_t)m->ln_ws_rows * H * 4));
     TZH_TRY(get((void **)&m->tok_ids, (size_t)T * 4));
     TZH_TRY(get((void **)&m->tok_pos, (size_t)T * 4));
     TZH_TRY(get((void **)&m->meta, (size_t)(2 * B + 1) * 4));
@@ -665,18 +672,18 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
         const DevLayer &d = m->layers[(size_t)li];
         const int cus = m->ctx->num_cus;
         TZH_TRY(tzh_linear_codes_launch(st, cus, m->h, d.qkv.w, d.qkv.s, d.qkv.b, m->qkv, TZH_F16, T, H, 3 * H,
-                                        TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f));
+                                        TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f, nullptr, 0));
         TZH_TRY(mark("qkv"));
         TZH_TRY(tzh_attention_launch(st, m->qkv, m->attn, d_cu, d_order, batch, 12, H));
         TZH_TRY(mark("attention"));
         TZH_TRY(tzh_linear_codes_launch(st, cus, m->attn, d.o.w, d.o.s, d.o.b, m->h1, TZH_F16, T, H, H,
-                                        TZH_EPI_BIAS_RES_LN, m->h, d.ln1_g, d.ln1_b, eps));
+                                        TZH_EPI_BIAS_RES_LN, m->h, d.ln1_g, d.ln1_b, eps, m->ln_ws, m->ln_ws_rows));
         TZH_TRY(mark("attn_out_ln"));
         TZH_TRY(tzh_linear_codes_launch(st, cus, m->h1, d.ffn1.w, d.ffn1.s, d.ffn1.b, m->inter, TZH_F16, T, H, 1536,
-                                        TZH_EPI_BIAS_GELU, nullptr, nullptr, nullptr, 0.0f));
+                                        TZH_EPI_BIAS_GELU, nullptr, nullptr, nullptr, 0.0f, nullptr, 0));
         TZH_TRY(mark("ffn1_gelu"));
         TZH_TRY(tzh_linear_codes_launch(st, cus, m->inter, d.ffn2.w, d.ffn2.s, d.ffn2.b, m->h, TZH_F16, T, 1536, H,
-                                        TZH_EPI_BIAS_RES_LN, m->h1, d.ln2_g, d.ln2_b, eps));
+                                        TZH_EPI_BIAS_RES_LN, m->h1, d.ln2_g, d.ln2_b, eps, m->ln_ws, m->ln_ws_rows));
         TZH_TRY(mark("ffn2_ln"));
     }
     if (outputs) {

@@ -29,7 +29,7 @@ constexpr int kMaxKeys = 512;
 constexpr int K_LD = kHeadDim + 8;     // halves per K row in LDS (80 B: conflict-free 16-byte reads)
 constexpr int V_LD = kMaxKeys + 8;     // halves per V^T row in LDS (1040 B: likewise)
 constexpr int kWaves = 8;              // waves per workgroup (2 workgroups per CU by LDS)
-constexpr int kQueryTiles = 2;         // 16-query tiles a wave carries at once
+constexpr int kQueryTiles = 1;         // 16-query tiles a wave carries at once
 constexpr float kLazyLog2 = 8.0f;      // softmax reference-point slack (exp2 units)
 
 // V^T row layout: within each 32-key group, the keys the PV operand of lane
@@ -108,9 +108,9 @@ __global__ void __launch_bounds__(NW * 64) attn_varlen_kernel(const _Float16 *__
     const int g = lane >> 4;   // lane row: k-slots 8g..8g+7, C rows 4g..4g+3
     const int ql = lane & 15;  // query (C column) owned by this lane in each tile
     const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
-    // Each wave carries QT 16-query tiles at once: they share every K and V
-    // fragment read, and their softmax chains are independent work for the
-    // scheduler to interleave.
+    // A wave can carry QT 16-query tiles at once (they share every K and V
+    // fragment read).  One tile per wave measured fastest on MI355X at the
+    // Arctic lengths: twice the tasks balance the waves of a block better.
     for (int q0 = w * 16 * QT; q0 < L; q0 += NW * 16 * QT) {
         half8_t qf[QT];
         float m[QT];  // running max of the raw scores

@@ -410,7 +410,7 @@ int tzh_widen_codes_launch(hipStream_t st, const int8_t *q, _Float16 *out, int64
 int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc,
                             const uint16_t *scale, const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k,
                             int64_t n, int32_t epilogue, const void *res, const float *gamma, const float *beta,
-                            float eps);
+                            float eps, float *ln_ws, int64_t ln_ws_rows);
 
 extern "C" int tzh_linear_w8(tzh_ctx *ctx, const void *a, int32_t a_dtype, const int8_t *wq, const uint16_t *scale,
                              const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k, int64_t n,
@@ -427,11 +427,18 @@ extern "C" int tzh_linear_w8(tzh_ctx *ctx, const void *a, int32_t a_dtype, const
          (epilogue == TZH_EPI_BIAS_RES_LN && n == 384 && residual && gamma && beta && res_dtype == c_dtype));
     if (a_dtype == TZH_F16 && (c_dtype == TZH_F16 || c_dtype == TZH_F32) && pipe_shape && a && wq && scale && c &&
         al16(a) && al16(c) && (!residual || al16(residual))) {
-        void *codes = nullptr;
-        TZH_TRY(tzh_ctx_scratch(ctx, (size_t)(n * k * 2), &codes));
-        TZH_TRY(tzh_widen_codes_launch(ctx->stream, wq, (_Float16 *)codes, n * k));
-        return tzh_linear_codes_launch(ctx->stream, ctx->num_cus, (const _Float16 *)a, (const _Float16 *)codes, scale,
-                                       bias, c, c_dtype, m, k, n, epilogue, residual, gamma, beta, eps);
+        // scratch: the widened codes, then (LayerNorm epilogue) the f32 rows
+        // of a split partial round of tiles
+        const size_t codes_bytes = ((size_t)(n * k * 2) + 255) / 256 * 256;
+        const int64_t ws_rows = epilogue == TZH_EPI_BIAS_RES_LN
+                                    ? std::min<int64_t>((m + 127) / 128, ctx->num_cus / 3 + 1) * 128
+                                    : 0;
+        void *scratch = nullptr;
+        TZH_TRY(tzh_ctx_scratch(ctx, codes_bytes + (size_t)ws_rows * 384 * 4, &scratch));
+        TZH_TRY(tzh_widen_codes_launch(ctx->stream, wq, (_Float16 *)scratch, n * k));
+        return tzh_linear_codes_launch(ctx->stream, ctx->num_cus, (const _Float16 *)a, (const _Float16 *)scratch,
+                                       scale, bias, c, c_dtype, m, k, n, epilogue, residual, gamma, beta, eps,
+                                       ws_rows ? (float *)((char *)scratch + codes_bytes) : nullptr, ws_rows);
     }
     return tzh_linear_w8_launch(ctx->stream, a, a_dtype, wq, scale, bias, c, c_dtype, m, k, n, epilogue, residual,
                                 res_dtype, gamma, beta, eps);

@@ -112,28 +112,56 @@ __device__ __forceinline__ void store_frag_f16(char *ws, const float (&v)[16], _
     wave_lds_order();
 }
 
-// Tile of rows x BK halves (k contiguous) as laid out in LDS.
-template <int BK>
+// Eight biased int8 weight codes (u = q + 128, little-endian in d0, d1) ->
+// f16 q, exactly: v_perm_b32 makes each code the low mantissa byte of an f16
+// with exponent 10 (bits 0x64uu = 1024 + u), and a packed f16 subtraction of
+// 1152 = 1024 + 128 leaves q; every value is an integer below 2048, so
+// nothing rounds.
+__device__ __forceinline__ half8_t codes_to_f16(uint32_t d0, uint32_t d1) {
+    const half2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    half8_t r;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const uint32_t d = i ? d1 : d0;
+        const half2_t lo = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, d, 0x04010400u)) - off;
+        const half2_t hi = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, d, 0x04030402u)) - off;
+        r[4 * i + 0] = lo[0];
+        r[4 * i + 1] = lo[1];
+        r[4 * i + 2] = hi[0];
+        r[4 * i + 3] = hi[1];
+    }
+    return r;
+}
+
+// Tile of rows x ROW_BYTES (k contiguous) as laid out in LDS.
+template <int ROW_BYTES_>
 struct TileFmt {
-    static constexpr int CPR = BK / 8;            // 16-byte chunks per row
-    static constexpr int ROW_BYTES = BK * 2;
+    static constexpr int ROW_BYTES = ROW_BYTES_;
+    static constexpr int CPR = ROW_BYTES / 16;    // 16-byte chunks per row
     static constexpr int RPI = 64 / CPR;          // rows per DMA instruction (64 lanes x 16 B)
     static constexpr int RPW = 256 / ROW_BYTES;   // rows sharing one 256-byte bank window
     __device__ static __forceinline__ int swz(int r) { return (r / RPW) & (CPR - 1); }
     // the swizzle of a DMA group's rows depends on the group index only
-    // through its parity (BK = 64: 8-row groups, 2 rows per window)
+    // through its parity (128-byte rows: 8-row groups, 2 rows per window)
     static constexpr bool PARITY = (RPI / RPW) % CPR != 0;
 };
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_>
+// W8: the weight codes stay one byte each (biased, u = q + 128) in HBM and
+// in LDS, which halves the weight stream, and are widened to f16 in
+// registers after each fragment read.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_, bool W8_ = false>
 struct PipeCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, NS = NS_;
+    static constexpr bool W8 = W8_;
     static constexpr int NW = WM * WN, THREADS = NW * 64;
     static constexpr int TMF = BM / WM / 32;  // token fragments per wave
     static constexpr int TNF = BN / WN / 32;  // weight fragments per wave
-    using F = TileFmt<BK>;
-    static constexpr int X_BYTES = BM * BK * 2, W_BYTES = BN * BK * 2, STAGE = X_BYTES + W_BYTES;
-    static constexpr int XG = BM / F::RPI, WG = BN / F::RPI;  // DMA instructions per tile
+    static constexpr int WEB = W8 ? 1 : 2;    // bytes per weight code
+    using FX = TileFmt<BK * 2>;
+    using FW = TileFmt<BK * WEB>;
+    static_assert(!W8 || BK % 32 == 0, "int8 weights: whole 16-byte chunks per half-wave");
+    static constexpr int X_BYTES = BM * BK * 2, W_BYTES = BN * BK * WEB, STAGE = X_BYTES + W_BYTES;
+    static constexpr int XG = BM / FX::RPI, WG = BN / FW::RPI;  // DMA instructions per tile
     static constexpr int LX = XG / NW, LW = WG / NW, L = LX + LW;
     static_assert(XG % NW == 0 && WG % NW == 0, "DMA groups must split evenly over the waves");
     static_assert(TMF >= 1 && TNF >= 1, "wave tile too small");
@@ -210,16 +238,20 @@ __device__ __forceinline__ void store4<float>(float *p, float a, float b, float 
     *(f32x4_t *)p = f32x4_t{a, b, c, d};
 }
 
-enum { EPI_BIAS = 0, EPI_GELU = 1, EPI_LN = 2 };
+// EPI_RES: bias + residual without the LayerNorm, stored as f32: the
+// pre-normalisation rows of a split LayerNorm tile (see launch_ln).
+enum { EPI_BIAS = 0, EPI_GELU = 1, EPI_LN = 2, EPI_RES = 3 };
 
-template <int EPI, typename TC, typename P>
+template <int EPI, typename TC, typename P, typename TR = TC>
 __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
-    const _Float16 *__restrict__ X, const _Float16 *__restrict__ Wc, const uint16_t *__restrict__ scale,
-    const float *__restrict__ bias, TC *__restrict__ C, int M, int K, int N, const TC *__restrict__ R,
+    const _Float16 *__restrict__ X, const void *__restrict__ Wc, const uint16_t *__restrict__ scale,
+    const float *__restrict__ bias, TC *__restrict__ C, int M, int K, int N, const TR *__restrict__ R,
     const float *__restrict__ gamma, const float *__restrict__ beta, float eps) {
-    using F = typename P::F;
+    using FX = typename P::FX;
+    using FW = typename P::FW;
     constexpr int BM = P::BM, BN = P::BN, BK = P::BK, NS = P::NS, TMF = P::TMF, TNF = P::TNF;
-    constexpr int ROWB = F::ROW_BYTES;
+    constexpr int XROWB = FX::ROW_BYTES, WROWB = FW::ROW_BYTES, WEB = P::WEB;
+    constexpr bool W8 = P::W8;
     constexpr bool LN = EPI == EPI_LN;
     static_assert(!LN || P::WN * TNF * 32 == BN, "LayerNorm tiles cover whole rows");
     constexpr int NPAR = LN ? 4 : 2;                        // per-column parameters kept in LDS
@@ -270,12 +302,15 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     // Each lane fetches one 16-byte chunk per DMA instruction: source address
     // = wave-uniform row base (scalar) + a small per-lane byte offset.
     const int wu = __builtin_amdgcn_readfirstlane(w);                // wave index, uniform
-    const int r_in = lane / F::CPR;                                  // row inside a DMA group
+    const int r_in = lane / FX::CPR;                                 // row inside an X DMA group
     // logical 16-byte chunk this lane fetches in an even / odd DMA group
-    const int chunk_e = (lane % F::CPR) ^ F::swz(r_in);
-    const int chunk_o = (lane % F::CPR) ^ F::swz(F::RPI + r_in);
-    const uint32_t w_loff_e = (uint32_t)(r_in * K + chunk_e * 8) * 2u;  // bytes, same for every unit
-    const uint32_t w_loff_o = (uint32_t)(r_in * K + chunk_o * 8) * 2u;
+    const int chunk_e = (lane % FX::CPR) ^ FX::swz(r_in);
+    const int chunk_o = (lane % FX::CPR) ^ FX::swz(FX::RPI + r_in);
+    const int rw_in = lane / FW::CPR;                                // row inside a W DMA group
+    const int wchunk_e = (lane % FW::CPR) ^ FW::swz(rw_in);
+    const int wchunk_o = (lane % FW::CPR) ^ FW::swz(FW::RPI + rw_in);
+    const uint32_t w_loff_e = (uint32_t)(rw_in * K * WEB + wchunk_e * 16);  // bytes, same for every unit
+    const uint32_t w_loff_o = (uint32_t)(rw_in * K * WEB + wchunk_o * 16);
     const char *const Xb = (const char *)X;
     const char *const Wb = (const char *)Wc;
     int iu = 0, ikt = 0;                                             // next stage to issue
@@ -286,25 +321,25 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
         const int m0 = unit_m0(i), n0 = unit_n0(i);
 #pragma unroll
         for (int i = 0; i < P::LX; i++) {
-            int r0 = m0 + (wu * P::LX + i) * F::RPI;
+            int r0 = m0 + (wu * P::LX + i) * FX::RPI;
             r0 = r0 < M ? r0 : M - 1;
             const int r = r0 + r_in < M ? r0 + r_in : M - 1;
             x_row0[i] = r0;
-            const int chunk = (F::PARITY && ((wu * P::LX + i) & 1)) ? chunk_o : chunk_e;
+            const int chunk = (FX::PARITY && ((wu * P::LX + i) & 1)) ? chunk_o : chunk_e;
             x_loff[i] = (uint32_t)((r - r0) * K + chunk * 8) * 2u;
         }
-        w_unit = Wb + (size_t)(n0 + wu * P::LW * F::RPI) * K * 2;
+        w_unit = Wb + (size_t)(n0 + wu * P::LW * FW::RPI) * K * WEB;
     };
     auto issue = [&](char *buf) __attribute__((always_inline)) {
         const size_t k0b = (size_t)ikt * BK * 2;
 #pragma unroll
         for (int i = 0; i < P::LX; i++)
-            dma16(Xb + ((size_t)x_row0[i] * K * 2 + k0b), x_loff[i], buf + (wu * P::LX + i) * F::RPI * ROWB);
+            dma16(Xb + ((size_t)x_row0[i] * K * 2 + k0b), x_loff[i], buf + (wu * P::LX + i) * FX::RPI * XROWB);
 #pragma unroll
         for (int i = 0; i < P::LW; i++)
-            dma16(w_unit + ((size_t)i * F::RPI * K * 2 + k0b),
-                  (F::PARITY && ((wu * P::LW + i) & 1)) ? w_loff_o : w_loff_e,
-                  buf + P::X_BYTES + (wu * P::LW + i) * F::RPI * ROWB);
+            dma16(w_unit + ((size_t)i * FW::RPI * K * WEB + (size_t)ikt * BK * WEB),
+                  (FW::PARITY && ((wu * P::LW + i) & 1)) ? w_loff_o : w_loff_e,
+                  buf + P::X_BYTES + (wu * P::LW + i) * FW::RPI * WROWB);
         if (++ikt == KT) {
             ikt = 0;
             if (++iu < count) set_unit(iu);
@@ -313,13 +348,19 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 
     // --- fragment read offsets -------------------------------------------
     const int l31 = lane & 31, half = lane >> 5;
-    const int fx = F::swz(l31);
+    // The MFMA takes 8 k-values per lane (lanes 32..63 the upper 8 of its 16).
+    // f16 weights: MFMA ks of a stage covers k = 16 ks .. 16 ks + 15.  int8
+    // weights: a 16-byte read holds 16 codes, so half-wave h takes k = 32 h +
+    // 8 ks .. 32 h + 8 ks + 7 in MFMA ks (BK = 64; BK = 32: 16 h + 8 ks), the
+    // X operand following the same k.
+    const int fx = FX::swz(l31), fw = FW::swz(l31);
     int xoff[BK / 16], woff[BK / 16];
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ks++) {
-        const int pc = ((2 * ks + half) ^ fx) << 4;
-        xoff[ks] = (wm * TMF * 32 + l31) * ROWB + pc;
-        woff[ks] = P::X_BYTES + (wn * TNF * 32 + l31) * ROWB + pc;
+        const int cx = W8 ? (BK / 16) * half + ks : 2 * ks + half;
+        xoff[ks] = (wm * TMF * 32 + l31) * XROWB + ((cx ^ fx) << 4);
+        const int cw = W8 ? (BK / 32) * half + ks / 2 : 2 * ks + half;  // W8: ks and ks+1 share a read
+        woff[ks] = P::X_BYTES + (wn * TNF * 32 + l31) * WROWB + ((cw ^ fw) << 4);
     }
 
     f32x16_t acc[TNF][TMF];
@@ -329,13 +370,21 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
         for (int b = 0; b < TMF; b++) acc[a][b] = f32x16_t{};
 
     auto compute = [&](const char *buf) __attribute__((always_inline)) {
+        u32x4_t wraw[TNF];
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ks++) {
             half8_t xf[TMF], wf[TNF];
 #pragma unroll
-            for (int b = 0; b < TMF; b++) xf[b] = *(const half8_t *)(buf + xoff[ks] + b * 32 * ROWB);
+            for (int b = 0; b < TMF; b++) xf[b] = *(const half8_t *)(buf + xoff[ks] + b * 32 * XROWB);
 #pragma unroll
-            for (int a = 0; a < TNF; a++) wf[a] = *(const half8_t *)(buf + woff[ks] + a * 32 * ROWB);
+            for (int a = 0; a < TNF; a++) {
+                if constexpr (W8) {
+                    if (ks % 2 == 0) wraw[a] = *(const u32x4_t *)(buf + woff[ks] + a * 32 * WROWB);
+                    wf[a] = codes_to_f16(wraw[a][2 * (ks % 2)], wraw[a][2 * (ks % 2) + 1]);
+                } else {
+                    wf[a] = *(const half8_t *)(buf + woff[ks] + a * 32 * WROWB);
+                }
+            }
 #pragma unroll
             for (int a = 0; a < TNF; a++)
 #pragma unroll
@@ -360,10 +409,15 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                         const f32x4_t s = *(const f32x4_t *)&par[0][n];
                         const f32x4_t bb = *(const f32x4_t *)&par[1][n];
                         float v[4];
+                        using RV4 = std::conditional_t<std::is_same<TR, float>::value, f32x4_t, half4_t>;
+                        RV4 res = {};
+                        if constexpr (EPI == EPI_RES) res = *(const RV4 *)(R + (size_t)(t < M ? t : M - 1) * N + n);
 #pragma unroll
                         for (int q = 0; q < 4; q++) {
                             v[q] = acc[a][b][4 * g + q] * s[q] + bb[q];  // sum * s + bias (matmul_w8a32.zig:55)
                             if (EPI == EPI_GELU) v[q] = gelu_fast(v[q]);
+                            // input + (sum * s + bias), as the LayerNorm epilogue forms it
+                            if (EPI == EPI_RES) v[q] = (float)res[q] + v[q];
                             if constexpr (STAGED) acc[a][b][4 * g + q] = v[q];
                         }
                         if constexpr (!STAGED)
@@ -535,22 +589,145 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 using BiasCfg = PipeCfg<128, 384, 64, 2, 4, 2>;      // n a multiple of 384
 using BiasCfgNarrow = PipeCfg<128, 128, 64, 2, 2, 4>;  // other multiples of 128
 using LnCfg = PipeCfg<128, 384, 64, 2, 4, 2>;
+// Pieces of the partial last round of a LayerNorm GEMM (12, 6 or 3 per
+// 128 x 384 tile; see launch_ln).
+using Piece64 = PipeCfg<64, 64, 64, 2, 2, 4>;
+using Piece128x64 = PipeCfg<128, 64, 64, 2, 2, 4>;
+using Piece128 = BiasCfgNarrow;
 
+template <typename T>
+struct NoDeduce {
+    using type = T;
+};
 
-template <int EPI, typename TC, typename P>
-int launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc, const uint16_t *scale,
-           const float *bias, TC *c, int M, int K, int N, const TC *res, const float *gamma, const float *beta,
-           float eps) {
+template <int EPI, typename TC, typename P, typename TR = TC>
+int launch(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, const uint16_t *scale,
+           const float *bias, TC *c, int M, int K, int N, const typename NoDeduce<TR>::type *res,
+           const float *gamma, const float *beta, float eps) {
     const int nbm = (M + P::BM - 1) / P::BM;
-    const int units = EPI == EPI_LN ? nbm : nbm * (N / P::BN);
+    const int nbn = N / P::BN;
     const int slots = num_cus * P::blocks_per_cu(EPI == EPI_LN);
-    // persistent blocks; a multiple of the XCD count when there are enough
-    // units (blocks without a unit return at once)
-    const int rounded = (units + kXcds - 1) / kXcds * kXcds;
-    const int grid = rounded < slots ? rounded : slots;
-    hipLaunchKernelGGL((linear_pipe_kernel<EPI, TC, P>), dim3(grid), dim3(P::THREADS), 0, st, x, wc, scale, bias, c,
-                       M, K, N, res, gamma, beta, eps);
+    // Persistent blocks.  Panel p goes to XCD p % 8 with its nbn units, so
+    // 8 * ceil(panels / 8) * nbn blocks give every unit a block of its own
+    // (blocks without a unit return at once); beyond that, one per slot.
+    const int64_t spread = (int64_t)kXcds * ((nbm + kXcds - 1) / kXcds) * nbn;
+    const int grid = spread < slots ? (int)spread : slots;
+    hipLaunchKernelGGL((linear_pipe_kernel<EPI, TC, P, TR>), dim3(grid), dim3(P::THREADS), 0, st, x, wc, scale, bias,
+                       c, M, K, N, res, gamma, beta, eps);
     TZH_LAUNCHED("linear_pipe_kernel");
+    return TZH_OK;
+}
+
+// LayerNorm of f32 pre-normalisation rows (residual already added) with the
+// statistics summed in exactly the order of the LayerNorm epilogue of
+// linear_pipe_kernel<EPI_LN, ., LnCfg>: the lane of wave column group wn and
+// half-wave h sums its columns 96 wn + 32 a + 8 g + 4 h + q in (a, g, q)
+// order, half-wave 1's sum is added to half-wave 0's, and the four groups
+// are added in order from 0; the squared deviations likewise.  A row
+// normalised here is therefore bit-identical to the same row normalised
+// inside the GEMM.  One wave per 8 rows, lane = 8 r + 2 wn + h.
+template <typename TO>
+__global__ void __launch_bounds__(256) ln_rows_kernel(const float *__restrict__ V, int rows,
+                                                      const float *__restrict__ gamma,
+                                                      const float *__restrict__ beta, float eps,
+                                                      TO *__restrict__ out) {
+    constexpr int WN = LnCfg::WN, TNF = LnCfg::TNF, BN = LnCfg::BN;
+    static_assert(WN == 4, "eight lanes per row");
+    const int lane = threadIdx.x & 63;
+    const int row = (int)(blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64) * 8 + lane / 8;
+    const int wn = (lane & 7) >> 1, h = lane & 1, base = lane & ~7;
+    const float *src = V + (size_t)(row < rows ? row : rows - 1) * BN;
+    f32x4_t v[TNF][4];
+#pragma unroll
+    for (int a = 0; a < TNF; a++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) v[a][g] = *(const f32x4_t *)(src + wn * TNF * 32 + a * 32 + 8 * g + 4 * h);
+    // sum over this lane's 48 columns, then the row total in the GEMM's order
+    auto row_total = [&](float own) __attribute__((always_inline)) {
+        const float part = own + __shfl_xor(own, 1, 64);  // on h = 0 lanes: half 0 + half 1
+        float tot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < WN; j++) tot += __shfl(part, base + 2 * j, 64);
+        return tot;
+    };
+    float sum = 0.0f;
+#pragma unroll
+    for (int a = 0; a < TNF; a++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) sum += v[a][g][q];
+    const float mean = row_total(sum) / (float)BN;
+    float sq = 0.0f;
+#pragma unroll
+    for (int a = 0; a < TNF; a++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float d = v[a][g][q] - mean;
+                sq += d * d;
+            }
+    const float inv_std = 1.0f / sqrtf(row_total(sq) / (float)BN + eps);
+    if (row >= rows) return;
+#pragma unroll
+    for (int a = 0; a < TNF; a++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int n = wn * TNF * 32 + a * 32 + 8 * g + 4 * h;
+            const f32x4_t gg = *(const f32x4_t *)(gamma + n);
+            const f32x4_t bt = *(const f32x4_t *)(beta + n);
+            float y[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) y[q] = ((v[a][g][q] - mean) * inv_std) * gg[q] + bt[q];
+            store4<TO>(out + (size_t)row * BN + n, y[0], y[1], y[2], y[3]);
+        }
+}
+
+// bias + residual + LayerNorm over 384-wide rows.  The 128-row tiles run in
+// whole rounds of one tile per CU slot; when the rows left over for a
+// partial last round would keep only a few CUs busy (at most slots / 3
+// tiles), those tiles are instead cut into 64 x 64, 128 x 64 or 128 x 128
+// pieces (the finest that fit one round), which store their pre-
+// normalisation rows to ws (f32, ws_rows rows) for ln_rows_kernel.  Every
+// output value comes out the same as it would from the whole-tile kernel:
+// the pieces run the same MFMA sequence per element, and ln_rows_kernel
+// sums the statistics in the tile epilogue's order.
+template <typename TC>
+int launch_ln(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, const uint16_t *scale,
+              const float *bias, TC *c, int M, int K, const TC *res, const float *gamma, const float *beta, float eps,
+              float *ws, int64_t ws_rows) {
+    constexpr int N = LnCfg::BN, BM = LnCfg::BM;
+    const int slots = num_cus * LnCfg::blocks_per_cu(true);
+    const int panels = (M + BM - 1) / BM;
+    const int full = panels / slots * slots;
+    const int rem = panels - full;
+    const int tail_rows = M - full * BM;
+    int per = 0;  // pieces per tile
+    if (rem > 0 && ws && tail_rows <= ws_rows)
+        for (int p : {12, 6, 3})
+            if ((int64_t)rem * p <= slots) {
+                per = p;
+                break;
+            }
+    const int m_main = per ? full * BM : M;
+    if (m_main > 0)
+        TZH_TRY((launch<EPI_LN, TC, LnCfg>(st, num_cus, x, wc, scale, bias, c, m_main, K, N, res, gamma, beta, eps)));
+    if (!per) return TZH_OK;
+    const _Float16 *xt = x + (size_t)m_main * K;
+    const TC *rt = res + (size_t)m_main * N;
+    if (per == 12)
+        TZH_TRY((launch<EPI_RES, float, Piece64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N, rt,
+                                                      nullptr, nullptr, 0.f)));
+    else if (per == 6)
+        TZH_TRY((launch<EPI_RES, float, Piece128x64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N, rt,
+                                                          nullptr, nullptr, 0.f)));
+    else
+        TZH_TRY((launch<EPI_RES, float, Piece128, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N, rt,
+                                                       nullptr, nullptr, 0.f)));
+    hipLaunchKernelGGL(ln_rows_kernel<TC>, dim3((unsigned)((tail_rows + 31) / 32)), dim3(256), 0, st, ws, tail_rows,
+                       gamma, beta, eps, c + (size_t)m_main * N);
+    TZH_LAUNCHED("ln_rows_kernel");
     return TZH_OK;
 }
 
@@ -593,10 +770,12 @@ int tzh_widen_codes_launch(hipStream_t st, const int8_t *q, _Float16 *out, int64
 }
 
 // f16 activations x f16 weight codes; output and residual both F16 or both F32.
+// ln_ws (f32, ln_ws_rows rows of 384; may be null) lets the LayerNorm
+// epilogue split a partial last round of tiles (see launch_ln).
 int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc,
                             const uint16_t *scale, const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k,
                             int64_t n, int32_t epilogue, const void *res, const float *gamma, const float *beta,
-                            float eps) {
+                            float eps, float *ln_ws, int64_t ln_ws_rows) {
     if (m < 0 || k <= 0 || n <= 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad GEMM shape");
     if (m == 0) return TZH_OK;  // matmul_w8a32.zig:24
     if (m > (int64_t)1 << 30 || k > 65536) return tzh_fail(TZH_ERR_TOO_LARGE, "GEMM shape too large");
@@ -620,10 +799,11 @@ int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, cons
     if (epilogue == TZH_EPI_BIAS_RES_LN) {
         if (N != LnCfg::BN) return tzh_fail(TZH_ERR_INVALID_ARGS, "LayerNorm epilogue needs n == 384 (got %d)", N);
         if (!res || !gamma || !beta) return tzh_fail(TZH_ERR_INVALID_ARGS, "null residual/gamma/beta");
-        return c16 ? launch<EPI_LN, _Float16, LnCfg>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K, N,
-                                                     (const _Float16 *)res, gamma, beta, eps)
-                   : launch<EPI_LN, float, LnCfg>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, N,
-                                                  (const float *)res, gamma, beta, eps);
+        if (ln_ws && !aligned16(ln_ws)) return tzh_fail(TZH_ERR_INVALID_ARGS, "LayerNorm workspace must be 16-byte aligned");
+        return c16 ? launch_ln<_Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K, (const _Float16 *)res,
+                                         gamma, beta, eps, ln_ws, ln_ws_rows)
+                   : launch_ln<float>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, (const float *)res, gamma,
+                                      beta, eps, ln_ws, ln_ws_rows);
     }
     return tzh_fail(TZH_ERR_INVALID_ARGS, "unknown epilogue %d", epilogue);
 }

@@ -15,7 +15,9 @@ Two subcommands:
 
 Dispatches are mapped to forward stages by kernel and launch order: both
 LayerNorm GEMMs are one kernel instantiation; the one launched after
-attention is attn_out_ln and the one after ffn1_gelu is ffn2_ln.
+attention is attn_out_ln and the one after ffn1_gelu is ffn2_ln.  The
+pieces of a split partial round (the residual-only GEMM) and their row
+LayerNorm belong to the LayerNorm GEMM launched just before them.
 
 FETCH_SIZE and WRITE_SIZE (KiB per dispatch, summed over the L2 channels)
 are scaled by what they read for the calibration multiply, whose true traffic
@@ -50,6 +52,8 @@ def stage_of(kernel: str, prev: str | None) -> str | None:
         return "ffn1_gelu"
     if "linear_pipe_kernelILi2E" in kernel:
         return "attn_out_ln" if prev == "attention" else "ffn2_ln" if prev == "ffn1_gelu" else None
+    if "linear_pipe_kernelILi3E" in kernel or "ln_rows_kernel" in kernel:
+        return prev if prev in ("attn_out_ln", "ffn2_ln") else None
     return None
 
 
@@ -64,22 +68,34 @@ def _rows(directory: str, suffix: str) -> list[dict]:
     return rows
 
 
-def trace_stats(directory: str) -> dict:
-    """{stage: (dispatches, average microseconds)} from a kernel trace."""
-    rows = sorted(_rows(directory, "kernel_trace.csv"), key=lambda r: int(r["Dispatch_Id"]))
+def _instances(seq):
+    """Groups (kernel name, value) dispatches in launch order into stage
+    instances: {stage: [summed value of each instance]}.  A dispatch that
+    continues the previous stage (the pieces of a split LayerNorm round)
+    adds to that stage's current instance."""
     acc, prev = {}, None
-    for r in rows:
-        st = stage_of(r["Kernel_Name"], prev)
+    for name, v in seq:
+        st = stage_of(name, prev)
         if st is None:
             continue
+        if st == prev and ("linear_pipe_kernelILi3E" in name or "ln_rows_kernel" in name):
+            acc[st][-1] += v
+        else:
+            acc.setdefault(st, []).append(v)
         prev = st
-        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
-        acc.setdefault(st, []).append(us)
+    return acc
+
+
+def trace_stats(directory: str) -> dict:
+    """{stage: (instances, average microseconds of kernel time per instance)}
+    from a kernel trace."""
+    rows = sorted(_rows(directory, "kernel_trace.csv"), key=lambda r: int(r["Dispatch_Id"]))
+    acc = _instances((r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3) for r in rows)
     return {k: (len(v), sum(v) / len(v)) for k, v in acc.items()}
 
 
 def counter_stats(directory: str, counter: str) -> tuple[dict, float]:
-    """({stage: average counter value per dispatch}, the calibration multiply's value)."""
+    """({stage: average counter value per stage instance}, the calibration multiply's value)."""
     per_dispatch = {}
     for r in _rows(directory, "counter_collection.csv"):
         if r["Counter_Name"] != counter:
@@ -87,16 +103,12 @@ def counter_stats(directory: str, counter: str) -> tuple[dict, float]:
         d = int(r["Dispatch_Id"])
         name, v = per_dispatch.get(d, (r["Kernel_Name"], 0.0))
         per_dispatch[d] = (name, v + float(r["Counter_Value"]))
-    acc, prev, cal = {}, None, 0.0
+    cal = 0.0
     for d in sorted(per_dispatch):
         name, v = per_dispatch[d]
         if "elementwise_kernel" in name:  # the calibration multiply (and torch's fills)
             cal = max(cal, v)
-        st = stage_of(name, prev)
-        if st is None:
-            continue
-        prev = st
-        acc.setdefault(st, []).append(v)
+    acc = _instances(per_dispatch[d] for d in sorted(per_dispatch))
     return {k: sum(v) / len(v) for k, v in acc.items()}, cal
 
 
@@ -140,13 +152,13 @@ def summarize(trace: str | None, fetch: str | None, write: str | None) -> str:
                    f"(scale {w_scale if w_scale is None else round(w_scale, 4)}); per-stage bytes below are "
                    "counter x scale.")
         out.append("")
-    out.append("| stage | dispatches | avg us | HBM read MB | HBM write MB |")
+    out.append("| stage | instances | avg us | HBM read MB | HBM write MB |")
     out.append("|---|---:|---:|---:|---:|")
     for st in STAGES:
         n, us = times.get(st, (0, float("nan")))
         rd = f_stats[st] * 1024 * f_scale if st in f_stats and f_scale else None
         wr = w_stats[st] * 1024 * w_scale if st in w_stats and w_scale else None
-        data["stages"][st] = {"dispatches": n, "avg_us": None if n == 0 else round(us, 2),
+        data["stages"][st] = {"instances": n, "avg_us": None if n == 0 else round(us, 2),
                               "read_bytes": None if rd is None else int(rd),
                               "write_bytes": None if wr is None else int(wr)}
         out.append(f"| {st} | {n} | {us:.1f} | {'' if rd is None else f'{rd / 1e6:.1f}'} | "

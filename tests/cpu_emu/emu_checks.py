@@ -221,6 +221,26 @@ def group_gemm():
             tol = 2e-3 * max(1.0, float(np.abs(ref).max()))
         err = float(np.abs(c - ref).max())
         assert err < tol, (m, k, n, epi, err)
+    # LayerNorm tiles past the last whole round are split into pieces and
+    # normalised by a separate kernel: those rows must match, bit for bit,
+    # the same rows computed inside whole tiles (the emulated device has 16
+    # CUs: 17 tiles = 16 whole + 1 split into 64 x 64 pieces)
+    for odt in (np.float16, np.float32):
+        m, k, n = 16 * 128 + 100, 128, 384
+        a, q, s, bias = problem(21, m, k, n)
+        a16 = a.astype(np.float16)
+        rng = np.random.default_rng(22)
+        res = rng.standard_normal((m, n)).astype(odt)
+        g = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        b = (0.1 * rng.standard_normal(n)).astype(np.float32)
+        split = linear(a16, q, s, bias, odt, _abi.EPI_BIAS_RES_LN, res, g, b)
+        whole = linear(np.ascontiguousarray(a16[100:]), q, s, bias, odt, _abi.EPI_BIAS_RES_LN,
+                       np.ascontiguousarray(res[100:]), g, b)
+        assert np.array_equal(split[2048:], whole[1948:]), odt
+        assert np.array_equal(split[100:2048], whole[:1948]), odt
+        ref = oracle.layernorm(res.astype(np.float32) + oracle.matmul_w8a32(a16.astype(np.float32), q, s, bias), g, b,
+                               1e-12)
+        assert np.abs(split - ref).max() < 2e-2
     w = (np.random.default_rng(12).standard_normal((64, 384)) * 0.02).astype(np.float32)
     w[0] = 0
     qg = np.empty((64, 384), np.int8)

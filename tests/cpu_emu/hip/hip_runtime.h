@@ -125,6 +125,19 @@ inline T __shfl_xor(T v, int mask, int width = 64) {
 }
 
 template <typename T>
+inline T __shfl(T v, int src_lane, int width = 64) {
+    static_assert(sizeof(T) <= 256, "slot too small");
+    const int lane = emu::lane_id();
+    std::memcpy(emu::wave_slot(lane), &v, sizeof(T));
+    emu::wave_barrier();
+    const int src = (src_lane & (width - 1)) | (lane & ~(width - 1));
+    T r;
+    std::memcpy(&r, emu::wave_slot(src), sizeof(T));
+    emu::wave_barrier();
+    return r;
+}
+
+template <typename T>
 inline T atomicAdd(T *p, T v) {  // fibers are cooperative on one OS thread
     T old = *p;
     *p = old + v;
@@ -205,6 +218,22 @@ inline emu_f32x4 mfma_16x16x32_args(emu_half8 a, emu_half8 b, emu_f32x4 c, int, 
 #define __builtin_amdgcn_mfma_f32_16x16x32_f16(...) emu::mfma_16x16x32_args(__VA_ARGS__)
 #define __builtin_amdgcn_exp2f(x) exp2f(x)
 #define __builtin_amdgcn_rcpf(x) (1.0f / (x))
+// v_perm_b32: byte i of the result is byte sel[i] of {src0 (bytes 4..7), src1 (bytes 0..3)};
+// 8..11 replicate a sign bit, 12 gives 0x00, 13.. give 0xff
+inline uint32_t __builtin_amdgcn_perm(uint32_t src0, uint32_t src1, uint32_t sel) {
+    const uint64_t in = ((uint64_t)src0 << 32) | src1;
+    uint32_t r = 0;
+    for (int i = 0; i < 4; i++) {
+        const uint32_t s = (sel >> (8 * i)) & 0xffu;
+        uint32_t b;
+        if (s >= 13) b = 0xffu;
+        else if (s == 12) b = 0u;
+        else if (s >= 8) b = ((in >> (8 * (2 * (s - 8) + 1) + 7)) & 1u) ? 0xffu : 0u;
+        else b = (uint32_t)(in >> (8 * s)) & 0xffu;
+        r |= b << (8 * i);
+    }
+    return r;
+}
 
 // ---------------------------------------------------------------------------
 // runtime API subset

@@ -28,7 +28,8 @@ def emu_env():
     res = subprocess.run(["make", "-s", "-j8", "-C", EMU], capture_output=True, text=True, timeout=900)
     assert res.returncode == 0, res.stderr[-3000:]
     env = dict(os.environ)
-    env["LD_PRELOAD"] = _asan_runtime()
+    # the sanitizer runtime must come first; anything already preloaded stays
+    env["LD_PRELOAD"] = " ".join(filter(None, [_asan_runtime(), os.environ.get("LD_PRELOAD")]))
     env["ASAN_OPTIONS"] = "detect_leaks=0"
     return env
 

@@ -1,0 +1,75 @@
+"""GPU checks of the split partial round of the LayerNorm GEMM (K3 with the
+bias + residual + LayerNorm epilogue, arctic.zig:716-746 / 779-809).
+
+The 128-row tiles run in whole rounds of one tile per CU; the tiles left
+for a partial last round are cut into 64 x 64, 128 x 64 or 128 x 128
+pieces whose pre-normalisation rows a separate kernel normalises.  Those
+rows must equal, bit for bit, the same rows computed inside whole tiles
+(the model's batch-order invariance depends on it), and match the oracle
+within the f16 bar of the other GEMM tests: |gpu - oracle| < 2e-2 on
+unit-variance LayerNorm outputs stored as f16."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tenzor_amd import _abi, check, lib
+
+pytestmark = pytest.mark.gpu
+N = 384
+
+
+def problem(seed, m, k):
+    rng = np.random.default_rng(seed)
+    a = rng.standard_normal((m, k)).astype(np.float16)
+    q = rng.integers(-127, 128, size=(N, k)).astype(np.int8)
+    s = np.array([oracle.f32_to_f16(v) for v in rng.uniform(0.001, 0.02, N).astype(np.float32)], np.uint16)
+    bias = rng.uniform(-0.1, 0.1, N).astype(np.float32)
+    res = rng.standard_normal((m, N)).astype(np.float16)
+    g = (1 + 0.1 * rng.standard_normal(N)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    return a, q, s, bias, res, g, b
+
+
+def ln_gemm(ctx, a, q, s, bias, res, g, b):
+    """f16 activations, f16 residual and output: the model's path."""
+    m, k = a.shape
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    A, Q, S, B, R, G, Bt = dev(a), dev(q), dev(s.view(np.int16)), dev(bias), dev(res), dev(g), dev(b)
+    out = torch.empty((m, N), dtype=torch.float16, device="cuda")
+    check(lib().tzh_linear_w8(ctx.handle, A.data_ptr(), _abi.F16, Q.data_ptr(), S.data_ptr(), B.data_ptr(),
+                              out.data_ptr(), _abi.F16, m, k, N, _abi.EPI_BIAS_RES_LN, R.data_ptr(), _abi.F16,
+                              G.data_ptr(), Bt.data_ptr(), 1e-12))
+    return out.cpu().numpy()
+
+
+# extra tiles past the whole rounds -> pieces per tile: 2 -> 12 (64 x 64),
+# 30 -> 6 (128 x 64), 60 -> 3 (128 x 128), 100 -> no split; partial tiles too
+@pytest.mark.parametrize("extra_rows,k", [(2 * 128 - 28, 384), (30 * 128, 1536), (60 * 128 - 5, 384),
+                                          (100 * 128, 384), (1, 1536)])
+def test_split_rows_match_whole_tiles(ctx, extra_rows, k):
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    whole_rows = cus * 128
+    m = whole_rows + extra_rows
+    a, q, s, bias, res, g, b = problem(extra_rows + k, m, k)
+    split = ln_gemm(ctx, a, q, s, bias, res, g, b)
+    # the same rows again, shifted so that every one lies in a whole tile
+    shift = m - whole_rows
+    whole = ln_gemm(ctx, a[shift:], q, s, bias, res[shift:], g, b)
+    assert np.array_equal(split[shift:].view(np.uint16), whole.view(np.uint16))
+    # the oracle on a sample of the tail rows and of the whole-round rows
+    rows = np.unique(np.concatenate([np.arange(whole_rows, m, max(1, extra_rows // 16)), [0, 1, whole_rows - 1, m - 1]]))
+    lin = oracle.matmul_w8a32(a[rows].astype(np.float32), q, s, bias)
+    ref = oracle.layernorm(res[rows].astype(np.float32) + lin, g, b, 1e-12)
+    err = np.abs(split[rows].astype(np.float32) - ref).max()
+    assert err < 2e-2, float(err)
+
+
+def test_small_batch_is_all_pieces(ctx):
+    """Fewer tiles than CUs (config-1-like sizes): every tile is split."""
+    for m in (1, 7, 128, 1000):
+        a, q, s, bias, res, g, b = problem(m, m, 384)
+        got = ln_gemm(ctx, a, q, s, bias, res, g, b)
+        ref = oracle.layernorm(res.astype(np.float32) + oracle.matmul_w8a32(a.astype(np.float32), q, s, bias), g, b,
+                               1e-12)
+        assert np.abs(got.astype(np.float32) - ref).max() < 2e-2, m
