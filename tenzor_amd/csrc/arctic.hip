@@ -24,7 +24,7 @@
 
 #include "safetensors.h"
 
-int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc,
+int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, int32_t w_format,
                             const uint16_t *scale, const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k,
                             int64_t n, int32_t epilogue, const void *res, const float *gamma, const float *beta,
                             float eps, float *ln_ws, int64_t ln_ws_rows);
@@ -183,13 +183,15 @@ struct DevTable {
     TableRef ref() const { return TableRef{f32, q8, scale}; }
 };
 
-// Weight codes in f16 with a per-row f16 scale: C = (X . codes) * scale + b.
-// int8 codes are widened exactly (|q| <= 127).  f32 weights (the reference's
-// f32 model, MatWeight.f32) become codes W * 2^k with a power-of-two scale
-// 2^-k per row, so the scaling itself is exact and only the f16 rounding of
-// W * 2^k remains.
+// Weight codes with a per-row f16 scale: C = (X . codes) * scale + b.
+// int8 codes stay one byte each, biased and stage-tiled for the GEMM
+// (TZH_WF_W8T; exact, |q| <= 127).  f32 weights (the reference's f32 model,
+// MatWeight.f32) become f16 codes W * 2^k with a power-of-two scale 2^-k per
+// row (TZH_WF_F16), so the scaling itself is exact and only the f16 rounding
+// of W * 2^k remains.
 struct DevLinear {
-    _Float16 *w = nullptr;
+    void *w = nullptr;
+    int32_t fmt = TZH_WF_F16;
     uint16_t *s = nullptr;
     float *b = nullptr;
 };
@@ -297,6 +299,36 @@ int upload_linear(tzh_model *m, std::initializer_list<std::pair<const tzh_mat_vi
         if (v->cols != cols) return tzh_fail(TZH_ERR_INVALID_ARGS, "%s has %d columns, expected %d", what, v->cols, cols);
         rows += v->rows;
     }
+    bool all_i8 = true;
+    for (auto &pb : parts) all_i8 = all_i8 && pb.first->dtype == TZH_I8;
+    if (all_i8 && rows % 384 == 0 && cols % 64 == 0) {
+        // biased codes u = q + 128, stage-tiled: block of 384 rows, k stage of
+        // 64 codes, row (the layout tile_codes_w8_kernel writes)
+        const int kts = cols / 64;
+        std::vector<uint8_t> t((size_t)(rows * cols));
+        std::vector<uint16_t> s;
+        std::vector<float> b;
+        int64_t r0 = 0;
+        for (auto &pb : parts) {
+            const tzh_mat_view *v = pb.first;
+            const int8_t *q = (const int8_t *)v->data;
+            for (int r = 0; r < v->rows; r++) {
+                const int64_t n = r0 + r;
+                for (int kt = 0; kt < kts; kt++) {
+                    uint8_t *dst = &t[(size_t)((((n / 384) * kts + kt) * 384 + n % 384) * 64)];
+                    const int8_t *src = q + (size_t)r * cols + (size_t)kt * 64;
+                    for (int c = 0; c < 64; c++) dst[c] = (uint8_t)src[c] ^ 0x80u;
+                }
+            }
+            s.insert(s.end(), (const uint16_t *)v->scale, (const uint16_t *)v->scale + v->rows);
+            b.insert(b.end(), pb.second, pb.second + v->rows);
+            r0 += v->rows;
+        }
+        out.fmt = TZH_WF_W8T;
+        TZH_TRY(upload<uint8_t>(m, (uint8_t **)&out.w, t.data(), t.size()));
+        TZH_TRY(upload<uint16_t>(m, &out.s, s.data(), s.size()));
+        return upload<float>(m, &out.b, b.data(), b.size());
+    }
     std::vector<uint16_t> w((size_t)(rows * cols));  // f16 bits of the codes
     std::vector<uint16_t> s((size_t)rows);
     std::vector<float> b((size_t)rows);
@@ -317,7 +349,8 @@ int upload_linear(tzh_model *m, std::initializer_list<std::pair<const tzh_mat_vi
         std::memcpy(b.data() + r0, pb.second, (size_t)v->rows * 4);
         r0 += v->rows;
     }
-    TZH_TRY(upload<_Float16>(m, &out.w, w.data(), w.size()));
+    out.fmt = TZH_WF_F16;
+    TZH_TRY(upload<_Float16>(m, (_Float16 **)&out.w, w.data(), w.size()));
     TZH_TRY(upload<uint16_t>(m, &out.s, s.data(), s.size()));
     return upload<float>(m, &out.b, b.data(), b.size());
 }
@@ -671,18 +704,18 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
     for (int32_t li = 0; li < n_layers; li++) {
         const DevLayer &d = m->layers[(size_t)li];
         const int cus = m->ctx->num_cus;
-        TZH_TRY(tzh_linear_codes_launch(st, cus, m->h, d.qkv.w, d.qkv.s, d.qkv.b, m->qkv, TZH_F16, T, H, 3 * H,
+        TZH_TRY(tzh_linear_codes_launch(st, cus, m->h, d.qkv.w, d.qkv.fmt, d.qkv.s, d.qkv.b, m->qkv, TZH_F16, T, H, 3 * H,
                                         TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f, nullptr, 0));
         TZH_TRY(mark("qkv"));
         TZH_TRY(tzh_attention_launch(st, m->qkv, m->attn, d_cu, d_order, batch, 12, H));
         TZH_TRY(mark("attention"));
-        TZH_TRY(tzh_linear_codes_launch(st, cus, m->attn, d.o.w, d.o.s, d.o.b, m->h1, TZH_F16, T, H, H,
+        TZH_TRY(tzh_linear_codes_launch(st, cus, m->attn, d.o.w, d.o.fmt, d.o.s, d.o.b, m->h1, TZH_F16, T, H, H,
                                         TZH_EPI_BIAS_RES_LN, m->h, d.ln1_g, d.ln1_b, eps, m->ln_ws, m->ln_ws_rows));
         TZH_TRY(mark("attn_out_ln"));
-        TZH_TRY(tzh_linear_codes_launch(st, cus, m->h1, d.ffn1.w, d.ffn1.s, d.ffn1.b, m->inter, TZH_F16, T, H, 1536,
+        TZH_TRY(tzh_linear_codes_launch(st, cus, m->h1, d.ffn1.w, d.ffn1.fmt, d.ffn1.s, d.ffn1.b, m->inter, TZH_F16, T, H, 1536,
                                         TZH_EPI_BIAS_GELU, nullptr, nullptr, nullptr, 0.0f, nullptr, 0));
         TZH_TRY(mark("ffn1_gelu"));
-        TZH_TRY(tzh_linear_codes_launch(st, cus, m->inter, d.ffn2.w, d.ffn2.s, d.ffn2.b, m->h, TZH_F16, T, 1536, H,
+        TZH_TRY(tzh_linear_codes_launch(st, cus, m->inter, d.ffn2.w, d.ffn2.fmt, d.ffn2.s, d.ffn2.b, m->h, TZH_F16, T, 1536, H,
                                         TZH_EPI_BIAS_RES_LN, m->h1, d.ln2_g, d.ln2_b, eps, m->ln_ws, m->ln_ws_rows));
         TZH_TRY(mark("ffn2_ln"));
     }

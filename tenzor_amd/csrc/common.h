@@ -40,6 +40,11 @@ void tzh_clear_error();
                             hipGetErrorString(e_));                                      \
     } while (0)
 
+// Device formats of the int8-model weight codes inside the library (not part
+// of the C ABI): f16 codes [n, k] row-major, or biased int8 codes stage-tiled
+// in 384-row blocks (gemm_pipe.hip).
+enum { TZH_WF_F16 = 0, TZH_WF_W8T = 1 };
+
 // ---------------------------------------------------------------------------
 // Context: one device, one stream.
 // ---------------------------------------------------------------------------

@@ -407,7 +407,8 @@ int tzh_linear_w8_launch(hipStream_t st, const void *a, int32_t a_dtype, const i
 }
 
 int tzh_widen_codes_launch(hipStream_t st, const int8_t *q, _Float16 *out, int64_t n);
-int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc,
+int tzh_tile_codes_w8_launch(hipStream_t st, const int8_t *q, uint8_t *out, int64_t n, int64_t k);
+int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, int32_t w_format,
                             const uint16_t *scale, const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k,
                             int64_t n, int32_t epilogue, const void *res, const float *gamma, const float *beta,
                             float eps, float *ln_ws, int64_t ln_ws_rows);
@@ -427,17 +428,24 @@ extern "C" int tzh_linear_w8(tzh_ctx *ctx, const void *a, int32_t a_dtype, const
          (epilogue == TZH_EPI_BIAS_RES_LN && n == 384 && residual && gamma && beta && res_dtype == c_dtype));
     if (a_dtype == TZH_F16 && (c_dtype == TZH_F16 || c_dtype == TZH_F32) && pipe_shape && a && wq && scale && c &&
         al16(a) && al16(c) && (!residual || al16(residual))) {
-        // scratch: the widened codes, then (LayerNorm epilogue) the f32 rows
-        // of a split partial round of tiles
-        const size_t codes_bytes = ((size_t)(n * k * 2) + 255) / 256 * 256;
+        // scratch: the codes in the model's format (stage-tiled biased int8
+        // when n is a multiple of 384 and the output f16, else widened to
+        // f16), then (LayerNorm epilogue) the f32 rows of a split partial
+        // round of tiles
+        const bool w8t = n % 384 == 0 && c_dtype == TZH_F16;
+        const size_t codes_bytes = ((size_t)(n * k * (w8t ? 1 : 2)) + 255) / 256 * 256;
         const int64_t ws_rows = epilogue == TZH_EPI_BIAS_RES_LN
                                     ? std::min<int64_t>((m + 127) / 128, ctx->num_cus / 3 + 1) * 128
                                     : 0;
         void *scratch = nullptr;
         TZH_TRY(tzh_ctx_scratch(ctx, codes_bytes + (size_t)ws_rows * 384 * 4, &scratch));
-        TZH_TRY(tzh_widen_codes_launch(ctx->stream, wq, (_Float16 *)scratch, n * k));
-        return tzh_linear_codes_launch(ctx->stream, ctx->num_cus, (const _Float16 *)a, (const _Float16 *)scratch,
-                                       scale, bias, c, c_dtype, m, k, n, epilogue, residual, gamma, beta, eps,
+        if (w8t)
+            TZH_TRY(tzh_tile_codes_w8_launch(ctx->stream, wq, (uint8_t *)scratch, n, k));
+        else
+            TZH_TRY(tzh_widen_codes_launch(ctx->stream, wq, (_Float16 *)scratch, n * k));
+        return tzh_linear_codes_launch(ctx->stream, ctx->num_cus, (const _Float16 *)a, scratch,
+                                       w8t ? TZH_WF_W8T : TZH_WF_F16, scale, bias, c, c_dtype, m, k, n, epilogue,
+                                       residual, gamma, beta, eps,
                                        ws_rows ? (float *)((char *)scratch + codes_bytes) : nullptr, ws_rows);
     }
     return tzh_linear_w8_launch(ctx->stream, a, a_dtype, wq, scale, bias, c, c_dtype, m, k, n, epilogue, residual,

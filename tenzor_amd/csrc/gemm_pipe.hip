@@ -149,10 +149,16 @@ struct TileFmt {
 // W8: the weight codes stay one byte each (biased, u = q + 128) in HBM and
 // in LDS, which halves the weight stream, and are widened to f16 in
 // registers after each fragment read.
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_, bool W8_ = false>
+// WTB > 0: the weight codes are stored stage-tiled: for each block of WTB
+// rows (a multiple of BN) and each k stage, the WTB x BK codes are one
+// contiguous span, rows BK codes apart (tile_codes_w8_kernel writes it), so
+// a stage's weight tile is read from consecutive memory.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_, bool W8_ = false, int WTB_ = 0>
 struct PipeCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, NS = NS_;
-    static constexpr bool W8 = W8_;
+    static constexpr bool W8 = W8_, WT = WTB_ > 0;
+    static constexpr int WTB = WTB_ > 0 ? WTB_ : BN_;
+    static_assert(WTB % BN_ == 0, "weight tile blocks hold whole column tiles");
     static constexpr int NW = WM * WN, THREADS = NW * 64;
     static constexpr int TMF = BM / WM / 32;  // token fragments per wave
     static constexpr int TNF = BN / WN / 32;  // weight fragments per wave
@@ -309,8 +315,9 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     const int rw_in = lane / FW::CPR;                                // row inside a W DMA group
     const int wchunk_e = (lane % FW::CPR) ^ FW::swz(rw_in);
     const int wchunk_o = (lane % FW::CPR) ^ FW::swz(FW::RPI + rw_in);
-    const uint32_t w_loff_e = (uint32_t)(rw_in * K * WEB + wchunk_e * 16);  // bytes, same for every unit
-    const uint32_t w_loff_o = (uint32_t)(rw_in * K * WEB + wchunk_o * 16);
+    const int w_pitch = P::WT ? WROWB : K * WEB;  // bytes between weight rows in memory
+    const uint32_t w_loff_e = (uint32_t)(rw_in * w_pitch + wchunk_e * 16);  // bytes, same for every unit
+    const uint32_t w_loff_o = (uint32_t)(rw_in * w_pitch + wchunk_o * 16);
     const char *const Xb = (const char *)X;
     const char *const Wb = (const char *)Wc;
     int iu = 0, ikt = 0;                                             // next stage to issue
@@ -328,7 +335,9 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
             const int chunk = (FX::PARITY && ((wu * P::LX + i) & 1)) ? chunk_o : chunk_e;
             x_loff[i] = (uint32_t)((r - r0) * K + chunk * 8) * 2u;
         }
-        w_unit = Wb + (size_t)(n0 + wu * P::LW * FW::RPI) * K * WEB;
+        w_unit = P::WT ? Wb + (size_t)(n0 / P::WTB) * KT * P::WTB * WROWB +
+                             (size_t)(n0 % P::WTB + wu * P::LW * FW::RPI) * WROWB
+                       : Wb + (size_t)(n0 + wu * P::LW * FW::RPI) * K * WEB;
     };
     auto issue = [&](char *buf) __attribute__((always_inline)) {
         const size_t k0b = (size_t)ikt * BK * 2;
@@ -337,7 +346,8 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
             dma16(Xb + ((size_t)x_row0[i] * K * 2 + k0b), x_loff[i], buf + (wu * P::LX + i) * FX::RPI * XROWB);
 #pragma unroll
         for (int i = 0; i < P::LW; i++)
-            dma16(w_unit + ((size_t)i * FW::RPI * K * WEB + (size_t)ikt * BK * WEB),
+            dma16(w_unit + (P::WT ? (size_t)ikt * P::WTB * WROWB + (size_t)i * FW::RPI * WROWB
+                                  : (size_t)i * FW::RPI * K * WEB + (size_t)ikt * BK * WEB),
                   (FW::PARITY && ((wu * P::LW + i) & 1)) ? w_loff_o : w_loff_e,
                   buf + P::X_BYTES + (wu * P::LW + i) * FW::RPI * WROWB);
         if (++ikt == KT) {
@@ -584,16 +594,42 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 }
 
 // Tile shapes (tokens x output columns x k per stage, waves, stages), chosen
-// by measurement on MI355X at the Arctic shapes (T = 67590 tokens):
+// by measurement on MI355X at the Arctic shapes (T = 67590 tokens), per
+// weight format:
+//   TZH_WF_F16: f16 codes, row-major [n, k] (any n multiple of 128; the f32
+//     model's power-of-two-scaled codes need it);
+//   TZH_WF_W8T: biased int8 codes u = q + 128, stage-tiled in 384-row
+//     blocks (tile_codes_w8_kernel; n a multiple of 384).  Half the weight
+//     bytes and one contiguous span per stage let a third stage fit in LDS:
+//     QKV 78 -> 73, FFN1 118 -> 114, FFN2 + LN 106 -> 98 us at T = 65536.
 // 128 x 384 tiles halve the L2 -> LDS operand traffic of 128 x 128 ones.
-using BiasCfg = PipeCfg<128, 384, 64, 2, 4, 2>;      // n a multiple of 384
-using BiasCfgNarrow = PipeCfg<128, 128, 64, 2, 2, 4>;  // other multiples of 128
-using LnCfg = PipeCfg<128, 384, 64, 2, 4, 2>;
-// Pieces of the partial last round of a LayerNorm GEMM (12, 6 or 3 per
+// The pieces cut a partial last round of a LayerNorm GEMM (12, 6 or 3 per
 // 128 x 384 tile; see launch_ln).
-using Piece64 = PipeCfg<64, 64, 64, 2, 2, 4>;
-using Piece128x64 = PipeCfg<128, 64, 64, 2, 2, 4>;
-using Piece128 = BiasCfgNarrow;
+constexpr int kWtBlock = 384;  // rows per stage-tiled weight block
+template <int WF>
+struct Cfgs;
+template <>
+struct Cfgs<TZH_WF_F16> {
+    using Bias = PipeCfg<128, 384, 64, 2, 4, 2>;       // n a multiple of 384
+    using Narrow = PipeCfg<128, 128, 64, 2, 2, 4>;     // other multiples of 128
+    using Ln = PipeCfg<128, 384, 64, 2, 4, 2>;
+    using Piece64 = PipeCfg<64, 64, 64, 2, 2, 4>;
+    using Piece128x64 = PipeCfg<128, 64, 64, 2, 2, 4>;
+    using Piece128 = Narrow;
+};
+template <>
+struct Cfgs<TZH_WF_W8T> {
+    using Bias = PipeCfg<128, 384, 64, 2, 4, 3, true, kWtBlock>;
+    using Narrow = Bias;  // n is always a multiple of 384
+    using Ln = Bias;
+    using Piece64 = PipeCfg<64, 64, 64, 2, 2, 4, true, kWtBlock>;
+    using Piece128x64 = PipeCfg<128, 64, 64, 2, 2, 4, true, kWtBlock>;
+    using Piece128 = PipeCfg<128, 128, 64, 2, 2, 4, true, kWtBlock>;
+};
+using LnCfg = Cfgs<TZH_WF_F16>::Ln;
+static_assert(Cfgs<TZH_WF_W8T>::Ln::WN == LnCfg::WN && Cfgs<TZH_WF_W8T>::Ln::TNF == LnCfg::TNF &&
+                  Cfgs<TZH_WF_W8T>::Ln::BN == LnCfg::BN,
+              "ln_rows_kernel follows one LayerNorm epilogue layout for both weight formats");
 
 template <typename T>
 struct NoDeduce {
@@ -693,12 +729,13 @@ __global__ void __launch_bounds__(256) ln_rows_kernel(const float *__restrict__ 
 // output value comes out the same as it would from the whole-tile kernel:
 // the pieces run the same MFMA sequence per element, and ln_rows_kernel
 // sums the statistics in the tile epilogue's order.
-template <typename TC>
+template <int WF, typename TC>
 int launch_ln(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, const uint16_t *scale,
               const float *bias, TC *c, int M, int K, const TC *res, const float *gamma, const float *beta, float eps,
               float *ws, int64_t ws_rows) {
-    constexpr int N = LnCfg::BN, BM = LnCfg::BM;
-    const int slots = num_cus * LnCfg::blocks_per_cu(true);
+    using C = Cfgs<WF>;
+    constexpr int N = C::Ln::BN, BM = C::Ln::BM;
+    const int slots = num_cus * C::Ln::blocks_per_cu(true);
     const int panels = (M + BM - 1) / BM;
     const int full = panels / slots * slots;
     const int rem = panels - full;
@@ -712,18 +749,19 @@ int launch_ln(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, co
             }
     const int m_main = per ? full * BM : M;
     if (m_main > 0)
-        TZH_TRY((launch<EPI_LN, TC, LnCfg>(st, num_cus, x, wc, scale, bias, c, m_main, K, N, res, gamma, beta, eps)));
+        TZH_TRY((launch<EPI_LN, TC, typename C::Ln>(st, num_cus, x, wc, scale, bias, c, m_main, K, N, res, gamma, beta,
+                                                     eps)));
     if (!per) return TZH_OK;
     const _Float16 *xt = x + (size_t)m_main * K;
     const TC *rt = res + (size_t)m_main * N;
     if (per == 12)
-        TZH_TRY((launch<EPI_RES, float, Piece64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N, rt,
+        TZH_TRY((launch<EPI_RES, float, typename C::Piece64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N, rt,
                                                       nullptr, nullptr, 0.f)));
     else if (per == 6)
-        TZH_TRY((launch<EPI_RES, float, Piece128x64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N, rt,
+        TZH_TRY((launch<EPI_RES, float, typename C::Piece128x64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N, rt,
                                                           nullptr, nullptr, 0.f)));
     else
-        TZH_TRY((launch<EPI_RES, float, Piece128, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N, rt,
+        TZH_TRY((launch<EPI_RES, float, typename C::Piece128, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N, rt,
                                                        nullptr, nullptr, 0.f)));
     hipLaunchKernelGGL(ln_rows_kernel<TC>, dim3((unsigned)((tail_rows + 31) / 32)), dim3(256), 0, st, ws, tail_rows,
                        gamma, beta, eps, c + (size_t)m_main * N);
@@ -731,13 +769,36 @@ int launch_ln(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, co
     return TZH_OK;
 }
 
-template <int EPI, typename TC>
-int launch_bias(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc, const uint16_t *scale,
+template <int WF, int EPI, typename TC>
+int launch_bias(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, const uint16_t *scale,
                 const float *bias, TC *c, int M, int K, int N) {
-    if (N % BiasCfg::BN == 0)
-        return launch<EPI, TC, BiasCfg>(st, num_cus, x, wc, scale, bias, c, M, K, N, nullptr, nullptr, nullptr, 0.f);
-    return launch<EPI, TC, BiasCfgNarrow>(st, num_cus, x, wc, scale, bias, c, M, K, N, nullptr, nullptr, nullptr,
-                                          0.f);
+    using C = Cfgs<WF>;
+    if (N % C::Bias::BN == 0)
+        return launch<EPI, TC, typename C::Bias>(st, num_cus, x, wc, scale, bias, c, M, K, N, nullptr, nullptr,
+                                                 nullptr, 0.f);
+    return launch<EPI, TC, typename C::Narrow>(st, num_cus, x, wc, scale, bias, c, M, K, N, nullptr, nullptr, nullptr,
+                                               0.f);
+}
+
+// int8 codes q[r][j] (n rows of k) -> biased codes u = q + 128 stage-tiled
+// for TZH_WF_W8T: u lands at ((r / 384 * (k / 64) + j / 64) * 384 + r % 384)
+// * 64 + j % 64.  One thread per 16 codes.
+__global__ void tile_codes_w8_kernel(const int8_t *__restrict__ q, uint8_t *__restrict__ out, int n, int k) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 16-byte group of the output
+    const int kt_count = k / 64;
+    if (i >= (int64_t)n * k / 16) return;
+    const int64_t o = i * 16;
+    const int c = (int)(o % 64);
+    const int64_t r_all = o / 64;  // row index inside the tiled layout (block, stage, row)
+    const int r = (int)(r_all % kWtBlock);
+    const int64_t bs = r_all / kWtBlock;
+    const int kt = (int)(bs % kt_count);
+    const int nb = (int)(bs / kt_count);
+    const int8_t *src = q + ((int64_t)nb * kWtBlock + r) * k + kt * 64 + c;
+    uint8_t v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) v[j] = (uint8_t)src[j] ^ 0x80u;
+    *(u32x4_t *)(out + o) = *(const u32x4_t *)v;
 }
 
 __global__ void widen_codes_kernel(const int8_t *__restrict__ q, _Float16 *__restrict__ out, int64_t n) {
@@ -769,10 +830,23 @@ int tzh_widen_codes_launch(hipStream_t st, const int8_t *q, _Float16 *out, int64
     return TZH_OK;
 }
 
-// f16 activations x f16 weight codes; output and residual both F16 or both F32.
-// ln_ws (f32, ln_ws_rows rows of 384; may be null) lets the LayerNorm
-// epilogue split a partial last round of tiles (see launch_ln).
-int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const _Float16 *wc,
+// int8 codes [n, k] -> the TZH_WF_W8T layout (n a multiple of 384, k of 64).
+int tzh_tile_codes_w8_launch(hipStream_t st, const int8_t *q, uint8_t *out, int64_t n, int64_t k) {
+    if (n % kWtBlock || k % 64 || n <= 0 || k <= 0)
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "tiled int8 weights need n %% 384 == 0 and k %% 64 == 0");
+    const int64_t groups = n * k / 16;
+    hipLaunchKernelGGL(tile_codes_w8_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, st, q, out, (int)n,
+                       (int)k);
+    TZH_LAUNCHED("tile_codes_w8_kernel");
+    return TZH_OK;
+}
+
+// f16 activations x weight codes in format w_format (TZH_WF_F16: f16
+// row-major; TZH_WF_W8T: tiled biased int8, f16 output only); output and
+// residual both F16 or both F32.  ln_ws (f32, ln_ws_rows rows of 384; may
+// be null) lets the LayerNorm epilogue split a partial last round of tiles
+// (see launch_ln).
+int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, int32_t w_format,
                             const uint16_t *scale, const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k,
                             int64_t n, int32_t epilogue, const void *res, const float *gamma, const float *beta,
                             float eps, float *ln_ws, int64_t ln_ws_rows) {
@@ -786,24 +860,40 @@ int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, cons
     if (c_dtype != TZH_F16 && c_dtype != TZH_F32) return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "output must be F16 or F32");
     const int M = (int)m, K = (int)k, N = (int)n;
     const bool c16 = c_dtype == TZH_F16;
+    if (w_format != TZH_WF_F16 && w_format != TZH_WF_W8T)
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "unknown weight format %d", w_format);
+    const bool w8t = w_format == TZH_WF_W8T;
+    if (w8t && (!c16 || N % kWtBlock))
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "tiled int8 weights need f16 output and n %% 384 == 0 (n=%d)", N);
     if (epilogue == TZH_EPI_BIAS || epilogue == TZH_EPI_BIAS_GELU) {
-        if (N % BiasCfgNarrow::BN || N > 1536)
-            return tzh_fail(TZH_ERR_INVALID_ARGS, "n=%d must be a multiple of %d and at most 1536", N,
-                            BiasCfgNarrow::BN);
+        if (N % 128 || N > 1536)
+            return tzh_fail(TZH_ERR_INVALID_ARGS, "n=%d must be a multiple of 128 and at most 1536", N);
+        if (w8t)
+            return epilogue == TZH_EPI_BIAS
+                       ? launch_bias<TZH_WF_W8T, EPI_BIAS, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M,
+                                                                     K, N)
+                       : launch_bias<TZH_WF_W8T, EPI_GELU, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M,
+                                                                     K, N);
         if (epilogue == TZH_EPI_BIAS)
-            return c16 ? launch_bias<EPI_BIAS, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K, N)
-                       : launch_bias<EPI_BIAS, float>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, N);
-        return c16 ? launch_bias<EPI_GELU, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K, N)
-                   : launch_bias<EPI_GELU, float>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, N);
+            return c16 ? launch_bias<TZH_WF_F16, EPI_BIAS, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c,
+                                                                     M, K, N)
+                       : launch_bias<TZH_WF_F16, EPI_BIAS, float>(st, num_cus, x, wc, scale, bias, (float *)c, M, K,
+                                                                  N);
+        return c16 ? launch_bias<TZH_WF_F16, EPI_GELU, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K,
+                                                                 N)
+                   : launch_bias<TZH_WF_F16, EPI_GELU, float>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, N);
     }
     if (epilogue == TZH_EPI_BIAS_RES_LN) {
         if (N != LnCfg::BN) return tzh_fail(TZH_ERR_INVALID_ARGS, "LayerNorm epilogue needs n == 384 (got %d)", N);
         if (!res || !gamma || !beta) return tzh_fail(TZH_ERR_INVALID_ARGS, "null residual/gamma/beta");
         if (ln_ws && !aligned16(ln_ws)) return tzh_fail(TZH_ERR_INVALID_ARGS, "LayerNorm workspace must be 16-byte aligned");
-        return c16 ? launch_ln<_Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K, (const _Float16 *)res,
-                                         gamma, beta, eps, ln_ws, ln_ws_rows)
-                   : launch_ln<float>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, (const float *)res, gamma,
-                                      beta, eps, ln_ws, ln_ws_rows);
+        if (w8t)
+            return launch_ln<TZH_WF_W8T, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K,
+                                                   (const _Float16 *)res, gamma, beta, eps, ln_ws, ln_ws_rows);
+        return c16 ? launch_ln<TZH_WF_F16, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K,
+                                                     (const _Float16 *)res, gamma, beta, eps, ln_ws, ln_ws_rows)
+                   : launch_ln<TZH_WF_F16, float>(st, num_cus, x, wc, scale, bias, (float *)c, M, K,
+                                                  (const float *)res, gamma, beta, eps, ln_ws, ln_ws_rows);
     }
     return tzh_fail(TZH_ERR_INVALID_ARGS, "unknown epilogue %d", epilogue);
 }
