@@ -56,9 +56,10 @@ __device__ __forceinline__ void dma16(const char *sbase, uint32_t voff, char *ld
 // accesses across it, and no fence means no wait for the ring's loads.
 __device__ __forceinline__ void lds_barrier_only() { asm volatile("s_barrier" ::: "memory"); }
 
-// Marks a vector store the stage waits count (the CPU emulation keeps its
-// own in-order record of vector memory ops; on the GPU vmcnt does).
+// Mark a vector store / load the stage waits count (the CPU emulation keeps
+// its own in-order record of vector memory ops; on the GPU vmcnt does).
 __device__ __forceinline__ void vmem_store_issued() {}
+__device__ __forceinline__ void vmem_load_issued() {}
 
 // Orders a wave's LDS writes before its later LDS reads of what other lanes
 // of the same wave wrote.  The LDS performs one wave's operations in issue
@@ -191,27 +192,31 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 }
 
 // Wait until at most L*A + E vector memory ops are outstanding, A chosen at
-// run time from {0..AMAX} (the largest A <= ahead) and E from {0, EXTRA}.
-// On gfx9 every vector memory op (loads, stores, direct-to-LDS loads)
-// retires from vmcnt in issue order, so when at least L*A + E ops were
-// issued after a stage's loads, this guarantees that stage has landed.  E
-// counts the epilogue stores issued after them: without it the ring would
-// wait for those stores too.
-template <int AMAX, int L, int EXTRA>
-__device__ __forceinline__ void wait_stage(int ahead, bool extra) {
+// run time from {0..AMAX} (the largest A <= ahead) and E from {0, E1, E2}
+// (extra = 0, 1, 2).  On gfx9 every vector memory op (loads, stores,
+// direct-to-LDS loads) retires from vmcnt in issue order, so when at least
+// L*A + E ops were issued after a stage's loads, this guarantees that stage
+// has landed.  E counts the epilogue's own loads and stores issued after
+// them: without it the ring would wait for those too.
+template <int AMAX, int L, int E1, int E2>
+__device__ __forceinline__ void wait_stage(int ahead, int extra) {
     if constexpr (AMAX == 0) {
-        if (extra)
-            wait_vm_lgkm0<EXTRA>();
+        if (extra == 2)
+            wait_vm_lgkm0<E2>();
+        else if (extra == 1)
+            wait_vm_lgkm0<E1>();
         else
             wait_vm_lgkm0<0>();
     } else {
         if (ahead >= AMAX) {
-            if (extra)
-                wait_vm_lgkm0<L * AMAX + EXTRA>();
+            if (extra == 2)
+                wait_vm_lgkm0<L * AMAX + E2>();
+            else if (extra == 1)
+                wait_vm_lgkm0<L * AMAX + E1>();
             else
                 wait_vm_lgkm0<L * AMAX>();
         } else {
-            wait_stage<AMAX - 1, L, EXTRA>(ahead, extra);
+            wait_stage<AMAX - 1, L, E1, E2>(ahead, extra);
         }
     }
 }
@@ -405,6 +410,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 
     using RV = std::conditional_t<std::is_same<TC, float>::value, f32x4_t, half4_t>;
 
+
     auto epilogue = [&](int i) __attribute__((always_inline)) {
         const int m0 = unit_m0(i), n0 = unit_n0(i);
         if constexpr (!LN) {
@@ -421,7 +427,10 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                         float v[4];
                         using RV4 = std::conditional_t<std::is_same<TR, float>::value, f32x4_t, half4_t>;
                         RV4 res = {};
-                        if constexpr (EPI == EPI_RES) res = *(const RV4 *)(R + (size_t)(t < M ? t : M - 1) * N + n);
+                        if constexpr (EPI == EPI_RES) {
+                            res = *(const RV4 *)(R + (size_t)(t < M ? t : M - 1) * N + n);
+                            vmem_load_issued();
+                        }
 #pragma unroll
                         for (int q = 0; q < 4; q++) {
                             v[q] = acc[a][b][4 * g + q] * s[q] + bb[q];  // sum * s + bias (matmul_w8a32.zig:55)
@@ -461,8 +470,10 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                 for (int a = 0; a < TNF; a++) {
                     RV res[4];
 #pragma unroll
-                    for (int g = 0; g < 4; g++)
+                    for (int g = 0; g < 4; g++) {
                         res[g] = *(const RV *)(R + (size_t)t * BN + wn * TNF * 32 + a * 32 + 8 * g + 4 * half);
+                        vmem_load_issued();
+                    }
 #pragma unroll
                     for (int g = 0; g < 4; g++) {
                         const int n = wn * TNF * 32 + a * 32 + 8 * g + 4 * half;
@@ -559,19 +570,22 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     for (int j = 0; j < NS - 1; j++)
         if (j < S) issue(bufs[j]);
 
-    // The stores of the most recent epilogue (per lane and (token fragment,
-    // weight fragment): two 16-byte stores of staged f16 rows, or one store
-    // per 4-column group of f32) were issued after the loads of stages up to
-    // last_epi + NS - 1; they are all issued exactly when the unit lies
-    // inside M (no lane of any store is masked off), and only then are they
-    // counted.
+    // The most recent epilogue issued, after the loads of stages up to
+    // last_epi + NS - 1: its residual loads (one per lane, token fragment,
+    // weight fragment and 4-column group; always issued, rows clamped to M)
+    // and its stores (two 16-byte stores of staged f16 rows per token and
+    // weight fragment, or one per 4-column group of f32), the stores all
+    // issued exactly when the unit lies inside M (no lane of any store is
+    // masked off), and only then counted.
+    constexpr int EPI_LOADS = (LN || EPI == EPI_RES) ? TMF * TNF * 4 : 0;
     constexpr int EPI_STORES = TMF * TNF * (STAGED ? 2 : 4);
     int last_epi = -NS;
     bool last_full = false;
     auto step = [&](auto jc, int s) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
         // own loads of stage s landed, own LDS reads done
-        wait_stage<NS - 2, P::L, EPI_STORES>(min(NS - 2, S - 1 - s), last_full && last_epi >= s - NS + 1);
+        wait_stage<NS - 2, P::L, EPI_LOADS, EPI_LOADS + EPI_STORES>(
+            min(NS - 2, S - 1 - s), last_epi >= s - NS + 1 ? (last_full ? 2 : 1) : 0);
         lds_barrier_only();  // every wave's loads of stage s landed; stage s-1 fully read
         const int kt = s % KT;
         if (s + NS - 1 < S) issue(bufs[(j + NS - 1) % NS]);

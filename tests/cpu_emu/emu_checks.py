@@ -241,6 +241,24 @@ def group_gemm():
         ref = oracle.layernorm(res.astype(np.float32) + oracle.matmul_w8a32(a16.astype(np.float32), q, s, bias), g, b,
                                1e-12)
         assert np.abs(split - ref).max() < 2e-2
+    # several LayerNorm tiles per persistent block (32 tiles on 16 CUs): the
+    # stage ring runs across tile boundaries, where each epilogue's residual
+    # loads and stores count in the stage waits
+    for odt in (np.float16, np.float32):
+        m, k, n = 32 * 128, 64, 384
+        a, q, s, bias = problem(23, m, k, n)
+        a16 = a.astype(np.float16)
+        rng = np.random.default_rng(24)
+        res = rng.standard_normal((m, n)).astype(odt)
+        g = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        b = (0.1 * rng.standard_normal(n)).astype(np.float32)
+        two = linear(a16, q, s, bias, odt, _abi.EPI_BIAS_RES_LN, res, g, b)
+        shifted = linear(np.ascontiguousarray(a16[128:]), q, s, bias, odt, _abi.EPI_BIAS_RES_LN,
+                         np.ascontiguousarray(res[128:]), g, b)
+        assert np.array_equal(two[128:], shifted), odt
+        ref = oracle.layernorm(res.astype(np.float32) + oracle.matmul_w8a32(a16.astype(np.float32), q, s, bias), g, b,
+                               1e-12)
+        assert np.abs(two - ref).max() < 2e-2
     w = (np.random.default_rng(12).standard_normal((64, 384)) * 0.02).astype(np.float32)
     w[0] = 0
     qg = np.empty((64, 384), np.int8)

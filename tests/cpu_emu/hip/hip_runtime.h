@@ -53,7 +53,7 @@ void launch(const char *name, dim3 grid, dim3 block, void (*body)(void *), void 
 // before its wait sees stale data and fails the parity checks
 void dma16(const void *src, void *lds_dst);
 void waitcnt_vm(int n);
-void vmem_marker();  // a vector memory op with no LDS effect (a store), in issue order
+void vmem_marker();  // a vector memory op with no LDS effect (a store or a register load), in issue order
 }  // namespace emu
 
 // the hooks gemm_pipe.hip takes from its target: DMA issue and LDS barrier
@@ -63,6 +63,7 @@ inline void dma16(const char *sbase, uint32_t voff, char *lds_base) {
 }
 inline void lds_barrier_only() { emu::syncthreads(); }
 inline void vmem_store_issued() { emu::vmem_marker(); }
+inline void vmem_load_issued() { emu::vmem_marker(); }
 // v_permlane32_swap_b32: lanes 32..63 of `lo` <-> lanes 0..31 of `hi`
 inline void lane_swap32(uint32_t &lo, uint32_t &hi) {
     const int lane = emu::lane_id();
