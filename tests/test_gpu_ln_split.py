@@ -73,3 +73,43 @@ def test_small_batch_is_all_pieces(ctx):
         ref = oracle.layernorm(res.astype(np.float32) + oracle.matmul_w8a32(a.astype(np.float32), q, s, bias), g, b,
                                1e-12)
         assert np.abs(got.astype(np.float32) - ref).max() < 2e-2, m
+
+
+def test_config3_gemm_pair_f16_boundaries(ctx):
+    """BASELINE config 3 shapes (T = 65536) through the model's path: f16
+    activations between the GELU GEMM (384 -> 1536) and the residual +
+    LayerNorm GEMM (1536 -> 384), int8 weights in the tiled device format.
+    The oracle runs in f32 on the same f16 inputs, with the intermediate
+    rounded to f16 as the GPU stores it; parity on sampled rows, exact
+    LayerNorm properties on every row."""
+    T, K, N1 = 65536, 384, 1536
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((T, K)).astype(np.float16)
+    q1 = rng.integers(-127, 128, size=(N1, K)).astype(np.int8)
+    s1 = np.array([oracle.f32_to_f16(v) for v in rng.uniform(0.001, 0.02, N1).astype(np.float32)], np.uint16)
+    b1 = rng.uniform(-0.1, 0.1, N1).astype(np.float32)
+    q2 = rng.integers(-127, 128, size=(K, N1)).astype(np.int8)
+    s2 = np.array([oracle.f32_to_f16(v) for v in rng.uniform(0.001, 0.02, K).astype(np.float32)], np.uint16)
+    b2 = rng.uniform(-0.1, 0.1, K).astype(np.float32)
+    g, bt = np.ones(K, np.float32), np.zeros(K, np.float32)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    X = dev(x)
+    H = torch.empty((T, N1), dtype=torch.float16, device="cuda")
+    Y = torch.empty((T, K), dtype=torch.float16, device="cuda")
+    Q1, S1, B1, Q2, S2, B2, G, Bt = (dev(q1), dev(s1.view(np.int16)), dev(b1), dev(q2), dev(s2.view(np.int16)),
+                                     dev(b2), dev(g), dev(bt))
+    check(lib().tzh_linear_w8(ctx.handle, X.data_ptr(), _abi.F16, Q1.data_ptr(), S1.data_ptr(), B1.data_ptr(),
+                              H.data_ptr(), _abi.F16, T, K, N1, _abi.EPI_BIAS_GELU, None, _abi.F16, None, None, 0.0))
+    check(lib().tzh_linear_w8(ctx.handle, H.data_ptr(), _abi.F16, Q2.data_ptr(), S2.data_ptr(), B2.data_ptr(),
+                              Y.data_ptr(), _abi.F16, T, N1, K, _abi.EPI_BIAS_RES_LN, X.data_ptr(), _abi.F16,
+                              G.data_ptr(), Bt.data_ptr(), 1e-12))
+    y = Y.cpu().numpy().astype(np.float32)
+    assert np.abs(y.mean(axis=1)).max() < 2e-3
+    assert np.abs(y.var(axis=1) - 1).max() < 5e-3
+    rows = np.sort(rng.choice(T, 256, replace=False))
+    xf = x[rows].astype(np.float32)
+    h = oracle.gelu(oracle.matmul_w8a32(xf, q1, s1, b1)).astype(np.float16).astype(np.float32)
+    ref = oracle.layernorm(xf + oracle.matmul_w8a32(h, q2, s2, b2), g, bt, 1e-12)
+    err = np.abs(y[rows] - ref)
+    assert err.max() < 1e-2, float(err.max())
+    assert np.sqrt((err ** 2).mean()) < 1e-3
