@@ -1,6 +1,6 @@
 """Per-stage figures of the Arctic forward from rocprofv3 output.
 
-Two subcommands:
+Subcommands:
 
     python -m tenzor_amd.profile_summary run
         One forward of the bench workload (config 5) plus one elementwise
@@ -12,6 +12,15 @@ Two subcommands:
         Reads the CSV output of those runs and prints a markdown summary with
         one row per forward stage, ending in a fenced JSON block that
         bench.py reads for `roofline.traffic`.
+
+    python -m tenzor_amd.profile_summary gemm
+        The config-3 GEMM pair (T = 65536: 384 -> 1536 + GELU, then
+        1536 -> 384 + residual + LayerNorm; f16 activations, int8 weights in
+        the model's device format) three times, for `rocprofv3 --pmc` passes.
+
+    python -m tenzor_amd.profile_summary counters DIR [DIR ...]
+        Per-kernel averages of the counters in those runs' CSV output, with
+        unit busy/stall fractions (see COUNTER_NOTES).
 
 Dispatches are mapped to forward stages by kernel and launch order: both
 LayerNorm GEMMs are one kernel instantiation; the one launched after
@@ -209,17 +218,106 @@ def run() -> None:
     print("forward and calibration multiply done", flush=True)
 
 
+def gemm() -> None:
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    import tenzor_amd
+    from tenzor_amd import _abi, check, lib
+
+    ctx = tenzor_amd.Context(0)
+    T, K, N1 = 65536, 384, 1536
+    rng = np.random.default_rng(9)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    X = dev(rng.standard_normal((T, K)).astype(np.float16))
+    H = torch.empty((T, N1), dtype=torch.float16, device="cuda")
+    Y = torch.empty((T, K), dtype=torch.float16, device="cuda")
+    Q1 = dev(rng.integers(-127, 128, size=(N1, K)).astype(np.int8))
+    Q2 = dev(rng.integers(-127, 128, size=(K, N1)).astype(np.int8))
+    S1 = dev(np.full(N1, 0x211F, np.int16))  # f16 0.01
+    S2 = dev(np.full(K, 0x211F, np.int16))
+    B1, B2 = dev(np.zeros(N1, np.float32)), dev(np.zeros(K, np.float32))
+    G, Bt = dev(np.ones(K, np.float32)), dev(np.zeros(K, np.float32))
+    for _ in range(3):
+        check(lib().tzh_linear_w8(ctx.handle, X.data_ptr(), _abi.F16, Q1.data_ptr(), S1.data_ptr(), B1.data_ptr(),
+                                  H.data_ptr(), _abi.F16, T, K, N1, _abi.EPI_BIAS_GELU, None, _abi.F16, None, None,
+                                  0.0))
+        check(lib().tzh_linear_w8(ctx.handle, H.data_ptr(), _abi.F16, Q2.data_ptr(), S2.data_ptr(), B2.data_ptr(),
+                                  Y.data_ptr(), _abi.F16, T, N1, K, _abi.EPI_BIAS_RES_LN, X.data_ptr(), _abi.F16,
+                                  G.data_ptr(), Bt.data_ptr(), C.c_float(1e-12)))
+    torch.cuda.synchronize()
+    print("config-3 GEMM pair done", flush=True)
+
+
+# MI355X: 8 XCDs of 32 CUs, 4 SIMDs per CU.  GRBM_GUI_ACTIVE is summed over
+# the XCDs; TA/TD/TCP `_sum` counters over one instance per CU; the SQ
+# cycle counters over the SIMDs (MFMA busy) or the CUs (LDS active).
+COUNTER_NOTES = {
+    "TA_TA_BUSY_sum": ("TA busy", 256),
+    "TD_TD_BUSY_sum": ("TD busy", 256),
+    "TD_TC_STALL_sum": ("TD stalled by the L1 (TC)", 256),
+    "TA_ADDR_STALLED_BY_TC_CYCLES_sum": ("TA address stalled by the L1", 256),
+    "TCP_PENDING_STALL_CYCLES_sum": ("L1 waiting for L2 data", 256),
+    "SQ_VALU_MFMA_BUSY_CYCLES": ("MFMA busy (per SIMD)", 1024),
+    "SQ_LDS_IDX_ACTIVE": ("LDS active (indexed ops)", 256),
+}
+
+
+def counters(dirs: list[str]) -> str:
+    per = {}
+    for d in dirs:
+        disp = {}
+        for r in _rows(d, "counter_collection.csv"):
+            key = (r["Dispatch_Id"], r["Counter_Name"])
+            disp[key] = (r["Kernel_Name"], disp.get(key, ("", 0.0))[1] + float(r["Counter_Value"]))
+        for (did, cname), (kname, v) in disp.items():
+            k = kname.split("(")[0][:110]
+            per.setdefault(k, {}).setdefault(cname, {})[(d, did)] = v
+    out = []
+    for k, cs in per.items():
+        if not any(x in k for x in ("linear_pipe_kernel", "ln_rows_kernel")):
+            continue
+        out.append(f"### `{k}`")
+        out.append("")
+        out.append("| counter | per dispatch | fraction of GPU-active cycles |")
+        out.append("|---|---:|---:|")
+        for cname in sorted(cs):
+            vals = cs[cname]
+            avg = sum(vals.values()) / len(vals)
+            frac = ""
+            if cname in COUNTER_NOTES:
+                # GRBM_GUI_ACTIVE of the same dispatches (same pass)
+                dispatches = list(vals)
+                g = [cs.get("GRBM_GUI_ACTIVE", {}).get(dk) for dk in dispatches]
+                g = [x for x in g if x]
+                if g:
+                    label, inst = COUNTER_NOTES[cname]
+                    frac = f"{avg / inst / (sum(g) / len(g) / 8):.0%} ({label})"
+            out.append(f"| {cname} | {avg:.4g} | {frac} |")
+        out.append("")
+    return "\n".join(out) + "\n"
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
     sub.add_parser("run")
+    sub.add_parser("gemm")
     s = sub.add_parser("summarize")
     s.add_argument("--trace")
     s.add_argument("--fetch")
     s.add_argument("--write")
+    c = sub.add_parser("counters")
+    c.add_argument("dirs", nargs="+")
     a = ap.parse_args(argv)
     if a.cmd == "run":
         run()
+    elif a.cmd == "gemm":
+        gemm()
+    elif a.cmd == "counters":
+        sys.stdout.write(counters(a.dirs))
     else:
         sys.stdout.write(summarize(a.trace, a.fetch, a.write))
     return 0
