@@ -636,14 +636,24 @@ struct Cfgs<TZH_WF_W8T> {
     using Bias = PipeCfg<128, 384, 64, 2, 4, 3, true, kWtBlock>;
     using Narrow = Bias;  // n is always a multiple of 384
     using Ln = Bias;
+    // short-k LayerNorm GEMMs (k <= 384): 64-row tiles of 4 waves, two
+    // workgroups per CU.  One workgroup's epilogue then overlaps the other's
+    // main loop, and a CU whose second workgroup has run out of tiles runs
+    // the last one alone at full speed, so a partial last round costs
+    // little.  Measured against Ln with the split last round: O-proj + LN
+    // 0.67-0.98 of the time at T = 4096 .. 100000 (55 -> 43 us at the
+    // headline's 67590); with k = 1536 it is slower at some sizes.
+    using LnShortK = PipeCfg<64, 384, 64, 1, 4, 2, true, kWtBlock>;
     using Piece64 = PipeCfg<64, 64, 64, 2, 2, 4, true, kWtBlock>;
     using Piece128x64 = PipeCfg<128, 64, 64, 2, 2, 4, true, kWtBlock>;
     using Piece128 = PipeCfg<128, 128, 64, 2, 2, 4, true, kWtBlock>;
 };
 using LnCfg = Cfgs<TZH_WF_F16>::Ln;
 static_assert(Cfgs<TZH_WF_W8T>::Ln::WN == LnCfg::WN && Cfgs<TZH_WF_W8T>::Ln::TNF == LnCfg::TNF &&
-                  Cfgs<TZH_WF_W8T>::Ln::BN == LnCfg::BN,
-              "ln_rows_kernel follows one LayerNorm epilogue layout for both weight formats");
+                  Cfgs<TZH_WF_W8T>::Ln::BN == LnCfg::BN && Cfgs<TZH_WF_W8T>::LnShortK::WN == LnCfg::WN &&
+                  Cfgs<TZH_WF_W8T>::LnShortK::TNF == LnCfg::TNF,
+              "one LayerNorm epilogue layout (statistics order) for every configuration and ln_rows_kernel");
+static_assert(Cfgs<TZH_WF_W8T>::LnShortK::blocks_per_cu(true) == 2, "two short-k LayerNorm workgroups per CU");
 
 template <typename T>
 struct NoDeduce {
@@ -734,7 +744,9 @@ __global__ void __launch_bounds__(256) ln_rows_kernel(const float *__restrict__ 
         }
 }
 
-// bias + residual + LayerNorm over 384-wide rows.  The 128-row tiles run in
+// bias + residual + LayerNorm over 384-wide rows.  Tiled int8 weights with
+// k <= 384 use the short-k configuration (two workgroups per CU, above).
+// Otherwise the 128-row tiles run in
 // whole rounds of one tile per CU slot; when the rows left over for a
 // partial last round would keep only a few CUs busy (at most slots / 3
 // tiles), those tiles are instead cut into 64 x 64, 128 x 64 or 128 x 128
@@ -749,6 +761,10 @@ int launch_ln(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, co
               float *ws, int64_t ws_rows) {
     using C = Cfgs<WF>;
     constexpr int N = C::Ln::BN, BM = C::Ln::BM;
+    if constexpr (WF == TZH_WF_W8T)
+        if (K <= 384)
+            return launch<EPI_LN, TC, typename C::LnShortK>(st, num_cus, x, wc, scale, bias, c, M, K, N, res, gamma,
+                                                            beta, eps);
     const int slots = num_cus * C::Ln::blocks_per_cu(true);
     const int panels = (M + BM - 1) / BM;
     const int full = panels / slots * slots;

@@ -224,9 +224,10 @@ def group_gemm():
     # LayerNorm tiles past the last whole round are split into pieces and
     # normalised by a separate kernel: those rows must match, bit for bit,
     # the same rows computed inside whole tiles (the emulated device has 16
-    # CUs: 17 tiles = 16 whole + 1 split into 64 x 64 pieces)
+    # CUs: 17 tiles = 16 whole + 1 split into 64 x 64 pieces; k > 384, since
+    # tiled int8 weights with k <= 384 use two workgroups per CU unsplit)
     for odt in (np.float16, np.float32):
-        m, k, n = 16 * 128 + 100, 128, 384
+        m, k, n = 16 * 128 + 100, 448, 384
         a, q, s, bias = problem(21, m, k, n)
         a16 = a.astype(np.float16)
         rng = np.random.default_rng(22)

@@ -44,9 +44,10 @@ def ln_gemm(ctx, a, q, s, bias, res, g, b):
 
 
 # extra tiles past the whole rounds -> pieces per tile: 2 -> 12 (64 x 64),
-# 30 -> 6 (128 x 64), 60 -> 3 (128 x 128), 100 -> no split; partial tiles too
-@pytest.mark.parametrize("extra_rows,k", [(2 * 128 - 28, 384), (30 * 128, 1536), (60 * 128 - 5, 384),
-                                          (100 * 128, 384), (1, 1536)])
+# 30 -> 6 (128 x 64), 60 -> 3 (128 x 128), 100 -> no split; partial tiles
+# too.  k = 384 takes the unsplit two-workgroups-per-CU configuration.
+@pytest.mark.parametrize("extra_rows,k", [(2 * 128 - 28, 448), (30 * 128, 1536), (60 * 128 - 5, 448),
+                                          (100 * 128, 448), (1, 1536), (2 * 128 - 28, 384)])
 def test_split_rows_match_whole_tiles(ctx, extra_rows, k):
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     whole_rows = cus * 128
@@ -66,9 +67,10 @@ def test_split_rows_match_whole_tiles(ctx, extra_rows, k):
 
 
 def test_small_batch_is_all_pieces(ctx):
-    """Fewer tiles than CUs (config-1-like sizes): every tile is split."""
-    for m in (1, 7, 128, 1000):
-        a, q, s, bias, res, g, b = problem(m, m, 384)
+    """Fewer tiles than CUs (config-1-like sizes): every tile is split
+    (k = 448), or the short-k configuration runs them (k = 384)."""
+    for m, k in ((1, 448), (7, 448), (128, 384), (1000, 448), (1000, 384)):
+        a, q, s, bias, res, g, b = problem(m, m, k)
         got = ln_gemm(ctx, a, q, s, bias, res, g, b)
         ref = oracle.layernorm(res.astype(np.float32) + oracle.matmul_w8a32(a.astype(np.float32), q, s, bias), g, b,
                                1e-12)
