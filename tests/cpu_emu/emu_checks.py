@@ -221,13 +221,29 @@ def group_gemm():
             tol = 2e-3 * max(1.0, float(np.abs(ref).max()))
         err = float(np.abs(c - ref).max())
         assert err < tol, (m, k, n, epi, err)
+    w = (np.random.default_rng(12).standard_normal((64, 384)) * 0.02).astype(np.float32)
+    w[0] = 0
+    qg = np.empty((64, 384), np.int8)
+    sg = np.empty(64, np.uint16)
+    check(L.tzh_quantize_rows(CTX, w.ctypes.data, 64, 384, qg.ctypes.data, sg.ctypes.data))
+    qo, so = oracle.quantize_rows(w)
+    assert np.array_equal(qg, qo) and np.array_equal(sg, so)
+    x = np.random.default_rng(13).standard_normal((9, 384)).astype(np.float32)
+    gg = np.ones(384, np.float32)
+    bt = np.zeros(384, np.float32)
+    y = x.copy()
+    check(L.tzh_layernorm_last_dim(CTX, y.ctypes.data, gg.ctypes.data, bt.ctypes.data, y.ctypes.data, 9, 384, 1e-12))
+    assert np.allclose(y, oracle.layernorm(x, gg, bt, 1e-12), atol=1e-4)
+
+
+def group_gemm_ln():
     # LayerNorm tiles past the last whole round are split into pieces and
     # normalised by a separate kernel: those rows must match, bit for bit,
     # the same rows computed inside whole tiles (the emulated device has 16
     # CUs: 17 tiles = 16 whole + 1 split into 64 x 64 pieces; k > 384, since
     # tiled int8 weights with k <= 384 use two workgroups per CU unsplit)
-    for odt in (np.float16, np.float32):
-        m, k, n = 16 * 128 + 100, 448, 384
+    for odt, k in ((np.float16, 448), (np.float32, 128)):  # f32 output: f16 codes, which split at any k
+        m, n = 16 * 128 + 100, 384
         a, q, s, bias = problem(21, m, k, n)
         a16 = a.astype(np.float16)
         rng = np.random.default_rng(22)
@@ -260,19 +276,6 @@ def group_gemm():
         ref = oracle.layernorm(res.astype(np.float32) + oracle.matmul_w8a32(a16.astype(np.float32), q, s, bias), g, b,
                                1e-12)
         assert np.abs(two - ref).max() < 2e-2
-    w = (np.random.default_rng(12).standard_normal((64, 384)) * 0.02).astype(np.float32)
-    w[0] = 0
-    qg = np.empty((64, 384), np.int8)
-    sg = np.empty(64, np.uint16)
-    check(L.tzh_quantize_rows(CTX, w.ctypes.data, 64, 384, qg.ctypes.data, sg.ctypes.data))
-    qo, so = oracle.quantize_rows(w)
-    assert np.array_equal(qg, qo) and np.array_equal(sg, so)
-    x = np.random.default_rng(13).standard_normal((9, 384)).astype(np.float32)
-    gg = np.ones(384, np.float32)
-    bt = np.zeros(384, np.float32)
-    y = x.copy()
-    check(L.tzh_layernorm_last_dim(CTX, y.ctypes.data, gg.ctypes.data, bt.ctypes.data, y.ctypes.data, 9, 384, 1e-12))
-    assert np.allclose(y, oracle.layernorm(x, gg, bt, 1e-12), atol=1e-4)
 
 
 def group_attention():
@@ -333,7 +336,8 @@ def group_arctic():
     check(L.tzh_arctic_free(m))
 
 
-GROUPS = {"eval": group_eval, "gemm": group_gemm, "attention": group_attention, "arctic": group_arctic}
+GROUPS = {"eval": group_eval, "gemm": group_gemm, "gemm_ln": group_gemm_ln, "attention": group_attention,
+          "arctic": group_arctic}
 
 if __name__ == "__main__":
     check(L.tzh_init(0, None, C.byref(CTX)))

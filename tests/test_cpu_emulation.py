@@ -34,12 +34,28 @@ def emu_env():
     return env
 
 
-@pytest.mark.parametrize("group", ["eval", "attention", "gemm"])
-def test_kernels_under_emulation(emu_env, group):
-    res = subprocess.run(["python", os.path.join(EMU, "emu_checks.py"), group], capture_output=True, text=True,
-                         env=emu_env, timeout=900, cwd=ROOT)
-    assert res.returncode == 0, (res.stdout + res.stderr)[-4000:]
-    assert "EMU CHECKS PASSED" in res.stdout
+GROUPS = ["eval", "attention", "gemm", "gemm_ln"]
+
+
+@pytest.fixture(scope="module")
+def emu_runs(emu_env):
+    """All groups started at once (each is single-threaded), so the module
+    takes as long as the slowest group."""
+    procs = {g: subprocess.Popen(["python", os.path.join(EMU, "emu_checks.py"), g], stdout=subprocess.PIPE,
+                                 stderr=subprocess.STDOUT, text=True, env=emu_env, cwd=ROOT)
+             for g in GROUPS}
+    yield procs
+    for p in procs.values():
+        if p.poll() is None:
+            p.kill()
+            p.wait()
+
+
+@pytest.mark.parametrize("group", GROUPS)
+def test_kernels_under_emulation(emu_runs, group):
+    out, _ = emu_runs[group].communicate(timeout=1200)
+    assert emu_runs[group].returncode == 0, out[-4000:]
+    assert "EMU CHECKS PASSED" in out
 
 
 def test_cpp_host_api_under_emulation(emu_env, tmp_path):
