@@ -2,6 +2,7 @@
 (lengths U[16,512], padded with id 0), CLS pooling + L2, on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
+    python bench.py --workload embed-docs    # the embed command's document path
 
 Prints one JSON line.  A step is one forward of the whole batch with the
 padded token ids already resident in HBM; `value` counts real (unpadded)
@@ -34,8 +35,7 @@ TRAFFIC_PROFILE = "arctic_b256_stage_profile.md"
 KERNELS = {
     "qkv": "linear_pipe_kernel bias, 384 -> 1152",
     "attention": "attn_varlen_kernel",
-    "attn_out_ln": "linear_pipe_kernel bias+residual+LayerNorm, 384 -> 384, + split last round "
-                   "(linear_pipe_kernel residual pieces, ln_rows_kernel)",
+    "attn_out_ln": "linear_pipe_kernel bias+residual+LayerNorm, 384 -> 384, 64-row tiles, two workgroups per CU",
     "ffn1_gelu": "linear_pipe_kernel bias+GELU, 384 -> 1536",
     "ffn2_ln": "linear_pipe_kernel bias+residual+LayerNorm, 1536 -> 384, + split last round "
                "(linear_pipe_kernel residual pieces, ln_rows_kernel)",
@@ -76,6 +76,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-stride", type=int, default=1, help="every k-th sequence of the batch")
+    ap.add_argument("--workload", choices=["forward", "embed-docs"], default="forward")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the forward is data-parallel over "
@@ -89,6 +90,8 @@ def main():
     from tenzor_amd.arctic import ModelWeights, forwardBatch
 
     assert torch.cuda.is_available(), "bench.py needs the GPU"
+    if args.workload == "embed-docs":
+        return embed_docs(args)
     cfg = synth.Config()
     weights = synth.quantize(synth.make_arctic_f32(SEED_WEIGHTS, cfg))  # N(0,0.02), gamma 1, beta 0
     ctx = tenzor_amd.Context(0)
@@ -214,6 +217,126 @@ def main():
                       f"{dt:.1f} s",
         }
     print(json.dumps(line), flush=True)
+    model.deinit()
+
+
+DOCS = 256
+
+
+def embed_docs(args):
+    """The embed command's document path (main.zig:786-933) over DOCS
+    synthetic documents per step: host tokenization, chunking, one batched
+    forward over every chunk, chunk mean + L2.  A step starts from host
+    text and ends with the embeddings in HBM; `value` counts pieces
+    (tokens before chunking).  Piece counts ~ U[16, 4000], avoiding 511..920
+    (one over-long chunk in the reference, an error here)."""
+    import torch
+
+    import tenzor_amd
+    from tenzor_amd import synth
+    from tenzor_amd.arctic import ModelWeights, embedDocuments, forwardBatch
+    from tenzor_amd.tokenizer import Tokenizer
+
+    cfg = synth.Config()
+    weights = synth.quantize(synth.make_arctic_f32(SEED_WEIGHTS, cfg))
+    ctx = tenzor_amd.Context(0)
+    model = ModelWeights.fromHost(ctx, weights, cfg)
+    vocab_bytes, words = synth.make_vocab(SEED_BATCH)
+    tok = Tokenizer.init()
+    tok.loadVocabFromBytes(vocab_bytes)
+    rng = np.random.default_rng(SEED_BATCH)
+    sizes = rng.integers(16, 4001, size=DOCS)
+    sizes = np.where((sizes > 510) & (sizes < 921), sizes + 410, sizes)
+    docs = [synth.make_text(int(1000 + i), words, int(n), plain=True) for i, n in enumerate(sizes)]
+    out = torch.empty((DOCS, cfg.hidden_size), device="cuda")
+    for _ in range(args.warmup):
+        counts = embedDocuments(out, docs, tok, model)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        embedDocuments(out, docs, tok, model)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    assert torch.isfinite(out).all()
+    pieces = int(sizes.sum())
+
+    # the same chunks through the forward alone, ids already in HBM
+    from tenzor_amd.tokenizer import chunk_count
+
+    chunk_ids, chunk_lens = [], []
+    for d in docs:
+        p = tok.encodeRaw(d)
+        for k in range(chunk_count(len(p))):
+            c = np.concatenate([[101], p[460 * k:min(460 * k + 510, len(p))], [102]]).astype(np.uint32)
+            chunk_ids.append(c)
+            chunk_lens.append(len(c))
+    flat = torch.from_numpy(np.concatenate(chunk_ids).view(np.int32)).cuda()
+    cout = torch.empty((len(chunk_lens), cfg.hidden_size), device="cuda")
+    forwardBatch(cout, flat, chunk_lens, model)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        forwardBatch(cout, flat, chunk_lens, model)
+    e.record()
+    torch.cuda.synchronize()
+    fwd_ms = s.elapsed_time(e) / args.steps
+
+    line = {
+        "metric": "documents/sec, embed document path (tokenize, 510/50 chunks, int8 arctic-embed-xs, mean + L2), 1 GPU",
+        "value": round(DOCS * args.steps / elapsed, 1),
+        "unit": "documents/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{DOCS} synthetic documents of U[16,4000] pieces (511..920 moved up by 410), "
+                        "synthetic 30522-line vocabulary",
+            "pieces_per_step": pieces,
+            "chunks_per_step": int(counts.sum()),
+            "chunk_tokens_per_step": int(sum(chunk_lens)),
+            "parallelism": "single GPU",
+        },
+        "pieces_per_s": round(pieces * args.steps / elapsed, 1),
+        "forward_only_ms": round(fwd_ms, 4),
+        "host_and_pooling_share": round(1 - fwd_ms / (elapsed / args.steps * 1e3), 4),
+    }
+    if not args.no_cpu_baseline:
+        import oracle
+        from oracle import wordpiece as wp
+
+        threads = min(16, os.cpu_count() or 1)
+        hw = synth.HostWeights(weights, cfg)
+        sample = list(range(0, DOCS, 32))
+        starts = np.concatenate([[0], np.cumsum(counts)])
+        sel = [j for d in sample for j in range(int(starts[d]), int(starts[d + 1]))]
+        flat_s = np.concatenate([chunk_ids[j] for j in sel]).astype(np.uint32)
+        lens_s = np.array([chunk_lens[j] for j in sel], np.int32)
+        offs = np.concatenate([[0], np.cumsum(lens_s)[:-1]]).astype(np.int64)
+        t0 = time.perf_counter()
+        emb = oracle.arctic_forward_batch(hw, flat_s, offs, lens_s, nthreads=threads)
+        k = 0
+        for d in sample:
+            n = int(counts[d])
+            wp.chunk_mean_l2(emb[k:k + n])
+            k += n
+        dt = time.perf_counter() - t0
+        line["cpu_baseline"] = {
+            "value": round(len(sample) / dt, 2),
+            "unit": "documents/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": f"{len(sample)} of the {DOCS} documents ({len(sel)} chunks), C restatement of the forward "
+                      f"+ the pooling; tokenization not timed; {dt:.1f} s",
+        }
+    print(json.dumps(line), flush=True)
+    tok.deinit()
     model.deinit()
 
 

@@ -321,6 +321,72 @@ int tzh_arctic_set_timing(tzh_model *model, int32_t enable);
  * not timed).  Waits for that forward to finish.  Either array may be NULL. */
 int tzh_arctic_launch_times(tzh_model *model, float *us, const char **names, int32_t capacity, int32_t *count);
 
+/* ------------------------------------------------------------------ */
+/* WordPiece tokenizer and the embed command's text paths              */
+/* ------------------------------------------------------------------ */
+
+/* io/tokenizer.Tokenizer (tokenizer.zig:9-15): vocabulary map, [UNK] 100,
+ * [CLS] 101, [SEP] 102, words over 200 bytes give [UNK].  Host object;
+ * encoding is read-only, so one tokenizer may serve several threads. */
+typedef struct tzh_tokenizer tzh_tokenizer;
+
+/* Tokenizer.init / deinit (tokenizer.zig:17-31); the vocabulary starts empty. */
+int tzh_tokenizer_create(tzh_tokenizer **out);
+int tzh_tokenizer_free(tzh_tokenizer *tok);
+
+/* Tokenizer.loadVocab / loadVocabFromBytes (tokenizer.zig:34-74): one token
+ * per line, its id the line index (empty lines count, a trailing '\r' is
+ * stripped, a repeated token takes the later index).  TZH_ERR_IO when the
+ * file cannot be read. */
+int tzh_tokenizer_load_vocab(tzh_tokenizer *tok, const char *path);
+int tzh_tokenizer_load_vocab_bytes(tzh_tokenizer *tok, const char *data, int64_t len);
+
+/* vocab.put(token, id), as the reference's tokenizer tests build their
+ * vocabularies (tokenizer.zig:291-437). */
+int tzh_tokenizer_put(tzh_tokenizer *tok, const char *token, int64_t len, uint32_t id);
+
+/* Tokenizer.encode (tokenizer.zig:78-118): [CLS] pieces [SEP] into
+ * out[0, capacity) (host), capacity >= 2 (else TZH_ERR_INVALID_ARGS, the
+ * reference's assert); pieces stop at capacity - 1, inside a word too.
+ * *n = number of ids written. */
+int tzh_tokenizer_encode(const tzh_tokenizer *tok, const char *text, int64_t len, uint32_t *out,
+                         int64_t capacity, int64_t *n);
+
+/* Tokenizer.encodeRaw (tokenizer.zig:122-151): the pieces of the whole
+ * text, no markers.  *n = number of pieces; TZH_ERR_TOO_LARGE (nothing
+ * written) when that exceeds capacity, so out = NULL, capacity = 0 asks
+ * for the size. */
+int tzh_tokenizer_encode_raw(const tzh_tokenizer *tok, const char *text, int64_t len, uint32_t *out,
+                             int64_t capacity, int64_t *n);
+
+/* Number of chunks runEmbed cuts a document of total_tokens pieces into
+ * (main.zig:803-806): 510-piece chunks every 460 pieces,
+ * 1 + (total - 461) / 460 of them above 510 pieces.  A tail of up to 410
+ * pieces past the last chunk is not embedded, as in the reference. */
+int tzh_embed_chunk_count(int64_t total_tokens, int64_t *count);
+
+/* runEmbed's document path (main.zig:786-933) for n_docs documents at
+ * once: each text (host bytes texts[d], lens[d]) is encodeRaw'd, cut into
+ * chunks [CLS] + pieces[460k, min(460k + 510, total)) + [SEP], and all
+ * chunks of all documents go through one batched forward; each document's
+ * chunk embeddings are then averaged (in chunk order, times 1/chunks) and
+ * L2-normalised (sequential sum of squares, divided by the norm when it is
+ * positive).  outputs: device f32 [n_docs, hidden].  chunk_counts (host,
+ * may be NULL) receives each document's chunk count.  A document of
+ * 511..920 pieces is TZH_ERR_TOO_LARGE: the reference copies such a
+ * document into one 512-id chunk buffer (main.zig:903-906), past its end.
+ * Returns once the ids are on the device; the forward and the pooling run
+ * on the model's stream. */
+int tzh_arctic_embed_documents(tzh_model *model, const tzh_tokenizer *tok, const char *const *texts,
+                               const int64_t *lens, int32_t n_docs, float *outputs, int32_t *chunk_counts);
+
+/* runEmbed's positional-text path (main.zig:935-1019): each text is
+ * encode'd into 512 ids ([CLS] ... [SEP], cut at 511) and the texts go
+ * through one batched forward.  outputs: device f32 [n_texts, hidden];
+ * n_tokens (host, may be NULL) receives each text's id count. */
+int tzh_arctic_embed_texts(tzh_model *model, const tzh_tokenizer *tok, const char *const *texts,
+                           const int64_t *lens, int32_t n_texts, float *outputs, int32_t *n_tokens);
+
 #ifdef __cplusplus
 }
 #endif

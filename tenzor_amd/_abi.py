@@ -141,6 +141,16 @@ PROTOTYPES = {
     "tzh_arctic_last_launch_count": (C.c_int, [vp]),
     "tzh_arctic_set_timing": (C.c_int, [vp, i32]),
     "tzh_arctic_launch_times": (C.c_int, [vp, C.POINTER(f32), C.POINTER(C.c_char_p), i32, C.POINTER(i32)]),
+    "tzh_tokenizer_create": (C.c_int, [pp]),
+    "tzh_tokenizer_free": (C.c_int, [vp]),
+    "tzh_tokenizer_load_vocab": (C.c_int, [vp, C.c_char_p]),
+    "tzh_tokenizer_load_vocab_bytes": (C.c_int, [vp, C.c_char_p, i64]),
+    "tzh_tokenizer_put": (C.c_int, [vp, C.c_char_p, i64, C.c_uint32]),
+    "tzh_tokenizer_encode": (C.c_int, [vp, C.c_char_p, i64, vp, i64, C.POINTER(i64)]),
+    "tzh_tokenizer_encode_raw": (C.c_int, [vp, C.c_char_p, i64, vp, i64, C.POINTER(i64)]),
+    "tzh_embed_chunk_count": (C.c_int, [i64, C.POINTER(i64)]),
+    "tzh_arctic_embed_documents": (C.c_int, [vp, vp, C.POINTER(C.c_char_p), C.POINTER(i64), i32, vp, C.POINTER(i32)]),
+    "tzh_arctic_embed_texts": (C.c_int, [vp, vp, C.POINTER(C.c_char_p), C.POINTER(i64), i32, vp, C.POINTER(i32)]),
 }
 
 

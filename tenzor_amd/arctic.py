@@ -94,3 +94,37 @@ def forwardBatch(outputs, ids, lengths, weights: ModelWeights, ctx: Context | No
     stride = int(ids.shape[1]) if ids.dim() == 2 else 0
     check(lib().tzh_arctic_forward_batch(weights.handle, C.c_void_p(outputs.data_ptr()), C.c_void_p(ids.data_ptr()),
                                          lengths.ctypes.data, batch, stride))
+
+
+def embedDocuments(outputs, texts, tokenizer, weights: ModelWeights) -> np.ndarray:
+    """runEmbed's document path (main.zig:786-933) for several documents at
+    once: chunks of 510 pieces every 460, one batched forward over all
+    chunks, mean of each document's chunk embeddings, L2.  outputs: device
+    f32 [len(texts), hidden].  Returns each document's chunk count."""
+    from .tokenizer import _text_array
+
+    keep, arr, lens = _text_array(texts)
+    n = len(keep)
+    if outputs.numel() != n * weights.config.hidden_size:
+        raise ValueError("outputs must hold len(texts) * hidden_size floats")
+    counts = np.zeros(max(n, 1), np.int32)
+    check(lib().tzh_arctic_embed_documents(weights.handle, tokenizer.handle, arr, lens.ctypes.data_as(C.POINTER(C.c_int64)),
+                                           n, C.c_void_p(outputs.data_ptr()),
+                                           counts.ctypes.data_as(C.POINTER(C.c_int32))))
+    return counts[:n]
+
+
+def embedTexts(outputs, texts, tokenizer, weights: ModelWeights) -> np.ndarray:
+    """runEmbed's positional-text path (main.zig:935-1019): each text
+    encoded into at most 512 ids, one batched forward.  outputs: device f32
+    [len(texts), hidden].  Returns each text's id count."""
+    from .tokenizer import _text_array
+
+    keep, arr, lens = _text_array(texts)
+    n = len(keep)
+    if outputs.numel() != n * weights.config.hidden_size:
+        raise ValueError("outputs must hold len(texts) * hidden_size floats")
+    counts = np.zeros(max(n, 1), np.int32)
+    check(lib().tzh_arctic_embed_texts(weights.handle, tokenizer.handle, arr, lens.ctypes.data_as(C.POINTER(C.c_int64)),
+                                       n, C.c_void_p(outputs.data_ptr()), counts.ctypes.data_as(C.POINTER(C.c_int32))))
+    return counts[:n]

@@ -18,7 +18,8 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libtenzor_hip.so"
-SOURCES = ["runtime.cpp", "safetensors.cpp", "ew.hip", "gemm.hip", "gemm_pipe.hip", "ew_jit.cpp", "attention.hip", "arctic.hip"]
+SOURCES = ["runtime.cpp", "safetensors.cpp", "ew.hip", "gemm.hip", "gemm_pipe.hip", "ew_jit.cpp", "attention.hip", "arctic.hip",
+           "tokenizer.cpp", "embed.hip"]
 
 # -ffp-contract=off: every multiply and add rounds separately unless a kernel
 # asks for an FMA explicitly (bit-exact elementwise chains).

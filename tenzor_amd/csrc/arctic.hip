@@ -739,6 +739,9 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
 
 }  // namespace
 
+tzh_ctx *tzh_model_ctx(const tzh_model *m) { return m->ctx; }
+int tzh_model_hidden(const tzh_model *m) { return m->cfg.hidden_size; }
+
 extern "C" int tzh_arctic_forward_batch(tzh_model *m, float *outputs, const uint32_t *ids, const int32_t *lengths,
                                         int32_t batch, int64_t ids_stride) {
     if (!outputs && batch > 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "null outputs");

@@ -8,6 +8,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "../../include/tenzor_hip.h"
 
@@ -78,6 +79,14 @@ int tzh_ctx_scratch(tzh_ctx *ctx, size_t bytes, void **out);
 // context's stream.
 int tzh_ctx_upload_program(tzh_ctx *ctx, const void *src, size_t bytes, const void **dev_out);
 
+// Host tokenizer (tokenizer.cpp) for the embedding entry points.
+size_t tzh_tokenize(const tzh_tokenizer *tok, const uint8_t *text, size_t len, uint32_t *out, size_t cap);
+void tzh_tokenize_raw(const tzh_tokenizer *tok, const uint8_t *text, size_t len, std::vector<uint32_t> &out);
+uint32_t tzh_tokenizer_cls(const tzh_tokenizer *tok);
+uint32_t tzh_tokenizer_sep(const tzh_tokenizer *tok);
+// The context and hidden size a model was uploaded with (arctic.hip).
+tzh_ctx *tzh_model_ctx(const tzh_model *m);
+int tzh_model_hidden(const tzh_model *m);
 // ---------------------------------------------------------------------------
 // Device helpers
 // ---------------------------------------------------------------------------

@@ -183,3 +183,51 @@ def packed(ids: np.ndarray, lengths: np.ndarray):
     offs[1:] = np.cumsum(lengths[:-1])
     flat = np.concatenate([ids[b, : int(lengths[b])] for b in range(len(lengths))]).astype(np.uint32)
     return flat, offs
+
+
+def make_vocab(seed: int, size: int = 30522) -> tuple[bytes, list]:
+    """A BERT-shaped vocab.txt of `size` lines (no real vocabulary is
+    available offline): [PAD], [unused*] up to id 99, [UNK] 100, [CLS] 101,
+    [SEP] 102, [MASK] 103, the ASCII punctuation, single letters and digits
+    with their "##" forms, then random lowercase words and "##" suffixes.
+    Returns (file bytes, the whole words of the vocabulary)."""
+    rng = np.random.default_rng(seed)
+    lines = ["[PAD]"] + [f"[unused{i}]" for i in range(99)] + ["[UNK]", "[CLS]", "[SEP]", "[MASK]"]
+    lines += list("!\"#$%&'()*+,-./:;<=>?@[\\]^_`{|}~")
+    chars = "abcdefghijklmnopqrstuvwxyz0123456789"
+    lines += list(chars) + ["##" + c for c in chars]
+    seen, words = set(lines), []
+    letters = np.array(list("abcdefghijklmnopqrstuvwxyz"))
+    while len(lines) < size:
+        w = "".join(rng.choice(letters, size=int(rng.integers(2, 9))))
+        tok = ("##" + w) if rng.random() < 0.3 else w
+        if tok in seen:
+            continue
+        seen.add(tok)
+        lines.append(tok)
+        if not tok.startswith("##"):
+            words.append(tok)
+    return ("\n".join(lines[:size]) + "\n").encode(), words
+
+
+def make_text(seed: int, words: list, n_words: int, plain: bool = False) -> bytes:
+    """Synthetic text of n_words words drawn from `words`.  plain: single
+    spaces only, so every word is exactly one piece; otherwise mixed case,
+    punctuation, tabs/newlines, out-of-vocabulary and run-together words."""
+    rng = np.random.default_rng(seed)
+    picks = [words[int(i)] for i in rng.integers(0, len(words), size=n_words)]
+    if plain:
+        return " ".join(picks).encode()
+    out = []
+    for w in picks:
+        r = rng.random()
+        if r < 0.1:
+            w = w.upper()
+        elif r < 0.15:
+            w = w + words[int(rng.integers(0, len(words)))]
+        elif r < 0.2:
+            w = w + "qzx"
+        out.append(w)
+        r = rng.random()
+        out.append(", " if r < 0.1 else ". " if r < 0.15 else "\t" if r < 0.17 else "\n" if r < 0.19 else " ")
+    return "".join(out).encode()

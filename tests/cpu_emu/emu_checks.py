@@ -336,8 +336,50 @@ def group_arctic():
     check(L.tzh_arctic_free(m))
 
 
+def group_embed():
+    # tokenizer -> chunks of every document -> one batched forward -> the
+    # chunk pooling kernel, against the same forward on the oracle's chunks
+    # and the oracle's pooling (one layer keeps the emulated forward short)
+    from oracle import wordpiece as wp
+
+    cfg = synth.Config(num_hidden_layers=1)
+    hw = synth.HostWeights(synth.quantize(synth.make_arctic_f32(77, cfg)), cfg)
+    m = C.c_void_p()
+    check(L.tzh_arctic_upload(CTX, C.byref(hw.struct), C.byref(m)))
+    data, words = synth.make_vocab(5)
+    vocab = wp.load_vocab_bytes(data)
+    tok = C.c_void_p()
+    check(L.tzh_tokenizer_create(C.byref(tok)))
+    check(L.tzh_tokenizer_load_vocab_bytes(tok, data, len(data)))
+    docs = [synth.make_text(6, words, 925, plain=True), synth.make_text(7, words, 30), b""]
+    arr = (C.c_char_p * 3)(*docs)
+    lens = np.array([len(d) for d in docs], np.int64)
+    out = np.empty((3, 384), np.float32)
+    counts = np.zeros(3, np.int32)
+    check(L.tzh_arctic_embed_documents(m, tok, arr, lens.ctypes.data_as(C.POINTER(C.c_int64)), 3, out.ctypes.data,
+                                       counts.ctypes.data_as(C.POINTER(C.c_int32))))
+    chunks = [wp.chunks(wp.encode_raw(vocab, d)) for d in docs]
+    assert counts.tolist() == [len(c) for c in chunks] == [2, 1, 1], counts
+    flat = np.array([i for c in chunks for ch in c for i in ch], np.uint32)
+    clen = np.array([len(ch) for c in chunks for ch in c], np.int32)
+    emb = np.empty((len(clen), 384), np.float32)
+    check(L.tzh_arctic_forward_batch(m, emb.ctypes.data, flat.ctypes.data, clen.ctypes.data, len(clen), 0))
+    ref = np.stack([wp.chunk_mean_l2(emb[0:2]), wp.chunk_mean_l2(emb[2:3]), wp.chunk_mean_l2(emb[3:4])])
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    ntok = np.zeros(3, np.int32)
+    check(L.tzh_arctic_embed_texts(m, tok, arr, lens.ctypes.data_as(C.POINTER(C.c_int64)), 3, out.ctypes.data,
+                                   ntok.ctypes.data_as(C.POINTER(C.c_int32))))
+    enc = [wp.encode(vocab, d, 512) for d in docs]
+    assert ntok.tolist() == [len(e) for e in enc] and ntok[0] == 512
+    flat = np.array([i for e in enc for i in e], np.uint32)
+    check(L.tzh_arctic_forward_batch(m, emb.ctypes.data, flat.ctypes.data, ntok.ctypes.data, 3, 0))
+    assert np.array_equal(out, emb[:3])
+    check(L.tzh_tokenizer_free(tok))
+    check(L.tzh_arctic_free(m))
+
+
 GROUPS = {"eval": group_eval, "gemm": group_gemm, "gemm_ln": group_gemm_ln, "attention": group_attention,
-          "arctic": group_arctic}
+          "arctic": group_arctic, "embed": group_embed}
 
 if __name__ == "__main__":
     check(L.tzh_init(0, None, C.byref(CTX)))
