@@ -11,6 +11,8 @@
 //
 //   auto w = tenzor::arctic::ModelWeights::fromSafeTensors(ctx, "model.safetensors");  // arctic.zig:113
 //   tenzor::arctic::forwardBatch(outputs, ids, lengths, stride, w);                    // arctic.zig:902-1013
+//   tenzor::io::Tokenizer tok; tok.loadVocab("vocab.txt");                             // tokenizer.zig:17-51
+//   tenzor::arctic::embedDocuments(outputs, docs, tok.handle(), w);                    // main.zig:786-933
 //
 // Shapes are template parameters, as comptime shapes are in Zig: element
 // types and broadcast compatibility are checked at compile time
@@ -498,5 +500,63 @@ inline void forwardBatch(float *outputs, const uint32_t *ids, const std::vector<
     check(tzh_arctic_forward_batch(weights.handle(), outputs, ids, lengths.data(), (int32_t)lengths.size(), stride));
 }
 
+// The embed command's document path (main.zig:786-933) for several
+// documents: outputs device f32 [texts.size(), hidden]; returns each
+// document's chunk count.
+inline std::vector<int32_t> embedDocuments(float *outputs, const std::vector<std::string> &texts,
+                                           const tzh_tokenizer *tok, const ModelWeights &weights) {
+    std::vector<const char *> ptrs;
+    std::vector<int64_t> lens;
+    for (const auto &t : texts) {
+        ptrs.push_back(t.data());
+        lens.push_back((int64_t)t.size());
+    }
+    std::vector<int32_t> counts(texts.size());
+    check(tzh_arctic_embed_documents(weights.handle(), tok, ptrs.data(), lens.data(), (int32_t)texts.size(), outputs,
+                                     counts.data()));
+    return counts;
+}
+
 }  // namespace arctic
+
+namespace io {
+
+// io/tokenizer.Tokenizer (tokenizer.zig:9-285).
+class Tokenizer {
+  public:
+    static constexpr uint32_t unk_id = 100, cls_id = 101, sep_id = 102;
+
+    Tokenizer() { check(tzh_tokenizer_create(&h_)); }  // Tokenizer.init
+    Tokenizer(const Tokenizer &) = delete;
+    ~Tokenizer() { tzh_tokenizer_free(h_); }
+
+    void loadVocab(const std::string &path) { check(tzh_tokenizer_load_vocab(h_, path.c_str())); }
+    void loadVocabFromBytes(const std::string &data) {
+        check(tzh_tokenizer_load_vocab_bytes(h_, data.data(), (int64_t)data.size()));
+    }
+    // vocab.put(token, id), as the reference's tests build vocabularies
+    void put(const std::string &token, uint32_t id) {
+        check(tzh_tokenizer_put(h_, token.data(), (int64_t)token.size(), id));
+    }
+    // [CLS] ... [SEP] into output (size >= 2); returns the id count
+    size_t encode(const std::string &text, uint32_t *output, size_t capacity) const {
+        int64_t n = 0;
+        check(tzh_tokenizer_encode(h_, text.data(), (int64_t)text.size(), output, (int64_t)capacity, &n));
+        return (size_t)n;
+    }
+    std::vector<uint32_t> encodeRaw(const std::string &text) const {
+        int64_t n = 0;
+        const int rc = tzh_tokenizer_encode_raw(h_, text.data(), (int64_t)text.size(), nullptr, 0, &n);
+        if (rc != TZH_OK && rc != TZH_ERR_TOO_LARGE) check(rc);
+        std::vector<uint32_t> out((size_t)n);
+        check(tzh_tokenizer_encode_raw(h_, text.data(), (int64_t)text.size(), out.data(), n, &n));
+        return out;
+    }
+    const tzh_tokenizer *handle() const { return h_; }
+
+  private:
+    tzh_tokenizer *h_ = nullptr;
+};
+
+}  // namespace io
 }  // namespace tenzor

@@ -195,8 +195,81 @@ int main(int argc, char **argv) {
         }
     });
 
+    // the reference's tokenizer tests (tokenizer.zig:291-437): vocabulary
+    // entries put directly, output capacity 32
+    run("tokenizer: the reference's known answers", [&] {
+        struct Case {
+            std::vector<std::pair<std::string, uint32_t>> vocab;
+            std::string text;
+            std::vector<uint32_t> expected;
+        };
+        const std::vector<std::pair<std::string, uint32_t>> special = {{"[UNK]", 100}, {"[CLS]", 101}, {"[SEP]", 102}};
+        std::vector<Case> cases = {
+            {{{"[PAD]", 0}, {"hello", 7592}, {"world", 2088}, {"##ing", 2075}, {"test", 3231}, {"##s", 1055}},
+             "hello world", {101, 7592, 2088, 102}},
+            {{{"test", 3231}, {"##ing", 2075}}, "testing", {101, 3231, 2075, 102}},
+            {{{"hello", 7592}}, "xyz", {101, 100, 102}},
+            {{{"hello", 7592}, {",", 1010}, {"world", 2088}}, "hello, world", {101, 7592, 1010, 2088, 102}},
+            {{{"hello", 7592}}, "HELLO", {101, 7592, 102}},
+        };
+        for (const auto &c : cases) {
+            io::Tokenizer tok;
+            for (const auto &e : special) tok.put(e.first, e.second);
+            for (const auto &e : c.vocab) tok.put(e.first, e.second);
+            uint32_t out[32];
+            const size_t n = tok.encode(c.text, out, 32);
+            EXPECT(std::vector<uint32_t>(out, out + n) == c.expected);
+            const auto raw = tok.encodeRaw(c.text);
+            EXPECT(std::vector<uint32_t>(c.expected.begin() + 1, c.expected.end() - 1) == raw);
+        }
+    });
+
     if (argc > 1) {
         const std::string dir = argv[1];
+        run("embed documents: vocab.txt + text -> pooled chunk embeddings", [&] {  // main.zig:786-933
+            auto weights = arctic::ModelWeights::fromSafeTensors(ctx, dir + "/model.safetensors");
+            io::Tokenizer tok;
+            tok.loadVocab(dir + "/vocab.txt");
+            const auto text = read_file<char>(dir + "/doc.txt");
+            const std::string doc(text.begin(), text.end());
+            const auto chunk_ids = read_file<uint32_t>(dir + "/chunk_ids.bin");   // the oracle's chunks
+            const auto chunk_lens = read_file<int32_t>(dir + "/chunk_lens.bin");
+            const size_t nc = chunk_lens.size();
+            EXPECT(nc >= 2);
+            // the library's own tokenizer gives the oracle's pieces
+            const auto pieces = tok.encodeRaw(doc);
+            int64_t planned = 0;
+            check(tzh_embed_chunk_count((int64_t)pieces.size(), &planned));
+            EXPECT(planned == (int64_t)nc);
+            EXPECT(std::vector<uint32_t>(chunk_ids.begin() + 1, chunk_ids.begin() + chunk_lens[0] - 1) ==
+                   std::vector<uint32_t>(pieces.begin(), pieces.begin() + chunk_lens[0] - 2));
+            void *d_out = nullptr, *d_ids = nullptr, *d_chunks = nullptr;
+            check(tzh_malloc(ctx.handle(), 384 * 4, &d_out));
+            check(tzh_malloc(ctx.handle(), chunk_ids.size() * 4, &d_ids));
+            check(tzh_malloc(ctx.handle(), nc * 384 * 4, &d_chunks));
+            const auto counts = arctic::embedDocuments((float *)d_out, {doc}, tok.handle(), weights);
+            EXPECT(counts.size() == 1 && (size_t)counts[0] == nc);
+            std::vector<float> got(384), emb(nc * 384);
+            check(tzh_memcpy_d2h(ctx.handle(), got.data(), d_out, 384 * 4));
+            check(tzh_memcpy_h2d(ctx.handle(), d_ids, chunk_ids.data(), chunk_ids.size() * 4));
+            arctic::forwardBatch((float *)d_chunks, (const uint32_t *)d_ids, chunk_lens, 0, weights);
+            check(tzh_memcpy_d2h(ctx.handle(), emb.data(), d_chunks, emb.size() * 4));
+            tzh_free(ctx.handle(), d_out);
+            tzh_free(ctx.handle(), d_ids);
+            tzh_free(ctx.handle(), d_chunks);
+            // main.zig:908-923 in its order, on the same chunk embeddings
+            float mean[384] = {}, norm = 0.0f;
+            for (size_t c = 0; c < nc; c++)
+                for (int j = 0; j < 384; j++) mean[j] += emb[c * 384 + j];
+            const float scale = 1.0f / (float)nc;
+            for (int j = 0; j < 384; j++) mean[j] *= scale;
+            for (int j = 0; j < 384; j++) {
+                const float sq = mean[j] * mean[j];
+                norm += sq;
+            }
+            norm = std::sqrt(norm);
+            for (int j = 0; j < 384; j++) EXPECT(got[j] == (norm > 0 ? mean[j] / norm : mean[j]));
+        });
         run("arctic integration: safetensors + tokens -> embeddings", [&] {  // arctic_integration_test.zig
             auto weights = arctic::ModelWeights::fromSafeTensors(ctx, dir + "/model.safetensors");
             const auto ids = read_file<uint32_t>(dir + "/ids.bin");

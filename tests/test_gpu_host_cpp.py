@@ -35,8 +35,20 @@ def test_cpp_host_api(tmp_path):
     hw = synth.HostWeights(w, cfg)
     expected = oracle.arctic_forward_batch(hw, flat, offs, lengths, nthreads=4)
     np.asarray(expected, np.float32).tofile(tmp_path / "expected.bin")
+    # the embed command's document path: a synthetic vocab.txt, a document
+    # of two chunks, and the oracle's chunk ids for it
+    from oracle import wordpiece as wp
+
+    vocab, words = synth.make_vocab(12)
+    (tmp_path / "vocab.txt").write_bytes(vocab)
+    doc = synth.make_text(13, words, 1000)
+    (tmp_path / "doc.txt").write_bytes(doc)
+    chunks = wp.chunks(wp.encode_raw(wp.load_vocab_bytes(vocab), doc))
+    np.array([i for c in chunks for i in c], np.uint32).tofile(tmp_path / "chunk_ids.bin")
+    np.array([len(c) for c in chunks], np.int32).tofile(tmp_path / "chunk_lens.bin")
     res = subprocess.run([EXE, str(tmp_path)], capture_output=True, text=True, timeout=120)
     print(res.stdout)
     assert res.returncode == 0, res.stdout + res.stderr
     assert "ALL PASSED" in res.stdout
     assert "PASS arctic integration" in res.stdout
+    assert "PASS embed documents" in res.stdout
