@@ -322,6 +322,62 @@ int tzh_arctic_set_timing(tzh_model *model, int32_t enable);
 int tzh_arctic_launch_times(tzh_model *model, float *us, const char **names, int32_t capacity, int32_t *count);
 
 /* ------------------------------------------------------------------ */
+/* The .tenzor file format (io/tenzor_format.zig)                      */
+/* ------------------------------------------------------------------ */
+
+/* tenzor_format.DType (tenzor_format.zig:25-37). */
+enum {
+    TZH_TZ_F32 = 0, TZH_TZ_F16 = 1, TZH_TZ_BF16 = 2, TZH_TZ_F64 = 3, TZH_TZ_I8 = 4, TZH_TZ_I16 = 5,
+    TZH_TZ_I32 = 6, TZH_TZ_I64 = 7, TZH_TZ_U8 = 8, TZH_TZ_U16 = 9, TZH_TZ_U32 = 10, TZH_TZ_U64 = 11
+};
+
+/* tenzor_format.TensorEntry (tenzor_format.zig:83-104), the 48-byte index
+ * entry exactly as stored in the file. */
+typedef struct {
+    uint64_t name_hash; /* FNV-1a of the tensor name */
+    uint8_t dtype;      /* TZH_TZ_* */
+    uint8_t ndim;
+    uint8_t pad_[2];
+    uint32_t shape[5];
+    uint64_t data_offset; /* from the start of the data section */
+    uint64_t data_size;   /* bytes */
+} tzh_tenzor_entry;
+
+typedef struct tzh_tenzor_file tzh_tenzor_file;
+
+/* hashName (tenzor_format.zig:107-114): 64-bit FNV-1a. */
+uint64_t tzh_tenzor_name_hash(const char *name, int64_t len);
+
+/* TenzorFile.open / close (tenzor_format.zig:140-204): maps the file
+ * read-only.  Bad magic, version or section bounds give
+ * TZH_ERR_INVALID_FORMAT (the reference's InvalidMagic, UnsupportedVersion,
+ * InvalidFormat); open or mmap failures TZH_ERR_IO.  Unlike the reference,
+ * every section and tensor is checked to lie inside the file. */
+int tzh_tenzor_open(const char *path, tzh_tenzor_file **out);
+int tzh_tenzor_close(tzh_tenzor_file *file);
+
+/* Header fields and the metadata JSON (a pointer into the mapping, not
+ * NUL-terminated).  Any output may be NULL. */
+int tzh_tenzor_info(const tzh_tenzor_file *file, uint32_t *tensor_count, const char **metadata_json,
+                    int64_t *metadata_size);
+
+/* TenzorFile.getTensor + getData (tenzor_format.zig:208-237): the first
+ * entry whose hash is the name's, and a host pointer to its bytes inside
+ * the mapping (valid until close).  TZH_ERR_MISSING_WEIGHT if absent. */
+int tzh_tenzor_get(const tzh_tenzor_file *file, const char *name, tzh_tenzor_entry *entry, const void **data);
+
+/* convertFromSafetensors (tenzor_format.zig:440-484, the `convert`
+ * command of main.zig:1028-1045): every tensor in header order, BOOL
+ * stored as u8, metadata "{}"; the file is byte-identical to the
+ * reference writer's. */
+int tzh_tenzor_convert_safetensors(const char *safetensors_path, const char *tenzor_path);
+
+/* ModelWeights from a .tenzor file: the names, dtypes and errors of
+ * tzh_arctic_load_safetensors (arctic.zig:113-166), with tensors read
+ * straight from the mapping. */
+int tzh_arctic_load_tenzor(tzh_ctx *ctx, const char *path, const tzh_arctic_config *config, tzh_model **out);
+
+/* ------------------------------------------------------------------ */
 /* WordPiece tokenizer and the embed command's text paths              */
 /* ------------------------------------------------------------------ */
 

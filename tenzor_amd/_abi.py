@@ -107,6 +107,12 @@ class ArcticWeights(C.Structure):
                 ("layer_norm_beta", C.c_void_p), ("layers", C.POINTER(LayerWeights))]
 
 
+class TenzorEntry(C.Structure):
+    """tzh_tenzor_entry: the 48-byte .tenzor index entry."""
+    _fields_ = [("name_hash", C.c_uint64), ("dtype", C.c_uint8), ("ndim", C.c_uint8), ("pad_", C.c_uint8 * 2),
+                ("shape", C.c_uint32 * 5), ("data_offset", C.c_uint64), ("data_size", C.c_uint64)]
+
+
 vp = C.c_void_p
 i32, i64, f32 = C.c_int32, C.c_int64, C.c_float
 pp = C.POINTER(C.c_void_p)
@@ -141,6 +147,13 @@ PROTOTYPES = {
     "tzh_arctic_last_launch_count": (C.c_int, [vp]),
     "tzh_arctic_set_timing": (C.c_int, [vp, i32]),
     "tzh_arctic_launch_times": (C.c_int, [vp, C.POINTER(f32), C.POINTER(C.c_char_p), i32, C.POINTER(i32)]),
+    "tzh_tenzor_name_hash": (C.c_uint64, [C.c_char_p, i64]),
+    "tzh_tenzor_open": (C.c_int, [C.c_char_p, pp]),
+    "tzh_tenzor_close": (C.c_int, [vp]),
+    "tzh_tenzor_info": (C.c_int, [vp, C.POINTER(C.c_uint32), C.POINTER(C.c_void_p), C.POINTER(i64)]),
+    "tzh_tenzor_get": (C.c_int, [vp, C.c_char_p, C.POINTER(TenzorEntry), C.POINTER(C.c_void_p)]),
+    "tzh_tenzor_convert_safetensors": (C.c_int, [C.c_char_p, C.c_char_p]),
+    "tzh_arctic_load_tenzor": (C.c_int, [vp, C.c_char_p, C.POINTER(ArcticConfig), pp]),
     "tzh_tokenizer_create": (C.c_int, [pp]),
     "tzh_tokenizer_free": (C.c_int, [vp]),
     "tzh_tokenizer_load_vocab": (C.c_int, [vp, C.c_char_p]),

@@ -36,6 +36,15 @@ class ModelWeights:
         return ModelWeights(h, ctx, config)
 
     @staticmethod
+    def fromTenzor(ctx: Context, path: str, config: Config = Config()) -> "ModelWeights":
+        """The same weights from a .tenzor file (tenzor_format.zig), read
+        from the mapped file."""
+        h = C.c_void_p()
+        cfg = config.to_c()
+        check(lib().tzh_arctic_load_tenzor(ctx.handle, str(path).encode(), C.byref(cfg), C.byref(h)))
+        return ModelWeights(h, ctx, config)
+
+    @staticmethod
     def fromHost(ctx: Context, weights: dict, config: Config = Config()) -> "ModelWeights":
         hw = HostWeights(weights, config)
         h = C.c_void_p()

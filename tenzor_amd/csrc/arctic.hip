@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "safetensors.h"
+#include "tenzor_file.h"
 
 int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, int32_t w_format,
                             const uint16_t *scale, const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k,
@@ -496,57 +497,101 @@ int upload_weights(tzh_model *m, const tzh_arctic_weights *w) {
 // ---------------------------------------------------------------------------
 // safetensors -> host views (arctic.zig:113-166, 258-287)
 // ---------------------------------------------------------------------------
+// Host tensors of a safetensors file (read into memory) or of a mapped
+// .tenzor file, looked up by name.
 struct HostStore {
     StFile st;
+    TzFile tz;
+    bool tenzor = false;
     std::vector<std::vector<uint8_t>> owned;  // aligned copies
 };
 
-const void *aligned_data(HostStore &hs, const StTensor &t) {
-    const uint8_t *p = hs.st.data(t);
+struct HostTensor {
+    int32_t dtype;  // TZH_*
+    std::vector<int64_t> shape;
+    const uint8_t *data;
+    size_t bytes;
+    int64_t numel() const {
+        int64_t n = 1;
+        for (int64_t d : shape) n *= d;
+        return n;
+    }
+};
+
+bool find_tensor(const HostStore &hs, const std::string &name, HostTensor &out) {
+    if (hs.tenzor) {
+        const tzh_tenzor_entry *e = hs.tz.find(name);
+        if (!e) return false;
+        out.dtype = tenzor_dtype_to_tzh(e->dtype);
+        out.shape.assign(e->shape, e->shape + (e->ndim < 5 ? e->ndim : 5));
+        out.data = hs.tz.data + e->data_offset;
+        out.bytes = (size_t)e->data_size;
+        return true;
+    }
+    const StTensor *t = hs.st.get(name);
+    if (!t) return false;
+    out.dtype = t->dtype;
+    out.shape = t->shape;
+    out.data = hs.st.data(*t);
+    out.bytes = (size_t)(t->end - t->start);
+    return true;
+}
+
+const void *aligned_data(HostStore &hs, const HostTensor &t) {
     const int es = st_dtype_size(t.dtype);
-    if (((uintptr_t)p % (uintptr_t)es) == 0) return p;  // safetensors.zig:147-161
-    hs.owned.emplace_back(p, p + (t.end - t.start));
+    if (((uintptr_t)t.data % (uintptr_t)es) == 0) return t.data;  // safetensors.zig:147-161
+    hs.owned.emplace_back(t.data, t.data + t.bytes);
     return hs.owned.back().data();
 }
 
+// The tensor's bytes must be its shape's worth (the formats do not check).
+int find_checked(HostStore &hs, const std::string &name, HostTensor &t) {
+    if (!find_tensor(hs, name, t)) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s", name.c_str());
+    if (t.dtype < 0) return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "Weight %s has an unknown dtype", name.c_str());
+    if ((uint64_t)t.numel() * (uint64_t)st_dtype_size(t.dtype) != t.bytes)
+        return tzh_fail(TZH_ERR_INVALID_FORMAT, "Weight %s: %zu bytes for its shape", name.c_str(), t.bytes);
+    return TZH_OK;
+}
+
 int get_f32(HostStore &hs, const std::string &name, const float **out) {
-    const StTensor *t = hs.st.get(name);
-    if (!t) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s", name.c_str());
-    if (t->dtype != TZH_F32) return tzh_fail(TZH_ERR_WRONG_DTYPE, "Weight %s has wrong dtype, expected F32", name.c_str());
-    *out = (const float *)aligned_data(hs, *t);
+    HostTensor t;
+    TZH_TRY(find_checked(hs, name, t));
+    if (t.dtype != TZH_F32) return tzh_fail(TZH_ERR_WRONG_DTYPE, "Weight %s has wrong dtype, expected F32", name.c_str());
+    *out = (const float *)aligned_data(hs, t);
     return TZH_OK;
 }
 
 int get_f32_alt(HostStore &hs, const std::string &primary, const std::string &alt, const float **out) {
-    if (hs.st.get(primary)) return get_f32(hs, primary, out);  // arctic.zig:245-256
+    HostTensor t;
+    if (find_tensor(hs, primary, t)) return get_f32(hs, primary, out);  // arctic.zig:245-256
     return get_f32(hs, alt, out);
 }
 
 int get_mat(HostStore &hs, const std::string &name, tzh_mat_view &v) {
-    const StTensor *t = hs.st.get(name);
-    if (!t) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s", name.c_str());
+    HostTensor t;
+    TZH_TRY(find_checked(hs, name, t));
     std::memset(&v, 0, sizeof v);
-    if (t->shape.size() != 2)
+    if (t.shape.size() != 2)
         return tzh_fail(TZH_ERR_INVALID_FORMAT, "Weight %s must be 2-D", name.c_str());
-    v.rows = (int32_t)t->shape[0];
-    v.cols = (int32_t)t->shape[1];
-    if (t->dtype == TZH_F32) {
+    v.rows = (int32_t)t.shape[0];
+    v.cols = (int32_t)t.shape[1];
+    if (t.dtype == TZH_F32) {
         v.dtype = TZH_F32;
-        v.data = aligned_data(hs, *t);
+        v.data = aligned_data(hs, t);
         return TZH_OK;
     }
-    if (t->dtype == TZH_I8) {  // arctic.zig:273-281
+    if (t.dtype == TZH_I8) {  // arctic.zig:273-281
         v.dtype = TZH_I8;
-        v.data = aligned_data(hs, *t);
+        v.data = aligned_data(hs, t);
         const std::string sname = name + ".scale";
-        const StTensor *s = hs.st.get(sname);
-        if (!s) return tzh_fail(TZH_ERR_MISSING_WEIGHT, "Missing weight: %s", sname.c_str());
-        if (s->dtype != TZH_F16) return tzh_fail(TZH_ERR_WRONG_DTYPE, "Weight %s has wrong dtype, expected F16", sname.c_str());
-        if (s->numel() != v.rows) return tzh_fail(TZH_ERR_INVALID_FORMAT, "%s has %lld entries, expected %d", sname.c_str(), (long long)s->numel(), v.rows);
-        v.scale = (const uint16_t *)aligned_data(hs, *s);
+        HostTensor s;
+        TZH_TRY(find_checked(hs, sname, s));
+        if (s.dtype != TZH_F16) return tzh_fail(TZH_ERR_WRONG_DTYPE, "Weight %s has wrong dtype, expected F16", sname.c_str());
+        if (s.numel() != v.rows) return tzh_fail(TZH_ERR_INVALID_FORMAT, "%s has %lld entries, expected %d", sname.c_str(), (long long)s.numel(), v.rows);
+        v.scale = (const uint16_t *)aligned_data(hs, s);
         return TZH_OK;
     }
-    return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "Weight %s has unsupported dtype %s", name.c_str(), st_dtype_name(t->dtype));
+    return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "Weight %s has unsupported dtype %s", name.c_str(), st_dtype_name(t.dtype));
 }
 
 }  // namespace
@@ -571,16 +616,10 @@ extern "C" int tzh_arctic_upload(tzh_ctx *ctx, const tzh_arctic_weights *weights
     return TZH_OK;
 }
 
-extern "C" int tzh_arctic_load_safetensors(tzh_ctx *ctx, const char *path, const tzh_arctic_config *config,
-                                           tzh_model **out) {
-    tzh_clear_error();
-    TZH_TRY(tzh_ctx_enter(ctx));
-    if (!out || !config) return tzh_fail(TZH_ERR_INVALID_ARGS, "null argument");
-    *out = nullptr;
-    HostStore hs;
-    TZH_TRY(st_load(path, hs.st));
-    hs.owned.reserve(hs.st.tensors.size());
-    const bool bert = hs.st.get("bert.embeddings.word_embeddings.weight") != nullptr;  // arctic.zig:131
+// ModelWeights.fromSafeTensors (arctic.zig:113-166) over either file format.
+static int load_from_store(tzh_ctx *ctx, HostStore &hs, const tzh_arctic_config *config, tzh_model **out) {
+    HostTensor probe;
+    const bool bert = find_tensor(hs, "bert.embeddings.word_embeddings.weight", probe);  // arctic.zig:131
     const std::string pre = bert ? "bert." : "";
     tzh_arctic_weights w;
     std::memset(&w, 0, sizeof w);
@@ -615,6 +654,29 @@ extern "C" int tzh_arctic_load_safetensors(tzh_ctx *ctx, const char *path, const
     }
     w.layers = layers.data();
     return tzh_arctic_upload(ctx, &w, out);
+}
+
+extern "C" int tzh_arctic_load_safetensors(tzh_ctx *ctx, const char *path, const tzh_arctic_config *config,
+                                           tzh_model **out) {
+    tzh_clear_error();
+    TZH_TRY(tzh_ctx_enter(ctx));
+    if (!out || !config || !path) return tzh_fail(TZH_ERR_INVALID_ARGS, "null argument");
+    *out = nullptr;
+    HostStore hs;
+    TZH_TRY(st_load(path, hs.st));
+    return load_from_store(ctx, hs, config, out);
+}
+
+extern "C" int tzh_arctic_load_tenzor(tzh_ctx *ctx, const char *path, const tzh_arctic_config *config,
+                                      tzh_model **out) {
+    tzh_clear_error();
+    TZH_TRY(tzh_ctx_enter(ctx));
+    if (!out || !config || !path) return tzh_fail(TZH_ERR_INVALID_ARGS, "null argument");
+    *out = nullptr;
+    HostStore hs;
+    hs.tenzor = true;
+    TZH_TRY(hs.tz.open(path));
+    return load_from_store(ctx, hs, config, out);
 }
 
 extern "C" int tzh_arctic_free(tzh_model *model) {
