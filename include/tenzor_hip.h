@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TZH_ABI_VERSION 1
+#define TZH_ABI_VERSION 2
 #define TZH_MAX_RANK 8 /* shape.zig:10 MAX_RANK */
 
 /* ------------------------------------------------------------------ */
@@ -118,7 +118,16 @@ typedef struct {
     int32_t ndim;     /* rank of this node's result */
     int64_t shape[TZH_MAX_RANK]; /* result shape (expr.zig ShapeOf) */
     double value;     /* TZH_NODE_CONSTANT: ScalarExpr.value (converted to dtype) */
+    int32_t aux;      /* TZH_NODE_LAYERNORM: index of the beta node (gamma is rhs) */
+    int32_t pad_;
+    int32_t perm[TZH_MAX_RANK]; /* TZH_NODE_TRANSPOSE: output axis i is input axis perm[i] */
 } tzh_node;
+/* Node fields per kind beyond kind/op/lhs/rhs/shape:
+ *   TZH_NODE_SOFTMAX    lhs = input, axis = softmax_axis (expr.zig:665-676)
+ *   TZH_NODE_LAYERNORM  lhs = input, rhs = gamma, aux = beta, axis = norm_dims
+ *                       (expr.zig:705-747); eps 1e-5 (layernorm.zig:15)
+ *   TZH_NODE_TRANSPOSE  lhs = input, perm (expr.zig:925-972)
+ *   TZH_NODE_RESHAPE    lhs = input (same element count, contiguous data) */
 
 /* A leaf tensor: contiguous row-major device data (Tensor.data, tensor.zig:28-60). */
 typedef struct {
@@ -134,6 +143,10 @@ typedef struct {
  * are evaluated in a single pass without temporaries; a reduce node fuses
  * the chain below it into its reduction.  Broadcasting follows NumPy rules
  * (shape.zig:168-204, strides.zig:92-121). */
+/* Node kinds evaluated: tensor, constant, unary, binary, reduce, and
+ * softmax, layernorm, transpose, reshape (executor.zig:363-535), which are
+ * computed into a temporary when another node reads them; matmul and gather
+ * give TZH_ERR_UNSUPPORTED_OP. */
 int tzh_eval_into(tzh_ctx *ctx, const tzh_node *tape, int32_t n_nodes,
                   const tzh_leaf *leaves, int32_t n_leaves, int32_t dtype, void *out);
 

@@ -54,6 +54,7 @@ OP = {name: i for i, name in enumerate([
 
 # NodeKind ordinals (expr.zig:137-149)
 NODE_TENSOR, NODE_CONSTANT, NODE_UNARY, NODE_BINARY, NODE_MATMUL, NODE_REDUCE = 0, 1, 2, 3, 4, 5
+NODE_RESHAPE, NODE_TRANSPOSE, NODE_SOFTMAX, NODE_LAYERNORM, NODE_GATHER = 6, 7, 8, 9, 10
 
 # epilogues
 EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RES_LN = 0, 1, 2
@@ -64,6 +65,7 @@ class Node(C.Structure):
         ("kind", C.c_int32), ("op", C.c_int32), ("lhs", C.c_int32), ("rhs", C.c_int32),
         ("leaf", C.c_int32), ("axis", C.c_int32), ("keepdims", C.c_int32), ("ndim", C.c_int32),
         ("shape", C.c_int64 * MAX_RANK), ("value", C.c_double),
+        ("aux", C.c_int32), ("pad_", C.c_int32), ("perm", C.c_int32 * MAX_RANK),
     ]
 
 

@@ -263,6 +263,117 @@ __global__ void __launch_bounds__(256) ew_reduce_cols_kernel(const EwProgram p, 
 }
 
 // ------------------------------------------------------------------------
+// Softmax, LayerNorm and transpose nodes (executor.zig:363-535).  Their
+// inputs are contiguous buffers: leaf tensors or materialised children.
+// ------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ T wave_max_t(T v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
+    return v;
+}
+template <typename T>
+__device__ __forceinline__ T wave_sum_t(T v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float exp_t(float x) { return expf(x); }
+__device__ __forceinline__ double exp_t(double x) { return exp(x); }
+__device__ __forceinline__ float sqrt_t(float x) { return sqrtf(x); }
+__device__ __forceinline__ double sqrt_t(double x) { return sqrt(x); }
+
+// softmaxRow (softmax.zig:38-137): max, exp(x - max) stored and summed, then
+// times 1 / sum.  One wave per row of the last axis.
+template <typename T>
+__global__ void __launch_bounds__(256) ew_softmax_rows_kernel(const T *__restrict__ x, T *__restrict__ y,
+                                                              int64_t rows, int64_t n) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
+    const int lane = threadIdx.x % 64;
+    if (r >= rows) return;
+    const T *xr = x + r * n;
+    T *yr = y + r * n;
+    T m = -INFINITY;
+    for (int64_t c = lane; c < n; c += 64) m = fmax(m, xr[c]);
+    m = wave_max_t(m);
+    T s = 0;
+    for (int64_t c = lane; c < n; c += 64) {
+        const T e = exp_t(xr[c] - m);
+        yr[c] = e;
+        s += e;
+    }
+    const T inv = (T)1 / wave_sum_t(s);
+    for (int64_t c = lane; c < n; c += 64) yr[c] = yr[c] * inv;
+}
+
+// softmaxAxis general case (softmax.zig:172-213): one thread per
+// (outer, inner) column of a middle or leading axis.
+template <typename T>
+__global__ void __launch_bounds__(256) ew_softmax_cols_kernel(const T *__restrict__ x, T *__restrict__ y,
+                                                              int64_t outer, int64_t n, int64_t inner) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= outer * inner) return;
+    const int64_t base = (idx / inner) * n * inner + idx % inner;
+    T m = -INFINITY;
+    for (int64_t a = 0; a < n; a++) m = fmax(m, x[base + a * inner]);
+    T s = 0;
+    for (int64_t a = 0; a < n; a++) {
+        const T e = exp_t(x[base + a * inner] - m);
+        y[base + a * inner] = e;
+        s += e;
+    }
+    const T inv = (T)1 / s;
+    for (int64_t a = 0; a < n; a++) y[base + a * inner] = y[base + a * inner] * inv;
+}
+
+// layerNorm (layernorm.zig:123-185): mean = sum * (1/N), variance = sum of
+// squared deviations * (1/N), 1 / sqrt(variance + eps), then
+// (x - mean) * inv_std * gamma + beta.  One wave per instance.
+template <typename T>
+__global__ void __launch_bounds__(256) ew_layernorm_kernel(const T *__restrict__ x, const T *__restrict__ g,
+                                                           const T *__restrict__ b, T *__restrict__ y,
+                                                           int64_t rows, int64_t n, T eps) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
+    const int lane = threadIdx.x % 64;
+    if (r >= rows) return;
+    const T *xr = x + r * n;
+    T *yr = y + r * n;
+    const T inv_n = (T)1 / (T)n;
+    T s = 0;
+    for (int64_t c = lane; c < n; c += 64) s += xr[c];
+    const T mean = wave_sum_t(s) * inv_n;
+    T v = 0;
+    for (int64_t c = lane; c < n; c += 64) {
+        const T d = xr[c] - mean;
+        v += d * d;
+    }
+    const T inv_std = (T)1 / sqrt_t(wave_sum_t(v) * inv_n + eps);
+    for (int64_t c = lane; c < n; c += 64) yr[c] = ((xr[c] - mean) * inv_std) * g[c] + b[c];
+}
+
+// transpose (transpose.zig): output element o at multi-index i reads the
+// input at sum_k i[k] * in_stride[perm[k]].
+struct TransposeArgs {
+    int32_t ndim;
+    int64_t out_shape[TZH_MAX_RANK];
+    int64_t src_stride[TZH_MAX_RANK];  // input stride of the axis that output axis k reads
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) ew_transpose_kernel(const T *__restrict__ x, T *__restrict__ y,
+                                                           const TransposeArgs a, int64_t numel) {
+    const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (o >= numel) return;
+    int64_t rem = o, src = 0;
+    for (int k = a.ndim - 1; k >= 0; k--) {
+        const int64_t i = rem % a.out_shape[k];
+        rem /= a.out_shape[k];
+        src += i * a.src_stride[k];
+    }
+    y[o] = x[src];
+}
+
+// ------------------------------------------------------------------------
 // host planner
 // ------------------------------------------------------------------------
 bool unary_ok(int op) {
@@ -384,9 +495,67 @@ struct Planner {
                 if (n.shape[i] != want[i]) return tzh_fail(TZH_ERR_SHAPE, "node %d: wrong reduce result shape", idx);
             return validate(n.lhs);
         }
+        case TZH_NODE_SOFTMAX: {
+            if (n.lhs < 0 || n.lhs >= idx) return tzh_fail(TZH_ERR_INVALID_ARGS, "node %d: bad input index", idx);
+            TZH_TRY(same_shape(idx, n.lhs));
+            if (n.axis < 0 || n.axis >= n.ndim) return tzh_fail(TZH_ERR_SHAPE, "node %d: softmax axis %d", idx, n.axis);
+            return validate(n.lhs);
+        }
+        case TZH_NODE_LAYERNORM: {
+            if (n.lhs < 0 || n.lhs >= idx || n.rhs < 0 || n.rhs >= idx || n.aux < 0 || n.aux >= idx)
+                return tzh_fail(TZH_ERR_INVALID_ARGS, "node %d: bad operand index", idx);
+            TZH_TRY(same_shape(idx, n.lhs));
+            if (n.axis < 1 || n.axis > n.ndim) return tzh_fail(TZH_ERR_SHAPE, "node %d: norm_dims %d", idx, n.axis);
+            for (int32_t pi : {n.rhs, n.aux}) {  // expr.zig:705-735: gamma/beta are the last norm_dims dims
+                const tzh_node &q = tape[pi];
+                if (q.ndim != n.axis)
+                    return tzh_fail(TZH_ERR_SHAPE, "Gamma/beta rank must equal normalized_dims (node %d)", idx);
+                for (int i = 0; i < n.axis; i++)
+                    if (q.shape[i] != n.shape[n.ndim - n.axis + i])
+                        return tzh_fail(TZH_ERR_SHAPE, "Gamma/beta shape must match last dimensions of input (node %d)", idx);
+            }
+            TZH_TRY(validate(n.lhs));
+            TZH_TRY(validate(n.rhs));
+            return validate(n.aux);
+        }
+        case TZH_NODE_TRANSPOSE: {
+            if (n.lhs < 0 || n.lhs >= idx) return tzh_fail(TZH_ERR_INVALID_ARGS, "node %d: bad input index", idx);
+            const tzh_node &c = tape[n.lhs];
+            if (c.ndim != n.ndim) return tzh_fail(TZH_ERR_SHAPE, "node %d: transpose rank mismatch", idx);
+            bool seen[TZH_MAX_RANK] = {};
+            for (int i = 0; i < n.ndim; i++) {  // expr.zig:932-952
+                const int p = n.perm[i];
+                if (p < 0 || p >= n.ndim || seen[p])
+                    return tzh_fail(TZH_ERR_SHAPE, "Invalid transpose permutation (node %d)", idx);
+                seen[p] = true;
+                if (n.shape[i] != c.shape[p]) return tzh_fail(TZH_ERR_SHAPE, "node %d: wrong transpose shape", idx);
+            }
+            return validate(n.lhs);
+        }
+        case TZH_NODE_RESHAPE: {
+            if (n.lhs < 0 || n.lhs >= idx) return tzh_fail(TZH_ERR_INVALID_ARGS, "node %d: bad input index", idx);
+            const tzh_node &c = tape[n.lhs];
+            if (numel_of(c.ndim, c.shape) != numel_of(n.ndim, n.shape))
+                return tzh_fail(TZH_ERR_SHAPE, "node %d: reshape changes the element count", idx);
+            return validate(n.lhs);
+        }
         default:
             return tzh_fail(TZH_ERR_UNSUPPORTED_OP, "node kind %d is not evaluated by this backend", n.kind);
         }
+    }
+
+    int same_shape(int32_t a, int32_t b) const {
+        const tzh_node &x = tape[a], &y = tape[b];
+        if (x.ndim != y.ndim) return tzh_fail(TZH_ERR_SHAPE, "node %d: shape mismatch with its input", a);
+        for (int i = 0; i < x.ndim; i++)
+            if (x.shape[i] != y.shape[i]) return tzh_fail(TZH_ERR_SHAPE, "node %d: shape mismatch with its input", a);
+        return TZH_OK;
+    }
+
+    // Nodes computed by a kernel of their own, read by chains as leaves.
+    static bool materialised_kind(int k) {
+        return k == TZH_NODE_REDUCE || k == TZH_NODE_SOFTMAX || k == TZH_NODE_LAYERNORM || k == TZH_NODE_TRANSPOSE ||
+               k == TZH_NODE_RESHAPE;
     }
 
     // Nodes evaluated into a temporary before the program that reads them
@@ -395,7 +564,7 @@ struct Planner {
 
     bool is_leafish(int32_t idx) const {
         const int k = tape[idx].kind;
-        return cut[(size_t)idx] || k == TZH_NODE_TENSOR || k == TZH_NODE_CONSTANT || k == TZH_NODE_REDUCE;
+        return cut[(size_t)idx] || k == TZH_NODE_TENSOR || k == TZH_NODE_CONSTANT || materialised_kind(k);
     }
     // value-stack depth to evaluate idx inline (Sethi-Ullman for a stack machine)
     int depth(int32_t idx) const {
@@ -523,7 +692,14 @@ struct Planner {
     int emit(EwProgram &p, int32_t idx, int sp, int vec, bool is_root) {
         const tzh_node &n = tape[idx];
         if (sp >= kMaxDepth) return tzh_fail(TZH_ERR_INVALID_ARGS, "internal: value stack overflow");
-        if (!is_root && (n.kind == TZH_NODE_REDUCE || cut[(size_t)idx])) {
+        if (n.kind == TZH_NODE_RESHAPE && tape[n.lhs].kind == TZH_NODE_TENSOR) {
+            // a reshaped leaf is the same contiguous data under another shape
+            int li;
+            TZH_TRY(add_leaf(p, leaves[tape[n.lhs].leaf].data, n.ndim, n.shape, vec, &li));
+            return push(p, EK_LEAF, 0, (int16_t)sp, (int16_t)li, 0.0);
+        }
+        // (a reduction's input program may itself be rooted at such a node)
+        if (materialised_kind(n.kind) || (!is_root && cut[(size_t)idx])) {
             void *buf = nullptr;
             TZH_TRY(materialise(idx, &buf));
             int li;
@@ -633,9 +809,82 @@ struct Planner {
         return TZH_OK;
     }
 
+    // Contiguous data of node idx: a leaf's own buffer, else a temporary.
+    int input_data(int32_t idx, const void **out) {
+        const tzh_node &n = tape[idx];
+        if (n.kind == TZH_NODE_TENSOR) {
+            *out = leaves[n.leaf].data;
+            return TZH_OK;
+        }
+        void *buf = nullptr;
+        TZH_TRY(materialise(idx, &buf));
+        *out = buf;
+        return TZH_OK;
+    }
+
+    template <typename T>
+    int launch_structural(int32_t idx, T *out) {
+        const tzh_node &n = tape[idx];
+        const int64_t numel = numel_of(n.ndim, n.shape);
+        if (n.kind == TZH_NODE_RESHAPE) return eval_into(n.lhs, out);  // executor.zig:481-495
+        const void *x = nullptr;
+        TZH_TRY(input_data(n.lhs, &x));
+        if (numel == 0) return TZH_OK;
+        if (n.kind == TZH_NODE_SOFTMAX) {
+            int64_t outer = 1, inner = 1;
+            const int64_t len = n.shape[n.axis];
+            for (int i = 0; i < n.axis; i++) outer *= n.shape[i];
+            for (int i = n.axis + 1; i < n.ndim; i++) inner *= n.shape[i];
+            if (inner == 1) {
+                hipLaunchKernelGGL((ew_softmax_rows_kernel<T>), dim3((unsigned)((outer + 3) / 4)), dim3(256), 0,
+                                   ctx->stream, (const T *)x, out, outer, len);
+                TZH_LAUNCHED("ew_softmax_rows_kernel");
+            } else {
+                hipLaunchKernelGGL((ew_softmax_cols_kernel<T>), dim3((unsigned)((outer * inner + 255) / 256)), dim3(256),
+                                   0, ctx->stream, (const T *)x, out, outer, len, inner);
+                TZH_LAUNCHED("ew_softmax_cols_kernel");
+            }
+            return TZH_OK;
+        }
+        if (n.kind == TZH_NODE_LAYERNORM) {
+            const void *g = nullptr, *b = nullptr;
+            TZH_TRY(input_data(n.rhs, &g));
+            TZH_TRY(input_data(n.aux, &b));
+            int64_t len = 1;
+            for (int i = n.ndim - n.axis; i < n.ndim; i++) len *= n.shape[i];
+            const int64_t rows = numel / len;
+            // layernorm.zig:15: default_eps is the f32 1e-5, widened for f64
+            hipLaunchKernelGGL((ew_layernorm_kernel<T>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, ctx->stream,
+                               (const T *)x, (const T *)g, (const T *)b, out, rows, len, (T)1e-5f);
+            TZH_LAUNCHED("ew_layernorm_kernel");
+            return TZH_OK;
+        }
+        // TZH_NODE_TRANSPOSE
+        const tzh_node &c = tape[n.lhs];
+        TransposeArgs a;
+        std::memset(&a, 0, sizeof a);
+        a.ndim = n.ndim;
+        int64_t in_stride[TZH_MAX_RANK];
+        int64_t st = 1;
+        for (int i = c.ndim - 1; i >= 0; i--) {
+            in_stride[i] = st;
+            st *= c.shape[i];
+        }
+        for (int i = 0; i < n.ndim; i++) {
+            a.out_shape[i] = n.shape[i];
+            a.src_stride[i] = in_stride[n.perm[i]];
+        }
+        hipLaunchKernelGGL((ew_transpose_kernel<T>), dim3((unsigned)((numel + 255) / 256)), dim3(256), 0, ctx->stream,
+                           (const T *)x, out, a, numel);
+        TZH_LAUNCHED("ew_transpose_kernel");
+        return TZH_OK;
+    }
+
     int eval_into(int32_t idx, void *out) {
         const tzh_node &n = tape[idx];
         const bool is64 = dtype == TZH_F64;
+        if (n.kind != TZH_NODE_REDUCE && materialised_kind(n.kind))
+            return is64 ? launch_structural<double>(idx, (double *)out) : launch_structural<float>(idx, (float *)out);
         if (n.kind == TZH_NODE_REDUCE)
             return is64 ? launch_reduce<double, 2>(idx, (double *)out) : launch_reduce<float, 4>(idx, (float *)out);
         return is64 ? launch_chain<double, 2>(idx, (double *)out) : launch_chain<float, 4>(idx, (float *)out);

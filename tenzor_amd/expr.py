@@ -17,6 +17,8 @@ from __future__ import annotations
 import ctypes as C
 from typing import Sequence
 
+import numpy as np
+
 from . import _abi, check, lib
 
 UNARY_OPS = ("neg", "abs", "exp", "log", "sqrt", "rsqrt", "sin", "cos", "tanh", "sigmoid", "relu", "gelu",
@@ -85,6 +87,10 @@ class Expr:
     def minimum(self, o): return BinaryExpr("min", self, as_expr(o, self.dtype))
 
     # reductions over all axes (expr.zig:323-342)
+    def softmax(self, axis: int): return SoftmaxExpr(self, axis)
+    def transpose(self, perm): return TransposeExpr(self, perm)
+    def reshape(self, shape): return ReshapeExpr(self, shape)
+
     def sum(self): return ReduceExpr("sum", self)
     def mean(self): return ReduceExpr("mean", self)
     def prod(self): return ReduceExpr("prod", self)
@@ -175,6 +181,71 @@ class ReduceExpr(Expr):
         self.dtype = input.dtype
 
 
+class SoftmaxExpr(Expr):
+    """SoftmaxExpr (expr.zig:665-696): softmax along one axis (negative
+    axes count from the end, shape.normalizeAxis)."""
+
+    kind = _abi.NODE_SOFTMAX
+
+    def __init__(self, input: Expr, axis: int):
+        nd = len(input.shape)
+        ax = axis + nd if axis < 0 else axis
+        if not 0 <= ax < nd:
+            raise ValueError(f"axis {axis} out of range for rank {nd}")
+        self.input, self.softmax_axis = input, ax
+        self.shape, self.dtype = input.shape, input.dtype
+
+
+class LayerNormExpr(Expr):
+    """LayerNormExpr (expr.zig:705-760): normalise over the last norm_dims
+    dimensions; gamma and beta have exactly those dimensions."""
+
+    kind = _abi.NODE_LAYERNORM
+
+    def __init__(self, input: Expr, gamma: Expr, beta: Expr, norm_dims: int = 1):
+        nd = len(input.shape)
+        if not 1 <= norm_dims <= nd:
+            raise ValueError(f"norm_dims {norm_dims} out of range for rank {nd}")
+        if len(gamma.shape) != norm_dims or len(beta.shape) != norm_dims:
+            raise TypeError("Gamma/beta rank must equal normalized_dims")
+        if tuple(gamma.shape) != tuple(input.shape[nd - norm_dims:]) or tuple(beta.shape) != tuple(gamma.shape):
+            raise TypeError("Gamma/beta shape must match last dimensions of input")
+        if not (input.dtype == gamma.dtype == beta.dtype):
+            raise TypeError("LayerNorm operands must share one element type")
+        self.input, self.gamma, self.beta, self.norm_dims = input, gamma, beta, norm_dims
+        self.shape, self.dtype = input.shape, input.dtype
+
+
+class TransposeExpr(Expr):
+    """TransposeExpr (expr.zig:925-990): output axis i is input axis perm[i]."""
+
+    kind = _abi.NODE_TRANSPOSE
+
+    def __init__(self, input: Expr, perm):
+        perm = tuple(int(p) for p in perm)
+        nd = len(input.shape)
+        if len(perm) != nd:
+            raise TypeError(f"Permutation length {len(perm)} must match rank {nd}")
+        if sorted(perm) != list(range(nd)):
+            raise TypeError("Invalid transpose permutation")
+        self.input, self.permutation = input, perm
+        self.shape = tuple(input.shape[p] for p in perm)
+        self.dtype = input.dtype
+
+
+class ReshapeExpr(Expr):
+    """ReshapeExpr: the same elements under another shape."""
+
+    kind = _abi.NODE_RESHAPE
+
+    def __init__(self, input: Expr, shape):
+        shape = tuple(int(d) for d in shape)
+        if int(np.prod(shape, dtype=np.int64)) != input.numel():
+            raise TypeError("Reshape must preserve the element count")
+        self.input = input
+        self.shape, self.dtype = shape, input.dtype
+
+
 def to_tape(expr: Expr):
     """Post-order node tape + leaf list (what a comptime walk emits)."""
     nodes, leaves, leaf_ids = [], [], {}
@@ -209,6 +280,20 @@ def to_tape(expr: Expr):
             if e.axes:
                 ax = e.axes[0]
                 n.axis = ax + len(e.input.shape) if ax < 0 else ax
+        elif isinstance(e, SoftmaxExpr):
+            n.lhs = visit(e.input)
+            n.axis = e.softmax_axis
+        elif isinstance(e, LayerNormExpr):
+            n.lhs = visit(e.input)
+            n.rhs = visit(e.gamma)
+            n.aux = visit(e.beta)
+            n.axis = e.norm_dims
+        elif isinstance(e, TransposeExpr):
+            n.lhs = visit(e.input)
+            for i, p in enumerate(e.permutation):
+                n.perm[i] = p
+        elif isinstance(e, ReshapeExpr):
+            n.lhs = visit(e.input)
         else:
             raise TypeError(f"unsupported expression node {type(e).__name__}")
         nodes.append(n)

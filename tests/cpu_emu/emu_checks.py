@@ -378,8 +378,63 @@ def group_embed():
     check(L.tzh_arctic_free(m))
 
 
+def eval_lib(expr):
+    nodes, leaves = to_tape(expr)
+    dt = np.float64 if expr.dtype == "float64" else np.float32
+    out = np.empty(expr.shape, dt)
+    arr = (_abi.Leaf * max(1, len(leaves)))()
+    for i, t in enumerate(leaves):
+        arr[i].data = t.data.data_ptr()
+        arr[i].ndim = len(t.shape)
+        for j, d in enumerate(t.shape):
+            arr[i].shape[j] = d
+    tape = (_abi.Node * len(nodes))(*nodes)
+    rc = L.tzh_eval_into(CTX, tape, len(nodes), arr, len(leaves), _abi.F64 if dt == np.float64 else _abi.F32,
+                         out.ctypes.data)
+    return rc, out
+
+
+def group_nodes():
+    # softmax / layernorm / transpose / reshape nodes, alone and read by
+    # chains and reductions, against the numpy restatement
+    from oracle import eval_nodes as en
+    from tenzor_amd.expr import LayerNormExpr
+
+    rng = np.random.default_rng(3)
+    for dt in (np.float32, np.float64):
+        x = (rng.standard_normal((3, 5, 70)) * 3).astype(dt)
+        y = rng.standard_normal((5, 70)).astype(dt)
+        g, b = rng.standard_normal(70).astype(dt), rng.standard_normal(70).astype(dt)
+        tx, ty, tg, tb = T(x, dt), T(y, dt), T(g, dt), T(b, dt)
+        host = {id(tx): x, id(ty): y, id(tg): g, id(tb): b}
+        tol = 1e-5 if dt == np.float32 else 1e-12
+        for e in [tx.softmax(-1), tx.softmax(1), tx.softmax(0), tx.transpose((2, 0, 1)), tx.transpose((1, 0, 2)),
+                  tx.reshape((15, 70)), tx.softmax(-1).mul(2.0).add(ty), LayerNormExpr(tx, tg, tb, 1),
+                  LayerNormExpr(tx.mul(ty), tg, tb, 1).transpose((0, 2, 1)), tx.softmax(-1).sum(),
+                  ReduceExpr("sum", tx.transpose((2, 1, 0)), (0,)), tx.reshape((5, 3, 70)).add(ty.reshape((5, 1, 70)))]:
+            rc, out = eval_lib(e)
+            assert rc == 0, L.tzh_last_error()
+            ref = en.evaluate(e, host)
+            assert np.abs(out - ref).max() <= tol * max(1.0, float(np.abs(ref).max())), (dt, type(e).__name__)
+        g2 = rng.standard_normal((5, 70)).astype(dt)
+        tg2, tb2 = T(g2, dt), T(g2, dt)
+        host.update({id(tg2): g2, id(tb2): g2})
+        e = LayerNormExpr(tx, tg2, tb2, 2)
+        rc, out = eval_lib(e)
+        assert rc == 0 and np.abs(out - en.evaluate(e, host)).max() <= 10 * tol
+    # errors the planner raises for malformed tapes
+    nodes, leaves = to_tape(T(np.zeros((2, 3), np.float32)).transpose((1, 0)))
+    nodes[1].perm[1] = 1  # not a permutation
+    tape = (_abi.Node * 2)(*nodes)
+    arr = (_abi.Leaf * 1)()
+    arr[0].data, arr[0].ndim, arr[0].shape[0], arr[0].shape[1] = leaves[0].data.data_ptr(), 2, 2, 3
+    out = np.empty((3, 2), np.float32)
+    assert L.tzh_eval_into(CTX, tape, 2, arr, 1, _abi.F32, out.ctypes.data) == -10  # TZH_ERR_SHAPE
+
+
 GROUPS = {"eval": group_eval, "gemm": group_gemm, "gemm_ln": group_gemm_ln, "attention": group_attention,
-          "arctic": group_arctic, "embed": group_embed}
+          "arctic": group_arctic, "embed": group_embed,
+          "nodes": group_nodes}
 
 if __name__ == "__main__":
     check(L.tzh_init(0, None, C.byref(CTX)))

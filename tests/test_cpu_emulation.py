@@ -34,7 +34,7 @@ def emu_env():
     return env
 
 
-GROUPS = ["eval", "attention", "gemm", "gemm_ln"]
+GROUPS = ["eval", "attention", "gemm", "gemm_ln", "nodes"]
 
 
 @pytest.fixture(scope="module")

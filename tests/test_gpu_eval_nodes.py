@@ -1,0 +1,94 @@
+"""GPU parity of the softmax, layernorm, transpose and reshape nodes of
+`eval` (executor.zig:363-535) against the numpy restatement
+(oracle/eval_nodes.py).  Bars: transpose and reshape bit-exact; softmax and
+layernorm within 1e-5 (f32) / 1e-12 (f64) of the restatement, relative to
+the largest output magnitude (exp, sqrt and summation order differ from
+numpy's by ulps; the reference's own order is unobservable)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import eval_nodes as en
+
+from tenzor_amd.expr import LayerNormExpr, ReduceExpr, Tensor, eval
+
+pytestmark = pytest.mark.gpu
+
+
+def leaf(a):
+    t = Tensor(torch.from_numpy(np.ascontiguousarray(a)).cuda())
+    return t
+
+
+def check_close(e, host, dt):
+    got = eval(e).cpu().numpy()
+    ref = en.evaluate(e, host)
+    tol = 1e-5 if dt == np.float32 else 1e-12
+    assert got.shape == ref.shape
+    assert np.abs(got - ref).max() <= tol * max(1.0, float(np.abs(ref).max()))
+    return got, ref
+
+
+def test_reference_known_answers():
+    """executor.zig:854-1030 through the GPU path."""
+    y = eval(leaf(np.array([[1, 2, 3], [0, 0, 0]], np.float32)).softmax(-1)).cpu().numpy()
+    assert np.allclose(y.sum(1), 1, atol=1e-5) and np.allclose(y[1], 1 / 3, atol=1e-5)
+    x = leaf(np.array([[1, 2, 3, 4], [10, 20, 30, 40]], np.float32))
+    g, b = leaf(np.ones(4, np.float32)), leaf(np.zeros(4, np.float32))
+    y = eval(LayerNormExpr(x, g, b, 1)).cpu().numpy()
+    assert np.allclose(y.mean(1), 0, atol=1e-5) and np.allclose(y[0], y[1], atol=1e-5)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_nodes_vs_restatement(dt):
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((6, 33, 300)) * 4).astype(dt)
+    y = rng.standard_normal((33, 300)).astype(dt)
+    g, b = rng.standard_normal(300).astype(dt), rng.standard_normal(300).astype(dt)
+    tx, ty, tg, tb = leaf(x), leaf(y), leaf(g), leaf(b)
+    host = {id(tx): x, id(ty): y, id(tg): g, id(tb): b}
+    for e in [tx.softmax(-1), tx.softmax(1), tx.softmax(0), LayerNormExpr(tx, tg, tb, 1),
+              tx.softmax(-1).mul(3.0).add(ty), LayerNormExpr(tx.mul(ty), tg, tb, 1).transpose((2, 0, 1)),
+              tx.softmax(-1).sum(), ReduceExpr("sum", tx.transpose((2, 1, 0)), (0,))]:
+        check_close(e, host, dt)
+    g2 = rng.standard_normal((33, 300)).astype(dt)
+    tg2 = leaf(g2)
+    host[id(tg2)] = g2
+    check_close(LayerNormExpr(tx, tg2, tg2, 2), host, dt)
+
+
+@pytest.mark.parametrize("perm", [(1, 0, 2, 3), (0, 2, 1, 3), (3, 2, 1, 0), (0, 1, 2, 3), (2, 0, 3, 1)])
+def test_transpose_bit_exact(perm):
+    """Includes the attention pattern [B,S,H,D] -> [B,H,S,D] (executor.zig:505-520)."""
+    x = np.random.default_rng(6).standard_normal((4, 128, 12, 32)).astype(np.float32)
+    got = eval(leaf(x).transpose(perm)).cpu().numpy()
+    assert np.array_equal(got, np.transpose(x, perm))
+
+
+def test_reshape_and_large_rows():
+    x = np.random.default_rng(7).standard_normal((4096, 1000)).astype(np.float32)
+    tx = leaf(x)
+    assert np.array_equal(eval(tx.reshape((1000, 4096))).cpu().numpy(), x.reshape(1000, 4096))
+    got = eval(tx.softmax(-1)).cpu().numpy()
+    assert np.abs(got - en.softmax(x, 1)).max() < 1e-6
+    assert np.abs(got.sum(1) - 1).max() < 1e-5
+
+
+def test_malformed_layernorm_is_rejected():
+    x = leaf(np.zeros((2, 4), np.float32))
+    g = leaf(np.zeros(3, np.float32))
+    with pytest.raises(TypeError):
+        LayerNormExpr(x, g, g, 1)  # the mirror's compile-time check
+    from tenzor_amd.expr import to_tape
+    e = LayerNormExpr(x, leaf(np.zeros(4, np.float32)), leaf(np.zeros(4, np.float32)), 1)
+    nodes, leaves = to_tape(e)
+    nodes[-1].axis = 3  # norm_dims beyond the rank
+    import ctypes as C
+    from tenzor_amd import _abi, lib
+    from tenzor_amd.expr import _ctx_for, _leaf_structs
+    out = torch.empty((2, 4), device="cuda")
+    tape = (_abi.Node * len(nodes))(*nodes)
+    rc = lib().tzh_eval_into(_ctx_for(0).handle, tape, len(nodes), _leaf_structs(leaves), len(leaves), _abi.F32,
+                             C.c_void_p(out.data_ptr()))
+    assert rc == -10  # TZH_ERR_SHAPE
+

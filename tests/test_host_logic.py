@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(_abi.PROTOTYPES), set(names) ^ set(_abi.PROTOTYPES)
-    assert lib.tzh_abi_version() == 1
+    assert lib.tzh_abi_version() == 2
 
 
 def test_init_without_gpu_fails_cleanly():
