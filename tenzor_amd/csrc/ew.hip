@@ -283,27 +283,45 @@ __device__ __forceinline__ double exp_t(double x) { return exp(x); }
 __device__ __forceinline__ float sqrt_t(float x) { return sqrtf(x); }
 __device__ __forceinline__ double sqrt_t(double x) { return sqrt(x); }
 
-// softmaxRow (softmax.zig:38-137): max, exp(x - max) stored and summed, then
-// times 1 / sum.  One wave per row of the last axis.
-template <typename T>
+template <typename T, int V>
+struct alignas(sizeof(T) * V) RowVec {
+    T v[V];
+};
+
+// softmaxRow (softmax.zig:38-137): max, exp(x - max) summed, then
+// exp(x - max) * (1 / sum) stored (recomputed rather than stored and
+// re-read: the same values, one pass less over memory).  One wave per row
+// of the last axis, V consecutive elements per lane and access.
+template <typename T, int V>
 __global__ void __launch_bounds__(256) ew_softmax_rows_kernel(const T *__restrict__ x, T *__restrict__ y,
                                                               int64_t rows, int64_t n) {
     const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
     const int lane = threadIdx.x % 64;
     if (r >= rows) return;
-    const T *xr = x + r * n;
-    T *yr = y + r * n;
+    const RowVec<T, V> *xr = (const RowVec<T, V> *)(x + r * n);
+    RowVec<T, V> *yr = (RowVec<T, V> *)(y + r * n);
+    const int64_t nv = n / V;
     T m = -INFINITY;
-    for (int64_t c = lane; c < n; c += 64) m = fmax(m, xr[c]);
+    for (int64_t c = lane; c < nv; c += 64) {
+        const RowVec<T, V> a = xr[c];
+#pragma unroll
+        for (int k = 0; k < V; k++) m = fmax(m, a.v[k]);
+    }
     m = wave_max_t(m);
     T s = 0;
-    for (int64_t c = lane; c < n; c += 64) {
-        const T e = exp_t(xr[c] - m);
-        yr[c] = e;
-        s += e;
+    for (int64_t c = lane; c < nv; c += 64) {
+        const RowVec<T, V> a = xr[c];
+#pragma unroll
+        for (int k = 0; k < V; k++) s += exp_t(a.v[k] - m);
     }
     const T inv = (T)1 / wave_sum_t(s);
-    for (int64_t c = lane; c < n; c += 64) yr[c] = yr[c] * inv;
+    for (int64_t c = lane; c < nv; c += 64) {
+        const RowVec<T, V> a = xr[c];
+        RowVec<T, V> o;
+#pragma unroll
+        for (int k = 0; k < V; k++) o.v[k] = exp_t(a.v[k] - m) * inv;
+        yr[c] = o;
+    }
 }
 
 // softmaxAxis general case (softmax.zig:172-213): one thread per
@@ -328,27 +346,44 @@ __global__ void __launch_bounds__(256) ew_softmax_cols_kernel(const T *__restric
 
 // layerNorm (layernorm.zig:123-185): mean = sum * (1/N), variance = sum of
 // squared deviations * (1/N), 1 / sqrt(variance + eps), then
-// (x - mean) * inv_std * gamma + beta.  One wave per instance.
-template <typename T>
+// (x - mean) * inv_std * gamma + beta.  One wave per instance, V
+// consecutive elements per lane and access.
+template <typename T, int V>
 __global__ void __launch_bounds__(256) ew_layernorm_kernel(const T *__restrict__ x, const T *__restrict__ g,
                                                            const T *__restrict__ b, T *__restrict__ y,
                                                            int64_t rows, int64_t n, T eps) {
     const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
     const int lane = threadIdx.x % 64;
     if (r >= rows) return;
-    const T *xr = x + r * n;
-    T *yr = y + r * n;
+    using RV = RowVec<T, V>;
+    const RV *xr = (const RV *)(x + r * n);
+    RV *yr = (RV *)(y + r * n);
+    const int64_t nv = n / V;
     const T inv_n = (T)1 / (T)n;
     T s = 0;
-    for (int64_t c = lane; c < n; c += 64) s += xr[c];
-    const T mean = wave_sum_t(s) * inv_n;
-    T v = 0;
-    for (int64_t c = lane; c < n; c += 64) {
-        const T d = xr[c] - mean;
-        v += d * d;
+    for (int64_t c = lane; c < nv; c += 64) {
+        const RV a = xr[c];
+#pragma unroll
+        for (int k = 0; k < V; k++) s += a.v[k];
     }
-    const T inv_std = (T)1 / sqrt_t(wave_sum_t(v) * inv_n + eps);
-    for (int64_t c = lane; c < n; c += 64) yr[c] = ((xr[c] - mean) * inv_std) * g[c] + b[c];
+    const T mean = wave_sum_t(s) * inv_n;
+    T var = 0;
+    for (int64_t c = lane; c < nv; c += 64) {
+        const RV a = xr[c];
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            const T d = a.v[k] - mean;
+            var += d * d;
+        }
+    }
+    const T inv_std = (T)1 / sqrt_t(wave_sum_t(var) * inv_n + eps);
+    for (int64_t c = lane; c < nv; c += 64) {
+        const RV a = xr[c], gg = ((const RV *)g)[c], bb = ((const RV *)b)[c];
+        RV o;
+#pragma unroll
+        for (int k = 0; k < V; k++) o.v[k] = ((a.v[k] - mean) * inv_std) * gg.v[k] + bb.v[k];
+        yr[c] = o;
+    }
 }
 
 // transpose (transpose.zig): output element o at multi-index i reads the
@@ -835,16 +870,23 @@ struct Planner {
             const int64_t len = n.shape[n.axis];
             for (int i = 0; i < n.axis; i++) outer *= n.shape[i];
             for (int i = n.axis + 1; i < n.ndim; i++) inner *= n.shape[i];
-            if (inner == 1) {
-                hipLaunchKernelGGL((ew_softmax_rows_kernel<T>), dim3((unsigned)((outer + 3) / 4)), dim3(256), 0,
-                                   ctx->stream, (const T *)x, out, outer, len);
-                TZH_LAUNCHED("ew_softmax_rows_kernel");
-            } else {
+            if (inner == 1) return softmax_rows<T>((const T *)x, out, outer, len);
+            if (outer * inner >= 65536) {  // enough columns for one thread each
                 hipLaunchKernelGGL((ew_softmax_cols_kernel<T>), dim3((unsigned)((outer * inner + 255) / 256)), dim3(256),
                                    0, ctx->stream, (const T *)x, out, outer, len, inner);
                 TZH_LAUNCHED("ew_softmax_cols_kernel");
+                return TZH_OK;
             }
-            return TZH_OK;
+            // few long columns: [outer, len, inner] -> [outer, inner, len],
+            // softmax along rows, and back
+            void *t1 = nullptr, *t2 = nullptr;
+            TZH_TRY(temp((size_t)numel * sizeof(T), &t1));
+            TZH_TRY(temp((size_t)numel * sizeof(T), &t2));
+            const int64_t s3[3] = {outer, len, inner}, s3t[3] = {outer, inner, len};
+            const int p021[3] = {0, 2, 1};
+            TZH_TRY(launch_transpose<T>((const T *)x, (T *)t1, 3, s3, p021));
+            TZH_TRY(softmax_rows<T>((const T *)t1, (T *)t2, outer * inner, len));
+            return launch_transpose<T>((const T *)t2, out, 3, s3t, p021);
         }
         if (n.kind == TZH_NODE_LAYERNORM) {
             const void *g = nullptr, *b = nullptr;
@@ -854,28 +896,67 @@ struct Planner {
             for (int i = n.ndim - n.axis; i < n.ndim; i++) len *= n.shape[i];
             const int64_t rows = numel / len;
             // layernorm.zig:15: default_eps is the f32 1e-5, widened for f64
-            hipLaunchKernelGGL((ew_layernorm_kernel<T>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, ctx->stream,
-                               (const T *)x, (const T *)g, (const T *)b, out, rows, len, (T)1e-5f);
+            constexpr int V = 16 / sizeof(T);
+            const dim3 grid((unsigned)((rows + 3) / 4));
+            if (len % V == 0 && aligned16(x) && aligned16(g) && aligned16(b) && aligned16(out))
+                hipLaunchKernelGGL((ew_layernorm_kernel<T, V>), grid, dim3(256), 0, ctx->stream, (const T *)x,
+                                   (const T *)g, (const T *)b, out, rows, len, (T)1e-5f);
+            else
+                hipLaunchKernelGGL((ew_layernorm_kernel<T, 1>), grid, dim3(256), 0, ctx->stream, (const T *)x,
+                                   (const T *)g, (const T *)b, out, rows, len, (T)1e-5f);
             TZH_LAUNCHED("ew_layernorm_kernel");
             return TZH_OK;
         }
         // TZH_NODE_TRANSPOSE
         const tzh_node &c = tape[n.lhs];
+        return launch_transpose<T>((const T *)x, out, n.ndim, c.shape, n.perm);
+    }
+
+    static bool aligned16(const void *p) { return ((uintptr_t)p % 16) == 0; }
+
+    int temp(size_t bytes, void **out) {
+        void *t = nullptr;
+        if (hipMalloc(&t, bytes ? bytes : 16) != hipSuccess) {
+            (void)hipGetLastError();
+            return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "temporary of %zu bytes failed", bytes);
+        }
+        temps.push_back(t);
+        *out = t;
+        return TZH_OK;
+    }
+
+    template <typename T>
+    int softmax_rows(const T *x, T *y, int64_t rows, int64_t len) {
+        constexpr int V = 16 / sizeof(T);
+        const dim3 grid((unsigned)((rows + 3) / 4));
+        if (len % V == 0 && aligned16(x) && aligned16(y))
+            hipLaunchKernelGGL((ew_softmax_rows_kernel<T, V>), grid, dim3(256), 0, ctx->stream, x, y, rows, len);
+        else
+            hipLaunchKernelGGL((ew_softmax_rows_kernel<T, 1>), grid, dim3(256), 0, ctx->stream, x, y, rows, len);
+        TZH_LAUNCHED("ew_softmax_rows_kernel");
+        return TZH_OK;
+    }
+
+    // y = x with its axes permuted: output axis i is input axis perm[i]
+    template <typename T>
+    int launch_transpose(const T *x, T *y, int nd, const int64_t *in_shape, const int32_t *perm) {
         TransposeArgs a;
         std::memset(&a, 0, sizeof a);
-        a.ndim = n.ndim;
+        a.ndim = nd;
         int64_t in_stride[TZH_MAX_RANK];
-        int64_t st = 1;
-        for (int i = c.ndim - 1; i >= 0; i--) {
+        int64_t st = 1, numel = 1;
+        for (int i = nd - 1; i >= 0; i--) {
             in_stride[i] = st;
-            st *= c.shape[i];
+            st *= in_shape[i];
         }
-        for (int i = 0; i < n.ndim; i++) {
-            a.out_shape[i] = n.shape[i];
-            a.src_stride[i] = in_stride[n.perm[i]];
+        for (int i = 0; i < nd; i++) {
+            a.out_shape[i] = in_shape[perm[i]];
+            a.src_stride[i] = in_stride[perm[i]];
+            numel *= in_shape[i];
         }
+        if (numel == 0) return TZH_OK;
         hipLaunchKernelGGL((ew_transpose_kernel<T>), dim3((unsigned)((numel + 255) / 256)), dim3(256), 0, ctx->stream,
-                           (const T *)x, out, a, numel);
+                           x, y, a, numel);
         TZH_LAUNCHED("ew_transpose_kernel");
         return TZH_OK;
     }

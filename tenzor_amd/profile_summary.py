@@ -251,6 +251,39 @@ def gemm() -> None:
     print("config-3 GEMM pair done", flush=True)
 
 
+def nodes() -> None:
+    """Times the eval node kinds (softmax, layernorm, transpose) at sizes
+    well above the caches and prints HBM throughput by algorithmic bytes
+    (each element read once and written once)."""
+    import numpy as np
+    import torch
+
+    from tenzor_amd.expr import LayerNormExpr, Tensor, evalInto
+
+    rng = np.random.default_rng(0)
+    x = Tensor(torch.from_numpy(rng.standard_normal((16384, 4096)).astype(np.float32)).cuda())
+    g = Tensor(torch.ones(4096, device="cuda"))
+    b = Tensor(torch.zeros(4096, device="cuda"))
+    a = Tensor(torch.from_numpy(rng.standard_normal((64, 512, 12, 32)).astype(np.float32)).cuda())
+    cases = [("softmax last axis [16384, 4096] f32", x.softmax(-1), x.numel()),
+             ("softmax axis 0 [16384, 4096] f32", x.softmax(0), x.numel()),
+             ("layernorm last dim [16384, 4096] f32", LayerNormExpr(x, g, b, 1), x.numel()),
+             ("transpose 0213 [64, 512, 12, 32] f32", a.transpose((0, 2, 1, 3)), a.numel())]
+    for name, e, n in cases:
+        out = torch.empty(e.shape, device="cuda")
+        for _ in range(3):
+            evalInto(e, out)
+        torch.cuda.synchronize()
+        s, t = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(20):
+            evalInto(e, out)
+        t.record()
+        torch.cuda.synchronize()
+        us = s.elapsed_time(t) / 20 * 1e3
+        print(f"{name}: {us:.1f} us, {2 * n * 4 / us / 1e3:.0f} GB/s", flush=True)
+
+
 # MI355X: 8 XCDs of 32 CUs, 4 SIMDs per CU.  GRBM_GUI_ACTIVE is summed over
 # the XCDs; TA/TD/TCP `_sum` counters over one instance per CU; the SQ
 # cycle counters over the SIMDs (MFMA busy) or the CUs (LDS active).
@@ -305,6 +338,7 @@ def main(argv=None) -> int:
     sub = ap.add_subparsers(dest="cmd", required=True)
     sub.add_parser("run")
     sub.add_parser("gemm")
+    sub.add_parser("nodes")
     s = sub.add_parser("summarize")
     s.add_argument("--trace")
     s.add_argument("--fetch")
@@ -316,6 +350,8 @@ def main(argv=None) -> int:
         run()
     elif a.cmd == "gemm":
         gemm()
+    elif a.cmd == "nodes":
+        nodes()
     elif a.cmd == "counters":
         sys.stdout.write(counters(a.dirs))
     else:
