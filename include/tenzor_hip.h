@@ -127,13 +127,18 @@ typedef struct {
  *   TZH_NODE_LAYERNORM  lhs = input, rhs = gamma, aux = beta, axis = norm_dims
  *                       (expr.zig:705-747); eps 1e-5 (layernorm.zig:15)
  *   TZH_NODE_TRANSPOSE  lhs = input, perm (expr.zig:925-972)
- *   TZH_NODE_RESHAPE    lhs = input (same element count, contiguous data) */
+ *   TZH_NODE_RESHAPE    lhs = input (same element count, contiguous data)
+ *   TZH_NODE_GATHER     lhs = table [vocab, embed], rhs = an integer index leaf;
+ *                       result shape = indices shape ++ [embed] (expr.zig:775-830).
+ *                       A row whose index is outside [0, vocab) is NaN (the
+ *                       reference panics in safe builds, gather.zig:17-21). */
 
 /* A leaf tensor: contiguous row-major device data (Tensor.data, tensor.zig:28-60). */
 typedef struct {
     const void *data; /* device pointer */
     int32_t ndim;
-    int32_t pad_;
+    int32_t dtype;    /* 0: the expression's element type; TZH_I32, TZH_U32, TZH_I64 or TZH_U64:
+                         the integer indices of a gather node (Tensor(u32, ...), executor.zig:425-477) */
     int64_t shape[TZH_MAX_RANK];
 } tzh_leaf;
 
@@ -144,9 +149,9 @@ typedef struct {
  * the chain below it into its reduction.  Broadcasting follows NumPy rules
  * (shape.zig:168-204, strides.zig:92-121). */
 /* Node kinds evaluated: tensor, constant, unary, binary, reduce, and
- * softmax, layernorm, transpose, reshape (executor.zig:363-535), which are
- * computed into a temporary when another node reads them; matmul and gather
- * give TZH_ERR_UNSUPPORTED_OP. */
+ * softmax, layernorm, transpose, reshape, gather (executor.zig:363-535),
+ * which are computed into a temporary when another node reads them; matmul
+ * gives TZH_ERR_UNSUPPORTED_OP. */
 int tzh_eval_into(tzh_ctx *ctx, const tzh_node *tape, int32_t n_nodes,
                   const tzh_leaf *leaves, int32_t n_leaves, int32_t dtype, void *out);
 

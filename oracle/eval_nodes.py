@@ -3,6 +3,7 @@ layernorm, transpose and reshape nodes (executor.zig:363-535) and of an
 expression tree that mixes them with exact elementwise ops.
 
 Only tests/ may import this module; it is the checker, never shipped.
+Gather is numpy's take on the table; rows outside it are NaN here.
 
 Pinning (tests/test_eval_nodes_oracle.py): the reference's own tests
 (executor.zig:854-1072, softmax.zig:357-490, transpose.zig:146-240),
@@ -53,6 +54,12 @@ def evaluate(expr, host: dict):
     if isinstance(expr, E.BinaryExpr):
         a, b = evaluate(expr.lhs, host), evaluate(expr.rhs, host)
         return {"add": np.add, "sub": np.subtract, "mul": np.multiply}[expr.op](a, b).astype(expr.dtype)
+    if isinstance(expr, E.GatherExpr):
+        table, idx = evaluate(expr.table, host), host[id(expr.indices)]
+        ok = (idx >= 0) & (idx < table.shape[0])
+        out = table[np.where(ok, idx, 0)].astype(table.dtype)
+        out[~ok] = np.nan  # a row outside the table is NaN (the reference panics)
+        return out
     if isinstance(expr, E.SoftmaxExpr):
         return softmax(evaluate(expr.input, host), expr.softmax_axis)
     if isinstance(expr, E.LayerNormExpr):

@@ -70,7 +70,7 @@ class Node(C.Structure):
 
 
 class Leaf(C.Structure):
-    _fields_ = [("data", C.c_void_p), ("ndim", C.c_int32), ("pad_", C.c_int32), ("shape", C.c_int64 * MAX_RANK)]
+    _fields_ = [("data", C.c_void_p), ("ndim", C.c_int32), ("dtype", C.c_int32), ("shape", C.c_int64 * MAX_RANK)]
 
 
 class MatView(C.Structure):

@@ -15,6 +15,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 namespace tzh_ew {
@@ -386,6 +387,22 @@ __global__ void __launch_bounds__(256) ew_layernorm_kernel(const T *__restrict__
     }
 }
 
+// gather (gather.zig:4-39): output row r is table row indices[r]; a row
+// whose index lies outside [0, vocab) is NaN.
+template <typename T, typename I>
+__global__ void __launch_bounds__(256) ew_gather_kernel(const T *__restrict__ table, const I *__restrict__ idx,
+                                                        T *__restrict__ y, int64_t vocab, int64_t embed,
+                                                        int64_t numel) {
+    const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (o >= numel) return;
+    const int64_t row = o / embed, j = o % embed;
+    const I k = idx[row];
+    bool ok;
+    if constexpr (std::is_signed<I>::value) ok = k >= 0 && (int64_t)k < vocab;
+    else ok = (uint64_t)k < (uint64_t)vocab;
+    y[o] = ok ? table[(int64_t)k * embed + j] : (T)NAN;
+}
+
 // transpose (transpose.zig): output element o at multi-index i reads the
 // input at sum_k i[k] * in_stride[perm[k]].
 struct TransposeArgs {
@@ -480,6 +497,8 @@ struct Planner {
             for (int i = 0; i < n.ndim; i++)
                 if (lf.shape[i] != n.shape[i]) return tzh_fail(TZH_ERR_SHAPE, "node %d: leaf shape mismatch", idx);
             if (!lf.data && numel_of(lf.ndim, lf.shape) > 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "leaf %d: null data", n.leaf);
+            if (lf.dtype != 0 && !index_leaf_read_by_gather(idx))
+                return tzh_fail(TZH_ERR_WRONG_DTYPE, "leaf %d: integer tensors are only gather indices", n.leaf);
             return TZH_OK;
         }
         case TZH_NODE_CONSTANT:
@@ -567,6 +586,20 @@ struct Planner {
             }
             return validate(n.lhs);
         }
+        case TZH_NODE_GATHER: {  // expr.zig:775-830
+            if (n.lhs < 0 || n.lhs >= idx || n.rhs < 0 || n.rhs >= idx)
+                return tzh_fail(TZH_ERR_INVALID_ARGS, "node %d: bad operand index", idx);
+            const tzh_node &t = tape[n.lhs], &ix = tape[n.rhs];
+            if (t.ndim != 2) return tzh_fail(TZH_ERR_SHAPE, "Gather table must be 2D [vocab, embed] (node %d)", idx);
+            if (ix.kind != TZH_NODE_TENSOR || ix.leaf < 0 || ix.leaf >= n_leaves || !is_index_dtype(leaves[ix.leaf].dtype))
+                return tzh_fail(TZH_ERR_WRONG_DTYPE, "Gather indices must be an integer tensor (node %d)", idx);
+            if (n.ndim != ix.ndim + 1 || n.shape[n.ndim - 1] != t.shape[1])
+                return tzh_fail(TZH_ERR_SHAPE, "node %d: wrong gather result shape", idx);
+            for (int i = 0; i < ix.ndim; i++)
+                if (n.shape[i] != ix.shape[i]) return tzh_fail(TZH_ERR_SHAPE, "node %d: wrong gather result shape", idx);
+            TZH_TRY(validate(n.lhs));
+            return validate(n.rhs);
+        }
         case TZH_NODE_RESHAPE: {
             if (n.lhs < 0 || n.lhs >= idx) return tzh_fail(TZH_ERR_INVALID_ARGS, "node %d: bad input index", idx);
             const tzh_node &c = tape[n.lhs];
@@ -577,6 +610,22 @@ struct Planner {
         default:
             return tzh_fail(TZH_ERR_UNSUPPORTED_OP, "node kind %d is not evaluated by this backend", n.kind);
         }
+    }
+
+    static bool is_index_dtype(int32_t d) { return d == TZH_I32 || d == TZH_U32 || d == TZH_I64 || d == TZH_U64; }
+
+    // An integer leaf node may be read only as a gather's indices.
+    bool index_leaf_read_by_gather(int32_t leaf_node) const {
+        bool read = false;
+        for (int32_t i = leaf_node + 1; i < n_nodes; i++) {
+            const tzh_node &t = tape[i];
+            const bool as_indices = t.kind == TZH_NODE_GATHER && t.rhs == leaf_node;
+            const bool other = (t.lhs == leaf_node) || (t.rhs == leaf_node && !as_indices) ||
+                               (t.kind == TZH_NODE_LAYERNORM && t.aux == leaf_node);
+            if (other) return false;
+            read = read || as_indices;
+        }
+        return read;
     }
 
     int same_shape(int32_t a, int32_t b) const {
@@ -590,7 +639,7 @@ struct Planner {
     // Nodes computed by a kernel of their own, read by chains as leaves.
     static bool materialised_kind(int k) {
         return k == TZH_NODE_REDUCE || k == TZH_NODE_SOFTMAX || k == TZH_NODE_LAYERNORM || k == TZH_NODE_TRANSPOSE ||
-               k == TZH_NODE_RESHAPE;
+               k == TZH_NODE_RESHAPE || k == TZH_NODE_GATHER;
     }
 
     // Nodes evaluated into a temporary before the program that reads them
@@ -905,6 +954,20 @@ struct Planner {
                 hipLaunchKernelGGL((ew_layernorm_kernel<T, 1>), grid, dim3(256), 0, ctx->stream, (const T *)x,
                                    (const T *)g, (const T *)b, out, rows, len, (T)1e-5f);
             TZH_LAUNCHED("ew_layernorm_kernel");
+            return TZH_OK;
+        }
+        if (n.kind == TZH_NODE_GATHER) {
+            const tzh_node &t = tape[n.lhs];
+            const tzh_leaf &il = leaves[tape[n.rhs].leaf];
+            const dim3 grid((unsigned)((numel + 255) / 256));
+            const T *tab = (const T *)x;
+            switch (il.dtype) {
+            case TZH_I32: hipLaunchKernelGGL((ew_gather_kernel<T, int32_t>), grid, dim3(256), 0, ctx->stream, tab, (const int32_t *)il.data, out, t.shape[0], t.shape[1], numel); break;
+            case TZH_U32: hipLaunchKernelGGL((ew_gather_kernel<T, uint32_t>), grid, dim3(256), 0, ctx->stream, tab, (const uint32_t *)il.data, out, t.shape[0], t.shape[1], numel); break;
+            case TZH_I64: hipLaunchKernelGGL((ew_gather_kernel<T, int64_t>), grid, dim3(256), 0, ctx->stream, tab, (const int64_t *)il.data, out, t.shape[0], t.shape[1], numel); break;
+            default: hipLaunchKernelGGL((ew_gather_kernel<T, uint64_t>), grid, dim3(256), 0, ctx->stream, tab, (const uint64_t *)il.data, out, t.shape[0], t.shape[1], numel); break;
+            }
+            TZH_LAUNCHED("ew_gather_kernel");
             return TZH_OK;
         }
         // TZH_NODE_TRANSPOSE

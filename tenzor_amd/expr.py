@@ -28,6 +28,8 @@ BINARY_OPS = ("add", "sub", "mul", "div", "pow", "max", "min", "mod", "atan2", "
 REDUCE_OPS = ("sum", "prod", "reduce_max", "reduce_min", "mean", "variance")
 
 _DTYPES = {"float32": _abi.F32, "float64": _abi.F64}
+# integer leaves, allowed only as gather indices (TZH_I32, TZH_I64)
+_INDEX_DTYPES = {"int32": 6, "int64": 7}
 
 
 def broadcast_shape(a: Sequence[int], b: Sequence[int]) -> tuple:
@@ -114,8 +116,9 @@ class Tensor(Expr):
     kind = _abi.NODE_TENSOR
 
     def __init__(self, data):
-        if data.dtype.is_floating_point is False or str(data.dtype).replace("torch.", "") not in _DTYPES:
-            raise TypeError(f"element type {data.dtype} is not supported (float32, float64)")
+        name = str(data.dtype).replace("torch.", "")
+        if name not in _DTYPES and name not in _INDEX_DTYPES:
+            raise TypeError(f"element type {data.dtype} is not supported (float32, float64; int32/int64 indices)")
         if not data.is_contiguous():
             raise ValueError("leaf tensors must be contiguous row-major")
         if len(data.shape) > _abi.MAX_RANK:
@@ -179,6 +182,22 @@ class ReduceExpr(Expr):
         self.axes, self.keepdims = tuple(axes), keepdims
         self.shape = reduce_shape(input.shape, self.axes, keepdims)
         self.dtype = input.dtype
+
+
+class GatherExpr(Expr):
+    """GatherExpr (expr.zig:775-830): rows of a 2-D table [vocab, embed]
+    picked by an integer index tensor; shape = indices.shape ++ [embed]."""
+
+    kind = _abi.NODE_GATHER
+
+    def __init__(self, table: Expr, indices: "Tensor"):
+        if len(table.shape) != 2:
+            raise TypeError(f"Gather table must be 2D [vocab, embed], got {len(table.shape)}D")
+        if not isinstance(indices, Tensor) or indices.dtype not in _INDEX_DTYPES:
+            raise TypeError("Gather indices must be an integer tensor")
+        self.table, self.indices = table, indices
+        self.shape = tuple(indices.shape) + (table.shape[1],)
+        self.dtype = table.dtype
 
 
 class SoftmaxExpr(Expr):
@@ -280,6 +299,9 @@ def to_tape(expr: Expr):
             if e.axes:
                 ax = e.axes[0]
                 n.axis = ax + len(e.input.shape) if ax < 0 else ax
+        elif isinstance(e, GatherExpr):
+            n.lhs = visit(e.table)
+            n.rhs = visit(e.indices)
         elif isinstance(e, SoftmaxExpr):
             n.lhs = visit(e.input)
             n.axis = e.softmax_axis
@@ -308,6 +330,7 @@ def _leaf_structs(leaves) -> "C.Array":
     for i, t in enumerate(leaves):
         arr[i].data = t.data.data_ptr()
         arr[i].ndim = len(t.shape)
+        arr[i].dtype = _INDEX_DTYPES.get(t.dtype, 0)
         for j, d in enumerate(t.shape):
             arr[i].shape[j] = d
     return arr

@@ -386,6 +386,7 @@ def eval_lib(expr):
     for i, t in enumerate(leaves):
         arr[i].data = t.data.data_ptr()
         arr[i].ndim = len(t.shape)
+        arr[i].dtype = {"int32": _abi.I32, "int64": _abi.I64}.get(t.dtype, 0)
         for j, d in enumerate(t.shape):
             arr[i].shape[j] = d
     tape = (_abi.Node * len(nodes))(*nodes)
@@ -428,6 +429,22 @@ def group_nodes():
         e = LayerNormExpr(tx, tg2, tb2, 2)
         rc, out = eval_lib(e)
         assert rc == 0 and np.abs(out - en.evaluate(e, host)).max() <= 10 * tol
+    # gather: int32 / int64 indices, a computed table, a chain after it,
+    # and a row outside the table (NaN)
+    from tenzor_amd.expr import GatherExpr
+
+    tab = rng.standard_normal((50, 36)).astype(np.float32)
+    tt = T(tab)
+    for it in (np.int32, np.int64):
+        idx = rng.integers(0, 50, size=(3, 7)).astype(it)
+        idx[1, 2] = 50
+        ti = T(idx, it)
+        host = {id(tt): tab, id(ti): idx}
+        for e in [GatherExpr(tt, ti), GatherExpr(tt.mul(2.0), ti).add(1.0)]:
+            rc, out = eval_lib(e)
+            assert rc == 0, L.tzh_last_error()
+            ref = en.evaluate(e, host)
+            assert np.array_equal(np.isnan(out), np.isnan(ref)) and np.array_equal(np.nan_to_num(out), np.nan_to_num(ref))
     # errors the planner raises for malformed tapes
     nodes, leaves = to_tape(T(np.zeros((2, 3), np.float32)).transpose((1, 0)))
     nodes[1].perm[1] = 1  # not a permutation

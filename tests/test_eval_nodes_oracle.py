@@ -87,3 +87,25 @@ def test_mirror_shapes_and_tape():
                                        _abi.NODE_TRANSPOSE]
     assert nodes[3].axis == 2 and nodes[3].rhs == 1 and nodes[3].aux == 2
     assert list(nodes[4].perm)[:3] == [1, 0, 2]
+
+
+def test_gather_oracle_and_mirror():
+    """The reference's gather known answer (executor.zig:1074-1115) through
+    the restatement; index rules of the mirror (expr.zig:775-830)."""
+    from tenzor_amd.expr import GatherExpr
+
+    tab = np.arange(1, 13, dtype=np.float32).reshape(4, 3)
+    t = Tensor.__new__(Tensor)
+    t.shape, t.dtype = (4, 3), "float32"
+    i = Tensor.__new__(Tensor)
+    i.shape, i.dtype = (3,), "int32"
+    e = GatherExpr(t, i)
+    assert e.shape == (3, 3)
+    got = en.evaluate(e, {id(t): tab, id(i): np.array([0, 2, 1], np.int32)})
+    assert got.tolist() == [[1, 2, 3], [7, 8, 9], [4, 5, 6]]
+    got = en.evaluate(e, {id(t): tab, id(i): np.array([0, 4, -1], np.int32)})
+    assert np.isnan(got[1:]).all() and got[0].tolist() == [1, 2, 3]
+    with pytest.raises(TypeError):
+        GatherExpr(t, t)  # float indices
+    nodes, leaves = to_tape(e)
+    assert nodes[-1].kind == _abi.NODE_GATHER and nodes[-1].lhs == 0 and nodes[-1].rhs == 1

@@ -92,3 +92,37 @@ def test_malformed_layernorm_is_rejected():
                              C.c_void_p(out.data_ptr()))
     assert rc == -10  # TZH_ERR_SHAPE
 
+
+
+def test_gather_reference_known_answers():
+    """executor.zig:1074-1168: rows of a [4, 3] table by [0, 2, 1]; a
+    [10, 4] table whose row i holds i, by [[0, 5, 9], [1, 2, 3]]."""
+    from tenzor_amd.expr import GatherExpr
+
+    table = leaf(np.arange(1, 13, dtype=np.float32).reshape(4, 3))
+    idx = Tensor(torch.tensor([0, 2, 1], dtype=torch.int32).cuda())
+    got = eval(GatherExpr(table, idx)).cpu().numpy()
+    assert got.tolist() == [[1, 2, 3], [7, 8, 9], [4, 5, 6]]
+    table = leaf(np.repeat(np.arange(10, dtype=np.float32), 4).reshape(10, 4))
+    idx = Tensor(torch.tensor([[0, 5, 9], [1, 2, 3]], dtype=torch.int64).cuda())
+    got = eval(GatherExpr(table, idx)).cpu().numpy()
+    assert got.shape == (2, 3, 4) and np.array_equal(got[..., 0], [[0, 5, 9], [1, 2, 3]])
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_gather_chains_and_out_of_range(dt):
+    from tenzor_amd.expr import GatherExpr
+
+    rng = np.random.default_rng(8)
+    tab = rng.standard_normal((30522, 384)).astype(dt)
+    idx = rng.integers(0, 30522, size=(16, 128)).astype(np.int32)
+    idx[3, 5] = 30522
+    idx[7, 0] = -1
+    tt, ti = leaf(tab), Tensor(torch.from_numpy(idx).cuda())
+    host = {id(tt): tab, id(ti): idx}
+    for e in [GatherExpr(tt, ti), GatherExpr(tt, ti).mul(2.0).add(1.0), GatherExpr(tt, ti).softmax(-1)]:
+        got = eval(e).cpu().numpy()
+        ref = en.evaluate(e, host)
+        nan = np.isnan(ref)
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.abs(got[~nan] - ref[~nan]).max() <= (1e-5 if dt == np.float32 else 1e-12) * max(1.0, np.abs(ref[~nan]).max())
