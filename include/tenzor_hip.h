@@ -128,6 +128,7 @@ typedef struct {
  *                       (expr.zig:705-747); eps 1e-5 (layernorm.zig:15)
  *   TZH_NODE_TRANSPOSE  lhs = input, perm (expr.zig:925-972)
  *   TZH_NODE_RESHAPE    lhs = input (same element count, contiguous data)
+ *   TZH_NODE_MATMUL     lhs, rhs (executor.zig:199-326)
  *   TZH_NODE_GATHER     lhs = table [vocab, embed], rhs = an integer index leaf;
  *                       result shape = indices shape ++ [embed] (expr.zig:775-830).
  *                       A row whose index is outside [0, vocab) is NaN (the
@@ -149,9 +150,11 @@ typedef struct {
  * the chain below it into its reduction.  Broadcasting follows NumPy rules
  * (shape.zig:168-204, strides.zig:92-121). */
 /* Node kinds evaluated: tensor, constant, unary, binary, reduce, and
- * softmax, layernorm, transpose, reshape, gather (executor.zig:363-535),
- * which are computed into a temporary when another node reads them; matmul
- * gives TZH_ERR_UNSUPPORTED_OP. */
+ * matmul, softmax, layernorm, transpose, reshape, gather
+ * (executor.zig:199-535), which are computed into a temporary when another
+ * node reads them.  Matmul follows numpy's rules: a 1-D lhs is a row and a
+ * 1-D rhs a column whose unit dimension the result drops; batch dimensions
+ * broadcast (at most 65 535 batches). */
 int tzh_eval_into(tzh_ctx *ctx, const tzh_node *tape, int32_t n_nodes,
                   const tzh_leaf *leaves, int32_t n_leaves, int32_t dtype, void *out);
 

@@ -3,7 +3,9 @@ layernorm, transpose and reshape nodes (executor.zig:363-535) and of an
 expression tree that mixes them with exact elementwise ops.
 
 Only tests/ may import this module; it is the checker, never shipped.
-Gather is numpy's take on the table; rows outside it are NaN here.
+Gather is numpy's take on the table; rows outside it are NaN here.  Matmul
+is numpy's matmul in float64, rounded to the element type (the reference's
+BLAS summation order is unobservable; tests bound the difference).
 
 Pinning (tests/test_eval_nodes_oracle.py): the reference's own tests
 (executor.zig:854-1072, softmax.zig:357-490, transpose.zig:146-240),
@@ -54,6 +56,9 @@ def evaluate(expr, host: dict):
     if isinstance(expr, E.BinaryExpr):
         a, b = evaluate(expr.lhs, host), evaluate(expr.rhs, host)
         return {"add": np.add, "sub": np.subtract, "mul": np.multiply}[expr.op](a, b).astype(expr.dtype)
+    if isinstance(expr, E.MatmulExpr):
+        a, b = evaluate(expr.lhs, host), evaluate(expr.rhs, host)
+        return np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(a.dtype)
     if isinstance(expr, E.GatherExpr):
         table, idx = evaluate(expr.table, host), host[id(expr.indices)]
         ok = (idx >= 0) & (idx < table.shape[0])

@@ -403,6 +403,47 @@ __global__ void __launch_bounds__(256) ew_gather_kernel(const T *__restrict__ ta
     y[o] = ok ? table[(int64_t)k * embed + j] : (T)NAN;
 }
 
+// matmul (executor.zig:199-326, matmul.zig): C[b] = A[b] B[b] over
+// broadcast batch dimensions, 16 x 16 output tiles staged through LDS, each
+// output summed over k in ascending order.
+struct MatmulArgs {
+    int32_t nb;  // batch dimensions of the output
+    int64_t batch_shape[TZH_MAX_RANK];
+    int64_t a_stride[TZH_MAX_RANK], b_stride[TZH_MAX_RANK];  // 0 where broadcast
+    int64_t m, k, n;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) ew_matmul_kernel(const T *__restrict__ A, const T *__restrict__ B,
+                                                        T *__restrict__ C, const MatmulArgs a) {
+    __shared__ T as[16][17], bs[16][17];
+    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    const int64_t row = (int64_t)blockIdx.y * 16 + ty, col = (int64_t)blockIdx.x * 16 + tx;
+    int64_t rem = blockIdx.z, ao = 0, bo = 0;
+    for (int d = a.nb - 1; d >= 0; d--) {
+        const int64_t i = rem % a.batch_shape[d];
+        rem /= a.batch_shape[d];
+        ao += i * a.a_stride[d];
+        bo += i * a.b_stride[d];
+    }
+    T acc = 0;
+    for (int64_t k0 = 0; k0 < a.k; k0 += 16) {
+        as[ty][tx] = (row < a.m && k0 + tx < a.k) ? A[ao + row * a.k + k0 + tx] : (T)0;
+        bs[ty][tx] = (k0 + ty < a.k && col < a.n) ? B[bo + (k0 + ty) * a.n + col] : (T)0;
+        __syncthreads();
+        const int kk = (int)(a.k - k0 < 16 ? a.k - k0 : 16);
+        for (int q = 0; q < kk; q++) acc += as[ty][q] * bs[q][tx];
+        __syncthreads();
+    }
+    if (row < a.m && col < a.n) C[(int64_t)blockIdx.z * a.m * a.n + row * a.n + col] = acc;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) ew_fill_kernel(T *__restrict__ y, int64_t numel) {
+    const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (o < numel) y[o] = (T)0;
+}
+
 // transpose (transpose.zig): output element o at multi-index i reads the
 // input at sum_k i[k] * in_stride[perm[k]].
 struct TransposeArgs {
@@ -586,6 +627,19 @@ struct Planner {
             }
             return validate(n.lhs);
         }
+        case TZH_NODE_MATMUL: {  // numpy matmul shape rules (executor.zig:199-326)
+            if (n.lhs < 0 || n.lhs >= idx || n.rhs < 0 || n.rhs >= idx)
+                return tzh_fail(TZH_ERR_INVALID_ARGS, "node %d: bad operand index", idx);
+            MatmulArgs ma;
+            int64_t want[TZH_MAX_RANK];
+            int wn = 0;
+            TZH_TRY(matmul_plan(idx, ma, want, &wn));
+            if (n.ndim != wn) return tzh_fail(TZH_ERR_SHAPE, "node %d: wrong matmul result rank", idx);
+            for (int i = 0; i < wn; i++)
+                if (n.shape[i] != want[i]) return tzh_fail(TZH_ERR_SHAPE, "node %d: wrong matmul result shape", idx);
+            TZH_TRY(validate(n.lhs));
+            return validate(n.rhs);
+        }
         case TZH_NODE_GATHER: {  // expr.zig:775-830
             if (n.lhs < 0 || n.lhs >= idx || n.rhs < 0 || n.rhs >= idx)
                 return tzh_fail(TZH_ERR_INVALID_ARGS, "node %d: bad operand index", idx);
@@ -610,6 +664,41 @@ struct Planner {
         default:
             return tzh_fail(TZH_ERR_UNSUPPORTED_OP, "node kind %d is not evaluated by this backend", n.kind);
         }
+    }
+
+    // Batch strides, m/k/n and the result shape of a matmul node: a 1-D lhs
+    // is a row [1, k] and a 1-D rhs a column [k, 1] whose unit dimension
+    // the result drops; batch dimensions broadcast.
+    int matmul_plan(int32_t idx, MatmulArgs &ma, int64_t *out_shape, int *out_nd) const {
+        const tzh_node &n = tape[idx], &l = tape[n.lhs], &r = tape[n.rhs];
+        if (l.ndim < 1 || r.ndim < 1) return tzh_fail(TZH_ERR_SHAPE, "node %d: matmul of a scalar", idx);
+        std::memset(&ma, 0, sizeof ma);
+        const int64_t m = l.ndim == 1 ? 1 : l.shape[l.ndim - 2], k = l.shape[l.ndim - 1];
+        const int64_t k2 = r.ndim == 1 ? r.shape[0] : r.shape[r.ndim - 2], nn = r.ndim == 1 ? 1 : r.shape[r.ndim - 1];
+        if (k != k2) return tzh_fail(TZH_ERR_SHAPE, "Matmul inner dimensions differ (node %d)", idx);
+        const int lb = l.ndim > 2 ? l.ndim - 2 : 0, rb = r.ndim > 2 ? r.ndim - 2 : 0;
+        const int nb = lb > rb ? lb : rb;
+        ma.nb = nb;
+        ma.m = m;
+        ma.k = k;
+        ma.n = nn;
+        int64_t as = m * k, bs = k * nn;
+        for (int i = nb - 1; i >= 0; i--) {
+            const int li = i - (nb - lb), ri = i - (nb - rb);
+            const int64_t ld = li >= 0 ? l.shape[li] : 1, rd = ri >= 0 ? r.shape[ri] : 1;
+            if (ld != rd && ld != 1 && rd != 1) return tzh_fail(TZH_ERR_SHAPE, "Matmul batch dimensions not broadcast compatible (node %d)", idx);
+            ma.batch_shape[i] = ld > rd ? ld : rd;
+            ma.a_stride[i] = ld == 1 ? 0 : as;
+            ma.b_stride[i] = rd == 1 ? 0 : bs;
+            if (li >= 0) as *= ld;
+            if (ri >= 0) bs *= rd;
+        }
+        int w = 0;
+        for (int i = 0; i < nb; i++) out_shape[w++] = ma.batch_shape[i];
+        if (l.ndim > 1) out_shape[w++] = m;
+        if (r.ndim > 1) out_shape[w++] = nn;
+        *out_nd = w;
+        return TZH_OK;
     }
 
     static bool is_index_dtype(int32_t d) { return d == TZH_I32 || d == TZH_U32 || d == TZH_I64 || d == TZH_U64; }
@@ -639,7 +728,7 @@ struct Planner {
     // Nodes computed by a kernel of their own, read by chains as leaves.
     static bool materialised_kind(int k) {
         return k == TZH_NODE_REDUCE || k == TZH_NODE_SOFTMAX || k == TZH_NODE_LAYERNORM || k == TZH_NODE_TRANSPOSE ||
-               k == TZH_NODE_RESHAPE || k == TZH_NODE_GATHER;
+               k == TZH_NODE_RESHAPE || k == TZH_NODE_GATHER || k == TZH_NODE_MATMUL;
     }
 
     // Nodes evaluated into a temporary before the program that reads them
@@ -954,6 +1043,26 @@ struct Planner {
                 hipLaunchKernelGGL((ew_layernorm_kernel<T, 1>), grid, dim3(256), 0, ctx->stream, (const T *)x,
                                    (const T *)g, (const T *)b, out, rows, len, (T)1e-5f);
             TZH_LAUNCHED("ew_layernorm_kernel");
+            return TZH_OK;
+        }
+        if (n.kind == TZH_NODE_MATMUL) {
+            const void *bdat = nullptr;
+            TZH_TRY(input_data(n.rhs, &bdat));
+            MatmulArgs ma;
+            int64_t shp[TZH_MAX_RANK];
+            int nd = 0;
+            TZH_TRY(matmul_plan(idx, ma, shp, &nd));
+            int64_t batches = 1;
+            for (int i = 0; i < ma.nb; i++) batches *= ma.batch_shape[i];
+            if (batches > 65535) return tzh_fail(TZH_ERR_TOO_LARGE, "matmul with %lld batches", (long long)batches);
+            if (ma.k == 0) {  // empty sums
+                hipLaunchKernelGGL((ew_fill_kernel<T>), dim3((unsigned)((numel + 255) / 256)), dim3(256), 0, ctx->stream, out, numel);
+                TZH_LAUNCHED("ew_fill_kernel");
+                return TZH_OK;
+            }
+            const dim3 grid((unsigned)((ma.n + 15) / 16), (unsigned)((ma.m + 15) / 16), (unsigned)batches);
+            hipLaunchKernelGGL((ew_matmul_kernel<T>), grid, dim3(256), 0, ctx->stream, (const T *)x, (const T *)bdat, out, ma);
+            TZH_LAUNCHED("ew_matmul_kernel");
             return TZH_OK;
         }
         if (n.kind == TZH_NODE_GATHER) {

@@ -89,6 +89,7 @@ class Expr:
     def minimum(self, o): return BinaryExpr("min", self, as_expr(o, self.dtype))
 
     # reductions over all axes (expr.zig:323-342)
+    def matmul(self, o): return MatmulExpr(self, o)
     def softmax(self, axis: int): return SoftmaxExpr(self, axis)
     def transpose(self, perm): return TransposeExpr(self, perm)
     def reshape(self, shape): return ReshapeExpr(self, shape)
@@ -182,6 +183,28 @@ class ReduceExpr(Expr):
         self.axes, self.keepdims = tuple(axes), keepdims
         self.shape = reduce_shape(input.shape, self.axes, keepdims)
         self.dtype = input.dtype
+
+
+class MatmulExpr(Expr):
+    """MatmulExpr (executor.zig:199-326): 1-D operands are a row / a column
+    whose unit dimension the result drops; batch dimensions broadcast."""
+
+    kind = _abi.NODE_MATMUL
+
+    def __init__(self, lhs: Expr, rhs: Expr):
+        if lhs.dtype != rhs.dtype:
+            raise TypeError(f"Type mismatch in matmul: {lhs.dtype} vs {rhs.dtype}")
+        ls, rs = tuple(lhs.shape), tuple(rhs.shape)
+        if not ls or not rs:
+            raise TypeError("matmul needs operands of rank >= 1")
+        k = ls[-1]
+        k2 = rs[0] if len(rs) == 1 else rs[-2]
+        if k != k2:
+            raise TypeError(f"Matmul inner dimensions differ: {k} vs {k2}")
+        batch = broadcast_shape(ls[:-2], rs[:-2]) if (len(ls) > 2 or len(rs) > 2) else ()
+        self.lhs, self.rhs = lhs, rhs
+        self.shape = tuple(batch) + ((ls[-2],) if len(ls) > 1 else ()) + ((rs[-1],) if len(rs) > 1 else ())
+        self.dtype = lhs.dtype
 
 
 class GatherExpr(Expr):
@@ -299,6 +322,9 @@ def to_tape(expr: Expr):
             if e.axes:
                 ax = e.axes[0]
                 n.axis = ax + len(e.input.shape) if ax < 0 else ax
+        elif isinstance(e, MatmulExpr):
+            n.lhs = visit(e.lhs)
+            n.rhs = visit(e.rhs)
         elif isinstance(e, GatherExpr):
             n.lhs = visit(e.table)
             n.rhs = visit(e.indices)

@@ -445,6 +445,19 @@ def group_nodes():
             assert rc == 0, L.tzh_last_error()
             ref = en.evaluate(e, host)
             assert np.array_equal(np.isnan(out), np.isnan(ref)) and np.array_equal(np.nan_to_num(out), np.nan_to_num(ref))
+    # matmul: 1-D / 2-D / batched / broadcast batches, a chain after it,
+    # softmax over its rows (executor.zig:675-970 shapes)
+    for sa, sb in [((7,), (7,)), ((7,), (7, 5)), ((9, 7), (7,)), ((9, 7), (7, 20)), ((3, 9, 7), (3, 7, 20)),
+                   ((3, 9, 7), (7, 20)), ((2, 1, 9, 7), (3, 7, 20)), ((33, 40), (40, 17))]:
+        A = rng.standard_normal(sa).astype(np.float32)
+        B = rng.standard_normal(sb).astype(np.float32)
+        ta, tb2 = T(A), T(B)
+        host = {id(ta): A, id(tb2): B}
+        for e in [ta.matmul(tb2), ta.matmul(tb2).mul(2.0)] + ([ta.matmul(tb2).softmax(-1)] if len(sb) > 1 else []):
+            rc, out = eval_lib(e)
+            assert rc == 0, L.tzh_last_error()
+            ref = en.evaluate(e, host)
+            assert out.shape == ref.shape and np.abs(out - ref).max() <= 1e-5 * max(1.0, float(np.abs(ref).max())), (sa, sb)
     # errors the planner raises for malformed tapes
     nodes, leaves = to_tape(T(np.zeros((2, 3), np.float32)).transpose((1, 0)))
     nodes[1].perm[1] = 1  # not a permutation

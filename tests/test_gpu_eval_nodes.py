@@ -126,3 +126,33 @@ def test_gather_chains_and_out_of_range(dt):
         nan = np.isnan(ref)
         assert np.array_equal(np.isnan(got), nan)
         assert np.abs(got[~nan] - ref[~nan]).max() <= (1e-5 if dt == np.float32 else 1e-12) * max(1.0, np.abs(ref[~nan]).max())
+
+
+def test_matmul_reference_known_answers():
+    """executor.zig:675-693 ([[1,2],[3,4]] @ [[5,6],[7,8]]) and 936-968
+    (softmax of Q @ K, rows summing to 1)."""
+    a = leaf(np.array([[1, 2], [3, 4]], np.float32))
+    b = leaf(np.array([[5, 6], [7, 8]], np.float32))
+    assert eval(a.matmul(b)).cpu().numpy().tolist() == [[19, 22], [43, 50]]
+    q = leaf(np.array([[1, 0, 0], [0, 1, 0]], np.float32))
+    k = leaf(np.array([[1, 0], [0, 1], [0, 0]], np.float32))
+    y = eval(q.matmul(k).softmax(-1)).cpu().numpy()
+    assert y.shape == (2, 2) and np.allclose(y.sum(1), 1, atol=1e-5)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_matmul_shapes_vs_restatement(dt):
+    rng = np.random.default_rng(9)
+    for sa, sb in [((64,), (64,)), ((64,), (64, 48)), ((100, 64), (64,)), ((129, 300), (300, 77)),
+                   ((12, 65, 32), (12, 32, 65)), ((4, 100, 384), (384, 128)), ((2, 1, 33, 16), (3, 16, 40))]:
+        A = rng.standard_normal(sa).astype(dt)
+        B = rng.standard_normal(sb).astype(dt)
+        ta, tb = leaf(A), leaf(B)
+        host = {id(ta): A, id(tb): B}
+        for e in [ta.matmul(tb), ta.matmul(tb).mul(0.5).add(1.0)]:
+            got = eval(e).cpu().numpy()
+            ref = en.evaluate(e, host)
+            # |sum error| <= k eps sum |a||b|; with unit normals that is below 1e-5 relative (f32)
+            tol = 2e-5 if dt == np.float32 else 1e-12
+            assert got.shape == ref.shape
+            assert np.abs(got - ref).max() <= tol * max(1.0, float(np.abs(ref).max())) * np.sqrt(sa[-1]), (sa, sb)
