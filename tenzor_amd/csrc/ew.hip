@@ -452,6 +452,45 @@ struct TransposeArgs {
     int64_t src_stride[TZH_MAX_RANK];  // input stride of the axis that output axis k reads
 };
 
+// Transposes that move the last axis: 32 x 32 tiles of (output last axis,
+// output axis that reads the input's last axis) through LDS, so that both
+// the reads and the writes run along a contiguous axis.
+struct TileTransposeArgs {
+    int32_t nrest;  // output axes other than the two tiled ones
+    int64_t rest_shape[TZH_MAX_RANK], rest_src[TZH_MAX_RANK], rest_dst[TZH_MAX_RANK];
+    int64_t n_l, n_q;  // extents of the output's last axis and of axis q
+    int64_t src_l;     // input stride of the axis the output's last axis reads
+    int64_t dst_q;     // output stride of axis q
+    int64_t nz;        // product of rest_shape
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) ew_transpose_tiled_kernel(const T *__restrict__ x, T *__restrict__ y,
+                                                                 const TileTransposeArgs a) {
+    __shared__ T tile[32][33];
+    const int tx = threadIdx.x % 32, ty = threadIdx.x / 32;
+    const int64_t l0 = (int64_t)blockIdx.x * 32, q0 = (int64_t)blockIdx.y * 32;
+    for (int64_t z = blockIdx.z; z < a.nz; z += gridDim.z) {
+        int64_t rem = z, sb = 0, db = 0;
+        for (int d = a.nrest - 1; d >= 0; d--) {
+            const int64_t i = rem % a.rest_shape[d];
+            rem /= a.rest_shape[d];
+            sb += i * a.rest_src[d];
+            db += i * a.rest_dst[d];
+        }
+        for (int j = ty; j < 32; j += 8) {
+            const int64_t l = l0 + j, q = q0 + tx;
+            if (l < a.n_l && q < a.n_q) tile[j][tx] = x[sb + l * a.src_l + q];
+        }
+        __syncthreads();
+        for (int j = ty; j < 32; j += 8) {
+            const int64_t q = q0 + j, l = l0 + tx;
+            if (l < a.n_l && q < a.n_q) y[db + q * a.dst_q + l] = tile[tx][j];
+        }
+        __syncthreads();
+    }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(256) ew_transpose_kernel(const T *__restrict__ x, T *__restrict__ y,
                                                            const TransposeArgs a, int64_t numel) {
@@ -1017,9 +1056,12 @@ struct Planner {
             }
             // few long columns: [outer, len, inner] -> [outer, inner, len],
             // softmax along rows, and back
-            void *t1 = nullptr, *t2 = nullptr;
-            TZH_TRY(temp((size_t)numel * sizeof(T), &t1));
-            TZH_TRY(temp((size_t)numel * sizeof(T), &t2));
+            // (the two staging buffers live in the context's grow-only scratch:
+            // a fresh allocation and free per call cost more than the kernels)
+            const size_t bytes = ((size_t)numel * sizeof(T) + 255) & ~(size_t)255;
+            void *scratch = nullptr;
+            TZH_TRY(tzh_ctx_scratch(ctx, 2 * bytes, &scratch));
+            void *t1 = scratch, *t2 = (char *)scratch + bytes;
             const int64_t s3[3] = {outer, len, inner}, s3t[3] = {outer, inner, len};
             const int p021[3] = {0, 2, 1};
             TZH_TRY(launch_transpose<T>((const T *)x, (T *)t1, 3, s3, p021));
@@ -1086,17 +1128,6 @@ struct Planner {
 
     static bool aligned16(const void *p) { return ((uintptr_t)p % 16) == 0; }
 
-    int temp(size_t bytes, void **out) {
-        void *t = nullptr;
-        if (hipMalloc(&t, bytes ? bytes : 16) != hipSuccess) {
-            (void)hipGetLastError();
-            return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "temporary of %zu bytes failed", bytes);
-        }
-        temps.push_back(t);
-        *out = t;
-        return TZH_OK;
-    }
-
     template <typename T>
     int softmax_rows(const T *x, T *y, int64_t rows, int64_t len) {
         constexpr int V = 16 / sizeof(T);
@@ -1127,6 +1158,38 @@ struct Planner {
             numel *= in_shape[i];
         }
         if (numel == 0) return TZH_OK;
+        int q = -1;
+        for (int i = 0; i < nd; i++)
+            if (perm[i] == nd - 1) q = i;
+        if (nd >= 2 && q != nd - 1) {  // the last axis moves: tiles through LDS
+            TileTransposeArgs t;
+            std::memset(&t, 0, sizeof t);
+            int64_t out_stride[TZH_MAX_RANK], os = 1;
+            for (int i = nd - 1; i >= 0; i--) {
+                out_stride[i] = os;
+                os *= a.out_shape[i];
+            }
+            t.n_l = a.out_shape[nd - 1];
+            t.n_q = a.out_shape[q];
+            t.src_l = a.src_stride[nd - 1];
+            t.dst_q = out_stride[q];
+            t.nz = 1;
+            for (int i = 0; i < nd - 1; i++) {
+                if (i == q) continue;
+                t.rest_shape[t.nrest] = a.out_shape[i];
+                t.rest_src[t.nrest] = a.src_stride[i];
+                t.rest_dst[t.nrest] = out_stride[i];
+                t.nz *= a.out_shape[i];
+                t.nrest++;
+            }
+            const int64_t gx = (t.n_l + 31) / 32, gy = (t.n_q + 31) / 32;
+            if (gx <= 0x7fffffff && gy <= 65535) {
+                const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)(t.nz < 65535 ? t.nz : 65535));
+                hipLaunchKernelGGL((ew_transpose_tiled_kernel<T>), grid, dim3(256), 0, ctx->stream, x, y, t);
+                TZH_LAUNCHED("ew_transpose_tiled_kernel");
+                return TZH_OK;
+            }
+        }
         hipLaunchKernelGGL((ew_transpose_kernel<T>), dim3((unsigned)((numel + 255) / 256)), dim3(256), 0, ctx->stream,
                            x, y, a, numel);
         TZH_LAUNCHED("ew_transpose_kernel");

@@ -445,6 +445,13 @@ def group_nodes():
             assert rc == 0, L.tzh_last_error()
             ref = en.evaluate(e, host)
             assert np.array_equal(np.isnan(out), np.isnan(ref)) and np.array_equal(np.nan_to_num(out), np.nan_to_num(ref))
+    # transposes that move the last axis (LDS tiles, partial edges) and
+    # those that keep it, bit-exact
+    xt = rng.standard_normal((3, 37, 5, 70)).astype(np.float32)
+    tt4 = T(xt)
+    for perm in [(0, 1, 3, 2), (3, 2, 1, 0), (1, 3, 0, 2), (0, 2, 1, 3), (2, 0, 1, 3)]:
+        rc, out = eval_lib(tt4.transpose(perm))
+        assert rc == 0 and np.array_equal(out, np.transpose(xt, perm)), perm
     # matmul: 1-D / 2-D / batched / broadcast batches, a chain after it,
     # softmax over its rows (executor.zig:675-970 shapes)
     for sa, sb in [((7,), (7,)), ((7,), (7, 5)), ((9, 7), (7,)), ((9, 7), (7, 20)), ((3, 9, 7), (3, 7, 20)),
