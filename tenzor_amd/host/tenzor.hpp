@@ -77,7 +77,9 @@ enum class OpTag : int32_t {
 
 // NodeKind (expr.zig:137-149)
 enum class NodeKind : int32_t { tensor = TZH_NODE_TENSOR, constant = TZH_NODE_CONSTANT, unary = TZH_NODE_UNARY,
-                                binary = TZH_NODE_BINARY, reduce = TZH_NODE_REDUCE };
+                                binary = TZH_NODE_BINARY, matmul = TZH_NODE_MATMUL, reduce = TZH_NODE_REDUCE,
+                                reshape = TZH_NODE_RESHAPE, transpose = TZH_NODE_TRANSPOSE,
+                                softmax = TZH_NODE_SOFTMAX, layernorm = TZH_NODE_LAYERNORM };
 
 template <typename T>
 constexpr int32_t dtype_of() {
@@ -169,6 +171,8 @@ struct Tape {
 template <OpTag op, typename Input> struct UnaryExpr;
 template <OpTag op, typename Lhs, typename Rhs> struct BinaryExpr;
 template <typename T> struct ScalarExpr;
+template <typename Input, int Axis> struct SoftmaxExpr;
+template <typename Input, int... Perm> struct TransposeExpr;
 
 // Methods every expression has (expr.zig:236-316): unary ops, binary ops
 // with an expression or a scalar, reductions.
@@ -194,6 +198,12 @@ struct ExprMethods {
     TZH_BINARY(add, add) TZH_BINARY(sub, sub) TZH_BINARY(mul, mul) TZH_BINARY(div, div) TZH_BINARY(pow, pow)
     TZH_BINARY(maximum, max) TZH_BINARY(minimum, min)
 #undef TZH_BINARY
+    // softmax(axis) (expr.zig:657-659); a negative axis counts from the end
+    template <int Axis>
+    SoftmaxExpr<Self, Axis> softmax() const { return SoftmaxExpr<Self, Axis>::init(self()); }
+    // transpose(perm) (expr.zig:914-916)
+    template <int... Perm>
+    TransposeExpr<Self, Perm...> transpose() const { return TransposeExpr<Self, Perm...>::init(self()); }
 };
 
 // A concrete tensor: Tensor(T, shape) (tensor.zig:28-249) with device data.
@@ -395,6 +405,103 @@ struct ReduceExpr : ExprMethods<ReduceExpr<op, Input, Axis, KeepDims>> {
         n.lhs = a;
         n.axis = Axis;
         n.keepdims = KeepDims ? 1 : 0;
+        return tape.push(n);
+    }
+};
+
+// SoftmaxExpr(Input, axis) (expr.zig:665-696)
+template <typename Input, int Axis>
+struct SoftmaxExpr : ExprMethods<SoftmaxExpr<Input, Axis>> {
+    static constexpr int ndim = (int)Input::shape.size();
+    static_assert(Axis >= -ndim && Axis < ndim, "softmax axis out of range");
+    static constexpr int softmax_axis = Axis < 0 ? Axis + ndim : Axis;  // shape.normalizeAxis
+    using ElementType = typename Input::ElementType;
+    static constexpr NodeKind kind = NodeKind::softmax;
+    static constexpr auto shape = Input::shape;
+    Input input;
+    static SoftmaxExpr init(const Input &in) {
+        SoftmaxExpr e;
+        e.input = in;
+        return e;
+    }
+    int32_t emit(Tape &tape) const {
+        const int32_t a = input.emit(tape);
+        tzh_node n = Tape::node_of(kind, shape);
+        n.lhs = a;
+        n.axis = softmax_axis;
+        return tape.push(n);
+    }
+};
+
+template <size_t N>
+constexpr bool is_permutation(const std::array<int, N> &p) {
+    for (size_t i = 0; i < N; i++) {
+        if (p[i] < 0 || p[i] >= (int)N) return false;
+        for (size_t j = 0; j < i; j++)
+            if (p[j] == p[i]) return false;
+    }
+    return true;
+}
+
+// TransposeExpr(Input, perm) (expr.zig:925-990): output axis i is input
+// axis perm[i].
+template <typename Input, int... Perm>
+struct TransposeExpr : ExprMethods<TransposeExpr<Input, Perm...>> {
+    static constexpr std::array<int, sizeof...(Perm)> perm{Perm...};
+    static_assert(sizeof...(Perm) == Input::shape.size(), "Permutation length must match rank");
+    static_assert(is_permutation(perm), "Invalid transpose permutation");
+    using ElementType = typename Input::ElementType;
+    static constexpr NodeKind kind = NodeKind::transpose;
+    static constexpr Shape<sizeof...(Perm)> shape{Input::shape[Perm]...};
+    Input input;
+    static TransposeExpr init(const Input &in) {
+        TransposeExpr e;
+        e.input = in;
+        return e;
+    }
+    int32_t emit(Tape &tape) const {
+        const int32_t a = input.emit(tape);
+        tzh_node n = Tape::node_of(kind, shape);
+        n.lhs = a;
+        for (size_t i = 0; i < perm.size(); i++) n.perm[i] = perm[i];
+        return tape.push(n);
+    }
+};
+
+// LayerNormExpr(Input, Gamma, Beta, norm_dims) (expr.zig:705-760)
+template <typename Input, typename Gamma, typename Beta, int NormDims = 1>
+struct LayerNormExpr : ExprMethods<LayerNormExpr<Input, Gamma, Beta, NormDims>> {
+    static constexpr int ndim = (int)Input::shape.size();
+    static_assert(NormDims >= 1 && NormDims <= ndim, "norm_dims out of range");
+    static_assert((int)Gamma::shape.size() == NormDims && (int)Beta::shape.size() == NormDims,
+                  "Gamma/beta rank must equal normalized_dims");
+    static constexpr bool params_match() {
+        for (int i = 0; i < NormDims; i++)
+            if (Gamma::shape[i] != Input::shape[ndim - NormDims + i] || Beta::shape[i] != Gamma::shape[i])
+                return false;
+        return true;
+    }
+    static_assert(params_match(), "Gamma/beta shape must match last dimensions of input");
+    using ElementType = typename Input::ElementType;
+    static constexpr NodeKind kind = NodeKind::layernorm;
+    static constexpr auto shape = Input::shape;
+    Input input;
+    Gamma gamma;
+    Beta beta;
+    static LayerNormExpr init(const Input &in, const Gamma &g, const Beta &b) {
+        LayerNormExpr e;
+        e.input = in;
+        e.gamma = g;
+        e.beta = b;
+        return e;
+    }
+    int32_t emit(Tape &tape) const {
+        const int32_t a = input.emit(tape), g = gamma.emit(tape), b = beta.emit(tape);
+        tzh_node n = Tape::node_of(kind, shape);
+        n.lhs = a;
+        n.rhs = g;
+        n.aux = b;
+        n.axis = NormDims;
         return tape.push(n);
     }
 };

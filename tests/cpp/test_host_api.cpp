@@ -195,6 +195,21 @@ int main(int argc, char **argv) {
         }
     });
 
+    run("softmax, transpose, layernorm nodes", [&] {  // executor.zig:876-1030
+        using Mat = Tensor<float, 2, 3>;
+        auto x = Mat::fromSlice(ctx, {1, 2, 3, 0, 0, 0});
+        const auto s = eval(ctx, x.softmax<-1>()).slice(ctx);
+        EXPECT(std::fabs(s[0] + s[1] + s[2] - 1.0f) < 1e-5f && std::fabs(s[3] - 1.0f / 3.0f) < 1e-5f);
+        const auto t = eval(ctx, x.transpose<1, 0>()).slice(ctx);
+        EXPECT(t == std::vector<float>({1, 0, 2, 0, 3, 0}));
+        using Row = Tensor<float, 3>;
+        auto g = Row::fromSlice(ctx, {1, 1, 1});
+        auto b = Row::fromSlice(ctx, {0, 0, 0});
+        auto y = Mat::fromSlice(ctx, {1, 2, 3, 10, 20, 30});
+        const auto l = eval(ctx, LayerNormExpr<Mat, Row, Row, 1>::init(y, g, b)).slice(ctx);
+        EXPECT(std::fabs(l[0] + l[1] + l[2]) < 1e-5f && std::fabs(l[0] - l[3]) < 1e-5f);
+    });
+
     // the reference's tokenizer tests (tokenizer.zig:291-437): vocabulary
     // entries put directly, output capacity 32
     run("tokenizer: the reference's known answers", [&] {

@@ -46,6 +46,12 @@ def test_header_compiles_with_the_reference_surface(tmp_path):
      "reduction axis out of range"),
     ("Tensor<float, 3> a; auto e = ReduceExpr<OpTag::add, Tensor<float, 3>>::init(a); (void)e;",
      "Unsupported reduce operation"),
+    # expr.zig:932-952 and 705-735
+    ("Tensor<float, 2, 3> a; auto e = a.transpose<0, 0>(); (void)e;", "Invalid transpose permutation"),
+    ("Tensor<float, 2, 3> a; auto e = a.transpose<1, 0, 2>(); (void)e;", "Permutation length must match rank"),
+    ("Tensor<float, 2, 3> a; Tensor<float, 4> g; auto e = LayerNormExpr<Tensor<float, 2, 3>, Tensor<float, 4>, "
+     "Tensor<float, 4>, 1>::init(a, g, g); (void)e;", "Gamma/beta shape must match last dimensions of input"),
+    ("Tensor<float, 2, 3> a; auto e = a.softmax<2>(); (void)e;", "softmax axis out of range"),
 ])
 def test_compile_time_errors_mirror_comptime_errors(tmp_path, body, message):
     res = compile_snippet(body, tmp_path)
