@@ -173,6 +173,7 @@ template <OpTag op, typename Lhs, typename Rhs> struct BinaryExpr;
 template <typename T> struct ScalarExpr;
 template <typename Input, int Axis> struct SoftmaxExpr;
 template <typename Input, int... Perm> struct TransposeExpr;
+template <typename Input, int64_t... Dims> struct ReshapeExpr;
 
 // Methods every expression has (expr.zig:236-316): unary ops, binary ops
 // with an expression or a scalar, reductions.
@@ -204,6 +205,9 @@ struct ExprMethods {
     // transpose(perm) (expr.zig:914-916)
     template <int... Perm>
     TransposeExpr<Self, Perm...> transpose() const { return TransposeExpr<Self, Perm...>::init(self()); }
+    // reshape(target_shape) (expr.zig:918-920)
+    template <int64_t... Dims>
+    ReshapeExpr<Self, Dims...> reshape() const { return ReshapeExpr<Self, Dims...>::init(self()); }
 };
 
 // A concrete tensor: Tensor(T, shape) (tensor.zig:28-249) with device data.
@@ -464,6 +468,27 @@ struct TransposeExpr : ExprMethods<TransposeExpr<Input, Perm...>> {
         tzh_node n = Tape::node_of(kind, shape);
         n.lhs = a;
         for (size_t i = 0; i < perm.size(); i++) n.perm[i] = perm[i];
+        return tape.push(n);
+    }
+};
+
+// ReshapeExpr(Input, target_shape): the same elements under another shape.
+template <typename Input, int64_t... Dims>
+struct ReshapeExpr : ExprMethods<ReshapeExpr<Input, Dims...>> {
+    using ElementType = typename Input::ElementType;
+    static constexpr NodeKind kind = NodeKind::reshape;
+    static constexpr Shape<sizeof...(Dims)> shape{Dims...};
+    static_assert(numel(shape) == numel(Input::shape), "Reshape must preserve the element count");
+    Input input;
+    static ReshapeExpr init(const Input &in) {
+        ReshapeExpr e;
+        e.input = in;
+        return e;
+    }
+    int32_t emit(Tape &tape) const {
+        const int32_t a = input.emit(tape);
+        tzh_node n = Tape::node_of(kind, shape);
+        n.lhs = a;
         return tape.push(n);
     }
 };

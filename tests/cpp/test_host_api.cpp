@@ -195,13 +195,15 @@ int main(int argc, char **argv) {
         }
     });
 
-    run("softmax, transpose, layernorm nodes", [&] {  // executor.zig:876-1030
+    run("softmax, transpose, reshape, layernorm nodes", [&] {  // executor.zig:876-1030
         using Mat = Tensor<float, 2, 3>;
         auto x = Mat::fromSlice(ctx, {1, 2, 3, 0, 0, 0});
         const auto s = eval(ctx, x.softmax<-1>()).slice(ctx);
         EXPECT(std::fabs(s[0] + s[1] + s[2] - 1.0f) < 1e-5f && std::fabs(s[3] - 1.0f / 3.0f) < 1e-5f);
         const auto t = eval(ctx, x.transpose<1, 0>()).slice(ctx);
         EXPECT(t == std::vector<float>({1, 0, 2, 0, 3, 0}));
+        const auto r = eval(ctx, x.reshape<3, 2>().add(1.0f)).slice(ctx);
+        EXPECT(r == std::vector<float>({2, 3, 4, 1, 1, 1}));
         using Row = Tensor<float, 3>;
         auto g = Row::fromSlice(ctx, {1, 1, 1});
         auto b = Row::fromSlice(ctx, {0, 0, 0});

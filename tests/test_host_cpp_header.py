@@ -52,6 +52,7 @@ def test_header_compiles_with_the_reference_surface(tmp_path):
     ("Tensor<float, 2, 3> a; Tensor<float, 4> g; auto e = LayerNormExpr<Tensor<float, 2, 3>, Tensor<float, 4>, "
      "Tensor<float, 4>, 1>::init(a, g, g); (void)e;", "Gamma/beta shape must match last dimensions of input"),
     ("Tensor<float, 2, 3> a; auto e = a.softmax<2>(); (void)e;", "softmax axis out of range"),
+    ("Tensor<float, 2, 3> a; auto e = a.reshape<4, 2>(); (void)e;", "Reshape must preserve the element count"),
 ])
 def test_compile_time_errors_mirror_comptime_errors(tmp_path, body, message):
     res = compile_snippet(body, tmp_path)
