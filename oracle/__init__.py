@@ -101,6 +101,17 @@ def matmul_w8a32(a, wq, scale, bias=None):
     return c
 
 
+def linear_f32(a, w, bias=None):
+    """The f32 model's linear (arctic.zig:609-621): C = A W^T, then += bias."""
+    a, w = _f32(a), _f32(w)
+    m, k = a.shape
+    n = w.shape[0]
+    c = np.empty((m, n), np.float32)
+    b = None if bias is None else _f32(bias)
+    lib().orc_linear_f32(a.ctypes.data, w.ctypes.data, None if b is None else b.ctypes.data, c.ctypes.data, m, k, n)
+    return c
+
+
 def layernorm(x, gamma, beta, eps):
     x = _f32(x)
     rows, n = x.reshape(-1, x.shape[-1]).shape

@@ -609,6 +609,10 @@ static int check_broadcast(const tzh_node *n, const tzh_node *l, const tzh_node 
         int64_t b = (i - (nd - r->ndim) >= 0) ? r->shape[i - (nd - r->ndim)] : 1;
         if (a != b && a != 1 && b != 1) return TZH_ERR_SHAPE;
         if (n->shape[i] != (a > b ? a : b)) return TZH_ERR_SHAPE;
+        /* @max(0, 1) = 1: the result has an element the empty operand
+           cannot supply; executor.zig:139-144 would index past its slice
+           (a bounds panic in a safe build), so this is an error here */
+        if ((a == 0 || b == 0) && n->shape[i] != 0) return TZH_ERR_SHAPE;
     }
     return 0;
 }

@@ -39,12 +39,8 @@ namespace {
 using namespace tzh_ew;
 
 // Chains run as generated kernels (ew_jit.cpp) unless the context asks for
-// the interpreter; the CPU emulation build has no run-time compiler.
-#ifdef TZH_EMULATION
-constexpr bool kHaveJit = false;
-#else
+// the interpreter.
 constexpr bool kHaveJit = true;
-#endif
 
 template <typename T, int V>
 struct Vec {
@@ -604,6 +600,13 @@ struct Planner {
                 const int64_t a = li >= 0 ? l.shape[li] : 1, b = ri >= 0 ? r.shape[ri] : 1;
                 if (a != b && a != 1 && b != 1) return tzh_fail(TZH_ERR_SHAPE, "Shapes not broadcast compatible (node %d)", idx);
                 if (n.shape[i] != (a > b ? a : b)) return tzh_fail(TZH_ERR_SHAPE, "node %d: wrong broadcast result shape", idx);
+                // shape.zig:196-200 takes @max, so an empty dimension against
+                // a 1 gives a result of extent 1 whose element would be read
+                // from the empty operand (the reference's slice access panics
+                // there in a safe build): refuse it instead of reading past
+                // an empty buffer.
+                if ((a == 0 || b == 0) && n.shape[i] != 0)
+                    return tzh_fail(TZH_ERR_SHAPE, "node %d: broadcast reads an element of an empty operand", idx);
             }
             TZH_TRY(validate(n.lhs));
             return validate(n.rhs);
@@ -840,6 +843,10 @@ struct Planner {
 
     int add_leaf(EwProgram &p, const void *ptr, int32_t lnd, const int64_t *lshape, int vec, int *leaf_idx) {
         if (p.n_leaves >= kMaxLeaves) return tzh_fail(TZH_ERR_INVALID_ARGS, "internal: too many leaves");
+        // every element of the program's output reads every leaf once, so a
+        // leaf with no elements can back only an empty program
+        if (p.numel > 0 && numel_of(lnd, lshape) == 0)
+            return tzh_fail(TZH_ERR_SHAPE, "internal: a non-empty program reads an empty operand");
         EwLeaf &lf = p.leaves[p.n_leaves];
         std::memset(&lf, 0, sizeof lf);
         lf.ptr = ptr;

@@ -13,15 +13,23 @@
 //
 // The op semantics and the program layout are the exact text the
 // interpreter kernels are compiled from (ew_shared.inc, stringified below).
+#include "ew_program.h"
+
+#ifndef TZH_EMULATION
 #include <hip/hiprtc.h>
+#else
+#include <dlfcn.h>
+#include <unistd.h>
+
+#include <cstdio>
+#include <cstdlib>
+#endif
 
 #include <cstring>
 #include <mutex>
 #include <string>
 #include <unordered_map>
 #include <vector>
-
-#include "ew_program.h"
 
 namespace tzh_ew {
 namespace {
@@ -228,6 +236,70 @@ std::string chain_source(const EwProgram &p, bool f64, int V) {
     return s;
 }
 
+#ifdef TZH_EMULATION
+// CPU emulation build (tests/cpu_emu; test infrastructure only): the same
+// generated text is compiled as C++ against the emulated runtime header,
+// with AddressSanitizer, into a shared object linked to the emulation
+// library, and its kernel is run on the emulator's fibers.  The compiler
+// and header directory are fixed when the emulation library is built.
+using EmuLaunch = void (*)(unsigned grid, const void *p, void *out);
+
+std::mutex g_mu;
+std::unordered_map<std::string, EmuLaunch> g_cache;  // key: source
+std::string g_dir;
+
+int emu_compile(const std::string &src, bool f64, EmuLaunch *out) {
+    if (g_dir.empty()) {
+        char tmpl[] = "/tmp/tzh_emu_jit_XXXXXX";
+        if (!mkdtemp(tmpl)) return tzh_fail(TZH_ERR_DEVICE, "emulated chain kernel: mkdtemp failed");
+        g_dir = tmpl;
+    }
+    Dl_info info{};
+    if (!dladdr((const void *)&jit_chain_launch, &info) || !info.dli_fname)
+        return tzh_fail(TZH_ERR_DEVICE, "emulated chain kernel: cannot locate the emulation library");
+    const std::string stem = g_dir + "/k" + std::to_string(g_cache.size());
+    const char *T = f64 ? "double" : "float";
+    std::string text = "#include \"hip/hip_runtime.h\"\n" + src;
+    text += "extern \"C\" void tzh_chain_emu_launch(unsigned grid, const void *p, void *out) {\n"
+            "    emu::launch_kernel(\"tzh_chain (generated)\", tzh_chain, dim3(grid), dim3(256),\n"
+            "                       *(const EwProgram *)p, (" + std::string(T) + " *)out);\n}\n";
+    FILE *f = std::fopen((stem + ".cpp").c_str(), "w");
+    if (!f) return tzh_fail(TZH_ERR_DEVICE, "emulated chain kernel: cannot write %s.cpp", stem.c_str());
+    std::fwrite(text.data(), 1, text.size(), f);
+    std::fclose(f);
+    const std::string cmd = std::string(TZH_EMU_CXX) + " -x c++ -std=c++17 -O1 -g -fPIC -shared -fsanitize=address" +
+                            " -ffp-contract=off -Wno-unused-result -I" + TZH_EMU_INC + " " + stem + ".cpp -x none " +
+                            info.dli_fname + " -o " + stem + ".so > " + stem + ".log 2>&1";
+    if (std::system(cmd.c_str()) != 0)
+        return tzh_fail(TZH_ERR_DEVICE, "emulated chain kernel: compile failed (see %s.log)", stem.c_str());
+    void *h = dlopen((stem + ".so").c_str(), RTLD_NOW | RTLD_LOCAL);
+    if (!h) return tzh_fail(TZH_ERR_DEVICE, "emulated chain kernel: %s", dlerror());
+    *out = (EmuLaunch)dlsym(h, "tzh_chain_emu_launch");
+    if (!*out) return tzh_fail(TZH_ERR_DEVICE, "emulated chain kernel: no launcher");
+    return TZH_OK;
+}
+
+}  // namespace
+
+int jit_chain_launch(tzh_ctx *ctx, const EwProgram &p, bool f64, int V, int grid, void *out) {
+    (void)ctx;
+    const std::string src = chain_source(p, f64, V);
+    EmuLaunch fn = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        auto it = g_cache.find(src);
+        if (it == g_cache.end()) {
+            TZH_TRY(emu_compile(src, f64, &fn));
+            g_cache.emplace(src, fn);
+        } else {
+            fn = it->second;
+        }
+    }
+    fn((unsigned)grid, &p, out);
+    return TZH_OK;
+}
+
+#else
 struct Compiled {
     hipModule_t module;
     hipFunction_t fn;
@@ -290,5 +362,7 @@ int jit_chain_launch(tzh_ctx *ctx, const EwProgram &p, bool f64, int V, int grid
     TZH_HIP(hipModuleLaunchKernel(k.fn, (unsigned)grid, 1, 1, 256, 1, 1, 0, ctx->stream, args, nullptr));
     return TZH_OK;
 }
+
+#endif
 
 }  // namespace tzh_ew

@@ -139,6 +139,23 @@ def group_eval():
         assert (ulp(out, ref) <= 2).all()
     out, _ = eval_both(ReduceExpr("sum", T(np.zeros(0, np.float32))))
     assert float(out) == 0.0
+    # regression: an empty operand under a scalar broadcast (shape.zig's
+    # @max(0, 1) = 1 gives a 1 x 4 result) was read through its null data
+    # pointer by the chain kernel; it is a shape error now, for the library
+    # and the oracle alike
+    class Null(Host):
+        def data_ptr(self):
+            return 0
+    ez = Tensor(Null(np.zeros((0, 4), np.float32))).add(1.0)
+    assert ez.shape == (1, 4)
+    nodes, leaves = to_tape(ez)
+    arr = (_abi.Leaf * 1)()
+    arr[0].data, arr[0].ndim, arr[0].shape[0], arr[0].shape[1] = None, 2, 0, 4
+    res = np.zeros(4, np.float32)
+    assert L.tzh_eval_into(CTX, (_abi.Node * len(nodes))(*nodes), len(nodes), arr, 1, _abi.F32,
+                           res.ctypes.data) == _abi.ERR_SHAPE
+    assert oracle.eval_tape(nodes, [np.zeros((0, 4), np.float32)], np.float32)[0] == _abi.ERR_SHAPE
+    assert eval_both(Tensor(Null(np.zeros((0, 4), np.float32))).add(Tensor(Null(np.zeros((0, 4), np.float32)))))[0].size == 0
     A = rng.uniform(-1, 1, (16, 64)).astype(np.float32)
     bb = rng.uniform(-1, 1, 64).astype(np.float32)
     c = rng.uniform(-1, 1, (16, 64)).astype(np.float32)

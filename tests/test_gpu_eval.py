@@ -12,12 +12,13 @@ from tests.conftest import ulp_diff
 
 pytestmark = pytest.mark.gpu
 
-# These cases were part of a GPU run that ended with the GPU in a memory-fault
-# state; CPU emulation of the kernels at the same shapes (tests/cpu_emu,
-# AddressSanitizer) found no out-of-bounds access or stuck barrier, so no
-# cause is known and they stay off the GPU.
-UNCLEARED = pytest.mark.skip(reason="uncleared: in a GPU run that faulted with no cause found; "
-                                    "checked by CPU emulation (tests/test_cpu_emulation.py) instead")
+# The first GPU run of this suite ended in a host SIGSEGV inside
+# tzh_eval_into during the deep-tree test, on a working tree that was never
+# committed; the nearest commit replays that tape cleanly on the CPU (host
+# planner under AddressSanitizer, interpreter and generated kernels
+# emulated at 33 x 65), so no cause is shown and the test stays off the GPU.
+SIGSEGV_UNEXPLAINED = pytest.mark.skip(
+    reason="host SIGSEGV in tzh_eval_into in the first GPU run (uncommitted code); no cause shown on the CPU")
 
 DEV = "cuda"
 
@@ -149,7 +150,7 @@ def test_scalar_constants(ctx):
     assert ulp_diff(out, ref).max() == 0
 
 
-@UNCLEARED
+@SIGSEGV_UNEXPLAINED
 def test_deep_tree_materialises_and_matches(ctx):
     """Right-deep nesting needs more stack than the kernel has: the planner
     evaluates subtrees first; results must not change."""
@@ -162,7 +163,6 @@ def test_deep_tree_materialises_and_matches(ctx):
     assert ((ulp_diff(out, ref) <= 8) | (np.abs(out - ref) < 1e-6)).all()
 
 
-@UNCLEARED
 def test_long_chain_over_32_nodes(ctx):
     x = T(np.linspace(-1, 1, 4097, dtype=np.float32))
     e = x
@@ -172,7 +172,6 @@ def test_long_chain_over_32_nodes(ctx):
     assert ulp_diff(out, ref).max() == 0
 
 
-@UNCLEARED
 @pytest.mark.parametrize("op", ["sum", "mean", "prod", "reduce_max", "reduce_min"])
 @pytest.mark.parametrize("axes,keep", [((), False), ((), True), ((0,), False), ((1,), True), ((2,), False)])
 def test_reduce_vs_oracle(ctx, op, axes, keep):
@@ -184,7 +183,6 @@ def test_reduce_vs_oracle(ctx, op, axes, keep):
     np.testing.assert_allclose(out, ref, rtol=2e-5 if op != "prod" else 2e-4)
 
 
-@UNCLEARED
 def test_reduce_feeds_chain(ctx):
     rng = np.random.default_rng(6)
     x = rng.standard_normal((40, 300)).astype(np.float32)
@@ -193,7 +191,6 @@ def test_reduce_feeds_chain(ctx):
     np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
 
 
-@UNCLEARED
 def test_f64_chain(ctx):
     rng = np.random.default_rng(7)
     a = rng.standard_normal((17, 31))
@@ -203,17 +200,25 @@ def test_f64_chain(ctx):
     np.testing.assert_allclose(out, ref, rtol=1e-14, atol=1e-15)
 
 
-@UNCLEARED
 def test_tail_and_empty(ctx):
     for n in (1, 3, 5, 255, 1027):
         x = np.arange(n, dtype=np.float32)
         out, ref = run_both(T(x).add(1.0).exp(), ctx)
         assert ((ulp_diff(out, ref) <= 2)).all()
     z = torch.empty(0, 4, device=DEV)
-    assert eval(Tensor(z).add(1.0), ctx).numel() == 0
+    # both operands empty: an empty result, nothing launched
+    assert eval(Tensor(z).add(Tensor(z)), ctx).numel() == 0
+    # shape.zig:196-200 takes @max(0, 1) = 1, so the scalar broadcast has
+    # one row that the empty operand cannot supply; the reference's slice
+    # access panics there, here it is a shape error (the kernel would read
+    # from the empty tensor's null pointer)
+    e = Tensor(z).add(1.0)
+    assert e.shape == (1, 4)
+    with pytest.raises(TzhError) as ei:
+        eval(e, ctx)
+    assert ei.value.code == _abi.ERR_SHAPE
 
 
-@UNCLEARED
 def test_errors_mirror_compile_errors(ctx):
     with pytest.raises(ValueError):
         BinaryExpr("add", T(np.zeros((2, 3))), T(np.zeros((4,))))

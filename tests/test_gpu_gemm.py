@@ -17,15 +17,7 @@ import torch
 import oracle
 from tenzor_amd import _abi, check, lib, quantize_rows_host
 
-# Every test of this file was part of a GPU run that ended with the GPU in a
-# memory-fault state; CPU emulation of every kernel at these exact shapes
-# (tests/cpu_emu, AddressSanitizer on every buffer and LDS array) showed no
-# out-of-bounds access or stuck barrier, so no cause is known and the cases
-# stay off the GPU.  The same kernels are covered on the GPU through the
-# Arctic forward tests (f16 activations) and on the CPU by the emulation.
-UNCLEARED = pytest.mark.skip(reason="uncleared: in a GPU run that faulted with no cause found; "
-                                    "checked by CPU emulation (tests/test_cpu_emulation.py) instead")
-pytestmark = [pytest.mark.gpu, UNCLEARED]
+pytestmark = pytest.mark.gpu
 
 
 def make_problem(seed, m, k, n, x_scale=1.0):

@@ -215,6 +215,45 @@ def test_forward_vs_huggingface_bert_float64():
     assert np.abs(ours - ref).max() < 1e-5
 
 
+def test_linear_f32_vs_float64():
+    """orc_linear_f32 (arctic.zig:609-621: sgemm, then += bias) against a
+    float64 product, within the f32 summation bound: a transposed operand, a
+    dropped or misplaced bias, or a wrong k stride exceed it by orders of
+    magnitude."""
+    rng = np.random.default_rng(21)
+    for m, k, n in [(1, 384, 384), (7, 384, 1536), (33, 1536, 384), (3, 37, 5)]:
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        b = rng.uniform(-0.1, 0.1, n).astype(np.float32)
+        ref = a.astype(np.float64) @ w.astype(np.float64).T + b
+        bound = (np.abs(a).astype(np.float64) @ np.abs(w).astype(np.float64).T) * (k + 2) * 2.0 ** -24 \
+            + np.abs(ref) * 2.0 ** -24 + 1e-30
+        got = oracle.linear_f32(a, w, b)
+        assert (np.abs(got - ref) <= bound).all(), (m, k, n)
+        # no bias: the product alone
+        assert (np.abs(oracle.linear_f32(a, w) - (ref - b)) <= bound).all()
+        # the bound is tight enough to see a dropped bias
+        assert not (np.abs(got - b - ref) <= bound).all()
+
+
+@pytest.mark.parametrize("lengths", [[128], [1, 7, 64]])
+def test_f32_forward_vs_huggingface_bert_float64(lengths):
+    """The f32 model (MatWeight.f32 linears, f32 tables; config 1 is batch 1
+    x 128) against transformers' BertModel run in float64 on the same f32
+    weights, not dequantised int8 ones: this pins orc_linear_f32 inside the
+    whole forward."""
+    from tests.golden.gen_golden import hf_embeddings
+
+    cfg = synth.Config()
+    w = synth.make_arctic_f32(3, cfg, ln_random=True)
+    hw = synth.HostWeights(w, cfg)
+    lengths = np.array(lengths, np.int32)
+    ids, _ = synth.make_batch(31, len(lengths), seq_len=int(lengths.max()))
+    ours = np.stack([oracle.arctic_forward(hw, ids[b, :L]) for b, L in enumerate(lengths)])
+    ref = hf_embeddings(w, cfg, ids, lengths)
+    assert np.abs(ours - ref).max() < 1e-5
+
+
 def test_forward_golden_fixture_and_batch_threads():
     g = np.load(os.path.join(GOLDEN, "arctic_small.npz"))
     cfg = synth.Config()
@@ -248,6 +287,18 @@ def HT(a, dt=np.float32):
 def run(expr, dt=np.float32):
     nodes, leaves = to_tape(expr)
     return oracle.eval_tape(nodes, [l.data.a for l in leaves], dt)
+
+
+def test_empty_operand_broadcast_is_an_error():
+    """shape.zig:196-200 gives [0, 4] + scalar the shape [1, 4] (@max(0, 1));
+    executor.zig:142-144 would then index the empty slice.  The restatement
+    refuses the tape (the GPU planner does the same) instead of reading past
+    the empty buffer; both operands empty stays a valid empty result."""
+    e = HT(np.zeros((0, 4))).add(1.0)
+    assert e.shape == (1, 4)
+    assert run(e)[0] == _abi.ERR_SHAPE
+    rc, out = run(HT(np.zeros((0, 4))).add(HT(np.zeros((0, 4)))))
+    assert rc == 0 and out.shape == (0, 4)
 
 
 def test_executor_known_answers():  # executor.zig:616-706, elementwise.zig:339-460, reduce.zig:241-350
