@@ -2,23 +2,23 @@
 
 Subcommands:
 
-    python -m tenzor_amd.profile_summary run
+    python bench_profile.py run
         One forward of the bench workload (config 5) plus one elementwise
         multiply that reads and writes CAL_BYTES, for `rocprofv3
         --kernel-trace` or `--pmc FETCH_SIZE` / `--pmc WRITE_SIZE` to
         observe (the program goes right after `--`).
 
-    python -m tenzor_amd.profile_summary summarize [--trace DIR] [--fetch DIR] [--write DIR]
+    python bench_profile.py summarize [--trace DIR] [--fetch DIR] [--write DIR]
         Reads the CSV output of those runs and prints a markdown summary with
         one row per forward stage, ending in a fenced JSON block that
         bench.py reads for `roofline.traffic`.
 
-    python -m tenzor_amd.profile_summary gemm
+    python bench_profile.py gemm
         The config-3 GEMM pair (T = 65536: 384 -> 1536 + GELU, then
         1536 -> 384 + residual + LayerNorm; f16 activations, int8 weights in
         the model's device format) three times, for `rocprofv3 --pmc` passes.
 
-    python -m tenzor_amd.profile_summary counters DIR [DIR ...]
+    python bench_profile.py counters DIR [DIR ...]
         Per-kernel averages of the counters in those runs' CSV output, with
         unit busy/stall fractions (see COUNTER_NOTES).
 
@@ -51,7 +51,7 @@ def stage_of(kernel: str, prev: str | None) -> str | None:
         return "pack_ids"
     if "embed_ln_kernel" in kernel:
         return "embed_ln"
-    if "attn_varlen_kernel" in kernel:
+    if "attn_varlen_kernel" in kernel or "attn_varlen_f32_kernel" in kernel:
         return "attention"
     if "cls_l2_kernel" in kernel:
         return "cls_l2"
@@ -127,10 +127,10 @@ PYTHONPATH=<repo>, the program right after `--`):
     rocprofv3 --kernel-trace --stats --output-format csv -d <out>/trace -o fwd -- \\
         python3 <repo>/bench.py --steps 5 --warmup 2 --no-cpu-baseline
     rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/fetch -o f -- \\
-        python3 <repo>/tenzor_amd/profile_summary.py run
+        python3 <repo>/bench_profile.py run
     rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/write -o w -- \\
-        python3 <repo>/tenzor_amd/profile_summary.py run
-    python3 <repo>/tenzor_amd/profile_summary.py summarize \\
+        python3 <repo>/bench_profile.py run
+    python3 <repo>/bench_profile.py summarize \\
         --trace <out>/trace --fetch <out>/fetch --write <out>/write
 """
 
@@ -219,6 +219,8 @@ def run() -> None:
 
 
 def gemm() -> None:
+    """Config 3 three times: f32 X [65536, 384] -> 1536 + GELU (f32), then
+    1536 -> 384 + residual (X) + LayerNorm (f32); int8 weights."""
     import ctypes as C
 
     import numpy as np
@@ -231,9 +233,9 @@ def gemm() -> None:
     T, K, N1 = 65536, 384, 1536
     rng = np.random.default_rng(9)
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
-    X = dev(rng.standard_normal((T, K)).astype(np.float16))
-    H = torch.empty((T, N1), dtype=torch.float16, device="cuda")
-    Y = torch.empty((T, K), dtype=torch.float16, device="cuda")
+    X = dev(rng.standard_normal((T, K)).astype(np.float32))
+    H = torch.empty((T, N1), dtype=torch.float32, device="cuda")
+    Y = torch.empty((T, K), dtype=torch.float32, device="cuda")
     Q1 = dev(rng.integers(-127, 128, size=(N1, K)).astype(np.int8))
     Q2 = dev(rng.integers(-127, 128, size=(K, N1)).astype(np.int8))
     S1 = dev(np.full(N1, 0x211F, np.int16))  # f16 0.01
@@ -241,11 +243,11 @@ def gemm() -> None:
     B1, B2 = dev(np.zeros(N1, np.float32)), dev(np.zeros(K, np.float32))
     G, Bt = dev(np.ones(K, np.float32)), dev(np.zeros(K, np.float32))
     for _ in range(3):
-        check(lib().tzh_linear_w8(ctx.handle, X.data_ptr(), _abi.F16, Q1.data_ptr(), S1.data_ptr(), B1.data_ptr(),
-                                  H.data_ptr(), _abi.F16, T, K, N1, _abi.EPI_BIAS_GELU, None, _abi.F16, None, None,
+        check(lib().tzh_linear_w8(ctx.handle, X.data_ptr(), _abi.F32, Q1.data_ptr(), S1.data_ptr(), B1.data_ptr(),
+                                  H.data_ptr(), _abi.F32, T, K, N1, _abi.EPI_BIAS_GELU, None, _abi.F32, None, None,
                                   0.0))
-        check(lib().tzh_linear_w8(ctx.handle, H.data_ptr(), _abi.F16, Q2.data_ptr(), S2.data_ptr(), B2.data_ptr(),
-                                  Y.data_ptr(), _abi.F16, T, N1, K, _abi.EPI_BIAS_RES_LN, X.data_ptr(), _abi.F16,
+        check(lib().tzh_linear_w8(ctx.handle, H.data_ptr(), _abi.F32, Q2.data_ptr(), S2.data_ptr(), B2.data_ptr(),
+                                  Y.data_ptr(), _abi.F32, T, N1, K, _abi.EPI_BIAS_RES_LN, X.data_ptr(), _abi.F32,
                                   G.data_ptr(), Bt.data_ptr(), C.c_float(1e-12)))
     torch.cuda.synchronize()
     print("config-3 GEMM pair done", flush=True)

@@ -165,7 +165,13 @@ int tzh_eval_into(tzh_ctx *ctx, const tzh_node *tape, int32_t n_nodes,
 /* c[i,j] = (sum_k a[i,k]*f32(wq[j,k])) * f32(scale[j]) + bias[j]
  * Replaces matmulTransposeB_f32_i8_rowScale_bias (matmul_w8a32.zig:14-57).
  * a f32 [m,k], wq i8 [n,k] row-major, scale f16 bits [n], bias f32 [n] (may be
- * NULL = zeros), c f32 [m,n]; all device pointers.  k must be a multiple of 64. */
+ * NULL = zeros), c f32 [m,n]; all device pointers; any m, k, n (k and n are
+ * padded with zero codes internally, as the tail loop of
+ * matmul_w8a32.zig:50-52 adds the last k % 8 products).  Each product
+ * a*q is formed on the MFMA from an exact f16 split a = hi + lo (|a| must stay
+ * below 65504, the f16 range) and summed in f32.  The int8 codes are
+ * rewritten into the kernel's tiled format in the context scratch on every
+ * call (and a copy of a with zero columns when k % 64 != 0). */
 int tzh_matmul_w8a32(tzh_ctx *ctx, const float *a, const int8_t *wq, const uint16_t *scale,
                      const float *bias, float *c, int64_t m, int64_t k, int64_t n);
 
@@ -177,9 +183,10 @@ enum {
 };
 
 /* General int8-weight linear with fused epilogue.  a_dtype and c_dtype are
- * TZH_F32 or TZH_F16; residual (EPI_BIAS_RES_LN only) has res_dtype
- * TZH_F32 or TZH_F16 and shape [m,n]; gamma/beta f32 [n].
- * Activations are rounded to f16 for the MFMA; accumulation is f32. */
+ * TZH_F32 or TZH_F16; residual (EPI_BIAS_RES_LN only) has res_dtype ==
+ * c_dtype and shape [m,n]; gamma/beta f32 [n].  f32 activations take the
+ * hi/lo split of tzh_matmul_w8a32, f16 ones one MFMA; accumulation is f32.
+ * Any k; f16 output needs n % 384 == 0, the LayerNorm epilogue n == 384. */
 int tzh_linear_w8(tzh_ctx *ctx, const void *a, int32_t a_dtype, const int8_t *wq,
                   const uint16_t *scale, const float *bias, void *c, int32_t c_dtype,
                   int64_t m, int64_t k, int64_t n, int32_t epilogue,
@@ -195,10 +202,12 @@ int tzh_layernorm_last_dim(tzh_ctx *ctx, const float *x, const float *gamma, con
 /* Multi-head self-attention core of selfAttention (arctic.zig:660-713) over
  * packed variable-length sequences: for every sequence b (tokens
  * cu_seqlens[b] .. cu_seqlens[b+1]) and head h, softmax(Q_h K_h^T /
- * sqrt(32)) V_h.  qkv: device f16 [T, 3*hidden] (Q | K | V columns), out:
- * device f16 [T, hidden], cu_seqlens: device int32 [batch+1].  head_dim must
- * be 32 and sequences at most 512 tokens. */
-int tzh_attention_varlen(tzh_ctx *ctx, const uint16_t *qkv, uint16_t *out, const int32_t *cu_seqlens,
+ * sqrt(32)) V_h.  qkv: device [T, 3*hidden] (Q | K | V columns), out: device
+ * [T, hidden], both of element type dtype (TZH_F32: products of f32
+ * operands formed from exact f16 hi/lo splits, f32 sums; TZH_F16: f16
+ * operands), cu_seqlens: device int32 [batch+1].  head_dim must be 32 and
+ * sequences at most 512 tokens. */
+int tzh_attention_varlen(tzh_ctx *ctx, const void *qkv, void *out, int32_t dtype, const int32_t *cu_seqlens,
                          int32_t batch, int32_t n_heads, int32_t hidden);
 
 /* Per-row symmetric int8 quantization with f16 scale, bit-exact to
@@ -318,6 +327,24 @@ int tzh_arctic_hidden(tzh_model *model, float *hidden, const uint32_t *ids, cons
 /* Single sequence (arctic.forward, arctic.zig:874-898): ids device u32 [seq_len]. */
 int tzh_arctic_forward(tzh_model *model, float *output, const uint32_t *token_ids, int64_t seq_len);
 
+/* One sequence of a ragged host batch: a Zig `[]const u32` as an extern struct. */
+typedef struct {
+    const uint32_t *ids;
+    uint64_t len;
+} tzh_ids_slice;
+
+/* The reference's host-memory entry points, same argument shapes:
+ * arctic.forwardBatch / forwardBatchParallel (arctic.zig:902-918, 959-1013:
+ * outputs []f32 [batch * hidden], token_ids_batch []const []const u32) and
+ * arctic.forward (arctic.zig:874-898: output []f32 [hidden], token_ids
+ * []const u32).  Host pointers: the ids are packed into pinned staging and
+ * uploaded with one copy; the call returns when the embeddings are in
+ * `outputs`.  The reference's InferenceContext / BatchContextPool / thread
+ * pool arguments have no counterpart: the model's context and stream do
+ * their work. */
+int tzh_arctic_forward_batch_host(tzh_model *model, float *outputs, const tzh_ids_slice *batch, int32_t batch_n);
+int tzh_arctic_forward_host(tzh_model *model, float *output, const uint32_t *token_ids, int64_t seq_len);
+
 /* Number of out-of-range token ids (>= vocab_size) seen since the model was
  * created.  Such ids are clamped to vocab_size-1 so the gather stays in
  * bounds (the reference panics on the slice bounds check in safe builds).
@@ -327,6 +354,17 @@ int tzh_arctic_bad_id_count(tzh_model *model, int32_t *count);
 /* Last-batch timing hook: number of kernel launches the previous
  * tzh_arctic_forward_batch enqueued (for launch-overhead accounting). */
 int tzh_arctic_last_launch_count(tzh_model *model);
+
+/* Activation precision of the forward (no counterpart in the reference,
+ * whose activations are always f32): TZH_F32 (the default: f32 activations
+ * in HBM, products of f32 operands from exact f16 hi/lo splits, f32 sums, as
+ * arctic.zig:599-635 computes) or TZH_F16 (opt-in: activations rounded to
+ * f16 between kernels, half the activation traffic).  A model whose linears
+ * hold f32 weights (MatWeight.f32, stored as f16 codes with power-of-two row
+ * scales) runs with f16 activations whatever is set; tzh_arctic_precision
+ * reports the precision the next forward uses. */
+int tzh_arctic_set_precision(tzh_model *model, int32_t dtype);
+int tzh_arctic_precision(tzh_model *model, int32_t *dtype);
 
 /* Launch tracing (no counterpart in the reference, whose CPU path has no
  * kernels to time): with timing enabled, every later forward records a HIP

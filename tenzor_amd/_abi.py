@@ -109,6 +109,11 @@ class ArcticWeights(C.Structure):
                 ("layer_norm_beta", C.c_void_p), ("layers", C.POINTER(LayerWeights))]
 
 
+class IdsSlice(C.Structure):
+    """tzh_ids_slice: one host sequence of a ragged batch."""
+    _fields_ = [("ids", C.c_void_p), ("len", C.c_uint64)]
+
+
 class TenzorEntry(C.Structure):
     """tzh_tenzor_entry: the 48-byte .tenzor index entry."""
     _fields_ = [("name_hash", C.c_uint64), ("dtype", C.c_uint8), ("ndim", C.c_uint8), ("pad_", C.c_uint8 * 2),
@@ -143,11 +148,15 @@ PROTOTYPES = {
     "tzh_arctic_free": (C.c_int, [vp]),
     "tzh_arctic_forward_batch": (C.c_int, [vp, vp, vp, vp, i32, i64]),
     "tzh_arctic_forward": (C.c_int, [vp, vp, vp, i64]),
+    "tzh_arctic_forward_batch_host": (C.c_int, [vp, vp, vp, i32]),
+    "tzh_arctic_forward_host": (C.c_int, [vp, vp, vp, i64]),
     "tzh_arctic_hidden": (C.c_int, [vp, vp, vp, vp, i32, i64, i32]),
-    "tzh_attention_varlen": (C.c_int, [vp, vp, vp, vp, i32, i32, i32]),
+    "tzh_attention_varlen": (C.c_int, [vp, vp, vp, i32, vp, i32, i32, i32]),
     "tzh_arctic_bad_id_count": (C.c_int, [vp, C.POINTER(i32)]),
     "tzh_arctic_last_launch_count": (C.c_int, [vp]),
     "tzh_arctic_set_timing": (C.c_int, [vp, i32]),
+    "tzh_arctic_set_precision": (C.c_int, [vp, i32]),
+    "tzh_arctic_precision": (C.c_int, [vp, C.POINTER(i32)]),
     "tzh_arctic_launch_times": (C.c_int, [vp, C.POINTER(f32), C.POINTER(C.c_char_p), i32, C.POINTER(i32)]),
     "tzh_tenzor_name_hash": (C.c_uint64, [C.c_char_p, i64]),
     "tzh_tenzor_open": (C.c_int, [C.c_char_p, pp]),

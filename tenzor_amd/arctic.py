@@ -15,7 +15,7 @@ import ctypes as C
 
 import numpy as np
 
-from . import Context, check, lib
+from . import Context, _abi, check, lib
 from .synth import Config, HostWeights
 
 InferenceContext = Context
@@ -58,6 +58,20 @@ class ModelWeights:
 
     def last_launch_count(self) -> int:
         return lib().tzh_arctic_last_launch_count(self.handle)
+
+    def set_precision(self, dtype: str) -> None:
+        """Activation precision of later forwards: "float32" (the default,
+        the reference's arithmetic) or "float16" (opt-in, f16 activations)."""
+        codes = {"float32": _abi.F32, "float16": _abi.F16}
+        if dtype not in codes:
+            raise ValueError(f"precision must be float32 or float16, not {dtype!r}")
+        check(lib().tzh_arctic_set_precision(self.handle, codes[dtype]))
+
+    @property
+    def precision(self) -> str:
+        d = C.c_int32()
+        check(lib().tzh_arctic_precision(self.handle, C.byref(d)))
+        return "float32" if d.value == _abi.F32 else "float16"
 
     def set_timing(self, enable: bool) -> None:
         """Record a HIP event around every kernel launch of later forwards."""
@@ -103,6 +117,21 @@ def forwardBatch(outputs, ids, lengths, weights: ModelWeights, ctx: Context | No
     stride = int(ids.shape[1]) if ids.dim() == 2 else 0
     check(lib().tzh_arctic_forward_batch(weights.handle, C.c_void_p(outputs.data_ptr()), C.c_void_p(ids.data_ptr()),
                                          lengths.ctypes.data, batch, stride))
+
+
+def forwardBatchHost(outputs: np.ndarray, token_ids_batch, weights: ModelWeights) -> None:
+    """arctic.forwardBatch with the reference's host arguments: outputs a host
+    f32 array of batch * hidden_size, token_ids_batch a list of host u32
+    sequences of any lengths (one upload, one batched forward)."""
+    seqs = [np.ascontiguousarray(np.asarray(t, dtype=np.uint32)) for t in token_ids_batch]
+    h = weights.config.hidden_size
+    if outputs.dtype != np.float32 or not outputs.flags.c_contiguous or outputs.size != len(seqs) * h:
+        raise ValueError("outputs must be a contiguous f32 array of batch * hidden_size")
+    arr = (_abi.IdsSlice * max(1, len(seqs)))()
+    for i, t in enumerate(seqs):
+        arr[i].ids = t.ctypes.data
+        arr[i].len = t.size
+    check(lib().tzh_arctic_forward_batch_host(weights.handle, outputs.ctypes.data, arr, len(seqs)))
 
 
 def embedDocuments(outputs, texts, tokenizer, weights: ModelWeights) -> np.ndarray:

@@ -1,7 +1,11 @@
 // Arctic-embed-xs encoder forward on gfx950 (replaces arctic.zig:113-1013).
 //
-// Activations live in HBM as f16 between kernels; every reduction,
-// accumulation and normalisation is f32.  Sequences of a batch are packed
+// Activations live in HBM as f32 between kernels, as in the reference
+// (arctic.zig:599-635 keeps every activation f32); the GEMMs and attention
+// form f32 products on the MFMA from exact f16 hi/lo splits, and every
+// reduction, accumulation and normalisation is f32.  An opt-in f16
+// activation mode (tzh_arctic_set_precision) halves the activation traffic
+// at f16 rounding.  Sequences of a batch are packed
 // back to back (cu_seqlens) so padded positions cost nothing and each
 // sequence is forwarded at its true length, as the reference's per-sequence
 // forward does (arctic.zig:874-898, 959-1013).
@@ -25,11 +29,11 @@
 #include "safetensors.h"
 #include "tenzor_file.h"
 
-int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, int32_t w_format,
-                            const uint16_t *scale, const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k,
-                            int64_t n, int32_t epilogue, const void *res, const float *gamma, const float *beta,
-                            float eps, float *ln_ws, int64_t ln_ws_rows);
-int tzh_attention_launch(hipStream_t st, const _Float16 *qkv, _Float16 *out, const int *cu_seqlens,
+int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t x_dtype, const void *wc,
+                            int32_t w_format, const uint16_t *scale, const float *bias, void *c, int32_t c_dtype,
+                            int64_t m, int64_t k, int64_t n, int64_t n_valid, int32_t epilogue, const void *res,
+                            const float *gamma, const float *beta, float eps, float *ln_ws, int64_t ln_ws_rows);
+int tzh_attention_launch(hipStream_t st, const void *qkv, void *out, int32_t dtype, const int *cu_seqlens,
                          const int *order, int batch, int n_heads, int hidden);
 
 namespace {
@@ -70,12 +74,13 @@ struct TableRef {
 
 // K2: x = (word[id] + pos[p]) + type[0], then LayerNorm (arctic.zig:543-585).
 // One wave per token, six columns per lane.
+template <typename TO>
 __global__ void __launch_bounds__(256) embed_ln_kernel(const uint32_t *__restrict__ tok_ids,
                                                        const int32_t *__restrict__ tok_pos, int64_t T,
                                                        TableRef word, TableRef pos, TableRef type,
                                                        const float *__restrict__ gamma,
                                                        const float *__restrict__ beta, float eps,
-                                                       _Float16 *__restrict__ out) {
+                                                       TO *__restrict__ out) {
     const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (t >= T) return;
@@ -103,17 +108,18 @@ __global__ void __launch_bounds__(256) embed_ln_kernel(const uint32_t *__restric
 #pragma unroll
     for (int q = 0; q < 6; q++) {
         const int c = lane + 64 * q;
-        out[t * H + c] = (_Float16)(((x[q] - mean) * inv_std) * gamma[c] + beta[c]);
+        out[t * H + c] = (TO)(((x[q] - mean) * inv_std) * gamma[c] + beta[c]);
     }
 }
 
 // K5: CLS row of every sequence, L2-normalised (arctic.zig:893-897, 851-863).
-__global__ void __launch_bounds__(256) cls_l2_kernel(const _Float16 *__restrict__ hidden, const int *__restrict__ cu,
+template <typename TI>
+__global__ void __launch_bounds__(256) cls_l2_kernel(const TI *__restrict__ hidden, const int *__restrict__ cu,
                                                      int batch, float *__restrict__ out) {
     const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (b >= batch) return;
-    const _Float16 *row = hidden + (int64_t)cu[b] * H;
+    const TI *row = hidden + (int64_t)cu[b] * H;
     float v[6], ss = 0.0f;
 #pragma unroll
     for (int q = 0; q < 6; q++) {
@@ -214,7 +220,11 @@ struct tzh_model {
     // workspace, grown on demand
     int64_t cap_tokens = 0;
     int cap_batch = 0;
-    _Float16 *h = nullptr, *h1 = nullptr, *qkv = nullptr, *attn = nullptr, *inter = nullptr;
+    // activation element type: TZH_F32 (the reference's) or TZH_F16 (opt-in);
+    // f32-weight linears (TZH_WF_F16 codes) run with f16 activations only
+    int32_t act = TZH_F32;
+    size_t cap_es = 0;       // activation bytes per element the workspace was sized for
+    void *h = nullptr, *h1 = nullptr, *qkv = nullptr, *attn = nullptr, *inter = nullptr;
     float *ln_ws = nullptr;  // f32 rows of a split LayerNorm GEMM round
     int64_t ln_ws_rows = 0;
     uint32_t *tok_ids = nullptr;
@@ -223,6 +233,13 @@ struct tzh_model {
     int *bad_ids = nullptr;
     int *host_meta = nullptr;  // pinned staging
     hipEvent_t meta_done = nullptr;
+    // host-slice entry points: pinned id staging, device ids and outputs
+    uint32_t *host_ids = nullptr;
+    int64_t host_ids_cap = 0;
+    uint32_t *dev_ids = nullptr;
+    int64_t dev_ids_cap = 0;
+    float *dev_out = nullptr;
+    int64_t dev_out_cap = 0;
     int last_launches = 0;
     // launch timing (tzh_arctic_set_timing): events[0] before the first
     // launch, events[i+1] after launch i, names[i] = its stage name
@@ -382,10 +399,11 @@ void free_workspace(tzh_model *m) {
     m->host_meta = nullptr;
     m->cap_tokens = 0;
     m->cap_batch = 0;
+    m->cap_es = 0;
 }
 
-int ensure_workspace(tzh_model *m, int64_t tokens, int batch) {
-    if (tokens <= m->cap_tokens && batch <= m->cap_batch) return TZH_OK;
+int ensure_workspace(tzh_model *m, int64_t tokens, int batch, size_t es) {
+    if (tokens <= m->cap_tokens && batch <= m->cap_batch && es <= m->cap_es) return TZH_OK;
     TZH_HIP(hipStreamSynchronize(m->ctx->stream));
     const int64_t T = std::max<int64_t>(tokens, m->cap_tokens);
     const int B = std::max(batch, m->cap_batch);
@@ -397,11 +415,12 @@ int ensure_workspace(tzh_model *m, int64_t tokens, int batch) {
         }
         return TZH_OK;
     };
-    TZH_TRY(get((void **)&m->h, (size_t)T * H * 2));
-    TZH_TRY(get((void **)&m->h1, (size_t)T * H * 2));
-    TZH_TRY(get((void **)&m->qkv, (size_t)T * 3 * H * 2));
-    TZH_TRY(get((void **)&m->attn, (size_t)T * H * 2));
-    TZH_TRY(get((void **)&m->inter, (size_t)T * 1536 * 2));
+    const size_t E = std::max(es, m->cap_es);
+    TZH_TRY(get((void **)&m->h, (size_t)T * H * E));
+    TZH_TRY(get((void **)&m->h1, (size_t)T * H * E));
+    TZH_TRY(get((void **)&m->qkv, (size_t)T * 3 * H * E));
+    TZH_TRY(get((void **)&m->attn, (size_t)T * H * E));
+    TZH_TRY(get((void **)&m->inter, (size_t)T * 1536 * E));
     // a split partial round is at most a third of the CUs' 128-row tiles
     m->ln_ws_rows = std::min<int64_t>((T + 127) / 128, m->ctx->num_cus / 3 + 1) * 128;
     TZH_TRY(get((void **)&m->ln_ws, (size_t)m->ln_ws_rows * H * 4));
@@ -415,6 +434,7 @@ int ensure_workspace(tzh_model *m, int64_t tokens, int batch) {
     }
     m->cap_tokens = T;
     m->cap_batch = B;
+    m->cap_es = E;
     return TZH_OK;
 }
 
@@ -447,6 +467,9 @@ void model_delete(tzh_model *m) {
     (void)hipSetDevice(m->ctx->device);
     (void)hipStreamSynchronize(m->ctx->stream);
     free_workspace(m);
+    if (m->host_ids) (void)hipHostFree(m->host_ids);
+    if (m->dev_ids) (void)hipFree(m->dev_ids);
+    if (m->dev_out) (void)hipFree(m->dev_out);
     for (void *p : m->allocs) (void)hipFree(p);
     if (m->meta_done) (void)hipEventDestroy(m->meta_done);
     for (hipEvent_t e : m->events) (void)hipEventDestroy(e);
@@ -716,7 +739,13 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
         T += lengths[b];
     }
     if (T > ((int64_t)1 << 30)) return tzh_fail(TZH_ERR_TOO_LARGE, "batch of %lld tokens is too large", (long long)T);
-    TZH_TRY(ensure_workspace(m, T, batch));
+    // f32 activations need the tiled int8 weight format on every linear
+    bool f16_codes = false;
+    for (const DevLayer &d : m->layers)
+        for (const DevLinear *l : {&d.qkv, &d.o, &d.ffn1, &d.ffn2}) f16_codes = f16_codes || l->fmt != TZH_WF_W8T;
+    const int32_t act = f16_codes ? TZH_F16 : m->act;
+    const size_t es = act == TZH_F32 ? 4 : 2;
+    TZH_TRY(ensure_workspace(m, T, batch, es));
     hipStream_t st = m->ctx->stream;
 
     // metadata: cu_seqlens and a longest-first order for attention
@@ -758,40 +787,56 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
                        (uint32_t)m->cfg.vocab_size, m->bad_ids);
     TZH_LAUNCHED("pack_ids_kernel");
     TZH_TRY(mark("pack_ids"));
-    hipLaunchKernelGGL(embed_ln_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, m->tok_ids, m->tok_pos, T,
-                       m->word.ref(), m->pos.ref(), m->type.ref(), m->emb_g, m->emb_b, m->cfg.layer_norm_eps, m->h);
+    if (act == TZH_F32)
+        hipLaunchKernelGGL(embed_ln_kernel<float>, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, m->tok_ids,
+                           m->tok_pos, T, m->word.ref(), m->pos.ref(), m->type.ref(), m->emb_g, m->emb_b,
+                           m->cfg.layer_norm_eps, (float *)m->h);
+    else
+        hipLaunchKernelGGL(embed_ln_kernel<_Float16>, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st, m->tok_ids,
+                           m->tok_pos, T, m->word.ref(), m->pos.ref(), m->type.ref(), m->emb_g, m->emb_b,
+                           m->cfg.layer_norm_eps, (_Float16 *)m->h);
     TZH_LAUNCHED("embed_ln_kernel");
     TZH_TRY(mark("embed_ln"));
     const float eps = m->cfg.layer_norm_eps;
     for (int32_t li = 0; li < n_layers; li++) {
         const DevLayer &d = m->layers[(size_t)li];
         const int cus = m->ctx->num_cus;
-        TZH_TRY(tzh_linear_codes_launch(st, cus, m->h, d.qkv.w, d.qkv.fmt, d.qkv.s, d.qkv.b, m->qkv, TZH_F16, T, H, 3 * H,
-                                        TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f, nullptr, 0));
+        TZH_TRY(tzh_linear_codes_launch(st, cus, m->h, act, d.qkv.w, d.qkv.fmt, d.qkv.s, d.qkv.b, m->qkv, act, T, H,
+                                        3 * H, 3 * H, TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f, nullptr, 0));
         TZH_TRY(mark("qkv"));
-        TZH_TRY(tzh_attention_launch(st, m->qkv, m->attn, d_cu, d_order, batch, 12, H));
+        TZH_TRY(tzh_attention_launch(st, m->qkv, m->attn, act, d_cu, d_order, batch, 12, H));
         TZH_TRY(mark("attention"));
-        TZH_TRY(tzh_linear_codes_launch(st, cus, m->attn, d.o.w, d.o.fmt, d.o.s, d.o.b, m->h1, TZH_F16, T, H, H,
+        TZH_TRY(tzh_linear_codes_launch(st, cus, m->attn, act, d.o.w, d.o.fmt, d.o.s, d.o.b, m->h1, act, T, H, H, H,
                                         TZH_EPI_BIAS_RES_LN, m->h, d.ln1_g, d.ln1_b, eps, m->ln_ws, m->ln_ws_rows));
         TZH_TRY(mark("attn_out_ln"));
-        TZH_TRY(tzh_linear_codes_launch(st, cus, m->h1, d.ffn1.w, d.ffn1.fmt, d.ffn1.s, d.ffn1.b, m->inter, TZH_F16, T, H, 1536,
-                                        TZH_EPI_BIAS_GELU, nullptr, nullptr, nullptr, 0.0f, nullptr, 0));
+        TZH_TRY(tzh_linear_codes_launch(st, cus, m->h1, act, d.ffn1.w, d.ffn1.fmt, d.ffn1.s, d.ffn1.b, m->inter, act,
+                                        T, H, 1536, 1536, TZH_EPI_BIAS_GELU, nullptr, nullptr, nullptr, 0.0f, nullptr,
+                                        0));
         TZH_TRY(mark("ffn1_gelu"));
-        TZH_TRY(tzh_linear_codes_launch(st, cus, m->inter, d.ffn2.w, d.ffn2.fmt, d.ffn2.s, d.ffn2.b, m->h, TZH_F16, T, 1536, H,
-                                        TZH_EPI_BIAS_RES_LN, m->h1, d.ln2_g, d.ln2_b, eps, m->ln_ws, m->ln_ws_rows));
+        TZH_TRY(tzh_linear_codes_launch(st, cus, m->inter, act, d.ffn2.w, d.ffn2.fmt, d.ffn2.s, d.ffn2.b, m->h, act, T,
+                                        1536, H, H, TZH_EPI_BIAS_RES_LN, m->h1, d.ln2_g, d.ln2_b, eps, m->ln_ws,
+                                        m->ln_ws_rows));
         TZH_TRY(mark("ffn2_ln"));
     }
     if (outputs) {
-        hipLaunchKernelGGL(cls_l2_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, st, m->h, d_cu, batch,
-                           outputs);
+        if (act == TZH_F32)
+            hipLaunchKernelGGL(cls_l2_kernel<float>, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, st,
+                               (const float *)m->h, d_cu, batch, outputs);
+        else
+            hipLaunchKernelGGL(cls_l2_kernel<_Float16>, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, st,
+                               (const _Float16 *)m->h, d_cu, batch, outputs);
         TZH_LAUNCHED("cls_l2_kernel");
         TZH_TRY(mark("cls_l2"));
     }
     if (hidden_out) {
         const int64_t n = T * H;
-        hipLaunchKernelGGL(f16_to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m->h, hidden_out,
-                           n);
-        TZH_LAUNCHED("f16_to_f32_kernel");
+        if (act == TZH_F32) {
+            TZH_HIP(hipMemcpyAsync(hidden_out, m->h, (size_t)n * 4, hipMemcpyDeviceToDevice, st));
+        } else {
+            hipLaunchKernelGGL(f16_to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                               (const _Float16 *)m->h, hidden_out, n);
+            TZH_LAUNCHED("f16_to_f32_kernel");
+        }
         TZH_TRY(mark("hidden_f32"));
     }
     m->timed = m->timing ? launches : 0;
@@ -823,7 +868,94 @@ extern "C" int tzh_arctic_forward(tzh_model *m, float *output, const uint32_t *t
     return tzh_arctic_forward_batch(m, output, token_ids, &len, 1, 0);
 }
 
+// Host-slice batch (arctic.forwardBatch / forwardBatchParallel argument
+// shapes): the sequences are packed into pinned staging, uploaded with one
+// copy, forwarded, and the embeddings copied back; returns when they are in
+// `outputs` (host).
+extern "C" int tzh_arctic_forward_batch_host(tzh_model *m, float *outputs, const tzh_ids_slice *batch,
+                                             int32_t batch_n) {
+    tzh_clear_error();
+    if (!m) return tzh_fail(TZH_ERR_INVALID_ARGS, "null model");
+    TZH_TRY(tzh_ctx_enter(m->ctx));
+    if (batch_n == 0) return TZH_OK;  // arctic.zig:967
+    if (batch_n < 0 || !outputs || !batch) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad batch arguments");
+    std::vector<int32_t> lengths((size_t)batch_n);
+    int64_t T = 0;
+    for (int32_t b = 0; b < batch_n; b++) {
+        const uint64_t L = batch[b].len;
+        if (L < 1 || L > (uint64_t)m->cfg.max_position_embeddings || !batch[b].ids)
+            return tzh_fail(TZH_ERR_INVALID_ARGS, "sequence %d has length %llu (must be 1..%d)", b,
+                            (unsigned long long)L, m->cfg.max_position_embeddings);
+        lengths[(size_t)b] = (int32_t)L;
+        T += (int64_t)L;
+    }
+    hipStream_t st = m->ctx->stream;
+    TZH_HIP(hipStreamSynchronize(st));  // the staging and device buffers are free again
+    if (T > m->host_ids_cap) {
+        if (m->host_ids) TZH_HIP(hipHostFree(m->host_ids));
+        m->host_ids = nullptr;
+        m->host_ids_cap = 0;
+        if (hipHostMalloc((void **)&m->host_ids, (size_t)T * 4, hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            m->host_ids = nullptr;
+            return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "pinned id staging of %lld ids failed", (long long)T);
+        }
+        m->host_ids_cap = T;
+    }
+    auto grow = [](void **p, int64_t &cap, int64_t want, size_t es) -> int {
+        if (want <= cap) return TZH_OK;
+        if (*p) TZH_HIP(hipFree(*p));
+        *p = nullptr;
+        cap = 0;
+        if (hipMalloc(p, (size_t)want * es) != hipSuccess) {
+            (void)hipGetLastError();
+            *p = nullptr;
+            return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "device buffer of %lld elements failed", (long long)want);
+        }
+        cap = want;
+        return TZH_OK;
+    };
+    TZH_TRY(grow((void **)&m->dev_ids, m->dev_ids_cap, T, 4));
+    TZH_TRY(grow((void **)&m->dev_out, m->dev_out_cap, (int64_t)batch_n * H, 4));
+    int64_t off = 0;
+    for (int32_t b = 0; b < batch_n; b++) {
+        std::memcpy(m->host_ids + off, batch[b].ids, (size_t)batch[b].len * 4);
+        off += (int64_t)batch[b].len;
+    }
+    TZH_HIP(hipMemcpyAsync(m->dev_ids, m->host_ids, (size_t)T * 4, hipMemcpyHostToDevice, st));
+    TZH_TRY(run_forward(m, m->dev_out, nullptr, m->dev_ids, lengths.data(), batch_n, 0, m->cfg.num_hidden_layers));
+    TZH_HIP(hipMemcpyAsync(outputs, m->dev_out, (size_t)batch_n * H * 4, hipMemcpyDeviceToHost, st));
+    TZH_HIP(hipStreamSynchronize(st));
+    return TZH_OK;
+}
+
+// One host sequence (arctic.forward argument shapes).
+extern "C" int tzh_arctic_forward_host(tzh_model *m, float *output, const uint32_t *token_ids, int64_t seq_len) {
+    if (seq_len <= 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "seq_len %lld out of range", (long long)seq_len);
+    const tzh_ids_slice one{token_ids, (uint64_t)seq_len};
+    return tzh_arctic_forward_batch_host(m, output, &one, 1);
+}
+
 extern "C" int tzh_arctic_last_launch_count(tzh_model *m) { return m ? m->last_launches : 0; }
+
+extern "C" int tzh_arctic_set_precision(tzh_model *m, int32_t dtype) {
+    tzh_clear_error();
+    if (!m) return tzh_fail(TZH_ERR_INVALID_ARGS, "null model");
+    if (dtype != TZH_F32 && dtype != TZH_F16)
+        return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "activation precision must be F32 or F16 (got %d)", dtype);
+    m->act = dtype;
+    return TZH_OK;
+}
+
+extern "C" int tzh_arctic_precision(tzh_model *m, int32_t *dtype) {
+    tzh_clear_error();
+    if (!m || !dtype) return tzh_fail(TZH_ERR_INVALID_ARGS, "null argument");
+    bool f16_codes = false;
+    for (const DevLayer &d : m->layers)
+        for (const DevLinear *l : {&d.qkv, &d.o, &d.ffn1, &d.ffn2}) f16_codes = f16_codes || l->fmt != TZH_WF_W8T;
+    *dtype = f16_codes ? TZH_F16 : m->act;
+    return TZH_OK;
+}
 
 extern "C" int tzh_arctic_set_timing(tzh_model *m, int32_t enable) {
     tzh_clear_error();

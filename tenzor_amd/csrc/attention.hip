@@ -211,30 +211,224 @@ __global__ void __launch_bounds__(NW * 64) attn_varlen_kernel(const _Float16 *__
     }
 }
 
+// f32 attention (the reference's arithmetic).  Q, K and V are split into
+// f16 pairs x = hi + lo (hi = f16(x), lo = f16(x - hi), exact to about 2^-22
+// relative) and every product a.b of two split operands is formed as
+// hi.hi + hi.lo + lo.hi on the MFMA with f32 accumulation (lo.lo is below
+// 2^-22 relative); the probabilities are split the same way for P V.  The
+// row sum adds the f32 probabilities on the VALU, so it is the sum of the
+// values P V weights with, to f32 rounding.  K and V^T are staged in LDS as
+// hi and lo planes (146 KiB: one workgroup per CU).
+constexpr int kWavesF32 = 8;
+
+__device__ __forceinline__ void split8(const f32x4_t &a, const f32x4_t &b, half8_t &hi, half8_t &lo) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        hi[i] = (_Float16)a[i];
+        hi[4 + i] = (_Float16)b[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        lo[i] = (_Float16)(a[i] - (float)hi[i]);
+        lo[4 + i] = (_Float16)(b[i] - (float)hi[4 + i]);
+    }
+}
+
+template <int NW>
+__global__ void __launch_bounds__(NW * 64) attn_varlen_f32_kernel(const float *__restrict__ qkv, int ld,
+                                                              float *__restrict__ out, int ld_out,
+                                                              const int *__restrict__ cu_seqlens,
+                                                              const int *__restrict__ order, int batch, int n_heads,
+                                                              int hidden, float scale_log2) {
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[2][kMaxKeys * K_LD];  // [hi, lo]
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[2][kHeadDim * V_LD];
+
+    // (sequence, head) of this block: as attn_varlen_kernel (head pairs of a
+    // sequence on one XCD)
+    int item, h;
+    if (n_heads % 2 == 0) {
+        const int pairs = n_heads / 2;
+        const int hp = (int)(blockIdx.x / 16) * 8 + (int)(blockIdx.x % 8);
+        item = hp / pairs;
+        h = 2 * (hp % pairs) + (int)(blockIdx.x / 8) % 2;
+    } else {
+        item = blockIdx.x / n_heads;
+        h = blockIdx.x % n_heads;
+    }
+    if (item >= batch) return;
+    const int b = order ? order[item] : item;
+    const int start = cu_seqlens[b];
+    const int L = min(max(cu_seqlens[b + 1] - start, 0), kMaxKeys);
+    const int Lp = (L + 63) & ~63;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+
+    const float *qbase = qkv + (size_t)start * ld + h * kHeadDim;
+    const float *kbase = qbase + hidden;
+    const float *vbase = qbase + 2 * hidden;
+
+    // K rows -> hi/lo planes; keys L..Lp-1 zero
+    for (int idx = tid; idx < Lp * 4; idx += NW * 64) {
+        const int key = idx >> 2, c = (idx & 3) * 8;
+        f32x4_t a = {0, 0, 0, 0}, bq = {0, 0, 0, 0};
+        if (key < L) {
+            a = *(const f32x4_t *)(kbase + (size_t)key * ld + c);
+            bq = *(const f32x4_t *)(kbase + (size_t)key * ld + c + 4);
+        }
+        half8_t hi, lo;
+        split8(a, bq, hi, lo);
+        *(half8_t *)(Ks[0] + key * K_LD + c) = hi;
+        *(half8_t *)(Ks[1] + key * K_LD + c) = lo;
+    }
+    // V^T -> hi/lo planes in the PV operand order (see the V^T layout note)
+    {
+        const int gq = lane & 3, kg = (lane >> 2) & 3, c = lane >> 4;
+        for (int kb = 128 * w; kb < Lp; kb += 128 * NW) {
+            const int k0 = kb + 32 * kg + 4 * gq;
+#pragma unroll
+            for (int part = 0; part < 2; part++) {
+                half8_t v[8];
+#pragma unroll
+                for (int r = 0; r < 8; r++) {
+                    const int key = k0 + (r & 3) + 16 * (r >> 2);
+                    f32x4_t a = {0, 0, 0, 0}, bq = {0, 0, 0, 0};
+                    if (key < L) {
+                        a = *(const f32x4_t *)(vbase + (size_t)key * ld + 8 * c);
+                        bq = *(const f32x4_t *)(vbase + (size_t)key * ld + 8 * c + 4);
+                    }
+                    half8_t hi, lo;
+                    split8(a, bq, hi, lo);
+                    v[r] = part ? lo : hi;
+                }
+#pragma unroll
+                for (int d = 0; d < 8; d++) {
+                    half8_t col;
+#pragma unroll
+                    for (int r = 0; r < 8; r++) col[r] = v[r][d];
+                    *(half8_t *)(Vt[part] + (8 * c + d) * V_LD + kb + 32 * kg + 8 * gq) = col;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    const int g = lane >> 4;
+    const int ql = lane & 15;
+    for (int q0 = w * 16; q0 < L; q0 += NW * 16) {
+        const int qrow = q0 + ql;
+        half8_t qh, qlo;
+        {
+            f32x4_t a = {0, 0, 0, 0}, bq = {0, 0, 0, 0};
+            if (qrow < L) {
+                a = *(const f32x4_t *)(qbase + (size_t)qrow * ld + g * 8);
+                bq = *(const f32x4_t *)(qbase + (size_t)qrow * ld + g * 8 + 4);
+            }
+            split8(a, bq, qh, qlo);
+        }
+        float m = -INFINITY, lsum = 0.0f;
+        f32x4_t o0 = {0, 0, 0, 0}, o1 = {0, 0, 0, 0};
+        for (int kb0 = 0; kb0 < Lp; kb0 += 64) {
+            f32x4_t s[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const half8_t kh = *(const half8_t *)(Ks[0] + (kb0 + 16 * t + ql) * K_LD + g * 8);
+                const half8_t kl = *(const half8_t *)(Ks[1] + (kb0 + 16 * t + ql) * K_LD + g * 8);
+                f32x4_t acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh, f32x4_t{0, 0, 0, 0}, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qlo, acc, 0, 0, 0);
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh, acc, 0, 0, 0);
+            }
+            if (kb0 + 64 > L) {
+                const int rem = L - kb0 - 4 * g;
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) s[t][i] = 16 * t + i >= rem ? -INFINITY : s[t][i];
+            }
+            float mx = s[0][0];
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[t][i]);
+            mx = max_over_rows(mx);
+            // lazy rescaling as in attn_varlen_kernel
+            if (wave_any((mx - m) * scale_log2 > kLazyLog2)) {
+                const float m_new = fmaxf(m, mx);
+                const float alpha = __builtin_amdgcn_exp2f((m - m_new) * scale_log2);
+                o0 *= alpha;
+                o1 *= alpha;
+                lsum *= alpha;
+                m = m_new;
+            }
+            const float mc = m * scale_log2;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    s[t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][i], scale_log2, -mc));
+                    lsum += s[t][i];
+                }
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                const int kv = kb0 + 32 * st + 8 * g;
+                const half8_t vah = *(const half8_t *)(Vt[0] + ql * V_LD + kv);
+                const half8_t val = *(const half8_t *)(Vt[1] + ql * V_LD + kv);
+                const half8_t vbh = *(const half8_t *)(Vt[0] + (16 + ql) * V_LD + kv);
+                const half8_t vbl = *(const half8_t *)(Vt[1] + (16 + ql) * V_LD + kv);
+                half8_t ph, pl;
+                split8(f32x4_t{s[2 * st][0], s[2 * st][1], s[2 * st][2], s[2 * st][3]},
+                       f32x4_t{s[2 * st + 1][0], s[2 * st + 1][1], s[2 * st + 1][2], s[2 * st + 1][3]}, ph, pl);
+                o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(val, ph, o0, 0, 0, 0);
+                o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vah, pl, o0, 0, 0, 0);
+                o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vah, ph, o0, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vbl, ph, o1, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vbh, pl, o1, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vbh, ph, o1, 0, 0, 0);
+            }
+        }
+        const float total = sum_over_rows(lsum);  // the query's whole row sum, in every lane row
+        if (qrow < L) {
+            const float inv = 1.0f / total;
+            float *dst = out + (size_t)(start + qrow) * ld_out + h * kHeadDim + 4 * g;
+            *(f32x4_t *)dst = o0 * inv;
+            *(f32x4_t *)(dst + 16) = o1 * inv;
+        }
+    }
+}
+
 }  // namespace
 
-// qkv: f16 [T, 3*hidden] (Q | K | V per token), out: f16 [T, hidden].
+// qkv: [T, 3*hidden] (Q | K | V per token), out: [T, hidden], both f16 or
+// both f32 (f32: the split-product kernel above).
 // order: sequence ids (longest first) so the long blocks start early.
-int tzh_attention_launch(hipStream_t st, const _Float16 *qkv, _Float16 *out, const int *cu_seqlens,
+int tzh_attention_launch(hipStream_t st, const void *qkv, void *out, int32_t dtype, const int *cu_seqlens,
                          const int *order, int batch, int n_heads, int hidden) {
     if (hidden != n_heads * kHeadDim)
         return tzh_fail(TZH_ERR_INVALID_ARGS, "attention kernel needs head_dim 32 (hidden %d, heads %d)", hidden,
                         n_heads);
+    if (dtype != TZH_F16 && dtype != TZH_F32) return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "attention needs F16 or F32");
     if (batch <= 0) return TZH_OK;
     const float scale = 1.0f / sqrtf((float)kHeadDim);  // arctic.zig:649
     const float scale_log2 = scale * 1.4426950408889634f;
     // head-pair layout: 16 blocks per 8 (sequence, head pair)s
     const int64_t blocks = n_heads % 2 == 0 ? ((int64_t)batch * (n_heads / 2) + 7) / 8 * 16 : (int64_t)batch * n_heads;
+    if (dtype == TZH_F32) {
+        hipLaunchKernelGGL((attn_varlen_f32_kernel<kWavesF32>), dim3((unsigned)blocks), dim3(kWavesF32 * 64), 0, st,
+                           (const float *)qkv, 3 * hidden, (float *)out, hidden, cu_seqlens, order, batch, n_heads,
+                           hidden, scale_log2);
+        TZH_LAUNCHED("attn_varlen_f32_kernel");
+        return TZH_OK;
+    }
     hipLaunchKernelGGL((attn_varlen_kernel<kWaves, kQueryTiles>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, st,
-                       qkv, 3 * hidden, out, hidden, cu_seqlens, order, batch, n_heads, hidden, scale_log2);
+                       (const _Float16 *)qkv, 3 * hidden, (_Float16 *)out, hidden, cu_seqlens, order, batch, n_heads,
+                       hidden, scale_log2);
     TZH_LAUNCHED("attn_varlen_kernel");
     return TZH_OK;
 }
 
-extern "C" int tzh_attention_varlen(tzh_ctx *ctx, const uint16_t *qkv, uint16_t *out, const int32_t *cu_seqlens,
-                                    int32_t batch, int32_t n_heads, int32_t hidden) {
+extern "C" int tzh_attention_varlen(tzh_ctx *ctx, const void *qkv, void *out, int32_t dtype,
+                                    const int32_t *cu_seqlens, int32_t batch, int32_t n_heads, int32_t hidden) {
     tzh_clear_error();
     TZH_TRY(tzh_ctx_enter(ctx));
+    if (dtype != TZH_F16 && dtype != TZH_F32) return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "attention needs F16 or F32");
     if (batch < 0 || n_heads <= 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad batch/heads");
     if (batch > 0 && (!qkv || !out || !cu_seqlens)) return tzh_fail(TZH_ERR_INVALID_ARGS, "null pointer");
     if (batch == 0) return TZH_OK;
@@ -247,6 +441,5 @@ extern "C" int tzh_attention_varlen(tzh_ctx *ctx, const uint16_t *qkv, uint16_t 
         if (L < 1 || L > kMaxKeys)
             return tzh_fail(TZH_ERR_INVALID_ARGS, "sequence %d has length %d (must be 1..%d)", b, L, kMaxKeys);
     }
-    return tzh_attention_launch(ctx->stream, (const _Float16 *)qkv, (_Float16 *)out, cu_seqlens, nullptr, batch,
-                                n_heads, hidden);
+    return tzh_attention_launch(ctx->stream, qkv, out, dtype, cu_seqlens, nullptr, batch, n_heads, hidden);
 }

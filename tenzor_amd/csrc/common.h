@@ -143,6 +143,18 @@ __device__ __forceinline__ float max_over_rows(float x) {
     return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
 }
 
+// Sum over the four lanes l % 16 + 16j (j = 0..3), the same value left in
+// all four: (x0 + x1) + (x2 + x3) up to the order of each addition's
+// operands.
+__device__ __forceinline__ float sum_over_rows(float x) {
+    uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+    lane_swap16(a, b);
+    x = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+    a = b = __builtin_bit_cast(uint32_t, x);
+    lane_swap32(a, b);
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
 // f32 -> f16 with round-to-nearest-even (v_cvt_f16_f32 honours the default RNE mode).
 __device__ __forceinline__ _Float16 to_f16(float x) { return (_Float16)x; }
 

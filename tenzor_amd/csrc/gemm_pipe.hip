@@ -1,12 +1,18 @@
-// K3 fast path: f16 activations x int8-valued weight codes on MFMA, with the
-// operand tiles streamed HBM/L2 -> LDS by the gfx950 direct-to-LDS loads
+// K3: activations x int8-valued weight codes on MFMA, with the operand tiles
+// streamed HBM/L2 -> LDS by the gfx950 direct-to-LDS loads
 // (global_load_lds_dwordx4) through an NS-deep ring of stage buffers.
 //
 //   C[t, n] = epi( (sum_k X[t,k] * Wc[n,k]) * f32(scale[n]) + bias[n] )
 //
-// Wc holds the int8 codes widened to f16 (exact: |q| <= 127), so the sums are
-// those of matmulTransposeB_f32_i8_rowScale_bias (matmul_w8a32.zig:14-57) on
-// f16-rounded activations.  Epilogues: bias, bias + GELU (arctic.zig:771-776),
+// the sums of matmulTransposeB_f32_i8_rowScale_bias (matmul_w8a32.zig:14-57).
+// Weight codes are exact in f16 (|q| <= 127).  f32 activations (the
+// reference's arithmetic) are split per fragment into an f16 pair x = hi + lo
+// + r: hi = f16(x), lo = f16(x - hi) (x - hi is exact in f32), |r| <=
+// 2^-22 |x| for |x| >= 2^-3 and <= 2^-25 otherwise; both halves go through
+// the MFMA against the same codes into one f32 accumulator, so every product
+// is that of an f32 operand to about 22 bits, summed in f32.  The split is
+// valid for |x| < 65504 (the f16 range); f16 activations (the opt-in fast
+// model path) take one MFMA.  Epilogues: bias, bias + GELU (arctic.zig:771-776),
 // bias + residual + LayerNorm over the full 384-wide row (arctic.zig:716-746,
 // layernorm.zig:26-117, two-pass mean / biased variance).
 //
@@ -154,9 +160,10 @@ struct TileFmt {
 // rows (a multiple of BN) and each k stage, the WTB x BK codes are one
 // contiguous span, rows BK codes apart (tile_codes_w8_kernel writes it), so
 // a stage's weight tile is read from consecutive memory.
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_, bool W8_ = false, int WTB_ = 0>
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_, bool W8_ = false, int WTB_ = 0, int XE_ = 2>
 struct PipeCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, NS = NS_;
+    static constexpr int XE = XE_;  // bytes per activation element: 2 (f16) or 4 (f32, split hi/lo)
     static constexpr bool W8 = W8_, WT = WTB_ > 0;
     static constexpr int WTB = WTB_ > 0 ? WTB_ : BN_;
     static_assert(WTB % BN_ == 0, "weight tile blocks hold whole column tiles");
@@ -164,10 +171,10 @@ struct PipeCfg {
     static constexpr int TMF = BM / WM / 32;  // token fragments per wave
     static constexpr int TNF = BN / WN / 32;  // weight fragments per wave
     static constexpr int WEB = W8 ? 1 : 2;    // bytes per weight code
-    using FX = TileFmt<BK * 2>;
+    using FX = TileFmt<BK * XE>;
     using FW = TileFmt<BK * WEB>;
     static_assert(!W8 || BK % 32 == 0, "int8 weights: whole 16-byte chunks per half-wave");
-    static constexpr int X_BYTES = BM * BK * 2, W_BYTES = BN * BK * WEB, STAGE = X_BYTES + W_BYTES;
+    static constexpr int X_BYTES = BM * BK * XE, W_BYTES = BN * BK * WEB, STAGE = X_BYTES + W_BYTES;
     static constexpr int XG = BM / FX::RPI, WG = BN / FW::RPI;  // DMA instructions per tile
     static constexpr int LX = XG / NW, LW = WG / NW, L = LX + LW;
     static_assert(XG % NW == 0 && WG % NW == 0, "DMA groups must split evenly over the waves");
@@ -176,11 +183,12 @@ struct PipeCfg {
     // LDS of one block (stage ring + parameter table + LayerNorm statistics
     // + per-wave output staging tiles) and how many such blocks a CU's
     // 160 KiB holds
-    static constexpr int lds_bytes(bool ln) {
-        return NS * STAGE + (ln ? 4 * BN * 4 + 2 * BM * WN * 4 : 2 * 1536 * 4) + NW * 2048;
+    // (staged: f16 output through the per-wave 2 KiB tiles)
+    static constexpr int lds_bytes(bool ln, bool staged = true) {
+        return NS * STAGE + (ln ? 4 * BN * 4 + 2 * BM * WN * 4 : 2 * 1536 * 4) + (staged ? NW * 2048 : 16);
     }
-    static constexpr int blocks_per_cu(bool ln) {
-        return 163840 / lds_bytes(ln) > 2 ? 2 : 163840 / lds_bytes(ln);
+    static constexpr int blocks_per_cu(bool ln, bool staged = true) {
+        return 163840 / lds_bytes(ln, staged) > 2 ? 2 : 163840 / lds_bytes(ln, staged);
     }
 };
 
@@ -253,16 +261,34 @@ __device__ __forceinline__ void store4<float>(float *p, float a, float b, float 
 // pre-normalisation rows of a split LayerNorm tile (see launch_ln).
 enum { EPI_BIAS = 0, EPI_GELU = 1, EPI_LN = 2, EPI_RES = 3 };
 
-template <int EPI, typename TC, typename P, typename TR = TC>
+// f32 fragment (8 consecutive k of one token) -> hi, lo f16 halves (see the
+// file comment).  Round-to-nearest both ways; x - hi is exact in f32.
+__device__ __forceinline__ void split_f32x8(const f32x4_t &a, const f32x4_t &b, half8_t &hi, half8_t &lo) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        hi[i] = (_Float16)a[i];
+        hi[4 + i] = (_Float16)b[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        lo[i] = (_Float16)(a[i] - (float)hi[i]);
+        lo[4 + i] = (_Float16)(b[i] - (float)hi[4 + i]);
+    }
+}
+
+template <int EPI, typename TC, typename P, typename TR = TC, typename TX = _Float16>
 __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
-    const _Float16 *__restrict__ X, const void *__restrict__ Wc, const uint16_t *__restrict__ scale,
+    const TX *__restrict__ X, const void *__restrict__ Wc, const uint16_t *__restrict__ scale,
     const float *__restrict__ bias, TC *__restrict__ C, int M, int K, int N, const TR *__restrict__ R,
-    const float *__restrict__ gamma, const float *__restrict__ beta, float eps) {
+    const float *__restrict__ gamma, const float *__restrict__ beta, float eps, int ldc, int n_valid) {
     using FX = typename P::FX;
     using FW = typename P::FW;
     constexpr int BM = P::BM, BN = P::BN, BK = P::BK, NS = P::NS, TMF = P::TMF, TNF = P::TNF;
     constexpr int XROWB = FX::ROW_BYTES, WROWB = FW::ROW_BYTES, WEB = P::WEB;
     constexpr bool W8 = P::W8;
+    constexpr int XE = (int)sizeof(TX);
+    constexpr bool XF32 = XE == 4;
+    static_assert(XE == P::XE, "configuration built for another activation type");
     constexpr bool LN = EPI == EPI_LN;
     static_assert(!LN || P::WN * TNF * 32 == BN, "LayerNorm tiles cover whole rows");
     constexpr int NPAR = LN ? 4 : 2;                        // per-column parameters kept in LDS
@@ -280,6 +306,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wm = w / P::WN, wn = w % P::WN;
     const int KT = K / BK;
+    const bool cvec = (ldc & 3) == 0 && ((uintptr_t)C & 15) == 0;
     const int nbn = N / BN;  // column tiles per row panel (1 with the LayerNorm epilogue)
     // Work units are (row panel, column tile) pairs.  Workgroups go to the
     // XCDs round-robin (block b on XCD b % 8) and each XCD has its own L2.
@@ -300,9 +327,11 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     auto unit_n0 = [&](int i) __attribute__((always_inline)) { return (slot + i * spx) % nbn * BN; };
 
     // per-column parameters -> LDS (visible after the first stage barrier)
+    // Columns n_valid .. N-1 are padding (zero codes): their parameters are
+    // never read from memory and their outputs never stored.
     for (int i = tid; i < N; i += P::THREADS) {
-        par[0][i] = f16_bits_to_f32(scale[i]);
-        par[1][i] = bias ? bias[i] : 0.0f;
+        par[0][i] = i < n_valid ? f16_bits_to_f32(scale[i]) : 0.0f;
+        par[1][i] = bias && i < n_valid ? bias[i] : 0.0f;
         if constexpr (LN) {
             par[2][i] = gamma[i];
             par[3][i] = beta[i];
@@ -314,9 +343,6 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     // = wave-uniform row base (scalar) + a small per-lane byte offset.
     const int wu = __builtin_amdgcn_readfirstlane(w);                // wave index, uniform
     const int r_in = lane / FX::CPR;                                 // row inside an X DMA group
-    // logical 16-byte chunk this lane fetches in an even / odd DMA group
-    const int chunk_e = (lane % FX::CPR) ^ FX::swz(r_in);
-    const int chunk_o = (lane % FX::CPR) ^ FX::swz(FX::RPI + r_in);
     const int rw_in = lane / FW::CPR;                                // row inside a W DMA group
     const int wchunk_e = (lane % FW::CPR) ^ FW::swz(rw_in);
     const int wchunk_o = (lane % FW::CPR) ^ FW::swz(FW::RPI + rw_in);
@@ -337,18 +363,19 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
             r0 = r0 < M ? r0 : M - 1;
             const int r = r0 + r_in < M ? r0 + r_in : M - 1;
             x_row0[i] = r0;
-            const int chunk = (FX::PARITY && ((wu * P::LX + i) & 1)) ? chunk_o : chunk_e;
-            x_loff[i] = (uint32_t)((r - r0) * K + chunk * 8) * 2u;
+            // logical 16-byte chunk that lands at this lane's slot of its tile row
+            const int chunk = (lane % FX::CPR) ^ FX::swz((wu * P::LX + i) * FX::RPI + r_in);
+            x_loff[i] = (uint32_t)((r - r0) * K * XE + chunk * 16);
         }
         w_unit = P::WT ? Wb + (size_t)(n0 / P::WTB) * KT * P::WTB * WROWB +
                              (size_t)(n0 % P::WTB + wu * P::LW * FW::RPI) * WROWB
                        : Wb + (size_t)(n0 + wu * P::LW * FW::RPI) * K * WEB;
     };
     auto issue = [&](char *buf) __attribute__((always_inline)) {
-        const size_t k0b = (size_t)ikt * BK * 2;
+        const size_t k0b = (size_t)ikt * BK * XE;
 #pragma unroll
         for (int i = 0; i < P::LX; i++)
-            dma16(Xb + ((size_t)x_row0[i] * K * 2 + k0b), x_loff[i], buf + (wu * P::LX + i) * FX::RPI * XROWB);
+            dma16(Xb + ((size_t)x_row0[i] * K * XE + k0b), x_loff[i], buf + (wu * P::LX + i) * FX::RPI * XROWB);
 #pragma unroll
         for (int i = 0; i < P::LW; i++)
             dma16(w_unit + (P::WT ? (size_t)ikt * P::WTB * WROWB + (size_t)i * FW::RPI * WROWB
@@ -368,12 +395,15 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     // weights: a 16-byte read holds 16 codes, so half-wave h takes k = 32 h +
     // 8 ks .. 32 h + 8 ks + 7 in MFMA ks (BK = 64; BK = 32: 16 h + 8 ks), the
     // X operand following the same k.
+    // f32 activations: the 8 k-values are two 16-byte chunks, 2 cx and 2 cx + 1.
     const int fx = FX::swz(l31), fw = FW::swz(l31);
-    int xoff[BK / 16], woff[BK / 16];
+    int xoff[BK / 16], xoff1[BK / 16], woff[BK / 16];
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ks++) {
         const int cx = W8 ? (BK / 16) * half + ks : 2 * ks + half;
-        xoff[ks] = (wm * TMF * 32 + l31) * XROWB + ((cx ^ fx) << 4);
+        const int row = (wm * TMF * 32 + l31) * XROWB;
+        xoff[ks] = row + (((XF32 ? 2 * cx : cx) ^ fx) << 4);
+        xoff1[ks] = row + (((2 * cx + 1) ^ fx) << 4);
         const int cw = W8 ? (BK / 32) * half + ks / 2 : 2 * ks + half;  // W8: ks and ks+1 share a read
         woff[ks] = P::X_BYTES + (wn * TNF * 32 + l31) * WROWB + ((cw ^ fw) << 4);
     }
@@ -388,9 +418,17 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
         u32x4_t wraw[TNF];
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ks++) {
-            half8_t xf[TMF], wf[TNF];
+            half8_t xf[TMF], xl[TMF], wf[TNF];
 #pragma unroll
-            for (int b = 0; b < TMF; b++) xf[b] = *(const half8_t *)(buf + xoff[ks] + b * 32 * XROWB);
+            for (int b = 0; b < TMF; b++) {
+                if constexpr (XF32) {
+                    const f32x4_t x0 = *(const f32x4_t *)(buf + xoff[ks] + b * 32 * XROWB);
+                    const f32x4_t x1 = *(const f32x4_t *)(buf + xoff1[ks] + b * 32 * XROWB);
+                    split_f32x8(x0, x1, xf[b], xl[b]);
+                } else {
+                    xf[b] = *(const half8_t *)(buf + xoff[ks] + b * 32 * XROWB);
+                }
+            }
 #pragma unroll
             for (int a = 0; a < TNF; a++) {
                 if constexpr (W8) {
@@ -405,6 +443,13 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 #pragma unroll
                 for (int b = 0; b < TMF; b++)
                     acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[a], xf[b], acc[a][b], 0, 0, 0);
+            if constexpr (XF32) {
+#pragma unroll
+                for (int a = 0; a < TNF; a++)
+#pragma unroll
+                    for (int b = 0; b < TMF; b++)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[a], xl[b], acc[a][b], 0, 0, 0);
+            }
         }
     };
 
@@ -440,8 +485,16 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                             if constexpr (STAGED) acc[a][b][4 * g + q] = v[q];
                         }
                         if constexpr (!STAGED)
-                            if (t < M) {
-                                store4<TC>(C + (size_t)t * N + n, v[0], v[1], v[2], v[3]);
+                            if (t < M && n < n_valid) {
+                                // 16-byte stores where rows keep that alignment; more store
+                                // instructions than the stage waits count only make them wait longer
+                                if (cvec && n + 4 <= n_valid) {
+                                    store4<TC>(C + (size_t)t * ldc + n, v[0], v[1], v[2], v[3]);
+                                } else {
+#pragma unroll
+                                    for (int q = 0; q < 4; q++)
+                                        if (n + q < n_valid) C[(size_t)t * ldc + n + q] = (TC)v[q];
+                                }
                                 vmem_store_issued();
                             }
                     }
@@ -452,8 +505,8 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                         float v[16];
 #pragma unroll
                         for (int e = 0; e < 16; e++) v[e] = acc[a][b][e];
-                        store_frag_f16(epi_ws + w * 2048, v, (_Float16 *)C + (size_t)t0 * N + n0 + wn * TNF * 32 + a * 32,
-                                       N, M - t0);
+                        store_frag_f16(epi_ws + w * 2048, v, (_Float16 *)C + (size_t)t0 * ldc + n0 + wn * TNF * 32 + a * 32,
+                                       ldc, M - t0);
                     }
                 }
             }
@@ -594,7 +647,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
             const int i = s / KT;
             epilogue(i);
             last_epi = s;
-            last_full = unit_m0(i) + BM <= M;
+            last_full = unit_m0(i) + BM <= M && unit_n0(i) + BN <= n_valid;
         }
     };
     for (int s = 0; s < S; s += NS) {
@@ -609,7 +662,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 
 // Tile shapes (tokens x output columns x k per stage, waves, stages), chosen
 // by measurement on MI355X at the Arctic shapes (T = 67590 tokens), per
-// weight format:
+// weight format and activation type:
 //   TZH_WF_F16: f16 codes, row-major [n, k] (any n multiple of 128; the f32
 //     model's power-of-two-scaled codes need it);
 //   TZH_WF_W8T: biased int8 codes u = q + 128, stage-tiled in 384-row
@@ -618,21 +671,23 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 //     QKV 78 -> 73, FFN1 118 -> 114, FFN2 + LN 106 -> 98 us at T = 65536.
 // 128 x 384 tiles halve the L2 -> LDS operand traffic of 128 x 128 ones.
 // The pieces cut a partial last round of a LayerNorm GEMM (12, 6 or 3 per
-// 128 x 384 tile; see launch_ln).
+// 128 x 384 tile; see launch_ln).  f32 activations double the X tile, so
+// their configurations keep two stages of 128 x 384 x 64 (112 KiB).
 constexpr int kWtBlock = 384;  // rows per stage-tiled weight block
-template <int WF>
+template <int WF, int XE>
 struct Cfgs;
 template <>
-struct Cfgs<TZH_WF_F16> {
+struct Cfgs<TZH_WF_F16, 2> {
     using Bias = PipeCfg<128, 384, 64, 2, 4, 2>;       // n a multiple of 384
     using Narrow = PipeCfg<128, 128, 64, 2, 2, 4>;     // other multiples of 128
     using Ln = PipeCfg<128, 384, 64, 2, 4, 2>;
+    using LnShortK = void;
     using Piece64 = PipeCfg<64, 64, 64, 2, 2, 4>;
     using Piece128x64 = PipeCfg<128, 64, 64, 2, 2, 4>;
     using Piece128 = Narrow;
 };
 template <>
-struct Cfgs<TZH_WF_W8T> {
+struct Cfgs<TZH_WF_W8T, 2> {
     using Bias = PipeCfg<128, 384, 64, 2, 4, 3, true, kWtBlock>;
     using Narrow = Bias;  // n is always a multiple of 384
     using Ln = Bias;
@@ -648,32 +703,46 @@ struct Cfgs<TZH_WF_W8T> {
     using Piece128x64 = PipeCfg<128, 64, 64, 2, 2, 4, true, kWtBlock>;
     using Piece128 = PipeCfg<128, 128, 64, 2, 2, 4, true, kWtBlock>;
 };
-using LnCfg = Cfgs<TZH_WF_F16>::Ln;
-static_assert(Cfgs<TZH_WF_W8T>::Ln::WN == LnCfg::WN && Cfgs<TZH_WF_W8T>::Ln::TNF == LnCfg::TNF &&
-                  Cfgs<TZH_WF_W8T>::Ln::BN == LnCfg::BN && Cfgs<TZH_WF_W8T>::LnShortK::WN == LnCfg::WN &&
-                  Cfgs<TZH_WF_W8T>::LnShortK::TNF == LnCfg::TNF,
+template <>
+struct Cfgs<TZH_WF_W8T, 4> {
+    using Bias = PipeCfg<128, 384, 64, 2, 4, 2, true, kWtBlock, 4>;
+    using Narrow = Bias;
+    using Ln = Bias;
+    using LnShortK = void;
+    using Piece64 = PipeCfg<64, 64, 64, 2, 2, 3, true, kWtBlock, 4>;
+    using Piece128x64 = PipeCfg<128, 64, 64, 2, 2, 2, true, kWtBlock, 4>;
+    using Piece128 = PipeCfg<128, 128, 64, 2, 2, 2, true, kWtBlock, 4>;
+};
+using LnCfg = Cfgs<TZH_WF_F16, 2>::Ln;
+static_assert(Cfgs<TZH_WF_W8T, 2>::Ln::WN == LnCfg::WN && Cfgs<TZH_WF_W8T, 2>::Ln::TNF == LnCfg::TNF &&
+                  Cfgs<TZH_WF_W8T, 2>::Ln::BN == LnCfg::BN && Cfgs<TZH_WF_W8T, 2>::LnShortK::WN == LnCfg::WN &&
+                  Cfgs<TZH_WF_W8T, 2>::LnShortK::TNF == LnCfg::TNF && Cfgs<TZH_WF_W8T, 4>::Ln::WN == LnCfg::WN &&
+                  Cfgs<TZH_WF_W8T, 4>::Ln::TNF == LnCfg::TNF && Cfgs<TZH_WF_W8T, 4>::Ln::BN == LnCfg::BN,
               "one LayerNorm epilogue layout (statistics order) for every configuration and ln_rows_kernel");
-static_assert(Cfgs<TZH_WF_W8T>::LnShortK::blocks_per_cu(true) == 2, "two short-k LayerNorm workgroups per CU");
+static_assert(Cfgs<TZH_WF_W8T, 2>::LnShortK::blocks_per_cu(true) == 2, "two short-k LayerNorm workgroups per CU");
+static_assert(Cfgs<TZH_WF_W8T, 4>::Bias::lds_bytes(false, false) <= 163840 &&
+                  Cfgs<TZH_WF_W8T, 4>::Ln::lds_bytes(true, false) <= 163840,
+              "f32-activation tiles fit the 160 KiB of LDS");
 
 template <typename T>
 struct NoDeduce {
     using type = T;
 };
 
-template <int EPI, typename TC, typename P, typename TR = TC>
-int launch(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, const uint16_t *scale,
-           const float *bias, TC *c, int M, int K, int N, const typename NoDeduce<TR>::type *res,
-           const float *gamma, const float *beta, float eps) {
+template <int EPI, typename TC, typename P, typename TR = TC, typename TX>
+int launch(hipStream_t st, int num_cus, const TX *x, const void *wc, const uint16_t *scale, const float *bias, TC *c,
+           int M, int K, int N, const typename NoDeduce<TR>::type *res, const float *gamma, const float *beta,
+           float eps, int ldc, int n_valid) {
     const int nbm = (M + P::BM - 1) / P::BM;
     const int nbn = N / P::BN;
-    const int slots = num_cus * P::blocks_per_cu(EPI == EPI_LN);
+    const int slots = num_cus * P::blocks_per_cu(EPI == EPI_LN, std::is_same<TC, _Float16>::value);
     // Persistent blocks.  Panel p goes to XCD p % 8 with its nbn units, so
     // 8 * ceil(panels / 8) * nbn blocks give every unit a block of its own
     // (blocks without a unit return at once); beyond that, one per slot.
     const int64_t spread = (int64_t)kXcds * ((nbm + kXcds - 1) / kXcds) * nbn;
     const int grid = spread < slots ? (int)spread : slots;
-    hipLaunchKernelGGL((linear_pipe_kernel<EPI, TC, P, TR>), dim3(grid), dim3(P::THREADS), 0, st, x, wc, scale, bias,
-                       c, M, K, N, res, gamma, beta, eps);
+    hipLaunchKernelGGL((linear_pipe_kernel<EPI, TC, P, TR, TX>), dim3(grid), dim3(P::THREADS), 0, st, x, wc, scale,
+                       bias, c, M, K, N, res, gamma, beta, eps, ldc, n_valid);
     TZH_LAUNCHED("linear_pipe_kernel");
     return TZH_OK;
 }
@@ -755,17 +824,18 @@ __global__ void __launch_bounds__(256) ln_rows_kernel(const float *__restrict__ 
 // output value comes out the same as it would from the whole-tile kernel:
 // the pieces run the same MFMA sequence per element, and ln_rows_kernel
 // sums the statistics in the tile epilogue's order.
-template <int WF, typename TC>
-int launch_ln(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, const uint16_t *scale,
-              const float *bias, TC *c, int M, int K, const TC *res, const float *gamma, const float *beta, float eps,
-              float *ws, int64_t ws_rows) {
-    using C = Cfgs<WF>;
+template <int WF, typename TC, typename TX>
+int launch_ln(hipStream_t st, int num_cus, const TX *x, const void *wc, const uint16_t *scale, const float *bias,
+              TC *c, int M, int K, const TC *res, const float *gamma, const float *beta, float eps, float *ws,
+              int64_t ws_rows) {
+    using C = Cfgs<WF, (int)sizeof(TX)>;
     constexpr int N = C::Ln::BN, BM = C::Ln::BM;
-    if constexpr (WF == TZH_WF_W8T)
+    constexpr bool staged = std::is_same<TC, _Float16>::value;
+    if constexpr (!std::is_void<typename C::LnShortK>::value)
         if (K <= 384)
             return launch<EPI_LN, TC, typename C::LnShortK>(st, num_cus, x, wc, scale, bias, c, M, K, N, res, gamma,
-                                                            beta, eps);
-    const int slots = num_cus * C::Ln::blocks_per_cu(true);
+                                                            beta, eps, N, N);
+    const int slots = num_cus * C::Ln::blocks_per_cu(true, staged);
     const int panels = (M + BM - 1) / BM;
     const int full = panels / slots * slots;
     const int rem = panels - full;
@@ -780,43 +850,46 @@ int launch_ln(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, co
     const int m_main = per ? full * BM : M;
     if (m_main > 0)
         TZH_TRY((launch<EPI_LN, TC, typename C::Ln>(st, num_cus, x, wc, scale, bias, c, m_main, K, N, res, gamma, beta,
-                                                     eps)));
+                                                     eps, N, N)));
     if (!per) return TZH_OK;
-    const _Float16 *xt = x + (size_t)m_main * K;
+    const TX *xt = x + (size_t)m_main * K;
     const TC *rt = res + (size_t)m_main * N;
     if (per == 12)
-        TZH_TRY((launch<EPI_RES, float, typename C::Piece64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N, rt,
-                                                      nullptr, nullptr, 0.f)));
+        TZH_TRY((launch<EPI_RES, float, typename C::Piece64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N,
+                                                                  rt, nullptr, nullptr, 0.f, N, N)));
     else if (per == 6)
-        TZH_TRY((launch<EPI_RES, float, typename C::Piece128x64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N, rt,
-                                                          nullptr, nullptr, 0.f)));
+        TZH_TRY((launch<EPI_RES, float, typename C::Piece128x64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K,
+                                                                      N, rt, nullptr, nullptr, 0.f, N, N)));
     else
-        TZH_TRY((launch<EPI_RES, float, typename C::Piece128, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N, rt,
-                                                       nullptr, nullptr, 0.f)));
+        TZH_TRY((launch<EPI_RES, float, typename C::Piece128, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N,
+                                                                   rt, nullptr, nullptr, 0.f, N, N)));
     hipLaunchKernelGGL(ln_rows_kernel<TC>, dim3((unsigned)((tail_rows + 31) / 32)), dim3(256), 0, st, ws, tail_rows,
                        gamma, beta, eps, c + (size_t)m_main * N);
     TZH_LAUNCHED("ln_rows_kernel");
     return TZH_OK;
 }
 
-template <int WF, int EPI, typename TC>
-int launch_bias(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, const uint16_t *scale,
-                const float *bias, TC *c, int M, int K, int N) {
-    using C = Cfgs<WF>;
+template <int WF, int EPI, typename TC, typename TX>
+int launch_bias(hipStream_t st, int num_cus, const TX *x, const void *wc, const uint16_t *scale, const float *bias,
+                TC *c, int M, int K, int N, int ldc, int n_valid) {
+    using C = Cfgs<WF, (int)sizeof(TX)>;
     if (N % C::Bias::BN == 0)
         return launch<EPI, TC, typename C::Bias>(st, num_cus, x, wc, scale, bias, c, M, K, N, nullptr, nullptr,
-                                                 nullptr, 0.f);
+                                                 nullptr, 0.f, ldc, n_valid);
     return launch<EPI, TC, typename C::Narrow>(st, num_cus, x, wc, scale, bias, c, M, K, N, nullptr, nullptr, nullptr,
-                                               0.f);
+                                               0.f, ldc, n_valid);
 }
 
 // int8 codes q[r][j] (n rows of k) -> biased codes u = q + 128 stage-tiled
-// for TZH_WF_W8T: u lands at ((r / 384 * (k / 64) + j / 64) * 384 + r % 384)
-// * 64 + j % 64.  One thread per 16 codes.
-__global__ void tile_codes_w8_kernel(const int8_t *__restrict__ q, uint8_t *__restrict__ out, int n, int k) {
+// for TZH_WF_W8T over the padded shape n_pad x k_pad (multiples of 384 and
+// 64): u lands at ((r / 384 * (k_pad / 64) + j / 64) * 384 + r % 384) * 64 +
+// j % 64; rows r >= n and columns j >= k hold code 0 (u = 128), which adds
+// nothing to any sum.  One thread per 16 codes.
+__global__ void tile_codes_w8_kernel(const int8_t *__restrict__ q, uint8_t *__restrict__ out, int n, int k,
+                                     int n_pad, int k_pad) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 16-byte group of the output
-    const int kt_count = k / 64;
-    if (i >= (int64_t)n * k / 16) return;
+    const int kt_count = k_pad / 64;
+    if (i >= (int64_t)n_pad * k_pad / 16) return;
     const int64_t o = i * 16;
     const int c = (int)(o % 64);
     const int64_t r_all = o / 64;  // row index inside the tiled layout (block, stage, row)
@@ -824,11 +897,27 @@ __global__ void tile_codes_w8_kernel(const int8_t *__restrict__ q, uint8_t *__re
     const int64_t bs = r_all / kWtBlock;
     const int kt = (int)(bs % kt_count);
     const int nb = (int)(bs / kt_count);
-    const int8_t *src = q + ((int64_t)nb * kWtBlock + r) * k + kt * 64 + c;
+    const int row = nb * kWtBlock + r, j0 = kt * 64 + c;
     uint8_t v[16];
+    if (row < n && j0 + 16 <= k) {
+        const int8_t *src = q + (int64_t)row * k + j0;
 #pragma unroll
-    for (int j = 0; j < 16; j++) v[j] = (uint8_t)src[j] ^ 0x80u;
+        for (int j = 0; j < 16; j++) v[j] = (uint8_t)src[j] ^ 0x80u;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = (row < n && j0 + j < k) ? (uint8_t)q[(int64_t)row * k + j0 + j] ^ 0x80u : 0x80u;
+    }
     *(u32x4_t *)(out + o) = *(const u32x4_t *)v;
+}
+
+// f32 rows [m, k] -> [m, k_pad] with zero columns k .. k_pad-1 (an
+// activation operand whose k is not a multiple of the stage depth).
+__global__ void pad_cols_f32_kernel(const float *__restrict__ x, float *__restrict__ y, int64_t m, int k, int k_pad) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m * k_pad) return;
+    const int64_t r = i / k_pad;
+    const int j = (int)(i % k_pad);
+    y[i] = j < k ? x[r * k + j] : 0.0f;
 }
 
 __global__ void widen_codes_kernel(const int8_t *__restrict__ q, _Float16 *__restrict__ out, int64_t n) {
@@ -860,69 +949,121 @@ int tzh_widen_codes_launch(hipStream_t st, const int8_t *q, _Float16 *out, int64
     return TZH_OK;
 }
 
-// int8 codes [n, k] -> the TZH_WF_W8T layout (n a multiple of 384, k of 64).
-int tzh_tile_codes_w8_launch(hipStream_t st, const int8_t *q, uint8_t *out, int64_t n, int64_t k) {
-    if (n % kWtBlock || k % 64 || n <= 0 || k <= 0)
-        return tzh_fail(TZH_ERR_INVALID_ARGS, "tiled int8 weights need n %% 384 == 0 and k %% 64 == 0");
-    const int64_t groups = n * k / 16;
+// int8 codes [n, k] -> the TZH_WF_W8T layout of the padded shape n_pad x
+// k_pad (multiples of 384 and 64, at least n and k).
+int tzh_tile_codes_w8_launch(hipStream_t st, const int8_t *q, uint8_t *out, int64_t n, int64_t k, int64_t n_pad,
+                             int64_t k_pad) {
+    if (n_pad % kWtBlock || k_pad % 64 || n <= 0 || k <= 0 || n > n_pad || k > k_pad)
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "tiled int8 weights need n_pad %% 384 == 0, k_pad %% 64 == 0");
+    const int64_t groups = n_pad * k_pad / 16;
     hipLaunchKernelGGL(tile_codes_w8_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, st, q, out, (int)n,
-                       (int)k);
+                       (int)k, (int)n_pad, (int)k_pad);
     TZH_LAUNCHED("tile_codes_w8_kernel");
     return TZH_OK;
 }
 
-// f16 activations x weight codes in format w_format (TZH_WF_F16: f16
-// row-major; TZH_WF_W8T: tiled biased int8, f16 output only); output and
-// residual both F16 or both F32.  ln_ws (f32, ln_ws_rows rows of 384; may
-// be null) lets the LayerNorm epilogue split a partial last round of tiles
-// (see launch_ln).
-int tzh_linear_codes_launch(hipStream_t st, int num_cus, const _Float16 *x, const void *wc, int32_t w_format,
-                            const uint16_t *scale, const float *bias, void *c, int32_t c_dtype, int64_t m, int64_t k,
-                            int64_t n, int32_t epilogue, const void *res, const float *gamma, const float *beta,
-                            float eps, float *ln_ws, int64_t ln_ws_rows) {
-    if (m < 0 || k <= 0 || n <= 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad GEMM shape");
+int tzh_pad_cols_f32_launch(hipStream_t st, const float *x, float *y, int64_t m, int64_t k, int64_t k_pad) {
+    if (m <= 0) return TZH_OK;
+    const int64_t n = m * k_pad;
+    hipLaunchKernelGGL(pad_cols_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, y, m, (int)k,
+                       (int)k_pad);
+    TZH_LAUNCHED("pad_cols_f32_kernel");
+    return TZH_OK;
+}
+
+// Activations x (f16: f16 or f32) x weight codes in format w_format
+// (TZH_WF_F16: f16 row-major, f16 activations only; TZH_WF_W8T: tiled
+// biased int8), output and residual both F16 or both F32.  The weight codes
+// may be padded: n is the padded column count the code layout holds and
+// n_valid <= n the columns that exist (scale and bias have n_valid entries;
+// C rows are n_valid apart); the bias epilogues run n in chunks of up to
+// 1536 columns.  ln_ws (f32, ln_ws_rows rows of 384; may be null) lets the
+// LayerNorm epilogue split a partial last round of tiles (see launch_ln).
+int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t x_dtype, const void *wc,
+                            int32_t w_format, const uint16_t *scale, const float *bias, void *c, int32_t c_dtype,
+                            int64_t m, int64_t k, int64_t n, int64_t n_valid, int32_t epilogue, const void *res,
+                            const float *gamma, const float *beta, float eps, float *ln_ws, int64_t ln_ws_rows) {
+    if (m < 0 || k <= 0 || n <= 0 || n_valid <= 0 || n_valid > n) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad GEMM shape");
     if (m == 0) return TZH_OK;  // matmul_w8a32.zig:24
-    if (m > (int64_t)1 << 30 || k > 65536) return tzh_fail(TZH_ERR_TOO_LARGE, "GEMM shape too large");
+    if (m > (int64_t)1 << 30 || k > 65536 || n > 65536) return tzh_fail(TZH_ERR_TOO_LARGE, "GEMM shape too large");
     if (k % 64) return tzh_fail(TZH_ERR_INVALID_ARGS, "k=%lld must be a multiple of 64", (long long)k);
     if (!x || !wc || !scale || !c) return tzh_fail(TZH_ERR_INVALID_ARGS, "null operand");
-    if (!aligned16(x) || !aligned16(wc) || !aligned16(c) || (res && !aligned16(res)))
+    if (!aligned16(x) || !aligned16(wc) || (res && !aligned16(res)) || ((uintptr_t)c & 3) ||
+        ((c_dtype == TZH_F16 || epilogue == TZH_EPI_BIAS_RES_LN) && !aligned16(c)))
         return tzh_fail(TZH_ERR_INVALID_ARGS, "operands must be 16-byte aligned");
     if (c_dtype != TZH_F16 && c_dtype != TZH_F32) return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "output must be F16 or F32");
-    const int M = (int)m, K = (int)k, N = (int)n;
-    const bool c16 = c_dtype == TZH_F16;
+    if (x_dtype != TZH_F16 && x_dtype != TZH_F32)
+        return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "activations must be F16 or F32");
+    const int M = (int)m, K = (int)k, N = (int)n, NV = (int)n_valid;
+    const bool c16 = c_dtype == TZH_F16, x32 = x_dtype == TZH_F32;
     if (w_format != TZH_WF_F16 && w_format != TZH_WF_W8T)
         return tzh_fail(TZH_ERR_INVALID_ARGS, "unknown weight format %d", w_format);
     const bool w8t = w_format == TZH_WF_W8T;
-    if (w8t && (!c16 || N % kWtBlock))
-        return tzh_fail(TZH_ERR_INVALID_ARGS, "tiled int8 weights need f16 output and n %% 384 == 0 (n=%d)", N);
+    if (w8t && N % kWtBlock) return tzh_fail(TZH_ERR_INVALID_ARGS, "tiled int8 weights need n %% 384 == 0 (n=%d)", N);
+    if (x32 && !w8t) return tzh_fail(TZH_ERR_INVALID_ARGS, "f32 activations need the tiled int8 weight format");
+    if (c16 && NV != N) return tzh_fail(TZH_ERR_INVALID_ARGS, "f16 output needs every column (n_valid == n)");
     if (epilogue == TZH_EPI_BIAS || epilogue == TZH_EPI_BIAS_GELU) {
-        if (N % 128 || N > 1536)
-            return tzh_fail(TZH_ERR_INVALID_ARGS, "n=%d must be a multiple of 128 and at most 1536", N);
-        if (w8t)
-            return epilogue == TZH_EPI_BIAS
-                       ? launch_bias<TZH_WF_W8T, EPI_BIAS, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M,
-                                                                     K, N)
-                       : launch_bias<TZH_WF_W8T, EPI_GELU, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M,
-                                                                     K, N);
-        if (epilogue == TZH_EPI_BIAS)
-            return c16 ? launch_bias<TZH_WF_F16, EPI_BIAS, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c,
-                                                                     M, K, N)
-                       : launch_bias<TZH_WF_F16, EPI_BIAS, float>(st, num_cus, x, wc, scale, bias, (float *)c, M, K,
-                                                                  N);
-        return c16 ? launch_bias<TZH_WF_F16, EPI_GELU, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K,
-                                                                 N)
-                   : launch_bias<TZH_WF_F16, EPI_GELU, float>(st, num_cus, x, wc, scale, bias, (float *)c, M, K, N);
+        if (N % 128) return tzh_fail(TZH_ERR_INVALID_ARGS, "n=%d must be a multiple of 128", N);
+        const bool gelu = epilogue == TZH_EPI_BIAS_GELU;
+        // column chunks of up to 1536 (the parameters of a chunk sit in LDS)
+        for (int j0 = 0; j0 < NV; j0 += 1536) {
+            const int nc = N - j0 < 1536 ? N - j0 : 1536, nv = NV - j0 < nc ? NV - j0 : nc;
+            const char *wj = (const char *)wc + (w8t ? (size_t)(j0 / kWtBlock) * K * kWtBlock : (size_t)j0 * K * 2);
+            const uint16_t *sj = scale + j0;
+            const float *bj = bias ? bias + j0 : nullptr;
+            int rc;
+            if (w8t && x32) {
+                rc = c16 ? (gelu ? launch_bias<TZH_WF_W8T, EPI_GELU, _Float16>(st, num_cus, (const float *)x, wj, sj, bj,
+                                                                              (_Float16 *)c + j0, M, K, nc, NV, nv)
+                                 : launch_bias<TZH_WF_W8T, EPI_BIAS, _Float16>(st, num_cus, (const float *)x, wj, sj, bj,
+                                                                              (_Float16 *)c + j0, M, K, nc, NV, nv))
+                         : (gelu ? launch_bias<TZH_WF_W8T, EPI_GELU, float>(st, num_cus, (const float *)x, wj, sj, bj,
+                                                                           (float *)c + j0, M, K, nc, NV, nv)
+                                 : launch_bias<TZH_WF_W8T, EPI_BIAS, float>(st, num_cus, (const float *)x, wj, sj, bj,
+                                                                           (float *)c + j0, M, K, nc, NV, nv));
+            } else if (w8t) {
+                rc = c16 ? (gelu ? launch_bias<TZH_WF_W8T, EPI_GELU, _Float16>(st, num_cus, (const _Float16 *)x, wj, sj,
+                                                                              bj, (_Float16 *)c + j0, M, K, nc, NV, nv)
+                                 : launch_bias<TZH_WF_W8T, EPI_BIAS, _Float16>(st, num_cus, (const _Float16 *)x, wj, sj,
+                                                                              bj, (_Float16 *)c + j0, M, K, nc, NV, nv))
+                         : (gelu ? launch_bias<TZH_WF_W8T, EPI_GELU, float>(st, num_cus, (const _Float16 *)x, wj, sj,
+                                                                           bj, (float *)c + j0, M, K, nc, NV, nv)
+                                 : launch_bias<TZH_WF_W8T, EPI_BIAS, float>(st, num_cus, (const _Float16 *)x, wj, sj,
+                                                                           bj, (float *)c + j0, M, K, nc, NV, nv));
+            } else {
+                rc = c16 ? (gelu ? launch_bias<TZH_WF_F16, EPI_GELU, _Float16>(st, num_cus, (const _Float16 *)x, wj, sj,
+                                                                              bj, (_Float16 *)c + j0, M, K, nc, NV, nv)
+                                 : launch_bias<TZH_WF_F16, EPI_BIAS, _Float16>(st, num_cus, (const _Float16 *)x, wj, sj,
+                                                                              bj, (_Float16 *)c + j0, M, K, nc, NV, nv))
+                         : (gelu ? launch_bias<TZH_WF_F16, EPI_GELU, float>(st, num_cus, (const _Float16 *)x, wj, sj,
+                                                                           bj, (float *)c + j0, M, K, nc, NV, nv)
+                                 : launch_bias<TZH_WF_F16, EPI_BIAS, float>(st, num_cus, (const _Float16 *)x, wj, sj,
+                                                                           bj, (float *)c + j0, M, K, nc, NV, nv));
+            }
+            TZH_TRY(rc);
+        }
+        return TZH_OK;
     }
     if (epilogue == TZH_EPI_BIAS_RES_LN) {
-        if (N != LnCfg::BN) return tzh_fail(TZH_ERR_INVALID_ARGS, "LayerNorm epilogue needs n == 384 (got %d)", N);
+        if (N != LnCfg::BN || NV != N)
+            return tzh_fail(TZH_ERR_INVALID_ARGS, "LayerNorm epilogue needs n == 384 (got %d)", NV);
         if (!res || !gamma || !beta) return tzh_fail(TZH_ERR_INVALID_ARGS, "null residual/gamma/beta");
         if (ln_ws && !aligned16(ln_ws)) return tzh_fail(TZH_ERR_INVALID_ARGS, "LayerNorm workspace must be 16-byte aligned");
+        if (w8t && x32)
+            return c16 ? launch_ln<TZH_WF_W8T, _Float16>(st, num_cus, (const float *)x, wc, scale, bias, (_Float16 *)c,
+                                                         M, K, (const _Float16 *)res, gamma, beta, eps, ln_ws,
+                                                         ln_ws_rows)
+                       : launch_ln<TZH_WF_W8T, float>(st, num_cus, (const float *)x, wc, scale, bias, (float *)c, M, K,
+                                                      (const float *)res, gamma, beta, eps, ln_ws, ln_ws_rows);
         if (w8t)
-            return launch_ln<TZH_WF_W8T, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K,
-                                                   (const _Float16 *)res, gamma, beta, eps, ln_ws, ln_ws_rows);
-        return c16 ? launch_ln<TZH_WF_F16, _Float16>(st, num_cus, x, wc, scale, bias, (_Float16 *)c, M, K,
-                                                     (const _Float16 *)res, gamma, beta, eps, ln_ws, ln_ws_rows)
-                   : launch_ln<TZH_WF_F16, float>(st, num_cus, x, wc, scale, bias, (float *)c, M, K,
+            return c16 ? launch_ln<TZH_WF_W8T, _Float16>(st, num_cus, (const _Float16 *)x, wc, scale, bias,
+                                                         (_Float16 *)c, M, K, (const _Float16 *)res, gamma, beta, eps,
+                                                         ln_ws, ln_ws_rows)
+                       : launch_ln<TZH_WF_W8T, float>(st, num_cus, (const _Float16 *)x, wc, scale, bias, (float *)c, M,
+                                                      K, (const float *)res, gamma, beta, eps, ln_ws, ln_ws_rows);
+        return c16 ? launch_ln<TZH_WF_F16, _Float16>(st, num_cus, (const _Float16 *)x, wc, scale, bias, (_Float16 *)c,
+                                                     M, K, (const _Float16 *)res, gamma, beta, eps, ln_ws, ln_ws_rows)
+                   : launch_ln<TZH_WF_F16, float>(st, num_cus, (const _Float16 *)x, wc, scale, bias, (float *)c, M, K,
                                                   (const float *)res, gamma, beta, eps, ln_ws, ln_ws_rows);
     }
     return tzh_fail(TZH_ERR_INVALID_ARGS, "unknown epilogue %d", epilogue);

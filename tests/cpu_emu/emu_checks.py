@@ -307,20 +307,27 @@ def group_attention():
         qkv = (rng.standard_normal((Tn, 3 * H)) * 1.5).astype(np.float32)
         if grow:
             qkv[:, H:2 * H] *= (0.2 + np.arange(Tn) / 30.0)[:, None]
-        qkv = qkv.astype(np.float16)
-        cu = np.zeros(len(lengths) + 1, np.int32)
-        cu[1:] = np.cumsum(lengths)
-        out = np.zeros((Tn, H), np.float16)
-        check(L.tzh_attention_varlen(CTX, qkv.ctypes.data, out.ctypes.data, cu.ctypes.data, len(lengths), 12, H))
-        q32 = qkv.astype(np.float32)
-        for bi, Ln in enumerate(lengths):
-            s0 = cu[bi]
-            for h in (0, 7, 11):
-                ref = oracle.attention_head(q32[s0:s0 + Ln, h * D:(h + 1) * D], q32[s0:s0 + Ln, H + h * D:H + (h + 1) * D],
-                                            q32[s0:s0 + Ln, 2 * H + h * D:2 * H + (h + 1) * D])
-                got = out[s0:s0 + Ln, h * D:(h + 1) * D].astype(np.float32)
-                v = q32[s0:s0 + Ln, 2 * H + h * D:2 * H + (h + 1) * D]
-                assert (np.abs(got - ref) <= 2 ** -9 * np.abs(v).max() + 2 ** -10 * np.abs(ref)).all(), (lengths, bi, h)
+        for dt in (np.float16, np.float32):
+            x = qkv.astype(dt)
+            cu = np.zeros(len(lengths) + 1, np.int32)
+            cu[1:] = np.cumsum(lengths)
+            out = np.zeros((Tn, H), dt)
+            check(L.tzh_attention_varlen(CTX, x.ctypes.data, out.ctypes.data, _abi.F32 if dt == np.float32 else _abi.F16,
+                                         cu.ctypes.data, len(lengths), 12, H))
+            q32 = x.astype(np.float32)
+            for bi, Ln in enumerate(lengths):
+                s0 = cu[bi]
+                for h in (0, 7, 11):
+                    ref = oracle.attention_head(q32[s0:s0 + Ln, h * D:(h + 1) * D],
+                                                q32[s0:s0 + Ln, H + h * D:H + (h + 1) * D],
+                                                q32[s0:s0 + Ln, 2 * H + h * D:2 * H + (h + 1) * D])
+                    got = out[s0:s0 + Ln, h * D:(h + 1) * D].astype(np.float32)
+                    vmax = np.abs(q32[s0:s0 + Ln, 2 * H + h * D:2 * H + (h + 1) * D]).max()
+                    if dt == np.float16:
+                        tol = 2 ** -9 * vmax + 2 ** -10 * np.abs(ref)
+                    else:
+                        tol = (2 ** -14 if grow else 2 ** -16) * vmax + 2 ** -18 * np.abs(ref)
+                    assert (np.abs(got - ref) <= tol).all(), (lengths, dt, bi, h, float(np.abs(got - ref).max()))
 
 
 def group_arctic():
@@ -334,12 +341,20 @@ def group_arctic():
     check(L.tzh_arctic_forward_batch(m, out.ctypes.data, ids.ctypes.data, lengths.ctypes.data, 3, 40))
     ref = np.stack([oracle.arctic_forward(hw, ids[b, :Ln]) for b, Ln in enumerate(lengths)])
     err = np.abs(out - ref).max()
-    print(f"  arctic emu vs oracle max-abs {err:.2e}", flush=True)
-    assert err < 1e-3
+    print(f"  arctic emu (f32 activations) vs oracle max-abs {err:.2e}", flush=True)
+    assert err < 1e-5
     hid = np.empty((int(lengths.sum()), 384), np.float32)
     check(L.tzh_arctic_hidden(m, hid.ctypes.data, ids.ctypes.data, lengths.ctypes.data, 3, 40, 1))
     r1 = oracle.arctic_hidden(hw, ids[0, :lengths[0]], 1)
+    assert np.abs(hid[:lengths[0]] - r1).max() < 1e-4
+    # the opt-in f16 activations
+    check(L.tzh_arctic_set_precision(m, _abi.F16))
+    out16 = np.empty((3, 384), np.float32)
+    check(L.tzh_arctic_forward_batch(m, out16.ctypes.data, ids.ctypes.data, lengths.ctypes.data, 3, 40))
+    assert np.abs(out16 - ref).max() < 1e-3
+    check(L.tzh_arctic_hidden(m, hid.ctypes.data, ids.ctypes.data, lengths.ctypes.data, 3, 40, 1))
     assert np.abs(hid[:lengths[0]] - r1).max() < 2e-2
+    check(L.tzh_arctic_set_precision(m, _abi.F32))
     flat, _ = synth.packed(ids, lengths)
     out2 = np.empty((3, 384), np.float32)
     check(L.tzh_arctic_forward_batch(m, out2.ctypes.data, flat.ctypes.data, lengths.ctypes.data, 3, 0))

@@ -25,6 +25,7 @@
 #define __forceinline__ inline
 #define __launch_bounds__(...)
 #define __shared__ static
+#define __align__(n) __attribute__((aligned(n)))
 
 struct dim3 {
     unsigned x = 1, y = 1, z = 1;
@@ -273,6 +274,12 @@ hipError_t hipEventDestroy(hipEvent_t e);
 hipError_t hipEventRecord(hipEvent_t e, hipStream_t s);
 hipError_t hipEventSynchronize(hipEvent_t e);
 hipError_t hipGetLastError();
+// device symbols are host arrays here: their address is the symbol itself
+#define HIP_SYMBOL(x) (&(x))
+inline hipError_t hipGetSymbolAddress(void **p, const void *sym) {
+    *p = const_cast<void *>(sym);
+    return hipSuccess;
+}
 const char *hipGetErrorString(hipError_t e);
 
 // hipLaunchKernelGGL(kernel, grid, block, shmem, stream, args...): every lane

@@ -3,7 +3,10 @@
 
 Bar: final L2-normalised embeddings within 1e-3
 max-abs and cosine >= 0.9999 of the reference path; token ids / packing /
-int8 codes bit-exact."""
+int8 codes bit-exact.  The default f32 activations (the reference's
+arithmetic) are held to a bar a hundred times tighter: 1e-5 max-abs on
+the embeddings, 1e-4 on the hidden states after any number of layers."""
+import contextlib
 import os
 
 import numpy as np
@@ -58,25 +61,51 @@ def gpu_hidden(model, ids, lengths, n_layers):
     return out.cpu().numpy()
 
 
-def assert_embedding_parity(got, ref):
+def assert_embedding_parity(got, ref, max_abs=1e-5):
+    """max_abs: 1e-5 for the f32 forward, the north star's 1e-3 for f16."""
     assert got.shape == ref.shape
     for i in range(ref.shape[0]):
         err = np.abs(got[i] - ref[i]).max()
         cs = cosine(got[i], ref[i])
-        assert err <= 1e-3 and cs >= 0.9999, (i, float(err), cs)
+        assert err <= max_abs and cs >= 0.9999, (i, float(err), cs)
 
 
+@contextlib.contextmanager
+def precision(model, dtype):
+    model.set_precision(dtype)
+    try:
+        yield
+    finally:
+        model.set_precision("float32")
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
 @pytest.mark.parametrize("n_layers", [0, 1, 3, 6])
-def test_hidden_states_layerwise(model, host, n_layers):
+def test_hidden_states_layerwise(model, host, n_layers, dtype):
     ids, lengths = synth.make_batch(21, 3, seq_len=96, min_len=5)
-    got = gpu_hidden(model, ids, lengths, n_layers)
+    with precision(model, dtype):
+        assert model.precision == dtype
+        got = gpu_hidden(model, ids, lengths, n_layers)
     off = 0
     for b, L in enumerate(lengths):
         ref = oracle.arctic_hidden(host, ids[b, :L], n_layers)
         err = np.abs(got[off:off + L] - ref)
-        # f16 storage between kernels: ~2^-11 relative per rounding
-        assert err.max() < 2e-2 and np.sqrt((err ** 2).mean()) < 3e-3, (n_layers, b, float(err.max()))
+        if dtype == "float32":
+            # f32 activations: f32-rounding-level differences only
+            assert err.max() < 1e-4 and np.sqrt((err ** 2).mean()) < 1e-5, (n_layers, b, float(err.max()))
+        else:
+            # f16 storage between kernels: ~2^-11 relative per rounding
+            assert err.max() < 2e-2 and np.sqrt((err ** 2).mean()) < 3e-3, (n_layers, b, float(err.max()))
         off += L
+
+
+def test_f16_forward_within_north_star(model, host):
+    """The opt-in f16 activation path still meets the north star's bar."""
+    ids, lengths = synth.make_batch(24, 8, seq_len=256)
+    with precision(model, "float16"):
+        got = gpu_embed(model, ids, lengths)
+    ref = np.stack([oracle.arctic_forward(host, ids[b, :lengths[b]]) for b in range(8)])
+    assert_embedding_parity(got, ref, max_abs=1e-3)
 
 
 def test_forward_batch_edge_lengths(model, host):
@@ -123,6 +152,26 @@ def test_single_sequence_forward(model, host):
     out = torch.empty(CFG.hidden_size, device="cuda")
     forward(out, d_ids, model)
     assert_embedding_parity(out.cpu().numpy()[None], oracle.arctic_forward(host, ids[0, :L])[None])
+
+
+def test_host_slice_entry_points(model, host):
+    """The reference's host arguments (arctic.zig:874-879, 902-907): host id
+    slices of different lengths in, host embeddings out; equal bit for bit
+    to the device-resident batch entry."""
+    from tenzor_amd.arctic import forwardBatchHost
+
+    ids, lengths = synth.make_batch(25, 5, seq_len=200)
+    seqs = [ids[b, :lengths[b]].copy() for b in range(5)]
+    out = np.zeros((5, CFG.hidden_size), np.float32)
+    forwardBatchHost(out, seqs, model)
+    assert np.array_equal(out, gpu_embed(model, ids, lengths))
+    one = np.zeros(CFG.hidden_size, np.float32)
+    check(lib().tzh_arctic_forward_host(model.handle, one.ctypes.data, seqs[2].ctypes.data, len(seqs[2])))
+    assert np.array_equal(one, out[2])
+    ref = np.stack([oracle.arctic_forward(host, s) for s in seqs[:2]])
+    assert_embedding_parity(out[:2], ref)
+    with pytest.raises(TzhError):
+        forwardBatchHost(np.zeros((1, CFG.hidden_size), np.float32), [np.zeros(0, np.uint32)], model)
 
 
 def test_golden_embeddings(model):
@@ -240,13 +289,15 @@ def test_f32_model_config1(ctx):
     m = ModelWeights.fromHost(ctx, w, CFG)
     try:
         hw = synth.HostWeights(w, CFG)
+        # f32 weights are stored as f16 codes, which run with f16 activations
+        assert m.precision == "float16"
         ids, lengths = synth.make_batch(31, 1, seq_len=128, fixed=True)
         got = gpu_embed(m, ids, lengths)
-        assert_embedding_parity(got, oracle.arctic_forward(hw, ids[0, :128])[None])
+        assert_embedding_parity(got, oracle.arctic_forward(hw, ids[0, :128])[None], max_abs=1e-3)
         ids, lengths = synth.make_batch(32, 6, seq_len=300)
         got = gpu_embed(m, ids, lengths)
         ref = np.stack([oracle.arctic_forward(hw, ids[b, :lengths[b]]) for b in range(6)])
-        assert_embedding_parity(got, ref)
+        assert_embedding_parity(got, ref, max_abs=1e-3)
     finally:
         m.deinit()
 
