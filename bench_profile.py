@@ -39,10 +39,20 @@ import csv
 import glob
 import json
 import os
+import re
 import sys
 
 CAL_BYTES = 1 << 30
 STAGES = ("pack_ids", "embed_ln", "qkv", "attention", "attn_out_ln", "ffn1_gelu", "ffn2_ln", "cls_l2")
+
+
+def epi_of(kernel: str) -> int | None:
+    """Epilogue template argument of a linear_pipe_kernel dispatch (mangled
+    or demangled name), None for other kernels."""
+    m = re.search(r"linear_pipe_kernelILi(\d)E|linear_pipe_kernel<(\d),", kernel)
+    if not m:
+        return None
+    return int(m.group(1) or m.group(2))
 
 
 def stage_of(kernel: str, prev: str | None) -> str | None:
@@ -55,13 +65,14 @@ def stage_of(kernel: str, prev: str | None) -> str | None:
         return "attention"
     if "cls_l2_kernel" in kernel:
         return "cls_l2"
-    if "linear_pipe_kernelILi0E" in kernel:
+    epi = epi_of(kernel)
+    if epi == 0:
         return "qkv"
-    if "linear_pipe_kernelILi1E" in kernel:
+    if epi == 1:
         return "ffn1_gelu"
-    if "linear_pipe_kernelILi2E" in kernel:
+    if epi == 2:
         return "attn_out_ln" if prev == "attention" else "ffn2_ln" if prev == "ffn1_gelu" else None
-    if "linear_pipe_kernelILi3E" in kernel or "ln_rows_kernel" in kernel:
+    if epi == 3 or "ln_rows_kernel" in kernel:
         return prev if prev in ("attn_out_ln", "ffn2_ln") else None
     return None
 
@@ -79,28 +90,44 @@ def _rows(directory: str, suffix: str) -> list[dict]:
 
 def _instances(seq):
     """Groups (kernel name, value) dispatches in launch order into stage
-    instances: {stage: [summed value of each instance]}.  A dispatch that
+    instances per forward precision: {"fp32" | "fp16": {stage: [summed
+    value of each instance]}}.  A forward runs from one pack_ids dispatch to
+    the next; its precision is that of its attention kernel.  A dispatch that
     continues the previous stage (the pieces of a split LayerNorm round)
     adds to that stage's current instance."""
-    acc, prev = {}, None
+    out = {}
+    fwd, prec, prev = {}, None, None
+
+    def flush():
+        if prec is not None:
+            tgt = out.setdefault(prec, {})
+            for k, v in fwd.items():
+                tgt.setdefault(k, []).extend(v)
+
     for name, v in seq:
         st = stage_of(name, prev)
         if st is None:
             continue
-        if st == prev and ("linear_pipe_kernelILi3E" in name or "ln_rows_kernel" in name):
-            acc[st][-1] += v
+        if st == "pack_ids":
+            flush()
+            fwd, prec = {}, None
+        if st == "attention":
+            prec = "fp32" if "attn_varlen_f32_kernel" in name else "fp16"
+        if st == prev and (epi_of(name) == 3 or "ln_rows_kernel" in name):
+            fwd[st][-1] += v
         else:
-            acc.setdefault(st, []).append(v)
+            fwd.setdefault(st, []).append(v)
         prev = st
-    return acc
+    flush()
+    return out
 
 
 def trace_stats(directory: str) -> dict:
-    """{stage: (instances, average microseconds of kernel time per instance)}
-    from a kernel trace."""
+    """{precision: {stage: (instances, average microseconds of kernel time
+    per instance)}} from a kernel trace."""
     rows = sorted(_rows(directory, "kernel_trace.csv"), key=lambda r: int(r["Dispatch_Id"]))
     acc = _instances((r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3) for r in rows)
-    return {k: (len(v), sum(v) / len(v)) for k, v in acc.items()}
+    return {p: {k: (len(v), sum(v) / len(v)) for k, v in a.items()} for p, a in acc.items()}
 
 
 def counter_stats(directory: str, counter: str) -> tuple[dict, float]:
@@ -118,7 +145,7 @@ def counter_stats(directory: str, counter: str) -> tuple[dict, float]:
         if "elementwise_kernel" in name:  # the calibration multiply (and torch's fills)
             cal = max(cal, v)
     acc = _instances(per_dispatch[d] for d in sorted(per_dispatch))
-    return {k: sum(v) / len(v) for k, v in acc.items()}, cal
+    return {p: {k: sum(v) / len(v) for k, v in a.items()} for p, a in acc.items()}, cal
 
 
 COMMANDS = """Commands (on one MI355X; rocprofv3 runs from /tmp with TMPDIR=/tmp and
@@ -148,7 +175,7 @@ def kernel_stats_table(directory: str, top: int = 10) -> list[str]:
 
 def summarize(trace: str | None, fetch: str | None, write: str | None) -> str:
     out = ["# Per-stage profile: int8 Arctic-embed-xs forward, batch 256 x seq 512", "", COMMANDS]
-    data: dict = {"stages": {}}
+    data: dict = {}
     times = trace_stats(trace) if trace else {}
     f_stats, f_cal = counter_stats(fetch, "FETCH_SIZE") if fetch else ({}, 0.0)
     w_stats, w_cal = counter_stats(write, "WRITE_SIZE") if write else ({}, 0.0)
@@ -161,22 +188,34 @@ def summarize(trace: str | None, fetch: str | None, write: str | None) -> str:
                    f"(scale {w_scale if w_scale is None else round(w_scale, 4)}); per-stage bytes below are "
                    "counter x scale.")
         out.append("")
-    out.append("| stage | instances | avg us | HBM read MB | HBM write MB |")
-    out.append("|---|---:|---:|---:|---:|")
-    for st in STAGES:
-        n, us = times.get(st, (0, float("nan")))
-        rd = f_stats[st] * 1024 * f_scale if st in f_stats and f_scale else None
-        wr = w_stats[st] * 1024 * w_scale if st in w_stats and w_scale else None
-        data["stages"][st] = {"instances": n, "avg_us": None if n == 0 else round(us, 2),
-                              "read_bytes": None if rd is None else int(rd),
-                              "write_bytes": None if wr is None else int(wr)}
-        out.append(f"| {st} | {n} | {us:.1f} | {'' if rd is None else f'{rd / 1e6:.1f}'} | "
-                   f"{'' if wr is None else f'{wr / 1e6:.1f}'} |")
+    for prec in ("fp32", "fp16"):
+        t = times.get(prec, {})
+        fs, ws = f_stats.get(prec, {}), w_stats.get(prec, {})
+        if not (t or fs or ws):
+            continue
+        key = "stages" if prec == "fp32" else "stages_fp16"
+        data[key] = {}
+        out.append(f"{prec} forward ({'the default: f32 activations' if prec == 'fp32' else 'opt-in f16 activations'}):")
+        out.append("")
+        out.append("| stage | instances | avg us | HBM read MB | HBM write MB |")
+        out.append("|---|---:|---:|---:|---:|")
+        for st in STAGES:
+            n, us = t.get(st, (0, float("nan")))
+            rd = fs[st] * 1024 * f_scale if st in fs and f_scale else None
+            wr = ws[st] * 1024 * w_scale if st in ws and w_scale else None
+            data[key][st] = {"instances": n, "avg_us": None if n == 0 else round(us, 2),
+                             "read_bytes": None if rd is None else int(rd),
+                             "write_bytes": None if wr is None else int(wr)}
+            out.append(f"| {st} | {n} | {us:.1f} | {'' if rd is None else f'{rd / 1e6:.1f}'} | "
+                       f"{'' if wr is None else f'{wr / 1e6:.1f}'} |")
+        out.append("")
     data["calibration"] = {"bytes": CAL_BYTES, "fetch_kib": f_cal, "write_kib": w_cal}
     if trace:
-        out += ["", "The two LayerNorm GEMMs are one kernel instantiation; the rows above separate",
-                "them by launch order. rocprofv3's own kernel summary of the trace run (5 timed",
-                "forwards + 2 warmup + 3 with per-launch events):", ""]
+        out += ["The two LayerNorm GEMMs are one kernel instantiation; the rows above separate",
+                "them by launch order.  The counter runs (bench_profile.py run) make one fp32",
+                "forward.  rocprofv3's own kernel summary of the trace run (bench.py: the fp16",
+                "forward first, 5 timed + 2 warmup, then the fp32 one, 5 timed + 2 warmup + 3",
+                "with per-launch events):", ""]
         out += kernel_stats_table(trace)
     out += ["", "```json", json.dumps(data, indent=1), "```", ""]
     return "\n".join(out)
@@ -308,11 +347,11 @@ def counters(dirs: list[str]) -> str:
             key = (r["Dispatch_Id"], r["Counter_Name"])
             disp[key] = (r["Kernel_Name"], disp.get(key, ("", 0.0))[1] + float(r["Counter_Value"]))
         for (did, cname), (kname, v) in disp.items():
-            k = kname.split("(")[0][:110]
+            k = kname.replace("(anonymous namespace)::", "").split("(")[0][:150]
             per.setdefault(k, {}).setdefault(cname, {})[(d, did)] = v
     out = []
     for k, cs in per.items():
-        if not any(x in k for x in ("linear_pipe_kernel", "ln_rows_kernel")):
+        if not any(x in k for x in ("linear_pipe_kernel", "ln_rows_kernel", "attn_varlen")):
             continue
         out.append(f"### `{k}`")
         out.append("")
@@ -335,6 +374,41 @@ def counters(dirs: list[str]) -> str:
     return "\n".join(out) + "\n"
 
 
+def kernels(trace: str, fetch: str | None, write: str | None, fetch_scale: float, write_scale: float) -> str:
+    """Per-kernel table of a run that is not a forward (config 2 or 3):
+    average duration from the trace, FETCH_SIZE / WRITE_SIZE per dispatch
+    times the calibration scales (measured in the forward's calibration
+    multiply: 1 GiB read gives FETCH_SIZE 0.5 GiB, 1 GiB written WRITE_SIZE
+    1 GiB)."""
+    def norm(k):
+        return k.replace("(anonymous namespace)::", "").split("(")[0][:120]
+
+    times = {}
+    for r in _rows(trace, "kernel_trace.csv"):
+        times.setdefault(norm(r["Kernel_Name"]), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
+    cnt = {}
+    for d, counter in ((fetch, "FETCH_SIZE"), (write, "WRITE_SIZE")):
+        if not d:
+            continue
+        per = {}
+        for r in _rows(d, "counter_collection.csv"):
+            if r["Counter_Name"] != counter:
+                continue
+            key = int(r["Dispatch_Id"])
+            name, v = per.get(key, (norm(r["Kernel_Name"]), 0.0))
+            per[key] = (name, v + float(r["Counter_Value"]))
+        for name, v in per.values():
+            cnt.setdefault(name, {}).setdefault(counter, []).append(v)
+    out = ["| kernel | calls | avg us | HBM read MB | HBM write MB |", "|---|---:|---:|---:|---:|"]
+    for k, v in sorted(times.items(), key=lambda kv: -sum(kv[1])):
+        c = cnt.get(k, {})
+        rd = sum(c["FETCH_SIZE"]) / len(c["FETCH_SIZE"]) * 1024 * fetch_scale / 1e6 if "FETCH_SIZE" in c else None
+        wr = sum(c["WRITE_SIZE"]) / len(c["WRITE_SIZE"]) * 1024 * write_scale / 1e6 if "WRITE_SIZE" in c else None
+        out.append(f"| `{k}` | {len(v)} | {sum(v) / len(v):.1f} | {'' if rd is None else f'{rd:.1f}'} | "
+                   f"{'' if wr is None else f'{wr:.1f}'} |")
+    return "\n".join(out) + "\n"
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -347,6 +421,12 @@ def main(argv=None) -> int:
     s.add_argument("--write")
     c = sub.add_parser("counters")
     c.add_argument("dirs", nargs="+")
+    k = sub.add_parser("kernels")
+    k.add_argument("--trace", required=True)
+    k.add_argument("--fetch")
+    k.add_argument("--write")
+    k.add_argument("--fetch-scale", type=float, default=2.0)
+    k.add_argument("--write-scale", type=float, default=1.0)
     a = ap.parse_args(argv)
     if a.cmd == "run":
         run()
@@ -356,6 +436,8 @@ def main(argv=None) -> int:
         nodes()
     elif a.cmd == "counters":
         sys.stdout.write(counters(a.dirs))
+    elif a.cmd == "kernels":
+        sys.stdout.write(kernels(a.trace, a.fetch, a.write, a.fetch_scale, a.write_scale))
     else:
         sys.stdout.write(summarize(a.trace, a.fetch, a.write))
     return 0
