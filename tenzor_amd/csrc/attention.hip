@@ -219,20 +219,7 @@ __global__ void __launch_bounds__(NW * 64) attn_varlen_kernel(const _Float16 *__
 // row sum adds the f32 probabilities on the VALU, so it is the sum of the
 // values P V weights with, to f32 rounding.  K and V^T are staged in LDS as
 // hi and lo planes (146 KiB: one workgroup per CU).
-constexpr int kWavesF32 = 8;
-
-__device__ __forceinline__ void split8(const f32x4_t &a, const f32x4_t &b, half8_t &hi, half8_t &lo) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        hi[i] = (_Float16)a[i];
-        hi[4 + i] = (_Float16)b[i];
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        lo[i] = (_Float16)(a[i] - (float)hi[i]);
-        lo[4 + i] = (_Float16)(b[i] - (float)hi[4 + i]);
-    }
-}
+constexpr int kWavesF32 = 16;
 
 template <int NW>
 __global__ void __launch_bounds__(NW * 64) attn_varlen_f32_kernel(const float *__restrict__ qkv, int ld,
@@ -275,7 +262,7 @@ __global__ void __launch_bounds__(NW * 64) attn_varlen_f32_kernel(const float *_
             bq = *(const f32x4_t *)(kbase + (size_t)key * ld + c + 4);
         }
         half8_t hi, lo;
-        split8(a, bq, hi, lo);
+        split_f32x8(a, bq, hi, lo);
         *(half8_t *)(Ks[0] + key * K_LD + c) = hi;
         *(half8_t *)(Ks[1] + key * K_LD + c) = lo;
     }
@@ -296,7 +283,7 @@ __global__ void __launch_bounds__(NW * 64) attn_varlen_f32_kernel(const float *_
                         bq = *(const f32x4_t *)(vbase + (size_t)key * ld + 8 * c + 4);
                     }
                     half8_t hi, lo;
-                    split8(a, bq, hi, lo);
+                    split_f32x8(a, bq, hi, lo);
                     v[r] = part ? lo : hi;
                 }
 #pragma unroll
@@ -322,7 +309,7 @@ __global__ void __launch_bounds__(NW * 64) attn_varlen_f32_kernel(const float *_
                 a = *(const f32x4_t *)(qbase + (size_t)qrow * ld + g * 8);
                 bq = *(const f32x4_t *)(qbase + (size_t)qrow * ld + g * 8 + 4);
             }
-            split8(a, bq, qh, qlo);
+            split_f32x8(a, bq, qh, qlo);
         }
         float m = -INFINITY, lsum = 0.0f;
         f32x4_t o0 = {0, 0, 0, 0}, o1 = {0, 0, 0, 0};
@@ -374,7 +361,7 @@ __global__ void __launch_bounds__(NW * 64) attn_varlen_f32_kernel(const float *_
                 const half8_t vbh = *(const half8_t *)(Vt[0] + (16 + ql) * V_LD + kv);
                 const half8_t vbl = *(const half8_t *)(Vt[1] + (16 + ql) * V_LD + kv);
                 half8_t ph, pl;
-                split8(f32x4_t{s[2 * st][0], s[2 * st][1], s[2 * st][2], s[2 * st][3]},
+                split_f32x8(f32x4_t{s[2 * st][0], s[2 * st][1], s[2 * st][2], s[2 * st][3]},
                        f32x4_t{s[2 * st + 1][0], s[2 * st + 1][1], s[2 * st + 1][2], s[2 * st + 1][3]}, ph, pl);
                 o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(val, ph, o0, 0, 0, 0);
                 o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(vah, pl, o0, 0, 0, 0);

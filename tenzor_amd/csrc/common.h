@@ -155,6 +155,43 @@ __device__ __forceinline__ float sum_over_rows(float x) {
     return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
 }
 
+// f32 -> f16 pair x = hi + lo + r for 8 values: hi = f16(x), lo = f16(x - hi),
+// both round-to-nearest-even (x - hi is exact in f32, so lo is x - hi
+// rounded once).  |r| <= 2^-22 |x| for |x| >= 2^-3 (x - hi is then an f16
+// normal) and <= 2^-25 below; valid for |x| < 65504.  On the GPU the low halves come from
+// v_fma_mixlo/mixhi_f16 (fma(-hi, 1, x) formed exactly from the f16 hi and
+// the f32 x, rounded once to f16), one instruction per value instead of a
+// widen, a subtract and a narrow.
+__device__ __forceinline__ uint32_t split_lo_pair(uint32_t hi2, float a, float b) {
+#ifdef TZH_EMULATION
+    const half2_t h = __builtin_bit_cast(half2_t, hi2);
+    const half2_t l = {(_Float16)(a - (float)h[0]), (_Float16)(b - (float)h[1])};
+    return __builtin_bit_cast(uint32_t, l);
+#else
+    uint32_t d;
+    asm("v_fma_mixlo_f16 %0, -%1, %3, %2 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(hi2), "v"(a), "v"(1.0f));
+    asm("v_fma_mixhi_f16 %0, -%1, %3, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(d) : "v"(hi2), "v"(b), "v"(1.0f));
+    return d;
+#endif
+}
+
+__device__ __forceinline__ void split_f32x8(const f32x4_t &a, const f32x4_t &b, half8_t &hi, half8_t &lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        h[i] = __builtin_bit_cast(uint32_t, half2_t{(_Float16)a[2 * i], (_Float16)a[2 * i + 1]});
+        h[2 + i] = __builtin_bit_cast(uint32_t, half2_t{(_Float16)b[2 * i], (_Float16)b[2 * i + 1]});
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        l[i] = split_lo_pair(h[i], a[2 * i], a[2 * i + 1]);
+        l[2 + i] = split_lo_pair(h[2 + i], b[2 * i], b[2 * i + 1]);
+    }
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    hi = __builtin_bit_cast(half8_t, u32x4v{h[0], h[1], h[2], h[3]});
+    lo = __builtin_bit_cast(half8_t, u32x4v{l[0], l[1], l[2], l[3]});
+}
+
 // f32 -> f16 with round-to-nearest-even (v_cvt_f16_f32 honours the default RNE mode).
 __device__ __forceinline__ _Float16 to_f16(float x) { return (_Float16)x; }
 

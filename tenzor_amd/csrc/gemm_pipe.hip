@@ -6,13 +6,14 @@
 //
 // the sums of matmulTransposeB_f32_i8_rowScale_bias (matmul_w8a32.zig:14-57).
 // Weight codes are exact in f16 (|q| <= 127).  f32 activations (the
-// reference's arithmetic) are split per fragment into an f16 pair x = hi + lo
-// + r: hi = f16(x), lo = f16(x - hi) (x - hi is exact in f32), |r| <=
-// 2^-22 |x| for |x| >= 2^-3 and <= 2^-25 otherwise; both halves go through
-// the MFMA against the same codes into one f32 accumulator, so every product
-// is that of an f32 operand to about 22 bits, summed in f32.  The split is
-// valid for |x| < 65504 (the f16 range); f16 activations (the opt-in fast
-// model path) take one MFMA.  Epilogues: bias, bias + GELU (arctic.zig:771-776),
+// reference's arithmetic) are split into an f16 pair x = hi + lo + r: hi =
+// f16(x), lo = f16(x - hi) (x - hi is exact in f32), |r| <= 2^-22 |x| for
+// |x| >= 2^-3 and <= 2^-25 otherwise (split_f32x8), once per stage, in
+// place in the LDS tile; both halves go through the MFMA against the same
+// codes into one f32 accumulator, so every product is that of an f32
+// operand to about 22 bits, summed in f32.  The split is valid for |x| <
+// 65504 (the f16 range); f16 activations (the opt-in fast model path) take
+// one MFMA.  Epilogues: bias, bias + GELU (arctic.zig:771-776),
 // bias + residual + LayerNorm over the full 384-wide row (arctic.zig:716-746,
 // layernorm.zig:26-117, two-pass mean / biased variance).
 //
@@ -119,6 +120,36 @@ __device__ __forceinline__ void store_frag_f16(char *ws, const float (&v)[16], _
     wave_lds_order();
 }
 
+// Stores one 32-token x 32-column f32 fragment given in the MFMA D layout
+// (as store_frag_f16) as whole 128-byte row pieces: each lane writes its
+// four 16-byte column chunks to a wave-private 4 KiB LDS tile (chunks
+// XOR-swizzled by row/2: conflict-free both ways), and each of the four
+// store instructions then writes eight complete rows.
+//   ws: the wave's staging tile; dst: &C[t0][c0]; ld: row pitch (elements,
+//   a multiple of 4 with dst 16-byte aligned); rows: how many of the 32
+//   tokens lie inside the matrix.  Issues four store instructions per lane
+//   (fewer where rows < 32).
+__device__ __forceinline__ void store_frag_f32(char *ws, const f32x16_t &v, float *dst, int ld, int rows) {
+    const int lane = threadIdx.x & 63, l31 = lane & 31, half = lane >> 5;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const int c = 2 * g + half;  // columns 4c .. 4c+3
+        *(f32x4_t *)(ws + l31 * 128 + ((c ^ ((l31 >> 1) & 7)) << 4)) =
+            f32x4_t{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+    }
+    wave_lds_order();
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int row = 8 * j + (lane >> 3), c = lane & 7;
+        const f32x4_t d = *(const f32x4_t *)(ws + row * 128 + ((c ^ ((row >> 1) & 7)) << 4));
+        if (row < rows) {
+            *(f32x4_t *)(dst + (size_t)row * ld + c * 4) = d;
+            vmem_store_issued();
+        }
+    }
+    wave_lds_order();
+}
+
 // Eight biased int8 weight codes (u = q + 128, little-endian in d0, d1) ->
 // f16 q, exactly: v_perm_b32 makes each code the low mantissa byte of an f16
 // with exponent 10 (bits 0x64uu = 1024 + u), and a packed f16 subtraction of
@@ -183,12 +214,16 @@ struct PipeCfg {
     // LDS of one block (stage ring + parameter table + LayerNorm statistics
     // + per-wave output staging tiles) and how many such blocks a CU's
     // 160 KiB holds
-    // (staged: f16 output through the per-wave 2 KiB tiles)
-    static constexpr int lds_bytes(bool ln, bool staged = true) {
-        return NS * STAGE + (ln ? 4 * BN * 4 + 2 * BM * WN * 4 : 2 * 1536 * 4) + (staged ? NW * 2048 : 16);
+    // (staged: output through per-wave LDS tiles, 2 KiB for f16 output and
+    // 4 KiB for f32 output of f32-activation configurations)
+    static constexpr int stage_tile(bool staged, bool f32_out) {
+        return !staged ? 16 : f32_out ? (XE == 4 ? NW * 4096 : 16) : NW * 2048;
     }
-    static constexpr int blocks_per_cu(bool ln, bool staged = true) {
-        return 163840 / lds_bytes(ln, staged) > 2 ? 2 : 163840 / lds_bytes(ln, staged);
+    static constexpr int lds_bytes(bool ln, bool staged = true, bool f32_out = false) {
+        return NS * STAGE + (ln ? 4 * BN * 4 + 2 * BM * WN * 4 : 2 * 1536 * 4) + stage_tile(staged, f32_out);
+    }
+    static constexpr int blocks_per_cu(bool ln, bool staged = true, bool f32_out = false) {
+        return 163840 / lds_bytes(ln, staged, f32_out) > 2 ? 2 : 163840 / lds_bytes(ln, staged, f32_out);
     }
 };
 
@@ -261,21 +296,6 @@ __device__ __forceinline__ void store4<float>(float *p, float a, float b, float 
 // pre-normalisation rows of a split LayerNorm tile (see launch_ln).
 enum { EPI_BIAS = 0, EPI_GELU = 1, EPI_LN = 2, EPI_RES = 3 };
 
-// f32 fragment (8 consecutive k of one token) -> hi, lo f16 halves (see the
-// file comment).  Round-to-nearest both ways; x - hi is exact in f32.
-__device__ __forceinline__ void split_f32x8(const f32x4_t &a, const f32x4_t &b, half8_t &hi, half8_t &lo) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        hi[i] = (_Float16)a[i];
-        hi[4 + i] = (_Float16)b[i];
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        lo[i] = (_Float16)(a[i] - (float)hi[i]);
-        lo[4 + i] = (_Float16)(b[i] - (float)hi[4 + i]);
-    }
-}
-
 template <int EPI, typename TC, typename P, typename TR = TC, typename TX = _Float16>
 __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     const TX *__restrict__ X, const void *__restrict__ Wc, const uint16_t *__restrict__ scale,
@@ -300,8 +320,15 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     __shared__ __attribute__((aligned(16))) char st3[NS > 3 ? P::STAGE : 16];
     __shared__ __attribute__((aligned(16))) float par[NPAR][MAXN];
     __shared__ float stat0[LN ? BM * P::WN : 1], stat1[LN ? BM * P::WN : 1];
-    constexpr bool STAGED = std::is_same<TC, _Float16>::value;  // f16 output goes through LDS
-    __shared__ __attribute__((aligned(16))) char epi_ws[STAGED ? P::NW * 2048 : 16];
+    // f16 output goes through LDS, except from the f32-activation LayerNorm
+    // kernel, which has no registers to spare for the staging
+    constexpr bool STAGED = std::is_same<TC, _Float16>::value && !(XF32 && LN);
+    // f32 output of the bias epilogues of the f32-activation configurations
+    // too (whole 128-byte row pieces per store instruction), for units whose
+    // columns all exist.  Not the LayerNorm epilogue: its 384 output columns
+    // are a small share of its traffic, and the staging would spill registers.
+    constexpr bool STAGED32 = std::is_same<TC, float>::value && P::XE == 4 && EPI != EPI_RES && EPI != EPI_LN;
+    __shared__ __attribute__((aligned(16))) char epi_ws[P::stage_tile(STAGED || STAGED32, STAGED32)];
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wm = w / P::WN, wn = w % P::WN;
@@ -408,12 +435,44 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
         woff[ks] = P::X_BYTES + (wn * TNF * 32 + l31) * WROWB + ((cw ^ fw) << 4);
     }
 
+    // the in-place split's row and chunk offsets (f32 activations)
+    const int sp_row = tid / (BK / 8), sp_p = tid % (BK / 8);
+    const int sp_c0 = ((2 * sp_p) ^ FX::swz(sp_row)) << 4, sp_c1 = ((2 * sp_p + 1) ^ FX::swz(sp_row)) << 4;
+
     f32x16_t acc[TNF][TMF];
 #pragma unroll
     for (int a = 0; a < TNF; a++)
 #pragma unroll
         for (int b = 0; b < TMF; b++) acc[a][b] = f32x16_t{};
 
+    auto split_stage = [&](char *buf) __attribute__((always_inline)) {
+        if constexpr (XF32) {
+            // Split the stage's f32 X tile in place, once per workgroup (every
+            // fragment is read by P::WN waves): each 32-byte group of 8
+            // consecutive k of a row, logical chunks 2p and 2p+1, becomes hi
+            // in chunk 2p and lo in chunk 2p+1.  Eight lanes take the eight
+            // groups of one row, so a read touches each bank the minimum
+            // number of times.
+            // Thread tid takes group tid % (BK/8) of rows tid / (BK/8) + i *
+            // ROWS; ROWS is a multiple of the swizzle period, so every i has
+            // the same chunk positions.
+            constexpr int ROWS = P::THREADS / (BK / 8);
+            static_assert((BM * (BK / 8)) % P::THREADS == 0 && ROWS % (FX::RPW * FX::CPR) == 0,
+                          "whole 8-value groups per thread, one swizzle pattern per thread");
+#pragma unroll
+            for (int i = 0; i < BM / ROWS; i++) {
+                char *row = buf + (i * ROWS + sp_row) * XROWB;
+                f32x4_t *c0 = (f32x4_t *)(row + sp_c0);
+                f32x4_t *c1 = (f32x4_t *)(row + sp_c1);
+                const f32x4_t x0 = *c0, x1 = *c1;
+                half8_t hi, lo;
+                split_f32x8(x0, x1, hi, lo);
+                *(half8_t *)c0 = hi;
+                *(half8_t *)c1 = lo;
+            }
+            lds_barrier();
+        }
+    };
     auto compute = [&](const char *buf) __attribute__((always_inline)) {
         u32x4_t wraw[TNF];
 #pragma unroll
@@ -421,13 +480,8 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
             half8_t xf[TMF], xl[TMF], wf[TNF];
 #pragma unroll
             for (int b = 0; b < TMF; b++) {
-                if constexpr (XF32) {
-                    const f32x4_t x0 = *(const f32x4_t *)(buf + xoff[ks] + b * 32 * XROWB);
-                    const f32x4_t x1 = *(const f32x4_t *)(buf + xoff1[ks] + b * 32 * XROWB);
-                    split_f32x8(x0, x1, xf[b], xl[b]);
-                } else {
-                    xf[b] = *(const half8_t *)(buf + xoff[ks] + b * 32 * XROWB);
-                }
+                xf[b] = *(const half8_t *)(buf + xoff[ks] + b * 32 * XROWB);
+                if constexpr (XF32) xl[b] = *(const half8_t *)(buf + xoff1[ks] + b * 32 * XROWB);
             }
 #pragma unroll
             for (int a = 0; a < TNF; a++) {
@@ -458,6 +512,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 
     auto epilogue = [&](int i) __attribute__((always_inline)) {
         const int m0 = unit_m0(i), n0 = unit_n0(i);
+        const bool st32 = STAGED32 && cvec && n0 + BN <= n_valid;  // uniform
         if constexpr (!LN) {
 #pragma unroll
             for (int b = 0; b < TMF; b++) {
@@ -482,10 +537,10 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                             if (EPI == EPI_GELU) v[q] = gelu_fast(v[q]);
                             // input + (sum * s + bias), as the LayerNorm epilogue forms it
                             if (EPI == EPI_RES) v[q] = (float)res[q] + v[q];
-                            if constexpr (STAGED) acc[a][b][4 * g + q] = v[q];
+                            if constexpr (STAGED || STAGED32) acc[a][b][4 * g + q] = v[q];
                         }
                         if constexpr (!STAGED)
-                            if (t < M && n < n_valid) {
+                            if (!st32 && t < M && n < n_valid) {
                                 // 16-byte stores where rows keep that alignment; more store
                                 // instructions than the stage waits count only make them wait longer
                                 if (cvec && n + 4 <= n_valid) {
@@ -509,6 +564,14 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                                        ldc, M - t0);
                     }
                 }
+                if constexpr (STAGED32)
+                    if (st32) {
+                        const int t0 = m0 + wm * TMF * 32 + b * 32;
+#pragma unroll
+                        for (int a = 0; a < TNF; a++)
+                            store_frag_f32(epi_ws + w * 4096, acc[a][b],
+                                           (float *)C + (size_t)t0 * ldc + n0 + wn * TNF * 32 + a * 32, ldc, M - t0);
+                    }
             }
         } else {
             float part[TMF];
@@ -588,7 +651,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 #pragma unroll
                         for (int q = 0; q < 4; q++) {
                             y[q] = ((acc[a][b][4 * g + q] - mean[b]) * inv_std) * gg[q] + bt[q];
-                            if constexpr (STAGED) acc[a][b][4 * g + q] = y[q];
+                            if constexpr (STAGED || STAGED32) acc[a][b][4 * g + q] = y[q];
                         }
                         if constexpr (!STAGED)
                             if (t < M) {
@@ -607,6 +670,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                                        BN, M - t0);
                     }
                 }
+
             }
         }
 #pragma unroll
@@ -642,6 +706,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
         lds_barrier_only();  // every wave's loads of stage s landed; stage s-1 fully read
         const int kt = s % KT;
         if (s + NS - 1 < S) issue(bufs[(j + NS - 1) % NS]);
+        split_stage(bufs[j]);
         compute(bufs[j]);
         if (kt == KT - 1) {
             const int i = s / KT;
@@ -720,9 +785,9 @@ static_assert(Cfgs<TZH_WF_W8T, 2>::Ln::WN == LnCfg::WN && Cfgs<TZH_WF_W8T, 2>::L
                   Cfgs<TZH_WF_W8T, 4>::Ln::TNF == LnCfg::TNF && Cfgs<TZH_WF_W8T, 4>::Ln::BN == LnCfg::BN,
               "one LayerNorm epilogue layout (statistics order) for every configuration and ln_rows_kernel");
 static_assert(Cfgs<TZH_WF_W8T, 2>::LnShortK::blocks_per_cu(true) == 2, "two short-k LayerNorm workgroups per CU");
-static_assert(Cfgs<TZH_WF_W8T, 4>::Bias::lds_bytes(false, false) <= 163840 &&
+static_assert(Cfgs<TZH_WF_W8T, 4>::Bias::lds_bytes(false, true, true) <= 163840 &&
                   Cfgs<TZH_WF_W8T, 4>::Ln::lds_bytes(true, false) <= 163840,
-              "f32-activation tiles fit the 160 KiB of LDS");
+              "f32-activation tiles with staged f32 output fit the 160 KiB of LDS");
 
 template <typename T>
 struct NoDeduce {
@@ -735,7 +800,8 @@ int launch(hipStream_t st, int num_cus, const TX *x, const void *wc, const uint1
            float eps, int ldc, int n_valid) {
     const int nbm = (M + P::BM - 1) / P::BM;
     const int nbn = N / P::BN;
-    const int slots = num_cus * P::blocks_per_cu(EPI == EPI_LN, std::is_same<TC, _Float16>::value);
+    constexpr bool f32_out = std::is_same<TC, float>::value && EPI != EPI_RES && EPI != EPI_LN;
+    const int slots = num_cus * P::blocks_per_cu(EPI == EPI_LN, std::is_same<TC, _Float16>::value || f32_out, f32_out);
     // Persistent blocks.  Panel p goes to XCD p % 8 with its nbn units, so
     // 8 * ceil(panels / 8) * nbn blocks give every unit a block of its own
     // (blocks without a unit return at once); beyond that, one per slot.
@@ -830,12 +896,13 @@ int launch_ln(hipStream_t st, int num_cus, const TX *x, const void *wc, const ui
               int64_t ws_rows) {
     using C = Cfgs<WF, (int)sizeof(TX)>;
     constexpr int N = C::Ln::BN, BM = C::Ln::BM;
-    constexpr bool staged = std::is_same<TC, _Float16>::value;
+    constexpr bool f32_out = false;  // LayerNorm outputs are not staged when f32
+    constexpr bool staged = std::is_same<TC, _Float16>::value && sizeof(TX) == 2;  // as the kernel decides
     if constexpr (!std::is_void<typename C::LnShortK>::value)
         if (K <= 384)
             return launch<EPI_LN, TC, typename C::LnShortK>(st, num_cus, x, wc, scale, bias, c, M, K, N, res, gamma,
                                                             beta, eps, N, N);
-    const int slots = num_cus * C::Ln::blocks_per_cu(true, staged);
+    const int slots = num_cus * C::Ln::blocks_per_cu(true, staged, f32_out);
     const int panels = (M + BM - 1) / BM;
     const int full = panels / slots * slots;
     const int rem = panels - full;
