@@ -175,6 +175,18 @@ int tzh_eval_into(tzh_ctx *ctx, const tzh_node *tape, int32_t n_nodes,
 int tzh_matmul_w8a32(tzh_ctx *ctx, const float *a, const int8_t *wq, const uint16_t *scale,
                      const float *bias, float *c, int64_t m, int64_t k, int64_t n);
 
+/* tzh_matmul_w8a32 without any device allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results as tzh_matmul_w8a32, but the tiled codes
+ * (and zero-padded rows of a when k % 64 != 0 or a is not 16-byte aligned)
+ * go to a static 32 MiB device workspace, one per GPU, held until the process
+ * ends: n_pad * k_pad (+ m * k_pad * 4) bytes must fit (n_pad, k_pad: n and k
+ * rounded up to 384 and 64), else TZH_ERR_TOO_LARGE.  Calls that overlap on
+ * one GPU (other streams or threads) share that workspace and race. */
+int tzh_matmul_w8a32_noalloc(tzh_ctx *ctx, const float *a, const int8_t *wq, const uint16_t *scale,
+                             const float *bias, float *c, int64_t m, int64_t k, int64_t n);
+
 /* Epilogues for tzh_linear_w8. */
 enum {
     TZH_EPI_BIAS = 0,          /* y = acc*s + b                         (arctic.zig:622-633) */

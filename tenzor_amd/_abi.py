@@ -138,6 +138,7 @@ PROTOTYPES = {
     "tzh_memcpy_d2h": (C.c_int, [vp, vp, vp, C.c_size_t]),
     "tzh_eval_into": (C.c_int, [vp, C.POINTER(Node), i32, C.POINTER(Leaf), i32, i32, vp]),
     "tzh_matmul_w8a32": (C.c_int, [vp, vp, vp, vp, vp, vp, i64, i64, i64]),
+    "tzh_matmul_w8a32_noalloc": (C.c_int, [vp, vp, vp, vp, vp, vp, i64, i64, i64]),
     "tzh_linear_w8": (C.c_int, [vp, vp, i32, vp, vp, vp, vp, i32, i64, i64, i64, i32, vp, i32, vp, vp, f32]),
     "tzh_layernorm_last_dim": (C.c_int, [vp, vp, vp, vp, vp, i64, i64, f32]),
     "tzh_quantize_rows": (C.c_int, [vp, vp, i64, i64, vp, vp]),

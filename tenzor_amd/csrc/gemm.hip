@@ -14,6 +14,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <mutex>
 
 int tzh_tile_codes_w8_launch(hipStream_t st, const int8_t *q, uint8_t *out, int64_t n, int64_t k, int64_t n_pad,
                              int64_t k_pad);
@@ -36,6 +37,33 @@ __global__ void pad_cols_kernel(const T *__restrict__ x, T *__restrict__ y, int6
 
 bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
+// Workspace of tzh_matmul_w8a32_noalloc: a file-scope device array, one per
+// GPU, held until the process ends.  Host code never passes `scratch`
+// itself (its host-side name is no device address): each device's address
+// is looked up once with hipGetSymbolAddress and kept in scratch_ptr.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+int noalloc_scratch(tzh_ctx *ctx, void **out) {
+    if (ctx->device < 0 || ctx->device >= kMaxDevices)
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "device %d out of range", ctx->device);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[ctx->device]) {  // the device is current (tzh_ctx_enter)
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return tzh_fail(TZH_ERR_DEVICE, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+        }
+        g_scratch_ptr[ctx->device] = p;
+    }
+    *out = g_scratch_ptr[ctx->device];
+    return TZH_OK;
+}
 
 // The workspace a linear needs: tiled codes, then (k % 64 != 0 or a
 // misaligned a) the zero-padded activation rows, then (LayerNorm epilogue)
@@ -130,4 +158,24 @@ extern "C" int tzh_matmul_w8a32(tzh_ctx *ctx, const float *a, const int8_t *wq, 
     TZH_TRY(tzh_ctx_enter(ctx));
     return linear(ctx, a, TZH_F32, wq, scale, bias, c, TZH_F32, m, k, n, TZH_EPI_BIAS, nullptr, TZH_F32, nullptr,
                   nullptr, 0.0f);
+}
+
+extern "C" int tzh_matmul_w8a32_noalloc(tzh_ctx *ctx, const float *a, const int8_t *wq, const uint16_t *scale,
+                                        const float *bias, float *c, int64_t m, int64_t k, int64_t n) {
+    tzh_clear_error();
+    TZH_TRY(tzh_ctx_enter(ctx));
+    if (m < 0 || k <= 0 || n <= 0 || m > (int64_t)1 << 30 || k > 65536 || n > 65536)
+        return linear(ctx, a, TZH_F32, wq, scale, bias, c, TZH_F32, m, k, n, TZH_EPI_BIAS, nullptr, TZH_F32, nullptr,
+                      nullptr, 0.0f);  // the same shape errors as tzh_matmul_w8a32
+    const size_t need = workspace_of(ctx, a, TZH_F32, m, k, n, false).total();
+    if (need > kNoAllocScratchBytes)
+        return tzh_fail(TZH_ERR_TOO_LARGE,
+                        "tzh_matmul_w8a32_noalloc needs %zu bytes of workspace for m=%lld k=%lld n=%lld; its static "
+                        "workspace holds %zu (the tiled codes, n_pad * k_pad bytes, plus m * k_pad * 4 when k %% 64 "
+                        "!= 0 or a is not 16-byte aligned)",
+                        need, (long long)m, (long long)k, (long long)n, kNoAllocScratchBytes);
+    void *ws = nullptr;
+    TZH_TRY(noalloc_scratch(ctx, &ws));
+    return linear(ctx, a, TZH_F32, wq, scale, bias, c, TZH_F32, m, k, n, TZH_EPI_BIAS, nullptr, TZH_F32, nullptr,
+                  nullptr, 0.0f, ws);
 }
