@@ -47,6 +47,9 @@ KERNELS = {
 }
 
 
+TIMING_REPS = 10  # launches of each stage between two events in the per-stage timing
+
+
 def host_facts():
     """(threads the CPU baseline uses, nproc, CPU model).  The threads are the
     CPUs this process may run on, at most 16: the GPU box's CPU share for
@@ -164,9 +167,12 @@ def main():
     value = real_tokens * args.steps / elapsed
     assert torch.isfinite(out).all()
 
-    # per-kernel durations inside the forward: HIP events around every launch
-    # on the forward's own stream (tzh_arctic_set_timing)
-    model.set_timing(True)
+    # per-kernel durations inside the forward: HIP events around every stage
+    # on the forward's own stream (tzh_arctic_set_timing), each stage issued
+    # TIMING_REPS times back to back between its events so that the cost of
+    # an event (a dispatch wait after each, about 15-20 us) is spread over
+    # the repetitions, as in a forward's own back-to-back launches
+    model.set_timing(True, reps=TIMING_REPS)
     per_stage = {}
     n_timed = 3
     for _ in range(n_timed):
@@ -196,7 +202,7 @@ def main():
     fwd_roof_us = sum(st["roof_us"] * st["launches"] for st in stages.values())
     # HBM bytes per launch of that stage, measured by rocprofv3 FETCH_SIZE and
     # WRITE_SIZE passes over the same workload (calibrated against a known
-    # copy; see profile_summary.py) and committed with the profile
+    # copy; see bench_profile.py) and committed with the profile
     measured = load_traffic(os.path.join(ROOT, "profiles", TRAFFIC_PROFILE)).get("stages", {}).get(dom_name, {})
     traffic = None
     if measured.get("read_bytes") is not None and measured.get("write_bytes") is not None:

@@ -152,13 +152,13 @@ COMMANDS = """Commands (on one MI355X; rocprofv3 runs from /tmp with TMPDIR=/tmp
 PYTHONPATH=<repo>, the program right after `--`):
 
     rocprofv3 --kernel-trace --stats --output-format csv -d <out>/trace -o fwd -- \\
-        python3 <repo>/bench.py --steps 5 --warmup 2 --no-cpu-baseline
+        python3 <repo>/bench.py --steps 5 --warmup 2 --no-cpu-baseline > <out>/trace.log
     rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/fetch -o f -- \\
         python3 <repo>/bench_profile.py run
     rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/write -o w -- \\
         python3 <repo>/bench_profile.py run
     python3 <repo>/bench_profile.py summarize \\
-        --trace <out>/trace --fetch <out>/fetch --write <out>/write
+        --trace <out>/trace --fetch <out>/fetch --write <out>/write --bench-log <out>/trace.log
 """
 
 
@@ -173,7 +173,29 @@ def kernel_stats_table(directory: str, top: int = 10) -> list[str]:
     return out
 
 
-def summarize(trace: str | None, fetch: str | None, write: str | None) -> str:
+def forward_sum_us(stages: dict) -> float | None:
+    """Kernel time of one forward: every stage's average times its launches
+    per forward (pack_ids runs once per forward)."""
+    n_fwd = (stages.get("pack_ids") or {}).get("instances") or 0
+    if not n_fwd:
+        return None
+    return sum(v["avg_us"] * v["instances"] / n_fwd for v in stages.values() if v["instances"] and v["avg_us"])
+
+
+def bench_line(path: str | None) -> dict:
+    """The JSON line a bench.py run printed into `path` ({} if none)."""
+    if not path:
+        return {}
+    try:
+        for line in open(path):
+            if line.startswith("{") and '"metric"' in line:
+                return json.loads(line)
+    except OSError:
+        pass
+    return {}
+
+
+def summarize(trace: str | None, fetch: str | None, write: str | None, bench_log: str | None = None) -> str:
     out = ["# Per-stage profile: int8 Arctic-embed-xs forward, batch 256 x seq 512", "", COMMANDS]
     data: dict = {}
     times = trace_stats(trace) if trace else {}
@@ -210,6 +232,24 @@ def summarize(trace: str | None, fetch: str | None, write: str | None) -> str:
                        f"{'' if wr is None else f'{wr / 1e6:.1f}'} |")
         out.append("")
     data["calibration"] = {"bytes": CAL_BYTES, "fetch_kib": f_cal, "write_kib": w_cal}
+    b = bench_line(bench_log)
+    if trace and b:
+        # rocprofv3's kernel times against the bench's own clock, same process
+        steps = {"fp32": b.get("ms_per_step"), "fp16": (b.get("fp16_forward") or {}).get("ms_per_step")}
+        out.append("Reconciliation with the bench line of the same trace run (kernel times summed per "
+                   "forward against the bench's timed step):")
+        out.append("")
+        out.append("| forward | kernel sum per forward, ms | bench ms_per_step | kernel sum / step |")
+        out.append("|---|---:|---:|---:|")
+        for prec, key in (("fp32", "stages"), ("fp16", "stages_fp16")):
+            tot = forward_sum_us(data.get(key, {}))
+            st = steps[prec]
+            if tot and st:
+                out.append(f"| {prec} | {tot / 1000:.3f} | {st:.3f} | {tot / 1000 / st:.3f} |")
+        out.append("")
+        data["reconciliation"] = {prec: {"kernel_sum_ms": round((forward_sum_us(data.get(key, {})) or 0) / 1000, 4),
+                                         "ms_per_step": steps[prec]}
+                                  for prec, key in (("fp32", "stages"), ("fp16", "stages_fp16"))}
     if trace:
         out += ["The two LayerNorm GEMMs are one kernel instantiation; the rows above separate",
                 "them by launch order.  The counter runs (bench_profile.py run) make one fp32",
@@ -419,6 +459,7 @@ def main(argv=None) -> int:
     s.add_argument("--trace")
     s.add_argument("--fetch")
     s.add_argument("--write")
+    s.add_argument("--bench-log", help="the output of the traced bench.py run (its JSON line)")
     c = sub.add_parser("counters")
     c.add_argument("dirs", nargs="+")
     k = sub.add_parser("kernels")
@@ -439,7 +480,7 @@ def main(argv=None) -> int:
     elif a.cmd == "kernels":
         sys.stdout.write(kernels(a.trace, a.fetch, a.write, a.fetch_scale, a.write_scale))
     else:
-        sys.stdout.write(summarize(a.trace, a.fetch, a.write))
+        sys.stdout.write(summarize(a.trace, a.fetch, a.write, a.bench_log))
     return 0
 
 

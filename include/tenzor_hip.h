@@ -379,13 +379,17 @@ int tzh_arctic_set_precision(tzh_model *model, int32_t dtype);
 int tzh_arctic_precision(tzh_model *model, int32_t *dtype);
 
 /* Launch tracing (no counterpart in the reference, whose CPU path has no
- * kernels to time): with timing enabled, every later forward records a HIP
- * event on the model's stream before its first and after each of its
- * kernel launches. */
+ * kernels to time): with timing enabled (enable = n >= 1), every later
+ * forward records a HIP event on the model's stream before its first and
+ * after each of its stages, and issues each stage after pack_ids n times
+ * back to back between its events (every such stage reads only buffers it
+ * does not write, so the result is unchanged), which spreads the cost of
+ * an event over n launches.  enable = 0 turns it off; n <= 1000. */
 int tzh_arctic_set_timing(tzh_model *model, int32_t enable);
 
 /* Per-launch durations of the most recent timed forward, in launch order:
- * us[i] (microseconds between the events around launch i) and names[i]
+ * us[i] (microseconds between the events around stage i, divided by the
+ * times it was issued) and names[i]
  * (static stage names: "pack_ids", "embed_ln", "qkv", "attention",
  * "attn_out_ln", "ffn1_gelu", "ffn2_ln", "cls_l2", "hidden_f32"), at most
  * `capacity` entries; *count = number of launches (0 if the last forward was

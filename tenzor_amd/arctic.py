@@ -73,9 +73,10 @@ class ModelWeights:
         check(lib().tzh_arctic_precision(self.handle, C.byref(d)))
         return "float32" if d.value == _abi.F32 else "float16"
 
-    def set_timing(self, enable: bool) -> None:
-        """Record a HIP event around every kernel launch of later forwards."""
-        check(lib().tzh_arctic_set_timing(self.handle, 1 if enable else 0))
+    def set_timing(self, enable: bool, reps: int = 1) -> None:
+        """Record a HIP event around every stage of later forwards, each stage
+        after the id packing issued `reps` times between its events."""
+        check(lib().tzh_arctic_set_timing(self.handle, max(1, int(reps)) if enable else 0))
 
     def launch_times(self) -> list:
         """[(stage name, microseconds)] of the most recent timed forward, in

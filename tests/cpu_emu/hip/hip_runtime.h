@@ -246,6 +246,7 @@ typedef struct emu_stream *hipStream_t;
 typedef struct emu_event *hipEvent_t;
 enum hipMemcpyKind { hipMemcpyHostToHost, hipMemcpyHostToDevice, hipMemcpyDeviceToHost, hipMemcpyDeviceToDevice };
 #define hipEventDisableTiming 2u
+#define hipEventDisableSystemFence 0x20000000u
 #define hipHostMallocDefault 0u
 #define hipStreamNonBlocking 1u
 
