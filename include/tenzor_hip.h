@@ -223,7 +223,7 @@ int tzh_attention_varlen(tzh_ctx *ctx, const void *qkv, void *out, int32_t dtype
                          int32_t batch, int32_t n_heads, int32_t hidden);
 
 /* Per-row symmetric int8 quantization with f16 scale, bit-exact to
- * quantize_arctic_xs.zig:152-173.  Device pointers: w f32 [rows,cols],
+ * quantize_arctic_xs.zig:94-115.  Device pointers: w f32 [rows,cols],
  * q i8 [rows,cols], scale f16 bits [rows]. */
 int tzh_quantize_rows(tzh_ctx *ctx, const float *w, int64_t rows, int64_t cols,
                       int8_t *q, uint16_t *scale);
@@ -231,9 +231,9 @@ int tzh_quantize_rows(tzh_ctx *ctx, const float *w, int64_t rows, int64_t cols,
 /* Host-side version of the same quantizer (host pointers, no device work). */
 int tzh_quantize_rows_host(const float *w, int64_t rows, int64_t cols, int8_t *q, uint16_t *scale);
 
-/* The quantize_arctic_xs tool (quantize_arctic_xs.zig:100-203): read a
+/* The quantize_arctic_xs tool (quantize_arctic_xs.zig:42-145, written at 139): read a
  * safetensors file, quantize every tensor shouldQuantize() selects
- * (quantize_arctic_xs.zig:80-92), write I8 `<name>` + F16 `<name>.scale`,
+ * (quantize_arctic_xs.zig:22-34), write I8 `<name>` + F16 `<name>.scale`,
  * copy the rest.  If n_quantized is not NULL it receives the count. */
 int tzh_quantize_safetensors(const char *in_path, const char *out_path, int32_t *n_quantized);
 
@@ -303,11 +303,11 @@ typedef struct tzh_model tzh_model;
 /* Upload host weights to HBM (MatWeight, arctic.zig:55-58; ModelWeights,
  * arctic.zig:100).  Encoder linears are I8 + F16 scale (MatWeight.q8) or
  * F32 (MatWeight.f32); other
- * dtypes give TZH_ERR_UNSUPPORTED_DTYPE.  On the device both become f16
- * codes with an f16 row scale: int8 codes widened exactly, f32 rows as
- * W * 2^k with scale 2^-k (only the f16 rounding of W * 2^k is inexact).
- * Embedding tables may be F32 or I8.  The model is bound to ctx's device
- * and stream. */
+ * dtypes give TZH_ERR_UNSUPPORTED_DTYPE.  On the device int8 codes stay
+ * one byte each (biased, u = q + 128, tiled in the GEMM's stage order) with
+ * their f16 row scale; f32 rows become f16 codes W * 2^k with scale 2^-k
+ * (only the f16 rounding of W * 2^k is inexact).  Embedding tables may be
+ * F32 or I8.  The model is bound to ctx's device and stream. */
 int tzh_arctic_upload(tzh_ctx *ctx, const tzh_arctic_weights *weights, tzh_model **out);
 
 /* ModelWeights.fromSafeTensors (arctic.zig:113-166): "bert." prefix

@@ -78,7 +78,7 @@ float orc_f16_to_f32(uint16_t h) {
 }
 
 /* ------------------------------------------------------------------ */
-/* A1 quantizer: quantize_arctic_xs.zig:152-173                        */
+/* A1 quantizer: quantize_arctic_xs.zig:94-115                        */
 /* ------------------------------------------------------------------ */
 void orc_quantize_rows(const float *w, int64_t rows, int64_t cols, int8_t *q, uint16_t *scale) {
     for (int64_t r = 0; r < rows; r++) {

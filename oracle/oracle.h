@@ -25,7 +25,7 @@ extern "C" {
 uint16_t orc_f32_to_f16(float x);
 float orc_f16_to_f32(uint16_t h);
 
-/* quantize_arctic_xs.zig:152-173 */
+/* quantize_arctic_xs.zig:94-115 */
 void orc_quantize_rows(const float *w, int64_t rows, int64_t cols, int8_t *q, uint16_t *scale);
 
 /* matmul_w8a32.zig:14-57 */

@@ -90,7 +90,7 @@ class Context:
 
 
 def quantize_rows_host(w):
-    """Host quantizer (quantize_arctic_xs.zig:152-173): f32 [rows, cols] ->
+    """Host quantizer (quantize_arctic_xs.zig:94-115): f32 [rows, cols] ->
     (int8 codes [rows, cols], f16 scale bits as uint16 [rows])."""
     import numpy as np
 

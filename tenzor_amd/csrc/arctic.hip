@@ -154,7 +154,7 @@ __global__ void __launch_bounds__(256) layernorm_rows_kernel(const float *x, con
     for (int c = lane; c < n; c += 64) y[r * n + c] = ((xr[c] - mean) * inv_std) * g[c] + bta[c];
 }
 
-// GPU quantizer, bit-exact to quantize_arctic_xs.zig:152-173: one wave per
+// GPU quantizer, bit-exact to quantize_arctic_xs.zig:94-115: one wave per
 // row; the max is order-independent and each code depends on its element only.
 __global__ void __launch_bounds__(256) quantize_rows_kernel(const float *__restrict__ w, int64_t rows, int64_t cols,
                                                             int8_t *__restrict__ q, uint16_t *__restrict__ scale) {

@@ -1,5 +1,5 @@
 // safetensors parse / load / write (io/safetensors.zig:172-409) and the
-// quantize_arctic_xs tool (quantize_arctic_xs.zig:80-203) on the host.
+// quantize_arctic_xs tool (quantize_arctic_xs.zig:42-145) on the host.
 #include "safetensors.h"
 
 #include <cmath>
@@ -274,7 +274,7 @@ int st_write(const char *path, const std::vector<StWrite> &tensors) {
 }
 
 // ---------------------------------------------------------------------------
-// quantizer (host): quantize_arctic_xs.zig:152-173
+// quantizer (host): quantize_arctic_xs.zig:94-115
 // ---------------------------------------------------------------------------
 extern "C" int tzh_quantize_rows_host(const float *w, int64_t rows, int64_t cols, int8_t *q, uint16_t *scale) {
     tzh_clear_error();
@@ -302,7 +302,7 @@ extern "C" int tzh_quantize_rows_host(const float *w, int64_t rows, int64_t cols
     return TZH_OK;
 }
 
-// quantize_arctic_xs.zig:80-92
+// quantize_arctic_xs.zig:22-34
 static bool should_quantize(const StTensor &t) {
     if (t.dtype != TZH_F32) return false;
     if (t.shape.size() != 2) return false;

@@ -3,7 +3,7 @@
 Weights follow the configurations' recipe: every matrix N(0, 0.02) in f32
 (biases N(0, 0.02) as well; LayerNorm gamma = 1, beta = 0 unless
 `ln_random`), then the 36 encoder linears quantized per row to int8 with f16
-scales (quantize_arctic_xs.zig:152-173).  Token batches put the [CLS] id
+scales (quantize_arctic_xs.zig:94-115).  Token batches put the [CLS] id
 101 first and draw the rest uniformly from [1000, 30521]; padded positions
 hold id 0.  Everything is numpy (PCG64) from one seed, so the GPU path and
 the CPU checker read identical bytes.
@@ -75,7 +75,7 @@ def make_arctic_f32(seed: int, cfg: Config = Config(), ln_random: bool = False) 
 
 
 def should_quantize(name: str, arr: np.ndarray) -> bool:
-    """quantize_arctic_xs.zig:80-92."""
+    """quantize_arctic_xs.zig:22-34."""
     return (arr.dtype == np.float32 and arr.ndim == 2 and name.endswith(".weight") and "LayerNorm" not in name
             and arr.shape[0] > 0 and arr.shape[1] > 0 and arr.size >= 4096)
 

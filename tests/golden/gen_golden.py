@@ -13,7 +13,7 @@ independent implementation before it is written:
     the model is constructed from the config, never downloaded.
   - quantize_cases.npz: constructed rows (zero row, ties, clamp) with codes
     and scales; checked against numpy's float16 conversion and the closed
-    form of quantize_arctic_xs.zig:152-173.
+    form of quantize_arctic_xs.zig:94-115.
   - chain_small.npz: exp((a + b) * c) inputs/outputs; checked against numpy
     float64 within 2 f32 ulp.
 

@@ -103,7 +103,7 @@ def _read_header(path):
 
 
 def test_quantize_tool_matches_reference_contract(tmp_path):
-    """quantize_arctic_xs.zig:80-203: the 36 encoder linears and the word and
+    """quantize_arctic_xs.zig:42-145: the 36 encoder linears and the word and
     position embeddings become I8 + F16 `.scale`; everything else is copied."""
     from safetensors.numpy import load_file, save_file
 

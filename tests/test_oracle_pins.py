@@ -54,7 +54,7 @@ def test_quantizer_known_answers():
     w[1, :6] = [127, -63.5, 0.5, -0.5, 1.5, 2.5]
     w[2, :] = 254.0  # scale 2.0 exactly -> codes 127
     q, s = oracle.quantize_rows(w)
-    assert s[0] == 0x3C00 and q[0].tolist() == [0] * 8           # zero row: scale 1 (quantize_arctic_xs.zig:161)
+    assert s[0] == 0x3C00 and q[0].tolist() == [0] * 8           # zero row: scale 1 (quantize_arctic_xs.zig:103)
     assert q[1, :6].tolist() == [127, -64, 1, -1, 2, 3]          # @round: half away from zero
     assert s[2] == np.float16(2.0).view(np.uint16) and q[2].tolist() == [127] * 8
 
