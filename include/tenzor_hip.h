@@ -187,6 +187,30 @@ int tzh_matmul_w8a32(tzh_ctx *ctx, const float *a, const int8_t *wq, const uint1
 int tzh_matmul_w8a32_noalloc(tzh_ctx *ctx, const float *a, const int8_t *wq, const uint16_t *scale,
                              const float *bias, float *c, int64_t m, int64_t k, int64_t n);
 
+/* ONNX Gemm (onnx/executor.zig:4561-4634) on the matrix cores: y[m,n] =
+ * alpha * op(A) op(B) + beta * C with op = transpose when trans_a / trans_b;
+ * A is stored [m,k] (or [k,m] when trans_a) with row pitch lda, B [k,n] (or
+ * [n,k]) with pitch ldb (the reference's a.shape[1] / b.shape[1]); C is NULL
+ * or [c_rows, c_cols] with c_rows in {1, m} and c_cols in {1, n},
+ * broadcast to [m,n]; y is contiguous [m,n].  Device pointers.  Products are
+ * exact f32 (v_mfma_f32_16x16x4_f32), sums f32 in another order than the
+ * reference's. */
+int tzh_gemm_f32(tzh_ctx *ctx, int32_t trans_a, int32_t trans_b, int64_t m, int64_t n, int64_t k, float alpha,
+                 const float *a, int64_t lda, const float *b, int64_t ldb, float beta, const float *c,
+                 int64_t c_rows, int64_t c_cols, float *y);
+
+/* ONNX MatMul (onnx/executor.zig:1489-1990), F32 or F64, on the matrix
+ * cores: NumPy matmul of contiguous A [..., m, k] and B [..., k, n] with
+ * broadcast batch dimensions; a 1-D A is a row and a 1-D B a column whose
+ * unit dimension the result drops; B of shape [] or [1] scales A
+ * elementwise (executor.zig:1545-1577); k == 0 gives zeros, any other zero
+ * dimension an empty result.  Writes the result's shape to y_shape (host,
+ * room for TZH_MAX_RANK) and *y_ndim, and the result to y (contiguous)
+ * unless y is NULL (a shape query). */
+int tzh_matmul_nd(tzh_ctx *ctx, int32_t dtype, const void *a, const int64_t *a_shape, int32_t a_ndim,
+                  const void *b, const int64_t *b_shape, int32_t b_ndim, void *y, int64_t *y_shape,
+                  int32_t *y_ndim);
+
 /* Epilogues for tzh_linear_w8. */
 enum {
     TZH_EPI_BIAS = 0,          /* y = acc*s + b                         (arctic.zig:622-633) */
@@ -305,9 +329,10 @@ typedef struct tzh_model tzh_model;
  * F32 (MatWeight.f32); other
  * dtypes give TZH_ERR_UNSUPPORTED_DTYPE.  On the device int8 codes stay
  * one byte each (biased, u = q + 128, tiled in the GEMM's stage order) with
- * their f16 row scale; f32 rows become f16 codes W * 2^k with scale 2^-k
- * (only the f16 rounding of W * 2^k is inexact).  Embedding tables may be
- * F32 or I8.  The model is bound to ctx's device and stream. */
+ * their f16 row scale; f32 linears stay f32 (computed exactly in f32 on the
+ * matrix cores); a layer that mixes the two becomes f16 codes W * 2^k with
+ * scale 2^-k.  Embedding tables may be F32 or I8.  The model is bound to
+ * ctx's device and stream. */
 int tzh_arctic_upload(tzh_ctx *ctx, const tzh_arctic_weights *weights, tzh_model **out);
 
 /* ModelWeights.fromSafeTensors (arctic.zig:113-166): "bert." prefix
@@ -372,9 +397,10 @@ int tzh_arctic_last_launch_count(tzh_model *model);
  * in HBM, products of f32 operands from exact f16 hi/lo splits, f32 sums, as
  * arctic.zig:599-635 computes) or TZH_F16 (opt-in: activations rounded to
  * f16 between kernels, half the activation traffic).  A model whose linears
- * hold f32 weights (MatWeight.f32, stored as f16 codes with power-of-two row
- * scales) runs with f16 activations whatever is set; tzh_arctic_precision
- * reports the precision the next forward uses. */
+ * hold f32 weights (MatWeight.f32) runs in f32 whatever is set (its linears
+ * on the f32 GEMM of tzh_gemm_f32); one that mixes f32 and int8 linears runs
+ * with f16 activations; tzh_arctic_precision reports the precision the next
+ * forward uses. */
 int tzh_arctic_set_precision(tzh_model *model, int32_t dtype);
 int tzh_arctic_precision(tzh_model *model, int32_t *dtype);
 

@@ -139,6 +139,8 @@ PROTOTYPES = {
     "tzh_eval_into": (C.c_int, [vp, C.POINTER(Node), i32, C.POINTER(Leaf), i32, i32, vp]),
     "tzh_matmul_w8a32": (C.c_int, [vp, vp, vp, vp, vp, vp, i64, i64, i64]),
     "tzh_matmul_w8a32_noalloc": (C.c_int, [vp, vp, vp, vp, vp, vp, i64, i64, i64]),
+    "tzh_gemm_f32": (C.c_int, [vp, i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64, i64, vp]),
+    "tzh_matmul_nd": (C.c_int, [vp, i32, vp, vp, i32, vp, vp, i32, vp, vp, vp]),
     "tzh_linear_w8": (C.c_int, [vp, vp, i32, vp, vp, vp, vp, i32, i64, i64, i64, i32, vp, i32, vp, vp, f32]),
     "tzh_layernorm_last_dim": (C.c_int, [vp, vp, vp, vp, vp, i64, i64, f32]),
     "tzh_quantize_rows": (C.c_int, [vp, vp, i64, i64, vp, vp]),

@@ -320,8 +320,27 @@ int upload_linear(tzh_model *m, std::initializer_list<std::pair<const tzh_mat_vi
         if (v->cols != cols) return tzh_fail(TZH_ERR_INVALID_ARGS, "%s has %d columns, expected %d", what, v->cols, cols);
         rows += v->rows;
     }
-    bool all_i8 = true;
-    for (auto &pb : parts) all_i8 = all_i8 && pb.first->dtype == TZH_I8;
+    bool all_i8 = true, all_f32 = true;
+    for (auto &pb : parts) {
+        all_i8 = all_i8 && pb.first->dtype == TZH_I8;
+        all_f32 = all_f32 && pb.first->dtype == TZH_F32;
+    }
+    if (all_f32) {
+        // MatWeight.f32 (arctic.zig:55-58): the rows as they are, [n, k]
+        // row-major, for the f32 GEMM on the matrix cores (gemm_fp.hip)
+        std::vector<float> w((size_t)(rows * cols)), b((size_t)rows);
+        int64_t r0 = 0;
+        for (auto &pb : parts) {
+            const tzh_mat_view *v = pb.first;
+            std::memcpy(w.data() + (size_t)r0 * cols, v->data, (size_t)v->rows * cols * 4);
+            std::memcpy(b.data() + r0, pb.second, (size_t)v->rows * 4);
+            r0 += v->rows;
+        }
+        out.fmt = TZH_WF_F32;
+        out.s = nullptr;
+        TZH_TRY(upload<float>(m, (float **)&out.w, w.data(), w.size()));
+        return upload<float>(m, &out.b, b.data(), b.size());
+    }
     if (all_i8 && rows % 384 == 0 && cols % 64 == 0) {
         // biased codes u = q + 128, stage-tiled: block of 384 rows, k stage of
         // 64 codes, row (the layout tile_codes_w8_kernel writes)
@@ -403,6 +422,42 @@ void free_workspace(tzh_model *m) {
     m->cap_tokens = 0;
     m->cap_batch = 0;
     m->cap_es = 0;
+}
+
+// The activation type a forward runs with: f32 weights (MatWeight.f32) run
+// in f32 on the f32 GEMM; int8 weights in the tiled format in the chosen
+// precision; f16 codes (a model that mixes f32 and int8 linears) in f16.
+int32_t model_act(const tzh_model *m) {
+    bool all_w8t = true, all_f32 = true;
+    for (const DevLayer &d : m->layers)
+        for (const DevLinear *l : {&d.qkv, &d.o, &d.ffn1, &d.ffn2}) {
+            all_w8t = all_w8t && l->fmt == TZH_WF_W8T;
+            all_f32 = all_f32 && l->fmt == TZH_WF_F32;
+        }
+    return all_f32 ? TZH_F32 : all_w8t ? m->act : TZH_F16;
+}
+
+// y[T, n] = ops(x[T, k] W^T) + C for an f32-weight linear (W [n, k]), ops =
+// bias add then `act_op` (or the bias add alone when act_op < 0).
+int linear_f32w(hipStream_t st, const float *x, const DevLinear &l, float *y, int64_t T, int64_t k, int64_t n,
+                int act_op, const float *residual) {
+    tzh_gemm_desc d;
+    d.m = T, d.n = n, d.k = k, d.lda = k, d.ldb = k, d.ldy = n;
+    d.bias = l.b;
+    d.ops[0] = TZH_OP_ADD;
+    d.n_ops = 1;
+    if (act_op >= 0) d.ops[d.n_ops++] = act_op;
+    if (residual) d.c = residual, d.beta = 1.0, d.c_rs = n, d.c_cs = 1;
+    return tzh_gemm_fp_launch(st, TZH_F32, false, true, x, l.w, y, d);
+}
+
+int layernorm_rows(hipStream_t st, const float *x, const float *g, const float *b, float *y, int64_t rows, int n,
+                   float eps) {
+    if (rows == 0) return TZH_OK;
+    hipLaunchKernelGGL(layernorm_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, g, b, y, rows,
+                       n, eps);
+    TZH_LAUNCHED("layernorm_rows_kernel");
+    return TZH_OK;
 }
 
 int ensure_workspace(tzh_model *m, int64_t tokens, int batch, size_t es) {
@@ -742,11 +797,7 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
         T += lengths[b];
     }
     if (T > ((int64_t)1 << 30)) return tzh_fail(TZH_ERR_TOO_LARGE, "batch of %lld tokens is too large", (long long)T);
-    // f32 activations need the tiled int8 weight format on every linear
-    bool f16_codes = false;
-    for (const DevLayer &d : m->layers)
-        for (const DevLinear *l : {&d.qkv, &d.o, &d.ffn1, &d.ffn2}) f16_codes = f16_codes || l->fmt != TZH_WF_W8T;
-    const int32_t act = f16_codes ? TZH_F16 : m->act;
+    const int32_t act = model_act(m);
     const size_t es = act == TZH_F32 ? 4 : 2;
     TZH_TRY(ensure_workspace(m, T, batch, es));
     hipStream_t st = m->ctx->stream;
@@ -821,7 +872,13 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
     for (int32_t li = 0; li < n_layers; li++) {
         const DevLayer &d = m->layers[(size_t)li];
         const int cus = m->ctx->num_cus;
+        // f32 weights: the f32 GEMM; a LayerNorm stage writes its pre-norm rows
+        // (x W^T + b, then + residual) into a buffer the stage does not read
+        // (inter for the O-projection, attn for FFN2) and normalises them
+        const bool f32w = d.qkv.fmt == TZH_WF_F32;
+        float *const hf = (float *)m->h, *const h1f = (float *)m->h1;
         TZH_TRY(stage("qkv", [&]() {
+            if (f32w) return linear_f32w(st, hf, d.qkv, (float *)m->qkv, T, H, 3 * H, -1, nullptr);
             return tzh_linear_codes_launch(st, cus, m->h, act, d.qkv.w, d.qkv.fmt, d.qkv.s, d.qkv.b, m->qkv, act, T,
                                            H, 3 * H, 3 * H, TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f, nullptr, 0);
         }));
@@ -829,16 +886,25 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
             return tzh_attention_launch(st, m->qkv, m->attn, act, d_cu, d_order, batch, 12, H);
         }));
         TZH_TRY(stage("attn_out_ln", [&]() {
+            if (f32w) {
+                TZH_TRY(linear_f32w(st, (const float *)m->attn, d.o, (float *)m->inter, T, H, H, -1, hf));
+                return layernorm_rows(st, (const float *)m->inter, d.ln1_g, d.ln1_b, h1f, T, H, eps);
+            }
             return tzh_linear_codes_launch(st, cus, m->attn, act, d.o.w, d.o.fmt, d.o.s, d.o.b, m->h1, act, T, H, H,
                                            H, TZH_EPI_BIAS_RES_LN, m->h, d.ln1_g, d.ln1_b, eps, m->ln_ws,
                                            m->ln_ws_rows);
         }));
         TZH_TRY(stage("ffn1_gelu", [&]() {
+            if (f32w) return linear_f32w(st, h1f, d.ffn1, (float *)m->inter, T, H, 1536, TZH_OP_GELU, nullptr);
             return tzh_linear_codes_launch(st, cus, m->h1, act, d.ffn1.w, d.ffn1.fmt, d.ffn1.s, d.ffn1.b, m->inter,
                                            act, T, H, 1536, 1536, TZH_EPI_BIAS_GELU, nullptr, nullptr, nullptr, 0.0f,
                                            nullptr, 0);
         }));
         TZH_TRY(stage("ffn2_ln", [&]() {
+            if (f32w) {
+                TZH_TRY(linear_f32w(st, (const float *)m->inter, d.ffn2, (float *)m->attn, T, 1536, H, -1, h1f));
+                return layernorm_rows(st, (const float *)m->attn, d.ln2_g, d.ln2_b, hf, T, H, eps);
+            }
             return tzh_linear_codes_launch(st, cus, m->inter, act, d.ffn2.w, d.ffn2.fmt, d.ffn2.s, d.ffn2.b, m->h,
                                            act, T, 1536, H, H, TZH_EPI_BIAS_RES_LN, m->h1, d.ln2_g, d.ln2_b, eps,
                                            m->ln_ws, m->ln_ws_rows);
@@ -978,10 +1044,7 @@ extern "C" int tzh_arctic_set_precision(tzh_model *m, int32_t dtype) {
 extern "C" int tzh_arctic_precision(tzh_model *m, int32_t *dtype) {
     tzh_clear_error();
     if (!m || !dtype) return tzh_fail(TZH_ERR_INVALID_ARGS, "null argument");
-    bool f16_codes = false;
-    for (const DevLayer &d : m->layers)
-        for (const DevLinear *l : {&d.qkv, &d.o, &d.ffn1, &d.ffn2}) f16_codes = f16_codes || l->fmt != TZH_WF_W8T;
-    *dtype = f16_codes ? TZH_F16 : m->act;
+    *dtype = model_act(m);
     return TZH_OK;
 }
 

@@ -44,7 +44,7 @@ void tzh_clear_error();
 // Device formats of the int8-model weight codes inside the library (not part
 // of the C ABI): f16 codes [n, k] row-major, or biased int8 codes stage-tiled
 // in 384-row blocks (gemm_pipe.hip).
-enum { TZH_WF_F16 = 0, TZH_WF_W8T = 1 };
+enum { TZH_WF_F16 = 0, TZH_WF_W8T = 1, TZH_WF_F32 = 2 };
 
 // ---------------------------------------------------------------------------
 // Context: one device, one stream.
@@ -78,6 +78,30 @@ int tzh_ctx_scratch(tzh_ctx *ctx, size_t bytes, void **out);
 // and returns its device address, valid for kernels enqueued next on the
 // context's stream.
 int tzh_ctx_upload_program(tzh_ctx *ctx, const void *src, size_t bytes, const void **dev_out);
+
+// f32 / f64 GEMM on the matrix cores (gemm_fp.hip): Y[b] = ops(alpha *
+// opA(A[b]) opB(B[b])) + beta * C, for b over the broadcast batch
+// dimensions; A[b] = a + sum_d idx_d * a_bstride[d] (0 where broadcast),
+// likewise B, and Y[b] = y + b * y_bstride.  lda / ldb / ldy are stored row
+// pitches.  ops[] are applied in order: TZH_OP_ADD adds bias[col], any
+// other code is that unary op (the elementwise engine's semantics).
+struct tzh_gemm_desc {
+    int64_t m = 0, n = 0, k = 0;
+    int64_t lda = 0, ldb = 0, ldy = 0;
+    int32_t nb = 0;
+    int64_t batch_shape[TZH_MAX_RANK] = {};
+    int64_t a_bstride[TZH_MAX_RANK] = {}, b_bstride[TZH_MAX_RANK] = {};
+    int64_t y_bstride = 0;
+    double alpha = 1.0, beta = 0.0;
+    const void *c = nullptr;  // beta * c[i * c_rs + j * c_cs]
+    int64_t c_rs = 0, c_cs = 0;
+    const void *bias = nullptr;
+    int32_t n_ops = 0;
+    int32_t ops[4] = {};
+};
+// a_trans: A stored [k][m]; b_trans: B stored [n][k].
+int tzh_gemm_fp_launch(hipStream_t st, int32_t dtype, bool a_trans, bool b_trans, const void *a, const void *b,
+                       void *y, const tzh_gemm_desc &d);
 
 // Host tokenizer (tokenizer.cpp) for the embedding entry points.
 size_t tzh_tokenize(const tzh_tokenizer *tok, const uint8_t *text, size_t len, uint32_t *out, size_t cap);

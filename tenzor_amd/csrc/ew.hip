@@ -400,45 +400,14 @@ __global__ void __launch_bounds__(256) ew_gather_kernel(const T *__restrict__ ta
 }
 
 // matmul (executor.zig:199-326, matmul.zig): C[b] = A[b] B[b] over
-// broadcast batch dimensions, 16 x 16 output tiles staged through LDS, each
-// output summed over k in ascending order.
+// broadcast batch dimensions, computed by the matrix-core GEMM of
+// gemm_fp.hip; these are the batch strides and sizes the planner derives.
 struct MatmulArgs {
     int32_t nb;  // batch dimensions of the output
     int64_t batch_shape[TZH_MAX_RANK];
     int64_t a_stride[TZH_MAX_RANK], b_stride[TZH_MAX_RANK];  // 0 where broadcast
     int64_t m, k, n;
 };
-
-template <typename T>
-__global__ void __launch_bounds__(256) ew_matmul_kernel(const T *__restrict__ A, const T *__restrict__ B,
-                                                        T *__restrict__ C, const MatmulArgs a) {
-    __shared__ T as[16][17], bs[16][17];
-    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-    const int64_t row = (int64_t)blockIdx.y * 16 + ty, col = (int64_t)blockIdx.x * 16 + tx;
-    int64_t rem = blockIdx.z, ao = 0, bo = 0;
-    for (int d = a.nb - 1; d >= 0; d--) {
-        const int64_t i = rem % a.batch_shape[d];
-        rem /= a.batch_shape[d];
-        ao += i * a.a_stride[d];
-        bo += i * a.b_stride[d];
-    }
-    T acc = 0;
-    for (int64_t k0 = 0; k0 < a.k; k0 += 16) {
-        as[ty][tx] = (row < a.m && k0 + tx < a.k) ? A[ao + row * a.k + k0 + tx] : (T)0;
-        bs[ty][tx] = (k0 + ty < a.k && col < a.n) ? B[bo + (k0 + ty) * a.n + col] : (T)0;
-        __syncthreads();
-        const int kk = (int)(a.k - k0 < 16 ? a.k - k0 : 16);
-        for (int q = 0; q < kk; q++) acc += as[ty][q] * bs[q][tx];
-        __syncthreads();
-    }
-    if (row < a.m && col < a.n) C[(int64_t)blockIdx.z * a.m * a.n + row * a.n + col] = acc;
-}
-
-template <typename T>
-__global__ void __launch_bounds__(256) ew_fill_kernel(T *__restrict__ y, int64_t numel) {
-    const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (o < numel) y[o] = (T)0;
-}
 
 // transpose (transpose.zig): output element o at multi-index i reads the
 // input at sum_k i[k] * in_stride[perm[k]].
@@ -504,17 +473,7 @@ __global__ void __launch_bounds__(256) ew_transpose_kernel(const T *__restrict__
 // ------------------------------------------------------------------------
 // host planner
 // ------------------------------------------------------------------------
-bool unary_ok(int op) {
-    switch (op) {
-    case TZH_OP_NEG: case TZH_OP_ABS: case TZH_OP_EXP: case TZH_OP_LOG: case TZH_OP_SQRT:
-    case TZH_OP_RSQRT: case TZH_OP_SIN: case TZH_OP_COS: case TZH_OP_TANH: case TZH_OP_SIGMOID:
-    case TZH_OP_RELU: case TZH_OP_GELU: case TZH_OP_SILU: case TZH_OP_SOFTPLUS:
-    case TZH_OP_FLOOR: case TZH_OP_CEIL: case TZH_OP_ROUND:
-        return true;
-    default:
-        return false;
-    }
-}
+using tzh_ew::unary_ok;
 
 bool binary_ok(int op) {
     switch (op) {
@@ -1094,26 +1053,7 @@ struct Planner {
             TZH_LAUNCHED("ew_layernorm_kernel");
             return TZH_OK;
         }
-        if (n.kind == TZH_NODE_MATMUL) {
-            const void *bdat = nullptr;
-            TZH_TRY(input_data(n.rhs, &bdat));
-            MatmulArgs ma;
-            int64_t shp[TZH_MAX_RANK];
-            int nd = 0;
-            TZH_TRY(matmul_plan(idx, ma, shp, &nd));
-            int64_t batches = 1;
-            for (int i = 0; i < ma.nb; i++) batches *= ma.batch_shape[i];
-            if (batches > 65535) return tzh_fail(TZH_ERR_TOO_LARGE, "matmul with %lld batches", (long long)batches);
-            if (ma.k == 0) {  // empty sums
-                hipLaunchKernelGGL((ew_fill_kernel<T>), dim3((unsigned)((numel + 255) / 256)), dim3(256), 0, ctx->stream, out, numel);
-                TZH_LAUNCHED("ew_fill_kernel");
-                return TZH_OK;
-            }
-            const dim3 grid((unsigned)((ma.n + 15) / 16), (unsigned)((ma.m + 15) / 16), (unsigned)batches);
-            hipLaunchKernelGGL((ew_matmul_kernel<T>), grid, dim3(256), 0, ctx->stream, (const T *)x, (const T *)bdat, out, ma);
-            TZH_LAUNCHED("ew_matmul_kernel");
-            return TZH_OK;
-        }
+        if (n.kind == TZH_NODE_MATMUL) return launch_matmul(idx, nullptr, 0, out);
         if (n.kind == TZH_NODE_GATHER) {
             const tzh_node &t = tape[n.lhs];
             const tzh_leaf &il = leaves[tape[n.rhs].leaf];
@@ -1203,9 +1143,99 @@ struct Planner {
         return TZH_OK;
     }
 
+    // Matmul node `mm` on the matrix cores (gemm_fp.hip), with `n_ops` fused
+    // epilogue ops (bias adds read `bias` as a row vector over the last axis).
+    int launch_matmul(int32_t mm, const void *bias, int n_ops, void *out, const int32_t *ops = nullptr) {
+        const tzh_node &n = tape[mm];
+        const void *adat = nullptr, *bdat = nullptr;
+        TZH_TRY(input_data(n.lhs, &adat));
+        TZH_TRY(input_data(n.rhs, &bdat));
+        MatmulArgs ma;
+        int64_t shp[TZH_MAX_RANK];
+        int nd = 0;
+        TZH_TRY(matmul_plan(mm, ma, shp, &nd));
+        tzh_gemm_desc d;
+        d.m = ma.m, d.n = ma.n, d.k = ma.k, d.lda = ma.k, d.ldb = ma.n, d.ldy = ma.n;
+        d.nb = ma.nb;
+        for (int i = 0; i < ma.nb; i++) {
+            d.batch_shape[i] = ma.batch_shape[i];
+            d.a_bstride[i] = ma.a_stride[i];
+            d.b_bstride[i] = ma.b_stride[i];
+        }
+        d.y_bstride = ma.m * ma.n;
+        d.bias = bias;
+        d.n_ops = n_ops;
+        for (int o = 0; o < n_ops; o++) d.ops[o] = ops[o];
+        return tzh_gemm_fp_launch(ctx->stream, dtype, false, false, adat, bdat, out, d);
+    }
+
+    // A row vector over the last axis of a result of rank nd: a leaf whose
+    // dimensions are all 1 but the last, which is n.
+    bool is_row_bias(int32_t idx, int nd, int64_t n) const {
+        const tzh_node &b = tape[idx];
+        if (b.kind != TZH_NODE_TENSOR || b.ndim < 1 || b.ndim > nd || b.shape[b.ndim - 1] != n) return false;
+        for (int i = 0; i < b.ndim - 1; i++)
+            if (b.shape[i] != 1) return false;
+        return true;
+    }
+
+    // FusedMatmulEpilogueKernel (fusion/codegen.zig:78-147; the plan of
+    // analyzer.zig:106-153, 268-297): a root that is unary ops and adds of
+    // one bias row vector over a matmul of its own shape is evaluated by the
+    // matmul kernel, the ops applied in order (innermost first) to each
+    // output.  *fused = false (nothing launched) when the root has another
+    // form.
+    int try_fused_matmul(int32_t idx, void *out, bool *fused) {
+        *fused = false;
+        const tzh_node &root = tape[idx];
+        int32_t chain[8];
+        int len = 0;
+        int32_t cur = idx, bias_node = -1;
+        while (len < 8) {
+            const tzh_node &n = tape[cur];
+            if (n.kind == TZH_NODE_MATMUL) break;
+            if (n.ndim != root.ndim) return TZH_OK;
+            for (int i = 0; i < n.ndim; i++)
+                if (n.shape[i] != root.shape[i]) return TZH_OK;
+            if (n.kind == TZH_NODE_UNARY && unary_ok(n.op)) {
+                chain[len++] = cur;
+                cur = n.lhs;
+            } else if (n.kind == TZH_NODE_BINARY && n.op == TZH_OP_ADD && root.ndim >= 1) {
+                const int64_t last = root.shape[root.ndim - 1];
+                int32_t next, b;
+                if (is_row_bias(n.rhs, root.ndim, last)) next = n.lhs, b = n.rhs;
+                else if (is_row_bias(n.lhs, root.ndim, last)) next = n.rhs, b = n.lhs;
+                else return TZH_OK;
+                if (bias_node >= 0 && leaves[tape[bias_node].leaf].data != leaves[tape[b].leaf].data) return TZH_OK;
+                bias_node = b;
+                chain[len++] = cur;
+                cur = next;
+            } else {
+                return TZH_OK;
+            }
+        }
+        const tzh_node &mm = tape[cur];
+        if (mm.kind != TZH_NODE_MATMUL || len == 0 || len > 4 || mm.ndim != root.ndim) return TZH_OK;
+        for (int i = 0; i < mm.ndim; i++)
+            if (mm.shape[i] != root.shape[i]) return TZH_OK;
+        if (numel_of(root.ndim, root.shape) == 0) return TZH_OK;  // nothing to compute: the chain path returns
+        int32_t ops[4];
+        for (int o = 0; o < len; o++) {
+            const tzh_node &n = tape[chain[len - 1 - o]];
+            ops[o] = n.kind == TZH_NODE_UNARY ? n.op : TZH_OP_ADD;
+        }
+        *fused = true;
+        return launch_matmul(cur, bias_node >= 0 ? leaves[tape[bias_node].leaf].data : nullptr, len, out, ops);
+    }
+
     int eval_into(int32_t idx, void *out) {
         const tzh_node &n = tape[idx];
         const bool is64 = dtype == TZH_F64;
+        if ((n.kind == TZH_NODE_UNARY || n.kind == TZH_NODE_BINARY) && !ctx->ew_interpreter) {
+            bool fused = false;
+            TZH_TRY(try_fused_matmul(idx, out, &fused));
+            if (fused) return TZH_OK;
+        }
         if (n.kind != TZH_NODE_REDUCE && materialised_kind(n.kind))
             return is64 ? launch_structural<double>(idx, (double *)out) : launch_structural<float>(idx, (float *)out);
         if (n.kind == TZH_NODE_REDUCE)

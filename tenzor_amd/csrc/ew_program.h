@@ -24,6 +24,19 @@ static_assert(sizeof(EwProgram) < 3800, "kernel argument block too large");
 
 FastDiv make_fastdiv(uint64_t d);
 
+// The unary ops unary_op<T> implements (simd.zig:107-315).
+inline bool unary_ok(int op) {
+    switch (op) {
+    case TZH_OP_NEG: case TZH_OP_ABS: case TZH_OP_EXP: case TZH_OP_LOG: case TZH_OP_SQRT:
+    case TZH_OP_RSQRT: case TZH_OP_SIN: case TZH_OP_COS: case TZH_OP_TANH: case TZH_OP_SIGMOID:
+    case TZH_OP_RELU: case TZH_OP_GELU: case TZH_OP_SILU: case TZH_OP_SOFTPLUS:
+    case TZH_OP_FLOOR: case TZH_OP_CEIL: case TZH_OP_ROUND:
+        return true;
+    default:
+        return false;
+    }
+}
+
 // Launch the generated single-pass kernel for chain program p (no reduce
 // node) writing p.numel elements of type f64 ? double : float to out, with
 // V outputs per thread and `grid` blocks of 256 threads; kernels are

@@ -387,6 +387,22 @@ def group_arctic():
     check(L.tzh_arctic_bad_id_count(m, C.byref(n)))
     assert n.value == 1
     check(L.tzh_arctic_free(m))
+    # the f32 model (MatWeight.f32 linears on the f32 GEMM), two layers
+    cfg2 = synth.Config(num_hidden_layers=2)
+    w32 = synth.make_arctic_f32(77, cfg2, ln_random=True)
+    hw32 = synth.HostWeights(w32, cfg2)
+    m32 = C.c_void_p()
+    check(L.tzh_arctic_upload(CTX, C.byref(hw32.struct), C.byref(m32)))
+    d = C.c_int32()
+    check(L.tzh_arctic_precision(m32, C.byref(d)))
+    assert d.value == _abi.F32
+    out32 = np.empty((3, 384), np.float32)
+    check(L.tzh_arctic_forward_batch(m32, out32.ctypes.data, ids.ctypes.data, lengths.ctypes.data, 3, 40))
+    ref32 = np.stack([oracle.arctic_forward(hw32, ids[b, :Ln]) for b, Ln in enumerate(lengths)])
+    err = np.abs(out32 - ref32).max()
+    print(f"  arctic emu (f32 weights) vs oracle max-abs {err:.2e}", flush=True)
+    assert err < 1e-5
+    check(L.tzh_arctic_free(m32))
 
 
 def group_embed():
@@ -528,7 +544,78 @@ def group_nodes():
     assert L.tzh_eval_into(CTX, tape, 2, arr, 1, _abi.F32, out.ctypes.data) == -10  # TZH_ERR_SHAPE
 
 
-GROUPS = {"eval": group_eval, "gemm": group_gemm, "gemm_ln": group_gemm_ln, "attention": group_attention,
+def group_gemm_fp():
+    """The matrix-core f32/f64 GEMM (gemm_fp.hip): ONNX Gemm for every
+    transpose flag and C shape, ONNX MatMul's shape branches, and the fused
+    matmul epilogue of the eval planner."""
+    from oracle import onnx_ops as oo
+
+    rng = np.random.default_rng(21)
+    for ta, tb in [(0, 0), (1, 0), (0, 1), (1, 1)]:
+        for (m, n, k), cshape, al in [((5, 7, 3), None, True), ((130, 20, 17), (1, 1), False), ((33, 129, 40), (129,), True),
+                                      ((64, 64, 16), (64, 1), True), ((9, 200, 0), (9, 200), False)]:
+            A = rng.standard_normal((k, m) if ta else (m, k)).astype(np.float32)
+            B = rng.standard_normal((n, k) if tb else (k, n)).astype(np.float32)
+            Cm = None if cshape is None else rng.standard_normal(cshape).astype(np.float32)
+            if al:
+                A, B = aligned(A), aligned(B)
+            y = aligned_empty((m, n), np.float32)
+            cr, cc = (0, 0) if Cm is None else ((1, Cm.shape[0]) if Cm.ndim == 1 else Cm.shape)
+            check(L.tzh_gemm_f32(CTX, ta, tb, m, n, k, 0.75, A.ctypes.data, A.shape[1], B.ctypes.data, B.shape[1], -1.5,
+                                 None if Cm is None else Cm.ctypes.data, cr, cc, y.ctypes.data))
+            ref = oo.gemm(A, B, Cm, 0.75, -1.5, bool(ta), bool(tb))
+            bound = (0.75 * (np.abs(A.T if ta else A).astype(np.float64) @ np.abs(B.T if tb else B)) * (k + 2) * 2.0 ** -23
+                     + 2.0 ** -22 * np.abs(ref) + 1e-30)
+            assert (np.abs(y - ref) <= bound).all(), (ta, tb, m, n, k, cshape)
+    # a padded row pitch (lda > k)
+    A = rng.standard_normal((10, 24)).astype(np.float32)
+    B = rng.standard_normal((13, 7)).astype(np.float32)
+    y = np.empty((10, 7), np.float32)
+    check(L.tzh_gemm_f32(CTX, 0, 0, 10, 7, 13, 1.0, A.ctypes.data, 24, B.ctypes.data, 7, 0.0, None, 0, 0, y.ctypes.data))
+    assert np.allclose(y, A[:, :13].astype(np.float64) @ B, rtol=1e-5, atol=1e-5)
+    # MatMul: the reference's test, its shape branches, f64, scalar B, zero dims
+    for dt in (np.float32, np.float64):
+        for sa, sb in [((2, 3), (3, 2)), ((7,), (7,)), ((7,), (7, 5)), ((9, 7), (7,)), ((3, 9, 7), (3, 7, 20)),
+                       ((3, 9, 7), (7, 20)), ((9, 7), (3, 7, 20)), ((2, 3, 9, 7), (2, 3, 7, 20)), ((2, 3, 9, 7), (7, 20)),
+                       ((2, 1, 9, 7), (3, 7, 20)), ((4, 6), ()), ((4, 6), (1,)), ((0, 5), (5, 3)), ((4, 0), (0, 3))]:
+            A = (np.arange(1, 7, dtype=dt).reshape(2, 3) if sa == (2, 3) else rng.standard_normal(sa).astype(dt))
+            B = (np.arange(1, 7, dtype=dt).reshape(3, 2) if sb == (3, 2) else rng.standard_normal(sb).astype(dt))
+            ys, yn = (C.c_int64 * 8)(), C.c_int32()
+            sha, shb = (C.c_int64 * 8)(*sa), (C.c_int64 * 8)(*sb)
+            dcode = _abi.F64 if dt == np.float64 else _abi.F32
+            check(L.tzh_matmul_nd(CTX, dcode, A.ctypes.data, sha, len(sa), B.ctypes.data, shb, len(sb), None, ys, C.byref(yn)))
+            ref = oo.matmul(A, B)
+            shape = tuple(ys[i] for i in range(yn.value))
+            assert shape == ref.shape, (sa, sb, shape, ref.shape)
+            y = np.full(shape, np.nan, dt)
+            check(L.tzh_matmul_nd(CTX, dcode, A.ctypes.data, sha, len(sa), B.ctypes.data, shb, len(sb),
+                                  y.ctypes.data if y.size else None, ys, C.byref(yn)))
+            tol = 2e-6 if dt == np.float32 else 1e-14
+            assert np.abs(y - ref).max(initial=0) <= tol * max(1.0, float(np.abs(ref).max(initial=0))) * np.sqrt(max(1, sa[-1]))
+            if sa == (2, 3):
+                assert y.tolist() == [[22, 28], [49, 64]]  # executor.zig:6288-6290
+    # the fused epilogue: known answer (codegen.zig:330-347), then fused vs
+    # the same ops over a materialised matmul, bit for bit
+    a, i2, bias = T(np.array([[1, 2], [3, 4]], np.float32)), T(np.eye(2, dtype=np.float32)), T(np.array([-10, 10], np.float32))
+    rc, out = eval_lib(UnaryExpr("relu", BinaryExpr("add", a.matmul(i2), bias)))
+    assert rc == 0 and out.tolist() == [[0, 12], [0, 14]]
+    for dt in (np.float32, np.float64):
+        A = rng.standard_normal((3, 37, 20)).astype(dt)
+        B = rng.standard_normal((20, 45)).astype(dt)
+        bv = rng.standard_normal(45).astype(dt)
+        ta_, tb_, tbias = T(A, dt), T(B, dt), T(bv, dt)
+        mm = ta_.matmul(tb_)
+        rc, mmv = eval_lib(mm)
+        assert rc == 0
+        tm = T(mmv, dt)
+        for build in [lambda x: UnaryExpr("relu", BinaryExpr("add", x, tbias)), lambda x: UnaryExpr("gelu", x),
+                      lambda x: UnaryExpr("silu", UnaryExpr("tanh", BinaryExpr("add", tbias, x)))]:
+            rc1, fused = eval_lib(build(mm))
+            rc2, split = eval_lib(build(tm))
+            assert rc1 == 0 and rc2 == 0 and np.array_equal(fused, split), dt
+
+
+GROUPS = {"eval": group_eval, "gemm_fp": group_gemm_fp, "gemm": group_gemm, "gemm_ln": group_gemm_ln, "attention": group_attention,
           "arctic": group_arctic, "embed": group_embed,
           "nodes": group_nodes}
 

@@ -11,7 +11,10 @@
 // assume: v_mfma_f32_32x32x16_f16 (A: row = lane%32, k = 8*(lane/32)+i;
 // B: col = lane%32, same k; D element e of lane l: row 8*(e/4) + 4*(l/32) +
 // e%4, col l%32) and v_mfma_f32_16x16x32_f16 (A/B: row/col = lane%16,
-// k = 8*(lane/16)+i; D element e: row 4*(l/16)+e, col l%16).
+// k = 8*(lane/16)+i; D element e: row 4*(l/16)+e, col l%16), and
+// v_mfma_f32_16x16x4_f32 / v_mfma_f64_16x16x4_f64 (A/B: one value per lane,
+// row/col = lane%16, k = lane/16; D element e: row 4*(l/16)+e in f32 and
+// row l/16+4*e in f64, col l%16).
 #pragma once
 
 #include <cmath>
@@ -205,9 +208,43 @@ inline emu_f32x4 mfma_16x16x32(emu_half8 a, emu_half8 b, emu_f32x4 c) {
     wave_barrier();
     return d;
 }
+
+struct MfmaIn64 {
+    double a, b;
+};
+
+// 16x16x4 with one f32 or f64 operand value per lane; T is the element type
+template <typename T, typename V>
+inline V mfma_16x16x4(T a, T b, V c) {
+    const int lane = lane_id();
+    MfmaIn64 in{(double)a, (double)b};
+    std::memcpy(wave_slot(lane), &in, sizeof in);
+    wave_barrier();
+    V d = c;
+    for (int e = 0; e < 4; e++) {
+        const int row = sizeof(T) == 4 ? 4 * (lane / 16) + e : lane / 16 + 4 * e, col = lane % 16;
+        T acc = 0;
+        for (int k = 0; k < 4; k++) {
+            MfmaIn64 ai, bi;
+            std::memcpy(&ai, wave_slot(row + 16 * k), sizeof ai);
+            std::memcpy(&bi, wave_slot(col + 16 * k), sizeof bi);
+            acc += (T)ai.a * (T)bi.b;
+        }
+        d[e] += acc;
+    }
+    wave_barrier();
+    return d;
+}
 }  // namespace emu
 
+typedef double emu_f64x4 __attribute__((ext_vector_type(4)));
 namespace emu {
+inline emu_f32x4 mfma_f32_16x16x4_args(float a, float b, emu_f32x4 c, int, int, int) {
+    return mfma_16x16x4<float, emu_f32x4>(a, b, c);
+}
+inline emu_f64x4 mfma_f64_16x16x4_args(double a, double b, emu_f64x4 c, int, int, int) {
+    return mfma_16x16x4<double, emu_f64x4>(a, b, c);
+}
 inline emu_f32x16 mfma_32x32x16_args(emu_half8 a, emu_half8 b, emu_f32x16 c, int, int, int) {
     return mfma_32x32x16(a, b, c);
 }
@@ -218,6 +255,8 @@ inline emu_f32x4 mfma_16x16x32_args(emu_half8 a, emu_half8 b, emu_f32x4 c, int, 
 // variadic so that brace-initialised operands (which contain commas) pass through
 #define __builtin_amdgcn_mfma_f32_32x32x16_f16(...) emu::mfma_32x32x16_args(__VA_ARGS__)
 #define __builtin_amdgcn_mfma_f32_16x16x32_f16(...) emu::mfma_16x16x32_args(__VA_ARGS__)
+#define __builtin_amdgcn_mfma_f32_16x16x4f32(...) emu::mfma_f32_16x16x4_args(__VA_ARGS__)
+#define __builtin_amdgcn_mfma_f64_16x16x4f64(...) emu::mfma_f64_16x16x4_args(__VA_ARGS__)
 #define __builtin_amdgcn_exp2f(x) exp2f(x)
 #define __builtin_amdgcn_rcpf(x) (1.0f / (x))
 // v_perm_b32: byte i of the result is byte sel[i] of {src0 (bytes 4..7), src1 (bytes 0..3)};
