@@ -435,42 +435,39 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
         woff[ks] = P::X_BYTES + (wn * TNF * 32 + l31) * WROWB + ((cw ^ fw) << 4);
     }
 
-    // the in-place split's row and chunk offsets (f32 activations)
-    const int sp_row = tid / (BK / 8), sp_p = tid % (BK / 8);
-    const int sp_c0 = ((2 * sp_p) ^ FX::swz(sp_row)) << 4, sp_c1 = ((2 * sp_p + 1) ^ FX::swz(sp_row)) << 4;
-
     f32x16_t acc[TNF][TMF];
 #pragma unroll
     for (int a = 0; a < TNF; a++)
 #pragma unroll
         for (int b = 0; b < TMF; b++) acc[a][b] = f32x16_t{};
 
-    auto split_stage = [&](char *buf) __attribute__((always_inline)) {
+    // f32 activations: each wave splits, in place, the X rows its own DMA
+    // groups loaded (rows wu*LX*RPI .. +LX*RPI), once its own loads of the
+    // stage have landed, in the step before the one that reads them; that
+    // step's barrier then makes them visible to every wave.
+    // Each 32-byte group of 8 consecutive k of a row, logical chunks 2p and
+    // 2p+1, becomes hi in chunk 2p and lo in chunk 2p+1; eight lanes take
+    // the eight groups of one row.
+    auto split_own = [&](char *buf) __attribute__((always_inline)) {
         if constexpr (XF32) {
-            // Split the stage's f32 X tile in place, once per workgroup (every
-            // fragment is read by P::WN waves): each 32-byte group of 8
-            // consecutive k of a row, logical chunks 2p and 2p+1, becomes hi
-            // in chunk 2p and lo in chunk 2p+1.  Eight lanes take the eight
-            // groups of one row, so a read touches each bank the minimum
-            // number of times.
-            // Thread tid takes group tid % (BK/8) of rows tid / (BK/8) + i *
-            // ROWS; ROWS is a multiple of the swizzle period, so every i has
-            // the same chunk positions.
-            constexpr int ROWS = P::THREADS / (BK / 8);
-            static_assert((BM * (BK / 8)) % P::THREADS == 0 && ROWS % (FX::RPW * FX::CPR) == 0,
-                          "whole 8-value groups per thread, one swizzle pattern per thread");
+            constexpr int GPR = BK / 8, ROWS_W = P::LX * FX::RPI;
+            static_assert((ROWS_W * GPR) % 64 == 0, "whole groups per lane");
+            // the offsets are recomputed here (a few VALU ops) rather than
+            // kept in registers across the whole kernel
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
 #pragma unroll
-            for (int i = 0; i < BM / ROWS; i++) {
-                char *row = buf + (i * ROWS + sp_row) * XROWB;
-                f32x4_t *c0 = (f32x4_t *)(row + sp_c0);
-                f32x4_t *c1 = (f32x4_t *)(row + sp_c1);
+            for (int c = 0; c < ROWS_W * GPR / 64; c++) {
+                const int g = c * 64 + ln, r = wu * ROWS_W + g / GPR, p = g % GPR;
+                char *row = buf + r * XROWB;
+                f32x4_t *c0 = (f32x4_t *)(row + (((2 * p) ^ FX::swz(r)) << 4));
+                f32x4_t *c1 = (f32x4_t *)(row + (((2 * p + 1) ^ FX::swz(r)) << 4));
                 const f32x4_t x0 = *c0, x1 = *c1;
                 half8_t hi, lo;
                 split_f32x8(x0, x1, hi, lo);
                 *(half8_t *)c0 = hi;
                 *(half8_t *)c1 = lo;
             }
-            lds_barrier();
         }
     };
     auto compute = [&](const char *buf) __attribute__((always_inline)) {
@@ -698,16 +695,36 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     constexpr int EPI_STORES = TMF * TNF * (STAGED ? 2 : 4);
     int last_epi = -NS;
     bool last_full = false;
+    // own loads of stage t landed (and own LDS reads done): at most the
+    // loads of the stages issued after t and the epilogue ops issued after
+    // them still outstanding
+    auto wait_own = [&](int t) __attribute__((always_inline)) {
+        wait_stage<NS - 2, P::L, EPI_LOADS, EPI_LOADS + EPI_STORES>(
+            min(NS - 2, S - 1 - t), last_epi >= t - NS + 1 ? (last_full ? 2 : 1) : 0);
+    };
+    if constexpr (XF32) {
+        wait_own(0);
+        wave_lds_order();
+        split_own(bufs[0]);
+    }
     auto step = [&](auto jc, int s) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
-        // own loads of stage s landed, own LDS reads done
-        wait_stage<NS - 2, P::L, EPI_LOADS, EPI_LOADS + EPI_STORES>(
-            min(NS - 2, S - 1 - s), last_epi >= s - NS + 1 ? (last_full ? 2 : 1) : 0);
-        lds_barrier_only();  // every wave's loads of stage s landed; stage s-1 fully read
+        if constexpr (XF32)
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // own split writes done (own loads of s waited for and split)
+        else
+            wait_own(s);
+        lds_barrier_only();  // every wave's stage s landed (and split); stage s-1 fully read
         const int kt = s % KT;
         if (s + NS - 1 < S) issue(bufs[(j + NS - 1) % NS]);
-        split_stage(bufs[j]);
         compute(bufs[j]);
+        // (before this step's epilogue, whose stores the wait would
+        // otherwise include, and whose registers the split would add to)
+        if constexpr (XF32)
+            if (s + 1 < S) {
+                wait_own(s + 1);
+                wave_lds_order();  // the lanes read slots their neighbours' loads wrote
+                split_own(bufs[(j + 1) % NS]);
+            }
         if (kt == KT - 1) {
             const int i = s / KT;
             epilogue(i);
