@@ -138,8 +138,10 @@ typedef struct {
 typedef struct {
     const void *data; /* device pointer */
     int32_t ndim;
-    int32_t dtype;    /* 0: the expression's element type; TZH_I32, TZH_U32, TZH_I64 or TZH_U64:
-                         the integer indices of a gather node (Tensor(u32, ...), executor.zig:425-477) */
+    int32_t dtype;    /* 0 or the expression's element type (TZH_F32 / TZH_F64): a value tensor;
+                         TZH_I32, TZH_U32, TZH_I64 or TZH_U64: the integer indices of a gather
+                         node (Tensor(u32, ...), executor.zig:425-477); anything else is
+                         TZH_ERR_WRONG_DTYPE */
     int64_t shape[TZH_MAX_RANK];
 } tzh_leaf;
 

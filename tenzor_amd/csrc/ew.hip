@@ -509,13 +509,38 @@ struct Planner {
     int32_t n_leaves;
     int32_t dtype;
     size_t es;
-    std::vector<void *> temps;
+    // Temporaries come from the stream-ordered allocator (hipMallocAsync on
+    // the context's stream) and go back to it after the kernels that read
+    // them, so an evaluation never waits on the host; where that allocator
+    // is unavailable, from hipMalloc, freed after one synchronisation.
+    std::vector<void *> temps, sync_temps;
+    bool no_async = false;
 
     ~Planner() {
-        if (!temps.empty()) {
-            hipStreamSynchronize(ctx->stream);
-            for (void *t : temps) hipFree(t);
+        for (void *t : temps) hipFreeAsync(t, ctx->stream);
+        if (sync_temps.empty()) return;
+        hipStreamSynchronize(ctx->stream);
+        for (void *t : sync_temps) hipFree(t);
+    }
+
+    int temporary(size_t bytes, void **out) {
+        void *t = nullptr;
+        if (!no_async) {
+            if (hipMallocAsync(&t, bytes ? bytes : es, ctx->stream) == hipSuccess) {
+                temps.push_back(t);
+                *out = t;
+                return TZH_OK;
+            }
+            (void)hipGetLastError();
+            no_async = true;
         }
+        if (hipMalloc(&t, bytes ? bytes : es) != hipSuccess) {
+            (void)hipGetLastError();
+            return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "temporary of %zu bytes failed", bytes);
+        }
+        sync_temps.push_back(t);
+        *out = t;
+        return TZH_OK;
     }
 
     int validate(int32_t idx) {
@@ -532,8 +557,13 @@ struct Planner {
             for (int i = 0; i < n.ndim; i++)
                 if (lf.shape[i] != n.shape[i]) return tzh_fail(TZH_ERR_SHAPE, "node %d: leaf shape mismatch", idx);
             if (!lf.data && numel_of(lf.ndim, lf.shape) > 0) return tzh_fail(TZH_ERR_INVALID_ARGS, "leaf %d: null data", n.leaf);
-            if (lf.dtype != 0 && !index_leaf_read_by_gather(idx))
-                return tzh_fail(TZH_ERR_WRONG_DTYPE, "leaf %d: integer tensors are only gather indices", n.leaf);
+            if (is_index_dtype(lf.dtype)) {
+                if (!index_leaf_read_by_gather(idx))
+                    return tzh_fail(TZH_ERR_WRONG_DTYPE, "leaf %d: integer tensors are only gather indices", n.leaf);
+            } else if (lf.dtype != 0 && lf.dtype != dtype) {
+                return tzh_fail(TZH_ERR_WRONG_DTYPE, "leaf %d: dtype %d is not the expression's element type %d",
+                                n.leaf, lf.dtype, dtype);
+            }
             return TZH_OK;
         }
         case TZH_NODE_CONSTANT:
@@ -857,11 +887,7 @@ struct Planner {
         const tzh_node &n = tape[idx];
         const size_t bytes = (size_t)numel_of(n.ndim, n.shape) * es;
         void *t = nullptr;
-        if (hipMalloc(&t, bytes ? bytes : es) != hipSuccess) {
-            (void)hipGetLastError();
-            return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "temporary of %zu bytes failed", bytes);
-        }
-        temps.push_back(t);
+        TZH_TRY(temporary(bytes, &t));
         TZH_TRY(eval_into(idx, t));
         *buf = t;
         return TZH_OK;
@@ -1021,13 +1047,12 @@ struct Planner {
                 return TZH_OK;
             }
             // few long columns: [outer, len, inner] -> [outer, inner, len],
-            // softmax along rows, and back
-            // (the two staging buffers live in the context's grow-only scratch:
-            // a fresh allocation and free per call cost more than the kernels)
-            const size_t bytes = ((size_t)numel * sizeof(T) + 255) & ~(size_t)255;
-            void *scratch = nullptr;
-            TZH_TRY(tzh_ctx_scratch(ctx, 2 * bytes, &scratch));
-            void *t1 = scratch, *t2 = (char *)scratch + bytes;
+            // softmax along rows, and back, through two stream-ordered
+            // temporaries
+            const size_t bytes = (size_t)numel * sizeof(T);
+            void *t1 = nullptr, *t2 = nullptr;
+            TZH_TRY(temporary(bytes, &t1));
+            TZH_TRY(temporary(bytes, &t2));
             const int64_t s3[3] = {outer, len, inner}, s3t[3] = {outer, inner, len};
             const int p021[3] = {0, 2, 1};
             TZH_TRY(launch_transpose<T>((const T *)x, (T *)t1, 3, s3, p021));

@@ -231,6 +231,9 @@ hipError_t hipMalloc(void **p, size_t n) {
     return hipSuccess;
 }
 hipError_t hipFree(void *p) { std::free(p); return hipSuccess; }
+// launches run to completion when issued, so a stream-ordered free is an immediate one
+hipError_t hipMallocAsync(void **p, size_t n, hipStream_t) { return hipMalloc(p, n); }
+hipError_t hipFreeAsync(void *p, hipStream_t) { return hipFree(p); }
 hipError_t hipHostMalloc(void **p, size_t n, unsigned) { return hipMalloc(p, n); }
 hipError_t hipHostFree(void *p) { return hipFree(p); }
 hipError_t hipMemcpy(void *d, const void *s, size_t n, hipMemcpyKind) { std::memmove(d, s, n); return hipSuccess; }

@@ -140,6 +140,16 @@ def group_eval():
     for n in (1, 3, 5, 255, 1027):
         out, ref = eval_both(T(np.arange(n, dtype=np.float32)).add(1.0).exp())
         assert (ulp(out, ref) <= 2).all()
+    # leaf dtypes: 0 or the element type is a value leaf; another float type
+    # or integers outside a gather are WRONG_DTYPE
+    xv = T(np.arange(6, dtype=np.float32))
+    nodes, leaves = to_tape(UnaryExpr("neg", xv))
+    tape = (_abi.Node * len(nodes))(*nodes)
+    yv = np.empty(6, np.float32)
+    for dtc, want in [(0, 0), (_abi.F32, 0), (_abi.F64, _abi.ERR_WRONG_DTYPE), (_abi.I32, _abi.ERR_WRONG_DTYPE)]:
+        arr = (_abi.Leaf * 1)()
+        arr[0].data, arr[0].ndim, arr[0].shape[0], arr[0].dtype = leaves[0].data.data_ptr(), 1, 6, dtc
+        assert L.tzh_eval_into(CTX, tape, len(nodes), arr, 1, _abi.F32, yv.ctypes.data) == want, dtc
     out, _ = eval_both(ReduceExpr("sum", T(np.zeros(0, np.float32))))
     assert float(out) == 0.0
     # regression: an empty operand under a scalar broadcast (shape.zig's

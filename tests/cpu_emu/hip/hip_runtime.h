@@ -299,6 +299,8 @@ hipError_t hipSetDevice(int d);
 hipError_t hipGetDeviceProperties(hipDeviceProp_t *p, int d);
 hipError_t hipMalloc(void **p, size_t n);
 hipError_t hipFree(void *p);
+hipError_t hipMallocAsync(void **p, size_t n, hipStream_t s);
+hipError_t hipFreeAsync(void *p, hipStream_t s);
 hipError_t hipHostMalloc(void **p, size_t n, unsigned flags);
 hipError_t hipHostFree(void *p);
 hipError_t hipMemcpy(void *d, const void *s, size_t n, hipMemcpyKind k);

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 import oracle
-from tenzor_amd import TzhError, _abi
+from tenzor_amd import TzhError, _abi, lib
 from tenzor_amd.expr import BinaryExpr, ReduceExpr, ScalarExpr, Tensor, UnaryExpr, eval, evalInto, to_tape
 from tests.conftest import ulp_diff
 
@@ -231,6 +231,26 @@ def test_errors_mirror_compile_errors(ctx):
     with pytest.raises(TzhError) as ei:
         eval(ReduceExpr("variance", T(np.zeros(3))), ctx)
     assert ei.value.code == _abi.ERR_UNSUPPORTED_OP
+
+
+def test_leaf_dtype_is_explicit(ctx):
+    """A value leaf may state the expression's element type or 0; another
+    float type, or integers outside a gather, is WRONG_DTYPE with its own
+    message."""
+    x = torch.arange(6, dtype=torch.float32, device=DEV)
+    nodes, leaves = to_tape(UnaryExpr("neg", Tensor(x)))
+    tape = (_abi.Node * len(nodes))(*nodes)
+    out = torch.empty(6, device=DEV)
+    for dt, ok in [(0, True), (_abi.F32, True), (_abi.F64, False), (_abi.I32, False)]:
+        arr = (_abi.Leaf * 1)()
+        arr[0].data, arr[0].ndim, arr[0].shape[0], arr[0].dtype = x.data_ptr(), 1, 6, dt
+        rc = lib().tzh_eval_into(ctx.handle, tape, len(nodes), arr, 1, _abi.F32, out.data_ptr())
+        if ok:
+            assert rc == 0 and out.cpu().tolist() == [-v for v in range(6)]
+        else:
+            assert rc == _abi.ERR_WRONG_DTYPE
+            msg = lib().tzh_last_error().decode()
+            assert ("element type" in msg) == (dt == _abi.F64) and ("gather" in msg) == (dt == _abi.I32), msg
 
 
 def test_config2_chain_medium(ctx):

@@ -140,6 +140,18 @@ def test_matmul_reference_known_answers():
     assert y.shape == (2, 2) and np.allclose(y.sum(1), 1, atol=1e-5)
 
 
+def test_matmul_many_batches_and_rows():
+    """More than 65535 batches ([70000, 2, 2] @ [2, 2]) and more than 2^20
+    rows: the GEMM's grid is one-dimensional over batches and tiles."""
+    rng = np.random.default_rng(12)
+    for sa, sb in [((70000, 2, 2), (2, 2)), (((1 << 20) + 5, 2), (2, 3))]:
+        A = rng.standard_normal(sa).astype(np.float32)
+        B = rng.standard_normal(sb).astype(np.float32)
+        got = eval(leaf(A).matmul(leaf(B))).cpu().numpy()
+        ref = np.matmul(A.astype(np.float64), B.astype(np.float64))
+        assert got.shape == ref.shape and np.abs(got - ref).max() <= 1e-5 * max(1.0, float(np.abs(ref).max()))
+
+
 @pytest.mark.parametrize("dt", [np.float32, np.float64])
 def test_matmul_shapes_vs_restatement(dt):
     rng = np.random.default_rng(9)
