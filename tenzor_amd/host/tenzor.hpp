@@ -174,6 +174,7 @@ template <typename T> struct ScalarExpr;
 template <typename Input, int Axis> struct SoftmaxExpr;
 template <typename Input, int... Perm> struct TransposeExpr;
 template <typename Input, int64_t... Dims> struct ReshapeExpr;
+template <typename Lhs, typename Rhs> struct MatmulExpr;
 
 // Methods every expression has (expr.zig:236-316): unary ops, binary ops
 // with an expression or a scalar, reductions.
@@ -208,6 +209,9 @@ struct ExprMethods {
     // reshape(target_shape) (expr.zig:918-920)
     template <int64_t... Dims>
     ReshapeExpr<Self, Dims...> reshape() const { return ReshapeExpr<Self, Dims...>::init(self()); }
+    // matmul(other) (expr.zig:290-294)
+    template <typename R>
+    MatmulExpr<Self, R> matmul(const R &rhs) const { return MatmulExpr<Self, R>::init(self(), rhs); }
 };
 
 // A concrete tensor: Tensor(T, shape) (tensor.zig:28-249) with device data.
@@ -468,6 +472,83 @@ struct TransposeExpr : ExprMethods<TransposeExpr<Input, Perm...>> {
         tzh_node n = Tape::node_of(kind, shape);
         n.lhs = a;
         for (size_t i = 0; i < perm.size(); i++) n.perm[i] = perm[i];
+        return tape.push(n);
+    }
+};
+
+// matmulCompatible / MatmulShape (shape.zig:206-274): the contracting
+// dimensions agree; [K] @ [K] is a scalar, [K] @ [K, N] is [N], [M, K] @ [K]
+// is [M], [M, K] @ [K, N] is [M, N]; otherwise both operands are matrices
+// with broadcast batch dimensions in front.
+template <size_t A, size_t B>
+constexpr bool matmul_compatible(const Shape<A> &a, const Shape<B> &b) {
+    if (A < 1 || B < 1) return false;
+    return a[A - 1] == (B >= 2 ? b[B - 2] : b[0]);
+}
+
+template <size_t A, size_t B>
+constexpr size_t matmul_rank() {
+    return (A == 1 && B == 1) ? 0 : (A == 1 || B == 1) && A + B == 3 ? 1 : (A > B ? A : B);
+}
+
+template <size_t A, size_t B>
+constexpr bool matmul_batch_ok(const Shape<A> &a, const Shape<B> &b) {
+    if (A < 2 || B < 2) return A + B <= 3;  // a vector operand only with a matrix or a vector
+    constexpr size_t nb = (A > B ? A : B) - 2;
+    for (size_t i = 0; i < nb; i++) {
+        const int64_t da = i < nb - (A - 2) ? 1 : a[i - (nb - (A - 2))];
+        const int64_t db = i < nb - (B - 2) ? 1 : b[i - (nb - (B - 2))];
+        if (da != db && da != 1 && db != 1) return false;
+    }
+    return true;
+}
+
+template <size_t A, size_t B>
+constexpr Shape<matmul_rank<A, B>()> matmul_shape(const Shape<A> &a, const Shape<B> &b) {
+    Shape<matmul_rank<A, B>()> out{};
+    if constexpr (A == 1 && B == 2) {
+        out[0] = b[1];
+    } else if constexpr (A == 2 && B == 1) {
+        out[0] = a[0];
+    } else if constexpr (A >= 2 && B >= 2) {
+        constexpr size_t nb = (A > B ? A : B) - 2;
+        for (size_t i = 0; i < nb; i++) {
+            const int64_t da = i < nb - (A - 2) ? 1 : a[i - (nb - (A - 2))];
+            const int64_t db = i < nb - (B - 2) ? 1 : b[i - (nb - (B - 2))];
+            out[i] = da > db ? da : db;
+        }
+        out[nb] = a[A - 2];
+        out[nb + 1] = b[B - 1];
+    }
+    return out;
+}
+
+// MatmulExpr(Lhs, Rhs) (expr.zig:515-560): same element type, the shape
+// rules above as compile-time errors.  Evaluated on the matrix cores; a
+// bias add and unary ops directly above it run in its epilogue.
+template <typename Lhs, typename Rhs>
+struct MatmulExpr : ExprMethods<MatmulExpr<Lhs, Rhs>> {
+    static_assert(std::is_same<typename Lhs::ElementType, typename Rhs::ElementType>::value,
+                  "MatmulExpr requires both operands to have the same element type");
+    static_assert(matmul_compatible(Lhs::shape, Rhs::shape), "Shapes not compatible for matmul");
+    static_assert(matmul_batch_ok(Lhs::shape, Rhs::shape), "Batch dimensions not broadcastable in matmul");
+    using ElementType = typename Lhs::ElementType;
+    static constexpr NodeKind kind = NodeKind::matmul;
+    static constexpr auto shape = matmul_shape(Lhs::shape, Rhs::shape);
+    Lhs lhs;
+    Rhs rhs;
+    static MatmulExpr init(const Lhs &l, const Rhs &r) {
+        MatmulExpr e;
+        e.lhs = l;
+        e.rhs = r;
+        return e;
+    }
+    int32_t emit(Tape &tape) const {
+        const int32_t a = lhs.emit(tape);
+        const int32_t b = rhs.emit(tape);
+        tzh_node n = Tape::node_of(kind, shape);
+        n.lhs = a;
+        n.rhs = b;
         return tape.push(n);
     }
 };

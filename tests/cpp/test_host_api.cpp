@@ -134,6 +134,33 @@ int main(int argc, char **argv) {
         for (int i = 0; i < 5; i++) EXPECT(r[i] == expected[i]);
     });
 
+    run("matmul with a fused bias + relu epilogue", [&] {  // codegen.zig:330-347
+        using Mat = Tensor<float, 2, 2>;
+        using Row = Tensor<float, 2>;
+        auto a = Mat::fromSlice(ctx, {1, 2, 3, 4});
+        auto eye = Mat::fromSlice(ctx, {1, 0, 0, 1});
+        auto bias = Row::fromSlice(ctx, {-10, 10});
+        EXPECT((eval(ctx, a.matmul(eye).add(bias).relu()).slice(ctx) == std::vector<float>{0, 12, 0, 14}));
+    });
+
+    run("batched and vector matmul shapes", [&] {  // shape.zig:206-274
+        using Batch = Tensor<float, 2, 1, 3>;
+        using Mat = Tensor<float, 3, 2>;
+        using Vec = Tensor<float, 3>;
+        auto a = Batch::fromSlice(ctx, {1, 2, 3, 4, 5, 6});
+        auto b = Mat::fromSlice(ctx, {1, 0, 0, 1, 1, 1});
+        auto v = Vec::fromSlice(ctx, {1, 1, 1});
+        auto ab = a.matmul(b);
+        static_assert(decltype(ab)::shape.size() == 3 && decltype(ab)::shape[0] == 2 &&
+                          decltype(ab)::shape[1] == 1 && decltype(ab)::shape[2] == 2,
+                      "batched shape");
+        EXPECT((eval(ctx, ab).slice(ctx) == std::vector<float>{4, 5, 10, 11}));
+        auto vb = v.matmul(b);  // [3] @ [3, 2] -> [2]
+        EXPECT((eval(ctx, vb).slice(ctx) == std::vector<float>{2, 2}));
+        auto vv = eval(ctx, v.matmul(v)).slice(ctx);  // [3] @ [3] -> scalar
+        EXPECT(vv.size() == 1 && vv[0] == 3.0f);
+    });
+
     run("config-2 chain exp((A + b) * c) vs oracle", [&] {
         constexpr int64_t R = 512, C = 4096;
         using Mat = Tensor<float, R, C>;

@@ -31,6 +31,19 @@ def test_header_compiles_with_the_reference_surface(tmp_path):
         auto s = eval(ctx, ReduceExpr<OpTag::sum, decltype(e), 1, true>::init(e));
         static_assert(decltype(s)::shape[0] == 4 && decltype(s)::shape[1] == 1, "reduced shape");
         evalInto(ctx, e, r.data());
+        // MatmulShape (shape.zig:221-274) at compile time
+        Tensor<float, 8, 5> bm;
+        auto mm = a.matmul(bm).add(Tensor<float, 5>{}).relu();
+        static_assert(decltype(mm)::shape.size() == 2 && decltype(mm)::shape[0] == 4 && decltype(mm)::shape[1] == 5, "mm");
+        Tensor<float, 3, 1, 4, 8> ba;
+        Tensor<float, 2, 8, 6> bb;
+        auto bmm = ba.matmul(bb);
+        constexpr auto bs = decltype(bmm)::shape;
+        static_assert(bs.size() == 4 && bs[0] == 3 && bs[1] == 2 && bs[2] == 4 && bs[3] == 6, "batched matmul shape");
+        auto mv = a.matmul(b);
+        static_assert(decltype(mv)::shape.size() == 1 && decltype(mv)::shape[0] == 4, "matrix-vector shape");
+        auto vv = b.matmul(b);
+        static_assert(decltype(vv)::shape.size() == 0, "vector-vector is a scalar");
         auto w = arctic::ModelWeights::fromSafeTensors(ctx, "m.safetensors");
         std::vector<int32_t> lengths{3};
         arctic::forwardBatch(nullptr, nullptr, lengths, 0, w);
@@ -53,6 +66,12 @@ def test_header_compiles_with_the_reference_surface(tmp_path):
      "Tensor<float, 4>, 1>::init(a, g, g); (void)e;", "Gamma/beta shape must match last dimensions of input"),
     ("Tensor<float, 2, 3> a; auto e = a.softmax<2>(); (void)e;", "softmax axis out of range"),
     ("Tensor<float, 2, 3> a; auto e = a.reshape<4, 2>(); (void)e;", "Reshape must preserve the element count"),
+    # shape.zig:206-216, 256-261
+    ("Tensor<float, 2, 3> a; Tensor<float, 4, 5> b; auto e = a.matmul(b); (void)e;", "Shapes not compatible for matmul"),
+    ("Tensor<float, 2, 4, 3> a; Tensor<float, 3, 3, 5> b; auto e = a.matmul(b); (void)e;",
+     "Batch dimensions not broadcastable in matmul"),
+    ("Tensor<float, 4, 3> a; Tensor<double, 3, 5> b; auto e = MatmulExpr<Tensor<float, 4, 3>, Tensor<double, 3, 5>>"
+     "::init(a, b); (void)e;", "same element type"),
 ])
 def test_compile_time_errors_mirror_comptime_errors(tmp_path, body, message):
     res = compile_snippet(body, tmp_path)
