@@ -33,8 +33,8 @@ int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t 
                             int32_t w_format, const uint16_t *scale, const float *bias, void *c, int32_t c_dtype,
                             int64_t m, int64_t k, int64_t n, int64_t n_valid, int32_t epilogue, const void *res,
                             const float *gamma, const float *beta, float eps, float *ln_ws, int64_t ln_ws_rows);
-int tzh_attention_launch(hipStream_t st, const void *qkv, void *out, int32_t dtype, const int *cu_seqlens,
-                         const int *order, int batch, int n_heads, int hidden);
+int tzh_attention_launch(hipStream_t st, int num_cus, unsigned *queue, const void *qkv, void *out, int32_t dtype,
+                         const int *cu_seqlens, const int *order, int batch, int n_heads, int hidden);
 
 namespace {
 
@@ -498,6 +498,8 @@ int ensure_workspace(tzh_model *m, int64_t tokens, int batch, size_t es) {
 
 int model_new(tzh_ctx *ctx, const tzh_arctic_config &cfg, tzh_model **out) {
     TZH_TRY(check_config(cfg));
+    unsigned *queue = nullptr;  // the attention's work queue, allocated now so that forwards never allocate it
+    TZH_TRY(tzh_ctx_work_queue(ctx, &queue));
     tzh_model *m = new (std::nothrow) tzh_model();
     if (!m) return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "model allocation failed");
     m->ctx = ctx;
@@ -883,7 +885,8 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
                                            H, 3 * H, 3 * H, TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f, nullptr, 0);
         }));
         TZH_TRY(stage("attention", [&]() {
-            return tzh_attention_launch(st, m->qkv, m->attn, act, d_cu, d_order, batch, 12, H);
+            return tzh_attention_launch(st, m->ctx->num_cus, m->ctx->work_queue, m->qkv, m->attn, act, d_cu, d_order,
+                                        batch, 12, H);
         }));
         TZH_TRY(stage("attn_out_ln", [&]() {
             if (f32w) {

@@ -67,12 +67,17 @@ struct tzh_ctx {
     void *prog_host = nullptr;
     hipEvent_t prog_ev[kProgSlots] = {};
     int prog_next = 0;
+    // work-queue counters of persistent kernels (zero between launches)
+    unsigned *work_queue = nullptr;
 };
 
 // Make ctx's device current for the calling thread.
 int tzh_ctx_enter(tzh_ctx *ctx);
 // Grow-only device scratch owned by the context (synchronises on growth).
 int tzh_ctx_scratch(tzh_ctx *ctx, size_t bytes, void **out);
+// The context's work-queue counters (allocated and zeroed on first use;
+// the kernels that take items from them leave them at zero).
+int tzh_ctx_work_queue(tzh_ctx *ctx, unsigned **out);
 // Stream-ordered upload of a small kernel descriptor (<= kProgSlotBytes):
 // copies `bytes` from src into the next device slot of the context's ring
 // and returns its device address, valid for kernels enqueued next on the

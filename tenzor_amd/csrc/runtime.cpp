@@ -79,6 +79,24 @@ extern "C" int tzh_init(int device, void *stream, tzh_ctx **out) {
     return TZH_OK;
 }
 
+int tzh_ctx_work_queue(tzh_ctx *ctx, unsigned **out) {
+    if (!ctx->work_queue) {
+        void *p = nullptr;
+        if (hipMalloc(&p, 256) != hipSuccess) {
+            (void)hipGetLastError();
+            return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "work-queue allocation failed");
+        }
+        if (hipMemset(p, 0, 256) != hipSuccess) {
+            (void)hipGetLastError();
+            hipFree(p);
+            return tzh_fail(TZH_ERR_DEVICE, "work-queue initialisation failed");
+        }
+        ctx->work_queue = (unsigned *)p;
+    }
+    *out = ctx->work_queue;
+    return TZH_OK;
+}
+
 int tzh_ctx_upload_program(tzh_ctx *ctx, const void *src, size_t bytes, const void **dev_out) {
     if (bytes > tzh_ctx::kProgSlotBytes) return tzh_fail(TZH_ERR_INVALID_ARGS, "internal: program of %zu bytes", bytes);
     if (!ctx->prog_dev) {
@@ -119,6 +137,7 @@ extern "C" int tzh_destroy(tzh_ctx *ctx) {
     if (ctx->prog_dev) hipFree(ctx->prog_dev);
     if (ctx->prog_host) hipHostFree(ctx->prog_host);
     if (ctx->scratch) hipFree(ctx->scratch);
+    if (ctx->work_queue) hipFree(ctx->work_queue);
     if (ctx->own_stream) hipStreamDestroy(ctx->stream);
     delete ctx;
     return TZH_OK;

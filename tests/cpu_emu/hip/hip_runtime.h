@@ -149,6 +149,13 @@ inline T atomicAdd(T *p, T v) {  // fibers are cooperative on one OS thread
     return old;
 }
 
+template <typename T>
+inline T atomicExch(T *p, T v) {
+    T old = *p;
+    *p = v;
+    return old;
+}
+
 using std::max;
 using std::min;
 using std::isnan;
