@@ -398,21 +398,30 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                              (size_t)(n0 % P::WTB + wu * P::LW * FW::RPI) * WROWB
                        : Wb + (size_t)(n0 + wu * P::LW * FW::RPI) * K * WEB;
     };
-    auto issue = [&](char *buf) __attribute__((always_inline)) {
-        const size_t k0b = (size_t)ikt * BK * XE;
-#pragma unroll
-        for (int i = 0; i < P::LX; i++)
-            dma16(Xb + ((size_t)x_row0[i] * K * XE + k0b), x_loff[i], buf + (wu * P::LX + i) * FX::RPI * XROWB);
-#pragma unroll
-        for (int i = 0; i < P::LW; i++)
-            dma16(w_unit + (P::WT ? (size_t)ikt * P::WTB * WROWB + (size_t)i * FW::RPI * WROWB
-                                  : (size_t)i * FW::RPI * K * WEB + (size_t)ikt * BK * WEB),
-                  (FW::PARITY && ((wu * P::LW + i) & 1)) ? w_loff_o : w_loff_e,
-                  buf + P::X_BYTES + (wu * P::LW + i) * FW::RPI * WROWB);
+    // A stage's loads: this wave's X pieces (i < LX) and weight pieces
+    // (i < LW), then the advance to the next stage's position.
+    auto issue_x = [&](char *buf, int i) __attribute__((always_inline)) {
+        dma16(Xb + ((size_t)x_row0[i] * K * XE + (size_t)ikt * BK * XE), x_loff[i],
+              buf + (wu * P::LX + i) * FX::RPI * XROWB);
+    };
+    auto issue_w = [&](char *buf, int i) __attribute__((always_inline)) {
+        dma16(w_unit + (P::WT ? (size_t)ikt * P::WTB * WROWB + (size_t)i * FW::RPI * WROWB
+                              : (size_t)i * FW::RPI * K * WEB + (size_t)ikt * BK * WEB),
+              (FW::PARITY && ((wu * P::LW + i) & 1)) ? w_loff_o : w_loff_e,
+              buf + P::X_BYTES + (wu * P::LW + i) * FW::RPI * WROWB);
+    };
+    auto advance = [&]() __attribute__((always_inline)) {
         if (++ikt == KT) {
             ikt = 0;
             if (++iu < count) set_unit(iu);
         }
+    };
+    auto issue = [&](char *buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < P::LX; i++) issue_x(buf, i);
+#pragma unroll
+        for (int i = 0; i < P::LW; i++) issue_w(buf, i);
+        advance();
     };
 
     // --- fragment read offsets -------------------------------------------
@@ -470,10 +479,26 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
             }
         }
     };
-    auto compute = [&](const char *buf) __attribute__((always_inline)) {
+    // nb: the stage buffer whose loads are issued during this compute, spread
+    // over its first KS k steps (f32 activations: issued back to back after
+    // the barrier, every wave's loads at once, the issue took 14 % of the
+    // GEMM; spread over two steps FFN1 went from 231 to 224 us, over four
+    // the two-stage ring waited for them; f16 activations: all at the
+    // first step, spreading measured 2 % slower); null: none
+    constexpr int KS = XF32 ? 2 : 1;
+    constexpr int XPER = (P::LX + KS - 1) / KS, WPER = (P::LW + KS - 1) / KS;
+    auto compute = [&](const char *buf, char *nb) __attribute__((always_inline)) {
         u32x4_t wraw[TNF];
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ks++) {
+            if (nb && ks < KS) {
+#pragma unroll
+                for (int i = ks * XPER; i < (ks + 1) * XPER; i++)
+                    if (i < P::LX) issue_x(nb, i);
+#pragma unroll
+                for (int i = ks * WPER; i < (ks + 1) * WPER; i++)
+                    if (i < P::LW) issue_w(nb, i);
+            }
             half8_t xf[TMF], xl[TMF], wf[TNF];
 #pragma unroll
             for (int b = 0; b < TMF; b++) {
@@ -715,8 +740,9 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
             wait_own(s);
         lds_barrier_only();  // every wave's stage s landed (and split); stage s-1 fully read
         const int kt = s % KT;
-        if (s + NS - 1 < S) issue(bufs[(j + NS - 1) % NS]);
-        compute(bufs[j]);
+        const bool more = s + NS - 1 < S;
+        compute(bufs[j], more ? bufs[(j + NS - 1) % NS] : nullptr);
+        if (more) advance();
         // (before this step's epilogue, whose stores the wait would
         // otherwise include, and whose registers the split would add to)
         if constexpr (XF32)
