@@ -70,8 +70,9 @@ def stage_of(kernel: str, prev: str | None) -> str | None:
         return "qkv"
     if epi == 1:
         return "ffn1_gelu"
-    if epi == 2:
-        return "attn_out_ln" if prev == "attention" else "ffn2_ln" if prev == "ffn1_gelu" else None
+    if epi == 2:  # (after its own stage: a repeated launch of a timing forward)
+        return ("attn_out_ln" if prev == "attention" else "ffn2_ln" if prev == "ffn1_gelu"
+                else prev if prev in ("attn_out_ln", "ffn2_ln") else None)
     if epi == 3 or "ln_rows_kernel" in kernel:
         return prev if prev in ("attn_out_ln", "ffn2_ln") else None
     return None
@@ -94,12 +95,15 @@ def _instances(seq):
     value of each instance]}}.  A forward runs from one pack_ids dispatch to
     the next; its precision is that of its attention kernel.  A dispatch that
     continues the previous stage (the pieces of a split LayerNorm round)
-    adds to that stage's current instance."""
+    adds to that stage's current instance.  Forwards that launch a stage
+    twice in a row (bench.py's per-launch timing forwards repeat each stage)
+    are left out, so that instances and averages are those of plain
+    forwards."""
     out = {}
-    fwd, prec, prev = {}, None, None
+    fwd, prec, prev, repeated = {}, None, None, False
 
     def flush():
-        if prec is not None:
+        if prec is not None and not repeated:
             tgt = out.setdefault(prec, {})
             for k, v in fwd.items():
                 tgt.setdefault(k, []).extend(v)
@@ -110,12 +114,13 @@ def _instances(seq):
             continue
         if st == "pack_ids":
             flush()
-            fwd, prec = {}, None
+            fwd, prec, repeated = {}, None, False
         if st == "attention":
             prec = "fp32" if "attn_varlen_f32_kernel" in name else "fp16"
         if st == prev and (epi_of(name) == 3 or "ln_rows_kernel" in name):
             fwd[st][-1] += v
         else:
+            repeated = repeated or st == prev
             fwd.setdefault(st, []).append(v)
         prev = st
     flush()
