@@ -132,3 +132,21 @@ def test_attention_rejects_bad_lengths(ctx):
     with pytest.raises(TzhError) as ei:
         check(lib().tzh_attention_varlen(ctx.handle, None, None, _abi.I8, None, 1, NH, H))
     assert ei.value.code == _abi.ERR_UNSUPPORTED_DTYPE
+
+
+def test_work_queue_across_launches(ctx):
+    """f32 attention takes (sequence, head) items from a work queue that each
+    launch returns to zero: more items than CUs, then a smaller batch, then
+    the first batch again (bit-identical: the queue changes which block
+    computes an item, not its sums)."""
+    rng = np.random.default_rng(21)
+    big = [int(x) for x in rng.integers(1, 513, 64)]
+    small = [int(x) for x in rng.integers(1, 513, 5)]
+    qb = rng.standard_normal((sum(big), 3 * H)).astype(np.float32)
+    qs = rng.standard_normal((sum(small), 3 * H)).astype(np.float32)
+    out1, cu1 = run(ctx, qb, big)
+    out2, cu2 = run(ctx, qs, small)
+    out3, _ = run(ctx, qb, big)
+    check_heads(out1, qb, big, cu1, (0, 11), True)
+    check_heads(out2, qs, small, cu2, range(NH), True)
+    assert np.array_equal(out1, out3)
