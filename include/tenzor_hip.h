@@ -244,7 +244,10 @@ int tzh_layernorm_last_dim(tzh_ctx *ctx, const float *x, const float *gamma, con
  * [T, hidden], both of element type dtype (TZH_F32: products of f32
  * operands formed from exact f16 hi/lo splits, f32 sums; TZH_F16: f16
  * operands), cu_seqlens: device int32 [batch+1].  head_dim must be 32 and
- * sequences at most 512 tokens. */
+ * sequences at most 512 tokens.  The f32 kernel takes (sequence, head)
+ * items from a work queue held by the context (two counters, allocated and
+ * zeroed at the first call, back at zero after every launch); calls on one
+ * context are ordered by its stream, so they never share it. */
 int tzh_attention_varlen(tzh_ctx *ctx, const void *qkv, void *out, int32_t dtype, const int32_t *cu_seqlens,
                          int32_t batch, int32_t n_heads, int32_t hidden);
 

@@ -86,7 +86,9 @@ int tzh_ctx_work_queue(tzh_ctx *ctx, unsigned **out) {
             (void)hipGetLastError();
             return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "work-queue allocation failed");
         }
-        if (hipMemset(p, 0, 256) != hipSuccess) {
+        // zeroed and waited for here: the context's stream may be one that
+        // does not wait for the default stream
+        if (hipMemset(p, 0, 256) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
             (void)hipGetLastError();
             hipFree(p);
             return tzh_fail(TZH_ERR_DEVICE, "work-queue initialisation failed");

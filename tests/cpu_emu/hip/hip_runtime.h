@@ -314,6 +314,7 @@ hipError_t hipMemcpy(void *d, const void *s, size_t n, hipMemcpyKind k);
 hipError_t hipMemcpyAsync(void *d, const void *s, size_t n, hipMemcpyKind k, hipStream_t st);
 hipError_t hipMemset(void *p, int v, size_t n);
 hipError_t hipStreamSynchronize(hipStream_t s);
+hipError_t hipDeviceSynchronize();
 hipError_t hipStreamCreateWithFlags(hipStream_t *s, unsigned f);
 hipError_t hipStreamDestroy(hipStream_t s);
 hipError_t hipEventCreateWithFlags(hipEvent_t *e, unsigned f);
