@@ -191,6 +191,9 @@ struct TileFmt {
 // rows (a multiple of BN) and each k stage, the WTB x BK codes are one
 // contiguous span, rows BK codes apart (tile_codes_w8_kernel writes it), so
 // a stage's weight tile is read from consecutive memory.
+// The tiled layout's k stages are 64 codes wide (TK); a configuration with
+// BK = 32 reads each tiled stage as two halves (rows TK codes apart in
+// memory, BK codes per row in LDS).
 template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_, bool W8_ = false, int WTB_ = 0, int XE_ = 2>
 struct PipeCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, NS = NS_;
@@ -198,6 +201,9 @@ struct PipeCfg {
     static constexpr bool W8 = W8_, WT = WTB_ > 0;
     static constexpr int WTB = WTB_ > 0 ? WTB_ : BN_;
     static_assert(WTB % BN_ == 0, "weight tile blocks hold whole column tiles");
+    static constexpr int TK = 64;                          // k codes per tiled stage in memory
+    static_assert(!WT || TK % BK_ == 0, "a k stage covers a whole part of a tiled stage");
+    static constexpr int SPT = WT ? TK / BK_ : 1;           // k stages per tiled stage
     static constexpr int NW = WM * WN, THREADS = NW * 64;
     static constexpr int TMF = BM / WM / 32;  // token fragments per wave
     static constexpr int TNF = BN / WN / 32;  // weight fragments per wave
@@ -373,7 +379,8 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     const int rw_in = lane / FW::CPR;                                // row inside a W DMA group
     const int wchunk_e = (lane % FW::CPR) ^ FW::swz(rw_in);
     const int wchunk_o = (lane % FW::CPR) ^ FW::swz(FW::RPI + rw_in);
-    const int w_pitch = P::WT ? WROWB : K * WEB;  // bytes between weight rows in memory
+    constexpr int WTROWB = P::TK * WEB;           // bytes per row of a tiled stage in memory
+    const int w_pitch = P::WT ? WTROWB : K * WEB;  // bytes between weight rows in memory
     const uint32_t w_loff_e = (uint32_t)(rw_in * w_pitch + wchunk_e * 16);  // bytes, same for every unit
     const uint32_t w_loff_o = (uint32_t)(rw_in * w_pitch + wchunk_o * 16);
     const char *const Xb = (const char *)X;
@@ -394,8 +401,8 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
             const int chunk = (lane % FX::CPR) ^ FX::swz((wu * P::LX + i) * FX::RPI + r_in);
             x_loff[i] = (uint32_t)((r - r0) * K * XE + chunk * 16);
         }
-        w_unit = P::WT ? Wb + (size_t)(n0 / P::WTB) * KT * P::WTB * WROWB +
-                             (size_t)(n0 % P::WTB + wu * P::LW * FW::RPI) * WROWB
+        w_unit = P::WT ? Wb + (size_t)(n0 / P::WTB) * K * P::WTB * WEB +
+                             (size_t)(n0 % P::WTB + wu * P::LW * FW::RPI) * WTROWB
                        : Wb + (size_t)(n0 + wu * P::LW * FW::RPI) * K * WEB;
     };
     // A stage's loads: this wave's X pieces (i < LX) and weight pieces
@@ -405,7 +412,8 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
               buf + (wu * P::LX + i) * FX::RPI * XROWB);
     };
     auto issue_w = [&](char *buf, int i) __attribute__((always_inline)) {
-        dma16(w_unit + (P::WT ? (size_t)ikt * P::WTB * WROWB + (size_t)i * FW::RPI * WROWB
+        dma16(w_unit + (P::WT ? (size_t)(ikt / P::SPT) * P::WTB * WTROWB + (size_t)(ikt % P::SPT) * WROWB +
+                                    (size_t)i * FW::RPI * WTROWB
                               : (size_t)i * FW::RPI * K * WEB + (size_t)ikt * BK * WEB),
               (FW::PARITY && ((wu * P::LW + i) & 1)) ? w_loff_o : w_loff_e,
               buf + P::X_BYTES + (wu * P::LW + i) * FW::RPI * WROWB);
@@ -814,9 +822,15 @@ struct Cfgs<TZH_WF_W8T, 2> {
 template <>
 struct Cfgs<TZH_WF_W8T, 4> {
     using Bias = PipeCfg<128, 384, 64, 2, 4, 2, true, kWtBlock, 4>;
-    using Narrow = Bias;
     using Ln = Bias;
-    using LnShortK = void;
+    // k <= 384 (the O-projection): two 4-wave workgroups of 64 x 384 tiles
+    // per CU, as for f16 activations; with f32 activations two of them fit
+    // in LDS only with 32-wide k stages (3 x 20 KiB each).  99.9 -> 95.4 us
+    // at the headline's T = 67590; for k = 1536 and the bias GEMMs the same
+    // layout measured slower (FFN2 + LN 228 -> 232 us, FFN1 224 -> 257, QKV
+    // 165 -> 187), so those keep the 8-wave 128-row tiles.
+    using LnShortK = PipeCfg<64, 384, 32, 1, 4, 3, true, kWtBlock, 4>;
+    using Narrow = Bias;
     using Piece64 = PipeCfg<64, 64, 64, 2, 2, 3, true, kWtBlock, 4>;
     using Piece128x64 = PipeCfg<128, 64, 64, 2, 2, 2, true, kWtBlock, 4>;
     using Piece128 = PipeCfg<128, 128, 64, 2, 2, 2, true, kWtBlock, 4>;

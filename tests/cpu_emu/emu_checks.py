@@ -269,6 +269,28 @@ def group_gemm():
             tol = 2e-3 * max(1.0, float(np.abs(ref).max()))
         err = float(np.abs(c - ref).max())
         assert err < tol, (m, k, n, epi, err)
+    # f32 activations with several units per persistent block (64-row tiles,
+    # two workgroups per CU: 32 slots on the emulated device), ragged last
+    # panel, the three epilogues
+    for m, k, n, epi in [(64 * 70 - 13, 64, 384, _abi.EPI_BIAS), (64 * 35 - 5, 128, 768, _abi.EPI_BIAS_GELU),
+                         (64 * 40 - 31, 128, 384, _abi.EPI_BIAS_RES_LN)]:
+        a, q, s, bias = problem(m + k, m, k, n, 0.1 if epi == _abi.EPI_BIAS_GELU else 1.0)
+        lin = oracle.matmul_w8a32(a, q, s, bias)
+        sf = s.view(np.float16).astype(np.float64)
+        bound = (np.abs(a) @ np.abs(q.astype(np.float64)).T) * sf * (2 ** -20 + k * 2 ** -23) + 1e-6
+        if epi == _abi.EPI_BIAS_RES_LN:
+            rng = np.random.default_rng(m)
+            res = rng.standard_normal((m, n)).astype(np.float32)
+            g = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+            b = (0.1 * rng.standard_normal(n)).astype(np.float32)
+            c = linear(a, q, s, bias, np.float32, epi, res, g, b)
+            err = float(np.abs(c - oracle.layernorm(res + lin, g, b, 1e-12)).max())
+            assert err < 1e-4, (m, k, n, err)
+        else:
+            c = linear(a, q, s, bias, np.float32, epi)
+            ref = oracle.gelu(lin) if epi == _abi.EPI_BIAS_GELU else lin
+            err = np.abs(c - ref)
+            assert (err <= bound * (1.13 if epi == _abi.EPI_BIAS_GELU else 1.0) + 1e-6).all(), (m, k, n, epi)
     w = (np.random.default_rng(12).standard_normal((64, 384)) * 0.02).astype(np.float32)
     w[0] = 0
     qg = np.empty((64, 384), np.int8)
