@@ -23,8 +23,9 @@ Subcommands:
         unit busy/stall fractions (see COUNTER_NOTES).
 
 Dispatches are mapped to forward stages by kernel and launch order: both
-LayerNorm GEMMs are one kernel instantiation; the one launched after
-attention is attn_out_ln and the one after ffn1_gelu is ffn2_ln.  The
+LayerNorm GEMMs are linear_pipe_kernel<2> (with f32 activations the k = 384
+one has a tile configuration of its own); the one launched after attention
+is attn_out_ln and the one after ffn1_gelu is ffn2_ln.  The
 pieces of a split partial round (the residual-only GEMM) and their row
 LayerNorm belong to the LayerNorm GEMM launched just before them.
 
@@ -256,8 +257,9 @@ def summarize(trace: str | None, fetch: str | None, write: str | None, bench_log
                                          "ms_per_step": steps[prec]}
                                   for prec, key in (("fp32", "stages"), ("fp16", "stages_fp16"))}
     if trace:
-        out += ["The two LayerNorm GEMMs are one kernel instantiation; the rows above separate",
-                "them by launch order.  The counter runs (bench_profile.py run) make one fp32",
+        out += ["Both LayerNorm GEMMs are linear_pipe_kernel<2> (in the fp32 forward the O-projection",
+                "with its own tile configuration); the rows above separate them by launch order.",
+                "The counter runs (bench_profile.py run) make one fp32",
                 "forward.  rocprofv3's own kernel summary of the trace run (bench.py: the fp16",
                 "forward first, 5 timed + 2 warmup, then the fp32 one, 5 timed + 2 warmup + 3",
                 "with per-launch events):", ""]
