@@ -490,9 +490,10 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     // nb: the stage buffer whose loads are issued during this compute, spread
     // over its first KS k steps (f32 activations: issued back to back after
     // the barrier, every wave's loads at once, the issue took 14 % of the
-    // GEMM; spread over two steps FFN1 went from 231 to 224 us, over four
-    // the two-stage ring waited for them; f16 activations: all at the
-    // first step, spreading measured 2 % slower); null: none
+    // GEMM; spread over two steps FFN1 went from 231 to 224 us, over three
+    // 221 -> 224 and over four the two-stage ring waited for them; f16
+    // activations: all at the first step, spreading measured 2 % slower);
+    // null: none
     constexpr int KS = XF32 ? 2 : 1;
     constexpr int XPER = (P::LX + KS - 1) / KS, WPER = (P::LW + KS - 1) / KS;
     auto compute = [&](const char *buf, char *nb) __attribute__((always_inline)) {
