@@ -842,7 +842,9 @@ static_assert(Cfgs<TZH_WF_W8T, 2>::Ln::WN == LnCfg::WN && Cfgs<TZH_WF_W8T, 2>::L
                   Cfgs<TZH_WF_W8T, 2>::LnShortK::TNF == LnCfg::TNF && Cfgs<TZH_WF_W8T, 4>::Ln::WN == LnCfg::WN &&
                   Cfgs<TZH_WF_W8T, 4>::Ln::TNF == LnCfg::TNF && Cfgs<TZH_WF_W8T, 4>::Ln::BN == LnCfg::BN,
               "one LayerNorm epilogue layout (statistics order) for every configuration and ln_rows_kernel");
-static_assert(Cfgs<TZH_WF_W8T, 2>::LnShortK::blocks_per_cu(true) == 2, "two short-k LayerNorm workgroups per CU");
+static_assert(Cfgs<TZH_WF_W8T, 2>::LnShortK::blocks_per_cu(true) == 2 &&
+                  Cfgs<TZH_WF_W8T, 4>::LnShortK::blocks_per_cu(true) == 2,
+              "two short-k LayerNorm workgroups per CU");
 static_assert(Cfgs<TZH_WF_W8T, 4>::Bias::lds_bytes(false, true, true) <= 163840 &&
                   Cfgs<TZH_WF_W8T, 4>::Ln::lds_bytes(true, false) <= 163840,
               "f32-activation tiles with staged f32 output fit the 160 KiB of LDS");
