@@ -95,6 +95,12 @@ int tzh_destroy(tzh_ctx *ctx);
 int tzh_sync(tzh_ctx *ctx);
 void *tzh_stream(tzh_ctx *ctx);
 
+/* Diagnostic, no counterpart in the reference: the size of the context's
+ * grow-only device scratch (which tzh_matmul_w8a32, tzh_linear_w8 and
+ * tzh_eval_into use for their workspaces) and how many device allocations
+ * have (re)sized it since tzh_init. */
+int tzh_ctx_scratch_info(tzh_ctx *ctx, int64_t *bytes, int64_t *allocs);
+
 int tzh_malloc(tzh_ctx *ctx, size_t bytes, void **dptr);
 int tzh_free(tzh_ctx *ctx, void *dptr);
 int tzh_memcpy_h2d(tzh_ctx *ctx, void *dst_device, const void *src_host, size_t bytes);
@@ -167,25 +173,33 @@ int tzh_eval_into(tzh_ctx *ctx, const tzh_node *tape, int32_t n_nodes,
 /* c[i,j] = (sum_k a[i,k]*f32(wq[j,k])) * f32(scale[j]) + bias[j]
  * Replaces matmulTransposeB_f32_i8_rowScale_bias (matmul_w8a32.zig:14-57).
  * a f32 [m,k], wq i8 [n,k] row-major, scale f16 bits [n], bias f32 [n] (may be
- * NULL = zeros), c f32 [m,n]; all device pointers; any m, k, n (k and n are
- * padded with zero codes internally, as the tail loop of
- * matmul_w8a32.zig:50-52 adds the last k % 8 products).  Each product
- * a*q is formed on the MFMA from an exact f16 split a = hi + lo (|a| must stay
- * below 65504, the f16 range) and summed in f32.  The int8 codes are
- * rewritten into the kernel's tiled format in the context scratch on every
- * call (and a copy of a with zero columns when k % 64 != 0). */
+ * NULL = zeros), c f32 [m,n]; all device pointers; any m, k, n >= 0 (k and n
+ * are padded with zero codes internally, as the tail loop of
+ * matmul_w8a32.zig:50-52 adds the last k % 8 products).  As in the
+ * reference, m == 0 or n == 0 does nothing (matmul_w8a32.zig:24) and k == 0
+ * writes c[i,j] = bias[j] (0 without a bias).  f32 arithmetic over the
+ * whole f32 range: each row of a is scaled by an exact power of two 2^e
+ * that puts its largest magnitude in [2^14, 2^15), each product a*q is
+ * formed on the MFMA from an exact f16 split of the scaled value (hi + lo,
+ * to 2^-22 relative for every value within 2^17 of its row's largest), the
+ * sums run in f32 and are multiplied by 2^-e (exact) before the scale and
+ * bias.  Rows holding inf or NaN give NaN where the reference gives inf or
+ * NaN.  The int8 codes are rewritten into the kernel's tiled format in the
+ * context scratch on every call (with the row exponents, and a copy of a
+ * with zero columns when k % 64 != 0). */
 int tzh_matmul_w8a32(tzh_ctx *ctx, const float *a, const int8_t *wq, const uint16_t *scale,
                      const float *bias, float *c, int64_t m, int64_t k, int64_t n);
 
 /* tzh_matmul_w8a32 without any device allocation.  No counterpart in the
  * reference: for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
- * arguments, kernels and results as tzh_matmul_w8a32, but the tiled codes
- * (and zero-padded rows of a when k % 64 != 0 or a is not 16-byte aligned)
- * go to a static 32 MiB device workspace, one per GPU, held until the process
- * ends: n_pad * k_pad (+ m * k_pad * 4) bytes must fit (n_pad, k_pad: n and k
- * rounded up to 384 and 64), else TZH_ERR_TOO_LARGE.  Calls that overlap on
- * one GPU (other streams or threads) share that workspace and race. */
+ * arguments, kernels and results as tzh_matmul_w8a32, but the tiled codes,
+ * the row exponents (and zero-padded rows of a when k % 64 != 0 or a is not
+ * 16-byte aligned) go to a static 32 MiB device workspace, one per GPU, held
+ * until the process ends: n_pad * k_pad + m * 4 (+ m * k_pad * 4) bytes,
+ * each rounded up to 256, must fit (n_pad, k_pad: n and k rounded up to 384
+ * and 64), else TZH_ERR_TOO_LARGE.  Calls that overlap on one GPU (other
+ * streams or threads) share that workspace and race. */
 int tzh_matmul_w8a32_noalloc(tzh_ctx *ctx, const float *a, const int8_t *wq, const uint16_t *scale,
                              const float *bias, float *c, int64_t m, int64_t k, int64_t n);
 
@@ -223,8 +237,10 @@ enum {
 /* General int8-weight linear with fused epilogue.  a_dtype and c_dtype are
  * TZH_F32 or TZH_F16; residual (EPI_BIAS_RES_LN only) has res_dtype ==
  * c_dtype and shape [m,n]; gamma/beta f32 [n].  f32 activations take the
- * hi/lo split of tzh_matmul_w8a32, f16 ones one MFMA; accumulation is f32.
- * Any k; f16 output needs n % 384 == 0, the LayerNorm epilogue n == 384. */
+ * row-scaled hi/lo split of tzh_matmul_w8a32 (f32 arithmetic over the whole
+ * f32 range), f16 ones one MFMA; accumulation is f32.  Any k >= 1 (k == 0
+ * only with the f32 bias epilogue, c = bias); m == 0 or n == 0 does
+ * nothing; f16 output needs n % 384 == 0, the LayerNorm epilogue n == 384. */
 int tzh_linear_w8(tzh_ctx *ctx, const void *a, int32_t a_dtype, const int8_t *wq,
                   const uint16_t *scale, const float *bias, void *c, int32_t c_dtype,
                   int64_t m, int64_t k, int64_t n, int32_t epilogue,
@@ -335,9 +351,15 @@ typedef struct tzh_model tzh_model;
  * dtypes give TZH_ERR_UNSUPPORTED_DTYPE.  On the device int8 codes stay
  * one byte each (biased, u = q + 128, tiled in the GEMM's stage order) with
  * their f16 row scale; f32 linears stay f32 (computed exactly in f32 on the
- * matrix cores); a layer that mixes the two becomes f16 codes W * 2^k with
- * scale 2^-k.  Embedding tables may be F32 or I8.  The model is bound to
- * ctx's device and stream. */
+ * matrix cores), each linear in its own format; a QKV whose three parts
+ * differ in dtype is held as one f32 matrix (int8 parts widened exactly to
+ * q * s).  Embedding tables may be F32 or I8.  The upload also bounds every
+ * activation the f32 forward splits into f16 halves, from the weights alone
+ * (LayerNorm outputs by sqrt(383) max|gamma| + max|beta|, each linear by
+ * its rows' sum |W| and |bias|): int8 GEMMs whose input bound reaches 2^15
+ * then run row-scaled (as tzh_matmul_w8a32), and a forward whose attention
+ * inputs' bound reaches 2^15 returns TZH_ERR_TOO_LARGE instead of computing
+ * NaN.  The model is bound to ctx's device and stream. */
 int tzh_arctic_upload(tzh_ctx *ctx, const tzh_arctic_weights *weights, tzh_model **out);
 
 /* ModelWeights.fromSafeTensors (arctic.zig:113-166): "bert." prefix
@@ -402,10 +424,11 @@ int tzh_arctic_last_launch_count(tzh_model *model);
  * in HBM, products of f32 operands from exact f16 hi/lo splits, f32 sums, as
  * arctic.zig:599-635 computes) or TZH_F16 (opt-in: activations rounded to
  * f16 between kernels, half the activation traffic).  A model whose linears
- * hold f32 weights (MatWeight.f32) runs in f32 whatever is set (its linears
- * on the f32 GEMM of tzh_gemm_f32); one that mixes f32 and int8 linears runs
- * with f16 activations; tzh_arctic_precision reports the precision the next
- * forward uses. */
+ * hold f32 weights (MatWeight.f32), or mixes f32 and int8 linears, runs in
+ * f32 whatever is set: each linear on its own format's GEMM (f32 weights on
+ * the f32 GEMM of tzh_gemm_f32, int8 weights on the int8 GEMM), as the
+ * reference loads each MatWeight independently (arctic.zig:55-58, 258-287).
+ * tzh_arctic_precision reports the precision the next forward uses. */
 int tzh_arctic_set_precision(tzh_model *model, int32_t dtype);
 int tzh_arctic_precision(tzh_model *model, int32_t *dtype);
 

@@ -132,6 +132,7 @@ PROTOTYPES = {
     "tzh_destroy": (C.c_int, [vp]),
     "tzh_sync": (C.c_int, [vp]),
     "tzh_stream": (vp, [vp]),
+    "tzh_ctx_scratch_info": (C.c_int, [vp, C.POINTER(i64), C.POINTER(i64)]),
     "tzh_malloc": (C.c_int, [vp, C.c_size_t, pp]),
     "tzh_free": (C.c_int, [vp, vp]),
     "tzh_memcpy_h2d": (C.c_int, [vp, vp, vp, C.c_size_t]),

@@ -32,9 +32,11 @@
 int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t x_dtype, const void *wc,
                             int32_t w_format, const uint16_t *scale, const float *bias, void *c, int32_t c_dtype,
                             int64_t m, int64_t k, int64_t n, int64_t n_valid, int32_t epilogue, const void *res,
-                            const float *gamma, const float *beta, float eps, float *ln_ws, int64_t ln_ws_rows);
+                            const float *gamma, const float *beta, float eps, float *ln_ws, int64_t ln_ws_rows,
+                            const int *rexp);
 int tzh_attention_launch(hipStream_t st, int num_cus, unsigned *queue, const void *qkv, void *out, int32_t dtype,
                          const int *cu_seqlens, const int *order, int batch, int n_heads, int hidden);
+int tzh_row_exp_launch(hipStream_t st, const float *a, int64_t m, int64_t k, int *e);
 
 namespace {
 
@@ -190,17 +192,22 @@ struct DevTable {
     TableRef ref() const { return TableRef{f32, q8, scale}; }
 };
 
-// Weight codes with a per-row f16 scale: C = (X . codes) * scale + b.
-// int8 codes stay one byte each, biased and stage-tiled for the GEMM
-// (TZH_WF_W8T; exact, |q| <= 127).  f32 weights (the reference's f32 model,
-// MatWeight.f32) become f16 codes W * 2^k with a power-of-two scale 2^-k per
-// row (TZH_WF_F16), so the scaling itself is exact and only the f16 rounding
-// of W * 2^k remains.
+// One linear of a layer, in one of two device formats, chosen per linear
+// as the reference's MatWeight is (arctic.zig:55-58):
+//   TZH_WF_W8T: int8 codes with a per-row f16 scale, C = (X . q) * s + b;
+//     the codes stay one byte each, biased and stage-tiled for the int8
+//     GEMM (exact, |q| <= 127);
+//   TZH_WF_F32: f32 weights [n, k] row-major for the f32 matrix-core GEMM
+//     (gemm_fp.hip), C = X W^T + b.
 struct DevLinear {
     void *w = nullptr;
-    int32_t fmt = TZH_WF_F16;
+    int32_t fmt = TZH_WF_F32;
     uint16_t *s = nullptr;
     float *b = nullptr;
+    // per concatenated part (Q, K, V for the QKV linear): the largest
+    // sum_k |W[j,k]| (int8: |q| * s) and the largest |bias[j]| over its rows,
+    // so that |output| <= gain * max|input| + bmax
+    float gain[3] = {}, bmax[3] = {};
 };
 
 struct DevLayer {
@@ -220,13 +227,21 @@ struct tzh_model {
     // workspace, grown on demand
     int64_t cap_tokens = 0;
     int cap_batch = 0;
-    // activation element type: TZH_F32 (the reference's) or TZH_F16 (opt-in);
-    // f32-weight linears (TZH_WF_F16 codes) run with f16 activations only
+    // activation element type chosen by tzh_arctic_set_precision: TZH_F32
+    // (the reference's) or TZH_F16 (opt-in, int8 models only)
     int32_t act = TZH_F32;
     size_t cap_es = 0;       // activation bytes per element the workspace was sized for
     void *h = nullptr, *h1 = nullptr, *qkv = nullptr, *attn = nullptr, *inter = nullptr;
     float *ln_ws = nullptr;  // f32 rows of a split LayerNorm GEMM round
     int64_t ln_ws_rows = 0;
+    // Range of the f32 forward's f16 hi/lo splits (set at upload from the
+    // weights): row_scaled when some int8 GEMM's input bound reaches 2^15
+    // (those GEMMs then run row-scaled, with rexp holding the row
+    // exponents); attn_bound, the bound of the attention's split inputs
+    // (|q| log2(e)/sqrt(32), |k|, |v|) over the layers
+    bool row_scaled = false;
+    float attn_bound = 0.0f;
+    int *rexp = nullptr;
     uint32_t *tok_ids = nullptr;
     int32_t *tok_pos = nullptr;
     int *meta = nullptr;  // device: cu[batch+1] | order[batch]
@@ -288,25 +303,15 @@ int upload_table(tzh_model *m, const tzh_mat_view &v, int64_t rows, DevTable &t,
     return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "Weight %s has unsupported dtype %d", what, v.dtype);
 }
 
-// f32 row -> f16 codes W * 2^k and the f16 bits of the scale 2^-k.  k puts
-// the row's largest magnitude in [2^13, 2^14), clamped to [-15, 24] so that
-// 2^-k is an exact f16 (normal or subnormal); an all-zero row gets k = 0.
-uint16_t f32_row_codes(const float *w, int cols, uint16_t *codes) {
-    float mx = 0.0f;
-    for (int i = 0; i < cols; i++) mx = std::max(mx, std::fabs(w[i]));
-    int k = 0;
-    if (mx > 0.0f && std::isfinite(mx)) {
-        int e;
-        std::frexp(mx, &e);  // mx in [2^(e-1), 2^e)
-        k = std::min(24, std::max(-15, 14 - e));
-    }
-    for (int i = 0; i < cols; i++) codes[i] = tzh_host_f32_to_f16(std::ldexp(w[i], k));
-    return tzh_host_f32_to_f16(std::ldexp(1.0f, -k));
-}
-
 // Concatenate the row blocks of several [rows_i, cols] linears into one
-// code matrix (QKV fusion) with its scales and biases.  Each block is int8
-// (I8 + F16 scale, the quantized model) or F32 (the f32 model).
+// matrix (QKV fusion) with its biases.  Each block is int8 (I8 + F16 scale,
+// the quantized model) or F32 (the f32 model).  Blocks that are all int8
+// become tiled codes (TZH_WF_W8T); otherwise the linear is f32
+// (TZH_WF_F32), its int8 blocks widened to f32(q) * f32(s), which is exact
+// (an 8-bit code times an 11-bit scale fits the f32 significand).  Only a
+// QKV whose three parts differ in dtype takes that widening; the product
+// (x . (q s)) then differs from the reference's (x . q) * s by the rounding
+// of f32 sums only.
 int upload_linear(tzh_model *m, std::initializer_list<std::pair<const tzh_mat_view *, const float *>> parts,
                   int cols, DevLinear &out, const char *what) {
     int64_t rows = 0;
@@ -320,19 +325,48 @@ int upload_linear(tzh_model *m, std::initializer_list<std::pair<const tzh_mat_vi
         if (v->cols != cols) return tzh_fail(TZH_ERR_INVALID_ARGS, "%s has %d columns, expected %d", what, v->cols, cols);
         rows += v->rows;
     }
-    bool all_i8 = true, all_f32 = true;
+    if (parts.size() > 3) return tzh_fail(TZH_ERR_INVALID_ARGS, "%s: too many parts", what);
+    int pi = 0;
     for (auto &pb : parts) {
-        all_i8 = all_i8 && pb.first->dtype == TZH_I8;
-        all_f32 = all_f32 && pb.first->dtype == TZH_F32;
+        const tzh_mat_view *v = pb.first;
+        float g = 0.0f, bm = 0.0f;
+        for (int r = 0; r < v->rows; r++) {
+            double l1 = 0.0;
+            if (v->dtype == TZH_F32) {
+                const float *w = (const float *)v->data + (size_t)r * cols;
+                for (int c = 0; c < cols; c++) l1 += std::fabs((double)w[c]);
+            } else {
+                const int8_t *q = (const int8_t *)v->data + (size_t)r * cols;
+                for (int c = 0; c < cols; c++) l1 += std::abs((int)q[c]);
+                l1 *= (double)tzh_host_f16_to_f32(((const uint16_t *)v->scale)[r]);
+            }
+            g = std::max(g, (float)l1);
+            bm = std::max(bm, std::fabs(pb.second[r]));
+        }
+        out.gain[pi] = g;
+        out.bmax[pi] = bm;
+        pi++;
     }
-    if (all_f32) {
+    bool all_i8 = true;
+    for (auto &pb : parts) all_i8 = all_i8 && pb.first->dtype == TZH_I8;
+    if (!all_i8 || rows % 384 != 0 || cols % 64 != 0) {
         // MatWeight.f32 (arctic.zig:55-58): the rows as they are, [n, k]
         // row-major, for the f32 GEMM on the matrix cores (gemm_fp.hip)
         std::vector<float> w((size_t)(rows * cols)), b((size_t)rows);
         int64_t r0 = 0;
         for (auto &pb : parts) {
             const tzh_mat_view *v = pb.first;
-            std::memcpy(w.data() + (size_t)r0 * cols, v->data, (size_t)v->rows * cols * 4);
+            float *dst = w.data() + (size_t)r0 * cols;
+            if (v->dtype == TZH_F32) {
+                std::memcpy(dst, v->data, (size_t)v->rows * cols * 4);
+            } else {
+                const int8_t *q = (const int8_t *)v->data;
+                const uint16_t *sc = (const uint16_t *)v->scale;
+                for (int r = 0; r < v->rows; r++) {
+                    const float s = tzh_host_f16_to_f32(sc[r]);
+                    for (int c = 0; c < cols; c++) dst[(size_t)r * cols + c] = (float)q[(size_t)r * cols + c] * s;
+                }
+            }
             std::memcpy(b.data() + r0, pb.second, (size_t)v->rows * 4);
             r0 += v->rows;
         }
@@ -341,56 +375,30 @@ int upload_linear(tzh_model *m, std::initializer_list<std::pair<const tzh_mat_vi
         TZH_TRY(upload<float>(m, (float **)&out.w, w.data(), w.size()));
         return upload<float>(m, &out.b, b.data(), b.size());
     }
-    if (all_i8 && rows % 384 == 0 && cols % 64 == 0) {
-        // biased codes u = q + 128, stage-tiled: block of 384 rows, k stage of
-        // 64 codes, row (the layout tile_codes_w8_kernel writes)
-        const int kts = cols / 64;
-        std::vector<uint8_t> t((size_t)(rows * cols));
-        std::vector<uint16_t> s;
-        std::vector<float> b;
-        int64_t r0 = 0;
-        for (auto &pb : parts) {
-            const tzh_mat_view *v = pb.first;
-            const int8_t *q = (const int8_t *)v->data;
-            for (int r = 0; r < v->rows; r++) {
-                const int64_t n = r0 + r;
-                for (int kt = 0; kt < kts; kt++) {
-                    uint8_t *dst = &t[(size_t)((((n / 384) * kts + kt) * 384 + n % 384) * 64)];
-                    const int8_t *src = q + (size_t)r * cols + (size_t)kt * 64;
-                    for (int c = 0; c < 64; c++) dst[c] = (uint8_t)src[c] ^ 0x80u;
-                }
-            }
-            s.insert(s.end(), (const uint16_t *)v->scale, (const uint16_t *)v->scale + v->rows);
-            b.insert(b.end(), pb.second, pb.second + v->rows);
-            r0 += v->rows;
-        }
-        out.fmt = TZH_WF_W8T;
-        TZH_TRY(upload<uint8_t>(m, (uint8_t **)&out.w, t.data(), t.size()));
-        TZH_TRY(upload<uint16_t>(m, &out.s, s.data(), s.size()));
-        return upload<float>(m, &out.b, b.data(), b.size());
-    }
-    std::vector<uint16_t> w((size_t)(rows * cols));  // f16 bits of the codes
-    std::vector<uint16_t> s((size_t)rows);
-    std::vector<float> b((size_t)rows);
-    uint16_t code16[256];
-    for (int c = 0; c < 256; c++) code16[c] = tzh_host_f32_to_f16((float)(int8_t)c);
+    // biased codes u = q + 128, stage-tiled: block of 384 rows, k stage of
+    // 64 codes, row (the layout tile_codes_w8_kernel writes)
+    const int kts = cols / 64;
+    std::vector<uint8_t> t((size_t)(rows * cols));
+    std::vector<uint16_t> s;
+    std::vector<float> b;
     int64_t r0 = 0;
     for (auto &pb : parts) {
         const tzh_mat_view *v = pb.first;
-        if (v->dtype == TZH_I8) {
-            const int8_t *q = (const int8_t *)v->data;
-            for (size_t i = 0; i < (size_t)v->rows * cols; i++) w[(size_t)r0 * cols + i] = code16[(uint8_t)q[i]];
-            std::memcpy(s.data() + r0, v->scale, (size_t)v->rows * 2);
-        } else {
-            const float *f = (const float *)v->data;
-            for (int r = 0; r < v->rows; r++)
-                s[(size_t)(r0 + r)] = f32_row_codes(f + (size_t)r * cols, cols, &w[(size_t)(r0 + r) * cols]);
+        const int8_t *q = (const int8_t *)v->data;
+        for (int r = 0; r < v->rows; r++) {
+            const int64_t n = r0 + r;
+            for (int kt = 0; kt < kts; kt++) {
+                uint8_t *dst = &t[(size_t)((((n / 384) * kts + kt) * 384 + n % 384) * 64)];
+                const int8_t *src = q + (size_t)r * cols + (size_t)kt * 64;
+                for (int c = 0; c < 64; c++) dst[c] = (uint8_t)src[c] ^ 0x80u;
+            }
         }
-        std::memcpy(b.data() + r0, pb.second, (size_t)v->rows * 4);
+        s.insert(s.end(), (const uint16_t *)v->scale, (const uint16_t *)v->scale + v->rows);
+        b.insert(b.end(), pb.second, pb.second + v->rows);
         r0 += v->rows;
     }
-    out.fmt = TZH_WF_F16;
-    TZH_TRY(upload<_Float16>(m, (_Float16 **)&out.w, w.data(), w.size()));
+    out.fmt = TZH_WF_W8T;
+    TZH_TRY(upload<uint8_t>(m, (uint8_t **)&out.w, t.data(), t.size()));
     TZH_TRY(upload<uint16_t>(m, &out.s, s.data(), s.size()));
     return upload<float>(m, &out.b, b.data(), b.size());
 }
@@ -408,11 +416,12 @@ int check_config(const tzh_arctic_config &c) {
 }
 
 void free_workspace(tzh_model *m) {
-    void *bufs[] = {m->h, m->h1, m->qkv, m->attn, m->inter, m->ln_ws, m->tok_ids, m->tok_pos, m->meta};
+    void *bufs[] = {m->h, m->h1, m->qkv, m->attn, m->inter, m->ln_ws, m->tok_ids, m->tok_pos, m->meta, m->rexp};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     m->h = m->h1 = m->qkv = m->attn = m->inter = nullptr;
     m->ln_ws = nullptr;
+    m->rexp = nullptr;
     m->ln_ws_rows = 0;
     m->tok_ids = nullptr;
     m->tok_pos = nullptr;
@@ -424,17 +433,15 @@ void free_workspace(tzh_model *m) {
     m->cap_es = 0;
 }
 
-// The activation type a forward runs with: f32 weights (MatWeight.f32) run
-// in f32 on the f32 GEMM; int8 weights in the tiled format in the chosen
-// precision; f16 codes (a model that mixes f32 and int8 linears) in f16.
+// The activation type a forward runs with: a model whose linears are all
+// int8 (TZH_WF_W8T) runs in the chosen precision; any model with an f32
+// linear runs in f32, each linear on its own format's GEMM (the f32 GEMM
+// takes f32 activations only).
 int32_t model_act(const tzh_model *m) {
-    bool all_w8t = true, all_f32 = true;
+    bool all_w8t = true;
     for (const DevLayer &d : m->layers)
-        for (const DevLinear *l : {&d.qkv, &d.o, &d.ffn1, &d.ffn2}) {
-            all_w8t = all_w8t && l->fmt == TZH_WF_W8T;
-            all_f32 = all_f32 && l->fmt == TZH_WF_F32;
-        }
-    return all_f32 ? TZH_F32 : all_w8t ? m->act : TZH_F16;
+        for (const DevLinear *l : {&d.qkv, &d.o, &d.ffn1, &d.ffn2}) all_w8t = all_w8t && l->fmt == TZH_WF_W8T;
+    return all_w8t ? m->act : TZH_F32;
 }
 
 // y[T, n] = ops(x[T, k] W^T) + C for an f32-weight linear (W [n, k]), ops =
@@ -482,6 +489,7 @@ int ensure_workspace(tzh_model *m, int64_t tokens, int batch, size_t es) {
     // a split partial round is at most a third of the CUs' 128-row tiles
     m->ln_ws_rows = std::min<int64_t>((T + 127) / 128, m->ctx->num_cus / 3 + 1) * 128;
     TZH_TRY(get((void **)&m->ln_ws, (size_t)m->ln_ws_rows * H * 4));
+    if (m->row_scaled) TZH_TRY(get((void **)&m->rexp, (size_t)T * 4));
     TZH_TRY(get((void **)&m->tok_ids, (size_t)T * 4));
     TZH_TRY(get((void **)&m->tok_pos, (size_t)T * 4));
     TZH_TRY(get((void **)&m->meta, (size_t)(2 * B + 1) * 4));
@@ -536,6 +544,48 @@ void model_delete(tzh_model *m) {
     delete m;
 }
 
+// Bounds on the f32 forward's activations, from the weights alone: a
+// LayerNorm output has |(x - mean) / std| <= sqrt(n - 1) (one element
+// against n - 1 equal ones), so |y| <= sqrt(383) max|gamma| + max|beta|; a
+// linear maps max|x| <= B to |y_j| <= B sum_k |W[j,k]| + |b_j|; attention
+// outputs are convex combinations of V rows; |gelu(x)| <= max(|x|, 0.17).
+// The f16 hi/lo split of an input is exact to 2^-22 for |x| < 65504; a
+// margin of two covers the rounding of these sums.  A GEMM whose input bound
+// reaches 2^15 makes the forward row-scale its int8 GEMMs (exact for any
+// f32 input); the attention's bound is checked at each forward.
+void set_range(tzh_model *m, const tzh_arctic_weights *w) {
+    constexpr float kLimit = 32768.0f;
+    auto ln_bound = [](const float *g, const float *b) {
+        float mg = 0.0f, mb = 0.0f;
+        for (int i = 0; i < H; i++) {
+            mg = std::max(mg, std::fabs(g[i]));
+            mb = std::max(mb, std::fabs(b[i]));
+        }
+        return std::sqrt((float)(H - 1)) * mg + mb;
+    };
+    auto out_bound = [](const DevLinear &l, int part, float in) { return in * l.gain[part] + l.bmax[part]; };
+    bool rs = false;
+    float attn = 0.0f;
+    auto need = [&](const DevLinear &l, float in) {
+        if (l.fmt == TZH_WF_W8T && !(in < kLimit)) rs = true;
+    };
+    float bh = ln_bound(w->layer_norm_gamma, w->layer_norm_beta);
+    for (size_t li = 0; li < m->layers.size(); li++) {
+        const DevLayer &d = m->layers[li];
+        const tzh_layer_weights &lw = w->layers[li];
+        need(d.qkv, bh);
+        const float bq = out_bound(d.qkv, 0, bh), bk = out_bound(d.qkv, 1, bh), bv = out_bound(d.qkv, 2, bh);
+        attn = std::max({attn, bq * 0.2551f, bk, bv});  // q is scaled by log2(e)/sqrt(32) before its split
+        need(d.o, bv);
+        const float bh1 = ln_bound(lw.attention.output_ln_gamma, lw.attention.output_ln_beta);
+        need(d.ffn1, bh1);
+        need(d.ffn2, std::max(out_bound(d.ffn1, 0, bh1), 0.17f));
+        bh = ln_bound(lw.ffn.output_ln_gamma, lw.ffn.output_ln_beta);
+    }
+    m->row_scaled = rs;
+    m->attn_bound = attn;
+}
+
 int upload_weights(tzh_model *m, const tzh_arctic_weights *w) {
     const tzh_arctic_config &c = m->cfg;
     TZH_TRY(upload_table(m, w->word_embeddings, c.vocab_size, m->word, "embeddings.word_embeddings.weight"));
@@ -574,6 +624,7 @@ int upload_weights(tzh_model *m, const tzh_arctic_weights *w) {
         TZH_TRY(upload<float>(m, &d.ln2_g, f.output_ln_gamma, H));
         TZH_TRY(upload<float>(m, &d.ln2_b, f.output_ln_beta, H));
     }
+    set_range(m, w);
     return TZH_OK;
 }
 
@@ -801,6 +852,11 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
     if (T > ((int64_t)1 << 30)) return tzh_fail(TZH_ERR_TOO_LARGE, "batch of %lld tokens is too large", (long long)T);
     const int32_t act = model_act(m);
     const size_t es = act == TZH_F32 ? 4 : 2;
+    if (act == TZH_F32 && !(m->attn_bound < 32768.0f))
+        return tzh_fail(TZH_ERR_TOO_LARGE,
+                        "the weights bound the attention's inputs (|q|/sqrt(32), |k|, |v|) only by %g; the f32 "
+                        "attention splits them into f16 halves, which needs a bound below 32768",
+                        (double)m->attn_bound);
     TZH_TRY(ensure_workspace(m, T, batch, es));
     hipStream_t st = m->ctx->stream;
 
@@ -874,43 +930,62 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
     for (int32_t li = 0; li < n_layers; li++) {
         const DevLayer &d = m->layers[(size_t)li];
         const int cus = m->ctx->num_cus;
-        // f32 weights: the f32 GEMM; a LayerNorm stage writes its pre-norm rows
-        // (x W^T + b, then + residual) into a buffer the stage does not read
-        // (inter for the O-projection, attn for FFN2) and normalises them
-        const bool f32w = d.qkv.fmt == TZH_WF_F32;
+        // Each linear runs on its own format's GEMM.  f32 weights: the f32
+        // GEMM (f32 activations; model_act makes the forward f32 whenever a
+        // linear is f32); a LayerNorm stage writes its pre-norm rows (x W^T +
+        // b, then + residual) into a buffer the stage does not read (inter
+        // for the O-projection, attn for FFN2) and normalises them.  int8
+        // weights: the int8 GEMM in the forward's precision.
+        for (const DevLinear *l : {&d.qkv, &d.o, &d.ffn1, &d.ffn2})
+            if ((l->fmt != TZH_WF_F32 && l->fmt != TZH_WF_W8T) || (l->fmt == TZH_WF_F32 && act != TZH_F32))
+                return tzh_fail(TZH_ERR_INVALID_ARGS, "layer %d: weight format %d cannot run with activation type %d", li,
+                                l->fmt, act);
         float *const hf = (float *)m->h, *const h1f = (float *)m->h1;
+        // row-scaled int8 GEMMs (set_range): the row exponents of input x [T, k]
+        const bool rs = m->row_scaled && act == TZH_F32;
+        auto rexp_of = [&](const void *x, int64_t k, const int **e) -> int {
+            *e = nullptr;
+            if (!rs) return TZH_OK;
+            *e = m->rexp;
+            return tzh_row_exp_launch(st, (const float *)x, T, k, m->rexp);
+        };
+        const int *ex = nullptr;
         TZH_TRY(stage("qkv", [&]() {
-            if (f32w) return linear_f32w(st, hf, d.qkv, (float *)m->qkv, T, H, 3 * H, -1, nullptr);
+            if (d.qkv.fmt == TZH_WF_F32) return linear_f32w(st, hf, d.qkv, (float *)m->qkv, T, H, 3 * H, -1, nullptr);
+            TZH_TRY(rexp_of(m->h, H, &ex));
             return tzh_linear_codes_launch(st, cus, m->h, act, d.qkv.w, d.qkv.fmt, d.qkv.s, d.qkv.b, m->qkv, act, T,
-                                           H, 3 * H, 3 * H, TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f, nullptr, 0);
+                                           H, 3 * H, 3 * H, TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f, nullptr, 0, ex);
         }));
         TZH_TRY(stage("attention", [&]() {
             return tzh_attention_launch(st, m->ctx->num_cus, m->ctx->work_queue, m->qkv, m->attn, act, d_cu, d_order,
                                         batch, 12, H);
         }));
         TZH_TRY(stage("attn_out_ln", [&]() {
-            if (f32w) {
+            if (d.o.fmt == TZH_WF_F32) {
                 TZH_TRY(linear_f32w(st, (const float *)m->attn, d.o, (float *)m->inter, T, H, H, -1, hf));
                 return layernorm_rows(st, (const float *)m->inter, d.ln1_g, d.ln1_b, h1f, T, H, eps);
             }
+            TZH_TRY(rexp_of(m->attn, H, &ex));
             return tzh_linear_codes_launch(st, cus, m->attn, act, d.o.w, d.o.fmt, d.o.s, d.o.b, m->h1, act, T, H, H,
                                            H, TZH_EPI_BIAS_RES_LN, m->h, d.ln1_g, d.ln1_b, eps, m->ln_ws,
-                                           m->ln_ws_rows);
+                                           m->ln_ws_rows, ex);
         }));
         TZH_TRY(stage("ffn1_gelu", [&]() {
-            if (f32w) return linear_f32w(st, h1f, d.ffn1, (float *)m->inter, T, H, 1536, TZH_OP_GELU, nullptr);
+            if (d.ffn1.fmt == TZH_WF_F32) return linear_f32w(st, h1f, d.ffn1, (float *)m->inter, T, H, 1536, TZH_OP_GELU, nullptr);
+            TZH_TRY(rexp_of(m->h1, H, &ex));
             return tzh_linear_codes_launch(st, cus, m->h1, act, d.ffn1.w, d.ffn1.fmt, d.ffn1.s, d.ffn1.b, m->inter,
                                            act, T, H, 1536, 1536, TZH_EPI_BIAS_GELU, nullptr, nullptr, nullptr, 0.0f,
-                                           nullptr, 0);
+                                           nullptr, 0, ex);
         }));
         TZH_TRY(stage("ffn2_ln", [&]() {
-            if (f32w) {
+            if (d.ffn2.fmt == TZH_WF_F32) {
                 TZH_TRY(linear_f32w(st, (const float *)m->inter, d.ffn2, (float *)m->attn, T, 1536, H, -1, h1f));
                 return layernorm_rows(st, (const float *)m->attn, d.ln2_g, d.ln2_b, hf, T, H, eps);
             }
+            TZH_TRY(rexp_of(m->inter, 1536, &ex));
             return tzh_linear_codes_launch(st, cus, m->inter, act, d.ffn2.w, d.ffn2.fmt, d.ffn2.s, d.ffn2.b, m->h,
                                            act, T, 1536, H, H, TZH_EPI_BIAS_RES_LN, m->h1, d.ln2_g, d.ln2_b, eps,
-                                           m->ln_ws, m->ln_ws_rows);
+                                           m->ln_ws, m->ln_ws_rows, ex);
         }));
     }
     if (outputs) {

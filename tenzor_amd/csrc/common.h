@@ -41,10 +41,10 @@ void tzh_clear_error();
                             hipGetErrorString(e_));                                      \
     } while (0)
 
-// Device formats of the int8-model weight codes inside the library (not part
-// of the C ABI): f16 codes [n, k] row-major, or biased int8 codes stage-tiled
-// in 384-row blocks (gemm_pipe.hip).
-enum { TZH_WF_F16 = 0, TZH_WF_W8T = 1, TZH_WF_F32 = 2 };
+// Device formats of a model's linear weights inside the library (not part of
+// the C ABI): biased int8 codes stage-tiled in 384-row blocks (gemm_pipe.hip),
+// or f32 weights [n, k] row-major (gemm_fp.hip).
+enum { TZH_WF_W8T = 1, TZH_WF_F32 = 2 };
 
 // ---------------------------------------------------------------------------
 // Context: one device, one stream.
@@ -60,6 +60,7 @@ struct tzh_ctx {
     // stream-ordered scratch used by eval for materialised reductions
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
+    int64_t scratch_allocs = 0;  // hipMalloc calls that (re)allocated the scratch
     // ring of kernel-program slots (device + pinned host staging)
     static constexpr int kProgSlots = 32;
     static constexpr size_t kProgSlotBytes = 4096;

@@ -11,6 +11,14 @@
 // adds only exact zeros to every sum, and padded output columns are never
 // stored.  The rewritten codes (and the padded rows) live in the context
 // scratch.
+//
+// f32 activations enter the MFMA as f16 halves hi + lo.  So that this is the
+// reference's f32 arithmetic for rows of any scale (f16 alone spans 2^-24 ..
+// 65504), row_exp_kernel first finds each row's largest magnitude and an
+// exponent e that puts it in [2^14, 2^15); the GEMM splits X[t,:] * 2^e[t]
+// and multiplies the sums by 2^-e[t] before the scale and bias.  Both steps
+// are exact (v_ldexp_f32), so the products carry the split's 2^-22 relative
+// residual for every value within 2^17 of its row's largest.
 #include "common.h"
 
 #include <algorithm>
@@ -21,9 +29,58 @@ int tzh_tile_codes_w8_launch(hipStream_t st, const int8_t *q, uint8_t *out, int6
 int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t x_dtype, const void *wc,
                             int32_t w_format, const uint16_t *scale, const float *bias, void *c, int32_t c_dtype,
                             int64_t m, int64_t k, int64_t n, int64_t n_valid, int32_t epilogue, const void *res,
-                            const float *gamma, const float *beta, float eps, float *ln_ws, int64_t ln_ws_rows);
+                            const float *gamma, const float *beta, float eps, float *ln_ws, int64_t ln_ws_rows,
+                            const int *rexp);
 
 namespace {
+
+// e[r] for the rows of a [m, k] (row pitch k): max_j |a[r, j]| * 2^e[r] lies
+// in [2^14, 2^15); 0 for a row of zeros or one whose largest magnitude is not
+// finite (inf and NaN then reach the sums as they are).  One wave per row.
+__global__ void __launch_bounds__(256) row_exp_kernel(const float *__restrict__ a, int64_t m, int64_t k,
+                                                      int *__restrict__ e) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
+    if (r >= m) return;  // whole waves: the shuffles below see every lane
+    const float *row = a + r * k;
+    float mx = 0.0f;
+    if ((k & 3) == 0 && ((uintptr_t)row & 15) == 0) {
+        for (int64_t j = 4 * lane; j < k; j += 256) {
+            const f32x4_t v = *(const f32x4_t *)(row + j);
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+        }
+    } else {
+        for (int64_t j = lane; j < k; j += 64) mx = fmaxf(mx, fabsf(row[j]));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if (lane == 0) {
+        int ex = 0;  // mx = f * 2^ex, f in [0.5, 1)
+        (void)frexpf(mx, &ex);
+        e[r] = (mx > 0.0f && isfinite(mx)) ? 15 - ex : 0;
+    }
+}
+
+}  // namespace
+
+// Row exponents of an f32 activation matrix [m, k] (row pitch k) for the
+// row-scaled GEMM (tzh_linear_codes_launch's rexp).
+int tzh_row_exp_launch(hipStream_t st, const float *a, int64_t m, int64_t k, int *e) {
+    if (m <= 0) return TZH_OK;
+    hipLaunchKernelGGL(row_exp_kernel, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, st, a, m, k, e);
+    TZH_LAUNCHED("row_exp_kernel");
+    return TZH_OK;
+}
+
+namespace {
+
+// c[i, j] = bias[j] (0 without a bias): the k == 0 product, an empty sum
+// times the scale plus the bias (matmul_w8a32.zig:40-55)
+__global__ void fill_bias_kernel(float *__restrict__ c, int64_t m, int64_t n, const float *__restrict__ bias) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m * n) return;
+    c[i] = bias ? bias[i % n] : 0.0f;
+}
 
 // rows [m, k] -> [m, k_pad] with zero columns k .. k_pad-1
 template <typename T>
@@ -66,12 +123,12 @@ int noalloc_scratch(tzh_ctx *ctx, void **out) {
 }
 
 // The workspace a linear needs: tiled codes, then (k % 64 != 0 or a
-// misaligned a) the zero-padded activation rows, then (LayerNorm epilogue)
-// the rows of a split partial round.
+// misaligned a) the zero-padded activation rows, then (f32 activations) the
+// row exponents, then (LayerNorm epilogue) the rows of a split partial round.
 struct Workspace {
-    size_t codes = 0, a = 0, ws = 0;
+    size_t codes = 0, a = 0, e = 0, ws = 0;
     int64_t ws_rows = 0;
-    size_t total() const { return codes + a + ws; }
+    size_t total() const { return codes + a + e + ws; }
 };
 
 Workspace workspace_of(const tzh_ctx *ctx, const void *a, int32_t a_dtype, int64_t m, int64_t k, int64_t n, bool ln) {
@@ -79,6 +136,7 @@ Workspace workspace_of(const tzh_ctx *ctx, const void *a, int32_t a_dtype, int64
     Workspace w;
     w.codes = round256((size_t)n_pad * (size_t)k_pad);
     if (k != k_pad || !al16(a)) w.a = round256((size_t)m * (size_t)k_pad * (a_dtype == TZH_F32 ? 4 : 2));
+    if (a_dtype == TZH_F32) w.e = round256((size_t)m * 4);
     w.ws_rows = ln ? std::min<int64_t>((m + 127) / 128, ctx->num_cus / 3 + 1) * 128 : 0;
     w.ws = (size_t)w.ws_rows * 384 * 4;
     return w;
@@ -89,14 +147,14 @@ Workspace workspace_of(const tzh_ctx *ctx, const void *a, int32_t a_dtype, int64
 int linear(tzh_ctx *ctx, const void *a, int32_t a_dtype, const int8_t *wq, const uint16_t *scale, const float *bias,
            void *c, int32_t c_dtype, int64_t m, int64_t k, int64_t n, int32_t epilogue, const void *residual,
            int32_t res_dtype, const float *gamma, const float *beta, float eps, void *scratch_ptr = nullptr) {
-    if (m < 0 || k <= 0 || n <= 0)
+    if (m < 0 || k < 0 || n < 0)
         return tzh_fail(TZH_ERR_INVALID_ARGS, "bad GEMM shape m=%lld k=%lld n=%lld", (long long)m, (long long)k,
                         (long long)n);
-    if (m == 0) return TZH_OK;  // matmul_w8a32.zig:24
+    if (m == 0 || n == 0) return TZH_OK;  // matmul_w8a32.zig:24
     if (m > (int64_t)1 << 30 || k > 65536 || n > 65536) return tzh_fail(TZH_ERR_TOO_LARGE, "GEMM shape too large");
     if ((a_dtype != TZH_F32 && a_dtype != TZH_F16) || (c_dtype != TZH_F32 && c_dtype != TZH_F16))
         return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "activations and output must be F32 or F16");
-    if (!a || !wq || !scale || !c) return tzh_fail(TZH_ERR_INVALID_ARGS, "null operand");
+    if (!c || (k > 0 && (!a || !wq || !scale))) return tzh_fail(TZH_ERR_INVALID_ARGS, "null operand");
     const bool ln = epilogue == TZH_EPI_BIAS_RES_LN;
     if (epilogue != TZH_EPI_BIAS && epilogue != TZH_EPI_BIAS_GELU && !ln)
         return tzh_fail(TZH_ERR_INVALID_ARGS, "unknown epilogue %d", epilogue);
@@ -105,6 +163,18 @@ int linear(tzh_ctx *ctx, const void *a, int32_t a_dtype, const int8_t *wq, const
         if (!residual || !gamma || !beta) return tzh_fail(TZH_ERR_INVALID_ARGS, "null residual/gamma/beta");
         if (res_dtype != c_dtype) return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "residual dtype must equal output dtype");
         if (!al16(residual)) return tzh_fail(TZH_ERR_INVALID_ARGS, "residual must be 16-byte aligned");
+    }
+    if (k == 0) {
+        // an empty sum: c = 0 * s + bias (matmul_w8a32.zig:40-55), the plain
+        // bias epilogue of the reference's signature only
+        if (epilogue != TZH_EPI_BIAS || c_dtype != TZH_F32)
+            return tzh_fail(TZH_ERR_INVALID_ARGS, "k == 0 is supported for the f32 bias epilogue only");
+        if ((uintptr_t)c & 3) return tzh_fail(TZH_ERR_INVALID_ARGS, "c is not aligned to its element");
+        const int64_t cnt = m * n;
+        hipLaunchKernelGGL(fill_bias_kernel, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, ctx->stream,
+                           (float *)c, m, n, bias);
+        TZH_LAUNCHED("fill_bias_kernel");
+        return TZH_OK;
     }
     const int64_t n_pad = (n + 383) / 384 * 384, k_pad = (k + 63) / 64 * 64;
     // f16 output is stored through whole-row tiles: every column must exist
@@ -120,6 +190,8 @@ int linear(tzh_ctx *ctx, const void *a, int32_t a_dtype, const int8_t *wq, const
     void *scratch = scratch_ptr;
     if (!scratch) TZH_TRY(tzh_ctx_scratch(ctx, wsz.total(), &scratch));
     uint8_t *codes = (uint8_t *)scratch;
+    int *rexp = wsz.e ? (int *)((char *)scratch + codes_bytes + a_bytes) : nullptr;
+    if (rexp) TZH_TRY(tzh_row_exp_launch(ctx->stream, (const float *)a, m, k, rexp));
     TZH_TRY(tzh_tile_codes_w8_launch(ctx->stream, wq, codes, n, k, n_pad, k_pad));
     const void *x = a;
     if (pad_a) {
@@ -135,9 +207,9 @@ int linear(tzh_ctx *ctx, const void *a, int32_t a_dtype, const int8_t *wq, const
         TZH_LAUNCHED("pad_cols_kernel");
         x = xp;
     }
-    float *ws = ws_rows ? (float *)((char *)scratch + codes_bytes + a_bytes) : nullptr;
+    float *ws = ws_rows ? (float *)((char *)scratch + codes_bytes + a_bytes + wsz.e) : nullptr;
     return tzh_linear_codes_launch(ctx->stream, ctx->num_cus, x, a_dtype, codes, TZH_WF_W8T, scale, bias, c, c_dtype,
-                                   m, k_pad, n_pad, n, epilogue, residual, gamma, beta, eps, ws, ws_rows);
+                                   m, k_pad, n_pad, n, epilogue, residual, gamma, beta, eps, ws, ws_rows, rexp);
 }
 
 }  // namespace
@@ -164,15 +236,17 @@ extern "C" int tzh_matmul_w8a32_noalloc(tzh_ctx *ctx, const float *a, const int8
                                         const float *bias, float *c, int64_t m, int64_t k, int64_t n) {
     tzh_clear_error();
     TZH_TRY(tzh_ctx_enter(ctx));
-    if (m < 0 || k <= 0 || n <= 0 || m > (int64_t)1 << 30 || k > 65536 || n > 65536)
+    // the shape errors, empty products and k == 0 of tzh_matmul_w8a32 (none
+    // of which uses the workspace)
+    if (m <= 0 || k <= 0 || n <= 0 || m > (int64_t)1 << 30 || k > 65536 || n > 65536)
         return linear(ctx, a, TZH_F32, wq, scale, bias, c, TZH_F32, m, k, n, TZH_EPI_BIAS, nullptr, TZH_F32, nullptr,
-                      nullptr, 0.0f);  // the same shape errors as tzh_matmul_w8a32
+                      nullptr, 0.0f);
     const size_t need = workspace_of(ctx, a, TZH_F32, m, k, n, false).total();
     if (need > kNoAllocScratchBytes)
         return tzh_fail(TZH_ERR_TOO_LARGE,
                         "tzh_matmul_w8a32_noalloc needs %zu bytes of workspace for m=%lld k=%lld n=%lld; its static "
-                        "workspace holds %zu (the tiled codes, n_pad * k_pad bytes, plus m * k_pad * 4 when k %% 64 "
-                        "!= 0 or a is not 16-byte aligned)",
+                        "workspace holds %zu (the tiled codes, n_pad * k_pad bytes, the row exponents, m * 4 bytes, "
+                        "plus m * k_pad * 4 when k %% 64 != 0 or a is not 16-byte aligned)",
                         need, (long long)m, (long long)k, (long long)n, kNoAllocScratchBytes);
     void *ws = nullptr;
     TZH_TRY(noalloc_scratch(ctx, &ws));

@@ -302,11 +302,18 @@ __device__ __forceinline__ void store4<float>(float *p, float a, float b, float 
 // pre-normalisation rows of a split LayerNorm tile (see launch_ln).
 enum { EPI_BIAS = 0, EPI_GELU = 1, EPI_LN = 2, EPI_RES = 3 };
 
-template <int EPI, typename TC, typename P, typename TR = TC, typename TX = _Float16>
+// RS (f32 activations only): row t of X enters the split as X[t,:] * 2^e[t]
+// with e = rexp[t] (row_exp_kernel: the row's largest magnitude lands in
+// [2^14, 2^15)), exact, and the epilogue takes the sums times 2^-e[t],
+// exact too; so the hi/lo split keeps its 2^-22 relative residual for every
+// value within 2^17 of its row's largest, whatever the row's scale, and no
+// finite row overflows the f16 halves.
+template <int EPI, typename TC, typename P, typename TR = TC, typename TX = _Float16, bool RS = false>
 __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     const TX *__restrict__ X, const void *__restrict__ Wc, const uint16_t *__restrict__ scale,
     const float *__restrict__ bias, TC *__restrict__ C, int M, int K, int N, const TR *__restrict__ R,
-    const float *__restrict__ gamma, const float *__restrict__ beta, float eps, int ldc, int n_valid) {
+    const float *__restrict__ gamma, const float *__restrict__ beta, float eps, int ldc, int n_valid,
+    const int *__restrict__ rexp) {
     using FX = typename P::FX;
     using FW = typename P::FW;
     constexpr int BM = P::BM, BN = P::BN, BK = P::BK, NS = P::NS, TMF = P::TMF, TNF = P::TNF;
@@ -315,6 +322,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     constexpr int XE = (int)sizeof(TX);
     constexpr bool XF32 = XE == 4;
     static_assert(XE == P::XE, "configuration built for another activation type");
+    static_assert(!RS || XF32, "row scaling is for f32 activations");
     constexpr bool LN = EPI == EPI_LN;
     static_assert(!LN || P::WN * TNF * 32 == BN, "LayerNorm tiles cover whole rows");
     constexpr int NPAR = LN ? 4 : 2;                        // per-column parameters kept in LDS
@@ -326,6 +334,9 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     __shared__ __attribute__((aligned(16))) char st3[NS > 3 ? P::STAGE : 16];
     __shared__ __attribute__((aligned(16))) float par[NPAR][MAXN];
     __shared__ float stat0[LN ? BM * P::WN : 1], stat1[LN ? BM * P::WN : 1];
+    // RS: the row exponents of the two most recent units (unit parity),
+    // written by the split of a unit's first stage, read by its epilogue
+    __shared__ int rx[RS ? 2 * BM : 1];
     // f16 output goes through LDS, except from the f32-activation LayerNorm
     // kernel, which has no registers to spare for the staging
     constexpr bool STAGED = std::is_same<TC, _Float16>::value && !(XF32 && LN);
@@ -465,7 +476,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     // Each 32-byte group of 8 consecutive k of a row, logical chunks 2p and
     // 2p+1, becomes hi in chunk 2p and lo in chunk 2p+1; eight lanes take
     // the eight groups of one row.
-    auto split_own = [&](char *buf) __attribute__((always_inline)) {
+    auto split_own = [&](char *buf, int t) __attribute__((always_inline)) {
         if constexpr (XF32) {
             constexpr int GPR = BK / 8, ROWS_W = P::LX * FX::RPI;
             static_assert((ROWS_W * GPR) % 64 == 0, "whole groups per lane");
@@ -473,13 +484,41 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
             // kept in registers across the whole kernel
             int ln = lane;
             asm volatile("" : "+v"(ln));
+            // RS: the split rows' exponents come from rexp at the split of a
+            // unit's first stage (no ring loads are in flight then: the
+            // compute step that follows issues the next ones), which also
+            // leaves them in rx for the unit's later splits and its epilogue
+            // (the eight lanes of a row are in one wave)
+            int ex[RS ? ROWS_W * GPR / 64 : 1] = {};
+            if constexpr (RS) {
+                const int u = t / KT;
+                if (t % KT == 0) {
+                    const int m0 = unit_m0(u);
+#pragma unroll
+                    for (int c = 0; c < ROWS_W * GPR / 64; c++) {
+                        const int g = c * 64 + ln, r = wu * ROWS_W + g / GPR;
+                        ex[c] = rexp[m0 + r < M ? m0 + r : M - 1];
+                        if (g % GPR == 0) rx[(u & 1) * BM + r] = ex[c];
+                    }
+                } else {
+#pragma unroll
+                    for (int c = 0; c < ROWS_W * GPR / 64; c++)
+                        ex[c] = rx[(u & 1) * BM + wu * ROWS_W + (c * 64 + ln) / GPR];
+                }
+            }
 #pragma unroll
             for (int c = 0; c < ROWS_W * GPR / 64; c++) {
                 const int g = c * 64 + ln, r = wu * ROWS_W + g / GPR, p = g % GPR;
                 char *row = buf + r * XROWB;
                 f32x4_t *c0 = (f32x4_t *)(row + (((2 * p) ^ FX::swz(r)) << 4));
                 f32x4_t *c1 = (f32x4_t *)(row + (((2 * p + 1) ^ FX::swz(r)) << 4));
-                const f32x4_t x0 = *c0, x1 = *c1;
+                f32x4_t x0 = *c0, x1 = *c1;
+                if constexpr (RS)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        x0[q] = __builtin_amdgcn_ldexpf(x0[q], ex[c]);
+                        x1[q] = __builtin_amdgcn_ldexpf(x1[q], ex[c]);
+                    }
                 half8_t hi, lo;
                 split_f32x8(x0, x1, hi, lo);
                 *(half8_t *)c0 = hi;
@@ -544,9 +583,20 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     auto epilogue = [&](int i) __attribute__((always_inline)) {
         const int m0 = unit_m0(i), n0 = unit_n0(i);
         const bool st32 = STAGED32 && cvec && n0 + BN <= n_valid;  // uniform
+        // RS: the sums of token fragment b times 2^-e of its row
+        auto unscale = [&](int b) __attribute__((always_inline)) {
+            if constexpr (RS) {
+                const int e = -rx[(i & 1) * BM + wm * TMF * 32 + b * 32 + l31];
+#pragma unroll
+                for (int a = 0; a < TNF; a++)
+#pragma unroll
+                    for (int q = 0; q < 16; q++) acc[a][b][q] = __builtin_amdgcn_ldexpf(acc[a][b][q], e);
+            }
+        };
         if constexpr (!LN) {
 #pragma unroll
             for (int b = 0; b < TMF; b++) {
+                unscale(b);
                 const int t = m0 + wm * TMF * 32 + b * 32 + l31;
 #pragma unroll
                 for (int a = 0; a < TNF; a++)
@@ -612,6 +662,8 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                 // the live registers stay within budget (no scratch spills)
                 int t = m0 + wm * TMF * 32 + b * 32 + l31;
                 t = t < M ? t : M - 1;
+                // RS: the sums times 2^-e of the fragment's row
+                const int ne = RS ? -rx[(i & 1) * BM + wm * TMF * 32 + b * 32 + l31] : 0;
                 float sum = 0.0f;
 #pragma unroll
                 for (int a = 0; a < TNF; a++) {
@@ -629,7 +681,9 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 #pragma unroll
                         for (int q = 0; q < 4; q++) {
                             // input + (sum * s + bias)  (arctic.zig:720)
-                            const float v = (float)res[g][q] + (acc[a][b][4 * g + q] * s[q] + bb[q]);
+                            const float acc_v = RS ? __builtin_amdgcn_ldexpf(acc[a][b][4 * g + q], ne)
+                                                   : acc[a][b][4 * g + q];
+                            const float v = (float)res[g][q] + (acc_v * s[q] + bb[q]);
                             acc[a][b][4 * g + q] = v;
                             sum += v;
                         }
@@ -739,7 +793,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     if constexpr (XF32) {
         wait_own(0);
         wave_lds_order();
-        split_own(bufs[0]);
+        split_own(bufs[0], 0);
     }
     auto step = [&](auto jc, int s) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
@@ -758,7 +812,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
             if (s + 1 < S) {
                 wait_own(s + 1);
                 wave_lds_order();  // the lanes read slots their neighbours' loads wrote
-                split_own(bufs[(j + 1) % NS]);
+                split_own(bufs[(j + 1) % NS], s + 1);
             }
         if (kt == KT - 1) {
             const int i = s / KT;
@@ -779,13 +833,11 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 
 // Tile shapes (tokens x output columns x k per stage, waves, stages), chosen
 // by measurement on MI355X at the Arctic shapes (T = 67590 tokens), per
-// weight format and activation type:
-//   TZH_WF_F16: f16 codes, row-major [n, k] (any n multiple of 128; the f32
-//     model's power-of-two-scaled codes need it);
-//   TZH_WF_W8T: biased int8 codes u = q + 128, stage-tiled in 384-row
-//     blocks (tile_codes_w8_kernel; n a multiple of 384).  Half the weight
-//     bytes and one contiguous span per stage let a third stage fit in LDS:
-//     QKV 78 -> 73, FFN1 118 -> 114, FFN2 + LN 106 -> 98 us at T = 65536.
+// activation type, for the weight format TZH_WF_W8T: biased int8 codes u =
+// q + 128, stage-tiled in 384-row blocks (tile_codes_w8_kernel; n a
+// multiple of 384).  Against f16 codes in row-major [n, k], half the weight
+// bytes and one contiguous span per stage let a third stage fit in LDS:
+// QKV 78 -> 73, FFN1 118 -> 114, FFN2 + LN 106 -> 98 us at T = 65536.
 // 128 x 384 tiles halve the L2 -> LDS operand traffic of 128 x 128 ones.
 // The pieces cut a partial last round of a LayerNorm GEMM (12, 6 or 3 per
 // 128 x 384 tile; see launch_ln).  f32 activations double the X tile, so
@@ -793,16 +845,6 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
 constexpr int kWtBlock = 384;  // rows per stage-tiled weight block
 template <int WF, int XE>
 struct Cfgs;
-template <>
-struct Cfgs<TZH_WF_F16, 2> {
-    using Bias = PipeCfg<128, 384, 64, 2, 4, 2>;       // n a multiple of 384
-    using Narrow = PipeCfg<128, 128, 64, 2, 2, 4>;     // other multiples of 128
-    using Ln = PipeCfg<128, 384, 64, 2, 4, 2>;
-    using LnShortK = void;
-    using Piece64 = PipeCfg<64, 64, 64, 2, 2, 4>;
-    using Piece128x64 = PipeCfg<128, 64, 64, 2, 2, 4>;
-    using Piece128 = Narrow;
-};
 template <>
 struct Cfgs<TZH_WF_W8T, 2> {
     using Bias = PipeCfg<128, 384, 64, 2, 4, 3, true, kWtBlock>;
@@ -836,9 +878,8 @@ struct Cfgs<TZH_WF_W8T, 4> {
     using Piece128x64 = PipeCfg<128, 64, 64, 2, 2, 2, true, kWtBlock, 4>;
     using Piece128 = PipeCfg<128, 128, 64, 2, 2, 2, true, kWtBlock, 4>;
 };
-using LnCfg = Cfgs<TZH_WF_F16, 2>::Ln;
-static_assert(Cfgs<TZH_WF_W8T, 2>::Ln::WN == LnCfg::WN && Cfgs<TZH_WF_W8T, 2>::Ln::TNF == LnCfg::TNF &&
-                  Cfgs<TZH_WF_W8T, 2>::Ln::BN == LnCfg::BN && Cfgs<TZH_WF_W8T, 2>::LnShortK::WN == LnCfg::WN &&
+using LnCfg = Cfgs<TZH_WF_W8T, 2>::Ln;
+static_assert(Cfgs<TZH_WF_W8T, 2>::LnShortK::WN == LnCfg::WN &&
                   Cfgs<TZH_WF_W8T, 2>::LnShortK::TNF == LnCfg::TNF && Cfgs<TZH_WF_W8T, 4>::Ln::WN == LnCfg::WN &&
                   Cfgs<TZH_WF_W8T, 4>::Ln::TNF == LnCfg::TNF && Cfgs<TZH_WF_W8T, 4>::Ln::BN == LnCfg::BN,
               "one LayerNorm epilogue layout (statistics order) for every configuration and ln_rows_kernel");
@@ -857,7 +898,7 @@ struct NoDeduce {
 template <int EPI, typename TC, typename P, typename TR = TC, typename TX>
 int launch(hipStream_t st, int num_cus, const TX *x, const void *wc, const uint16_t *scale, const float *bias, TC *c,
            int M, int K, int N, const typename NoDeduce<TR>::type *res, const float *gamma, const float *beta,
-           float eps, int ldc, int n_valid) {
+           float eps, int ldc, int n_valid, const int *rexp) {
     const int nbm = (M + P::BM - 1) / P::BM;
     const int nbn = N / P::BN;
     constexpr bool f32_out = std::is_same<TC, float>::value && EPI != EPI_RES && EPI != EPI_LN;
@@ -867,8 +908,17 @@ int launch(hipStream_t st, int num_cus, const TX *x, const void *wc, const uint1
     // (blocks without a unit return at once); beyond that, one per slot.
     const int64_t spread = (int64_t)kXcds * ((nbm + kXcds - 1) / kXcds) * nbn;
     const int grid = spread < slots ? (int)spread : slots;
-    hipLaunchKernelGGL((linear_pipe_kernel<EPI, TC, P, TR, TX>), dim3(grid), dim3(P::THREADS), 0, st, x, wc, scale,
-                       bias, c, M, K, N, res, gamma, beta, eps, ldc, n_valid);
+    if constexpr (sizeof(TX) == 4) {
+        if (rexp) {
+            hipLaunchKernelGGL((linear_pipe_kernel<EPI, TC, P, TR, TX, true>), dim3(grid), dim3(P::THREADS), 0, st, x,
+                               wc, scale, bias, c, M, K, N, res, gamma, beta, eps, ldc, n_valid, rexp);
+            TZH_LAUNCHED("linear_pipe_kernel");
+            return TZH_OK;
+        }
+    }
+    if (rexp) return tzh_fail(TZH_ERR_INVALID_ARGS, "row scaling needs f32 activations");
+    hipLaunchKernelGGL((linear_pipe_kernel<EPI, TC, P, TR, TX, false>), dim3(grid), dim3(P::THREADS), 0, st, x, wc,
+                       scale, bias, c, M, K, N, res, gamma, beta, eps, ldc, n_valid, nullptr);
     TZH_LAUNCHED("linear_pipe_kernel");
     return TZH_OK;
 }
@@ -953,15 +1003,14 @@ __global__ void __launch_bounds__(256) ln_rows_kernel(const float *__restrict__ 
 template <int WF, typename TC, typename TX>
 int launch_ln(hipStream_t st, int num_cus, const TX *x, const void *wc, const uint16_t *scale, const float *bias,
               TC *c, int M, int K, const TC *res, const float *gamma, const float *beta, float eps, float *ws,
-              int64_t ws_rows) {
+              int64_t ws_rows, const int *rexp) {
     using C = Cfgs<WF, (int)sizeof(TX)>;
     constexpr int N = C::Ln::BN, BM = C::Ln::BM;
     constexpr bool f32_out = false;  // LayerNorm outputs are not staged when f32
     constexpr bool staged = std::is_same<TC, _Float16>::value && sizeof(TX) == 2;  // as the kernel decides
-    if constexpr (!std::is_void<typename C::LnShortK>::value)
-        if (K <= 384)
-            return launch<EPI_LN, TC, typename C::LnShortK>(st, num_cus, x, wc, scale, bias, c, M, K, N, res, gamma,
-                                                            beta, eps, N, N);
+    if (K <= 384)
+        return launch<EPI_LN, TC, typename C::LnShortK>(st, num_cus, x, wc, scale, bias, c, M, K, N, res, gamma, beta,
+                                                        eps, N, N, rexp);
     const int slots = num_cus * C::Ln::blocks_per_cu(true, staged, f32_out);
     const int panels = (M + BM - 1) / BM;
     const int full = panels / slots * slots;
@@ -977,19 +1026,20 @@ int launch_ln(hipStream_t st, int num_cus, const TX *x, const void *wc, const ui
     const int m_main = per ? full * BM : M;
     if (m_main > 0)
         TZH_TRY((launch<EPI_LN, TC, typename C::Ln>(st, num_cus, x, wc, scale, bias, c, m_main, K, N, res, gamma, beta,
-                                                     eps, N, N)));
+                                                     eps, N, N, rexp)));
     if (!per) return TZH_OK;
     const TX *xt = x + (size_t)m_main * K;
     const TC *rt = res + (size_t)m_main * N;
+    const int *et = rexp ? rexp + m_main : nullptr;
     if (per == 12)
         TZH_TRY((launch<EPI_RES, float, typename C::Piece64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N,
-                                                                  rt, nullptr, nullptr, 0.f, N, N)));
+                                                                  rt, nullptr, nullptr, 0.f, N, N, et)));
     else if (per == 6)
         TZH_TRY((launch<EPI_RES, float, typename C::Piece128x64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K,
-                                                                      N, rt, nullptr, nullptr, 0.f, N, N)));
+                                                                      N, rt, nullptr, nullptr, 0.f, N, N, et)));
     else
         TZH_TRY((launch<EPI_RES, float, typename C::Piece128, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N,
-                                                                   rt, nullptr, nullptr, 0.f, N, N)));
+                                                                   rt, nullptr, nullptr, 0.f, N, N, et)));
     hipLaunchKernelGGL(ln_rows_kernel<TC>, dim3((unsigned)((tail_rows + 31) / 32)), dim3(256), 0, st, ws, tail_rows,
                        gamma, beta, eps, c + (size_t)m_main * N);
     TZH_LAUNCHED("ln_rows_kernel");
@@ -998,13 +1048,13 @@ int launch_ln(hipStream_t st, int num_cus, const TX *x, const void *wc, const ui
 
 template <int WF, int EPI, typename TC, typename TX>
 int launch_bias(hipStream_t st, int num_cus, const TX *x, const void *wc, const uint16_t *scale, const float *bias,
-                TC *c, int M, int K, int N, int ldc, int n_valid) {
+                TC *c, int M, int K, int N, int ldc, int n_valid, const int *rexp) {
     using C = Cfgs<WF, (int)sizeof(TX)>;
     if (N % C::Bias::BN == 0)
         return launch<EPI, TC, typename C::Bias>(st, num_cus, x, wc, scale, bias, c, M, K, N, nullptr, nullptr,
-                                                 nullptr, 0.f, ldc, n_valid);
+                                                 nullptr, 0.f, ldc, n_valid, rexp);
     return launch<EPI, TC, typename C::Narrow>(st, num_cus, x, wc, scale, bias, c, M, K, N, nullptr, nullptr, nullptr,
-                                               0.f, ldc, n_valid);
+                                               0.f, ldc, n_valid, rexp);
 }
 
 // int8 codes q[r][j] (n rows of k) -> biased codes u = q + 128 stage-tiled
@@ -1037,44 +1087,9 @@ __global__ void tile_codes_w8_kernel(const int8_t *__restrict__ q, uint8_t *__re
     *(u32x4_t *)(out + o) = *(const u32x4_t *)v;
 }
 
-// f32 rows [m, k] -> [m, k_pad] with zero columns k .. k_pad-1 (an
-// activation operand whose k is not a multiple of the stage depth).
-__global__ void pad_cols_f32_kernel(const float *__restrict__ x, float *__restrict__ y, int64_t m, int k, int k_pad) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= m * k_pad) return;
-    const int64_t r = i / k_pad;
-    const int j = (int)(i % k_pad);
-    y[i] = j < k ? x[r * k + j] : 0.0f;
-}
-
-__global__ void widen_codes_kernel(const int8_t *__restrict__ q, _Float16 *__restrict__ out, int64_t n) {
-    const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
-    if (i + 8 <= n) {
-        const uint2 v = *(const uint2 *)(q + i);
-        half8_t h;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            h[j] = (_Float16)(float)(int8_t)(v.x >> (8 * j));
-            h[4 + j] = (_Float16)(float)(int8_t)(v.y >> (8 * j));
-        }
-        *(half8_t *)(out + i) = h;
-    } else {
-        for (int64_t j = i; j < n; j++) out[j] = (_Float16)(float)q[j];
-    }
-}
-
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
-
-// int8 codes -> f16 codes (exact), n elements.
-int tzh_widen_codes_launch(hipStream_t st, const int8_t *q, _Float16 *out, int64_t n) {
-    if (n <= 0) return TZH_OK;
-    const int64_t threads = (n + 7) / 8;
-    hipLaunchKernelGGL(widen_codes_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, q, out, n);
-    TZH_LAUNCHED("widen_codes_kernel");
-    return TZH_OK;
-}
 
 // int8 codes [n, k] -> the TZH_WF_W8T layout of the padded shape n_pad x
 // k_pad (multiples of 384 and 64, at least n and k).
@@ -1089,27 +1104,20 @@ int tzh_tile_codes_w8_launch(hipStream_t st, const int8_t *q, uint8_t *out, int6
     return TZH_OK;
 }
 
-int tzh_pad_cols_f32_launch(hipStream_t st, const float *x, float *y, int64_t m, int64_t k, int64_t k_pad) {
-    if (m <= 0) return TZH_OK;
-    const int64_t n = m * k_pad;
-    hipLaunchKernelGGL(pad_cols_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, y, m, (int)k,
-                       (int)k_pad);
-    TZH_LAUNCHED("pad_cols_f32_kernel");
-    return TZH_OK;
-}
-
-// Activations x (f16: f16 or f32) x weight codes in format w_format
-// (TZH_WF_F16: f16 row-major, f16 activations only; TZH_WF_W8T: tiled
-// biased int8), output and residual both F16 or both F32.  The weight codes
-// may be padded: n is the padded column count the code layout holds and
-// n_valid <= n the columns that exist (scale and bias have n_valid entries;
-// C rows are n_valid apart); the bias epilogues run n in chunks of up to
-// 1536 columns.  ln_ws (f32, ln_ws_rows rows of 384; may be null) lets the
-// LayerNorm epilogue split a partial last round of tiles (see launch_ln).
+// Activations x (f16 or f32) x weight codes in format w_format (TZH_WF_W8T:
+// tiled biased int8), output and residual both F16 or both F32.  The weight
+// codes may be padded: n is the padded column count the code layout holds
+// and n_valid <= n the columns that exist (scale and bias have n_valid
+// entries; C rows are n_valid apart); the bias epilogues run n in chunks of
+// up to 1536 columns.  ln_ws (f32, ln_ws_rows rows of 384; may be null) lets
+// the LayerNorm epilogue split a partial last round of tiles (see
+// launch_ln).  rexp (f32 activations; may be null): the row exponents of
+// row_exp_kernel, which scale each row into the split's range.
 int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t x_dtype, const void *wc,
                             int32_t w_format, const uint16_t *scale, const float *bias, void *c, int32_t c_dtype,
                             int64_t m, int64_t k, int64_t n, int64_t n_valid, int32_t epilogue, const void *res,
-                            const float *gamma, const float *beta, float eps, float *ln_ws, int64_t ln_ws_rows) {
+                            const float *gamma, const float *beta, float eps, float *ln_ws, int64_t ln_ws_rows,
+                            const int *rexp) {
     if (m < 0 || k <= 0 || n <= 0 || n_valid <= 0 || n_valid > n) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad GEMM shape");
     if (m == 0) return TZH_OK;  // matmul_w8a32.zig:24
     if (m > (int64_t)1 << 30 || k > 65536 || n > 65536) return tzh_fail(TZH_ERR_TOO_LARGE, "GEMM shape too large");
@@ -1123,51 +1131,31 @@ int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t 
         return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "activations must be F16 or F32");
     const int M = (int)m, K = (int)k, N = (int)n, NV = (int)n_valid;
     const bool c16 = c_dtype == TZH_F16, x32 = x_dtype == TZH_F32;
-    if (w_format != TZH_WF_F16 && w_format != TZH_WF_W8T)
-        return tzh_fail(TZH_ERR_INVALID_ARGS, "unknown weight format %d", w_format);
-    const bool w8t = w_format == TZH_WF_W8T;
-    if (w8t && N % kWtBlock) return tzh_fail(TZH_ERR_INVALID_ARGS, "tiled int8 weights need n %% 384 == 0 (n=%d)", N);
-    if (x32 && !w8t) return tzh_fail(TZH_ERR_INVALID_ARGS, "f32 activations need the tiled int8 weight format");
+    if (w_format != TZH_WF_W8T) return tzh_fail(TZH_ERR_INVALID_ARGS, "unknown weight format %d", w_format);
+    if (N % kWtBlock) return tzh_fail(TZH_ERR_INVALID_ARGS, "tiled int8 weights need n %% 384 == 0 (n=%d)", N);
     if (c16 && NV != N) return tzh_fail(TZH_ERR_INVALID_ARGS, "f16 output needs every column (n_valid == n)");
+    if (rexp && !x32) return tzh_fail(TZH_ERR_INVALID_ARGS, "row scaling needs f32 activations");
+    // one call per (activation type, output type): f(x, c) with typed pointers
+    auto typed = [&](auto &&f) -> int {
+        if (x32)
+            return c16 ? f((const float *)x, (_Float16 *)c) : f((const float *)x, (float *)c);
+        return c16 ? f((const _Float16 *)x, (_Float16 *)c) : f((const _Float16 *)x, (float *)c);
+    };
     if (epilogue == TZH_EPI_BIAS || epilogue == TZH_EPI_BIAS_GELU) {
-        if (N % 128) return tzh_fail(TZH_ERR_INVALID_ARGS, "n=%d must be a multiple of 128", N);
         const bool gelu = epilogue == TZH_EPI_BIAS_GELU;
         // column chunks of up to 1536 (the parameters of a chunk sit in LDS)
         for (int j0 = 0; j0 < NV; j0 += 1536) {
             const int nc = N - j0 < 1536 ? N - j0 : 1536, nv = NV - j0 < nc ? NV - j0 : nc;
-            const char *wj = (const char *)wc + (w8t ? (size_t)(j0 / kWtBlock) * K * kWtBlock : (size_t)j0 * K * 2);
+            const char *wj = (const char *)wc + (size_t)(j0 / kWtBlock) * K * kWtBlock;
             const uint16_t *sj = scale + j0;
             const float *bj = bias ? bias + j0 : nullptr;
-            int rc;
-            if (w8t && x32) {
-                rc = c16 ? (gelu ? launch_bias<TZH_WF_W8T, EPI_GELU, _Float16>(st, num_cus, (const float *)x, wj, sj, bj,
-                                                                              (_Float16 *)c + j0, M, K, nc, NV, nv)
-                                 : launch_bias<TZH_WF_W8T, EPI_BIAS, _Float16>(st, num_cus, (const float *)x, wj, sj, bj,
-                                                                              (_Float16 *)c + j0, M, K, nc, NV, nv))
-                         : (gelu ? launch_bias<TZH_WF_W8T, EPI_GELU, float>(st, num_cus, (const float *)x, wj, sj, bj,
-                                                                           (float *)c + j0, M, K, nc, NV, nv)
-                                 : launch_bias<TZH_WF_W8T, EPI_BIAS, float>(st, num_cus, (const float *)x, wj, sj, bj,
-                                                                           (float *)c + j0, M, K, nc, NV, nv));
-            } else if (w8t) {
-                rc = c16 ? (gelu ? launch_bias<TZH_WF_W8T, EPI_GELU, _Float16>(st, num_cus, (const _Float16 *)x, wj, sj,
-                                                                              bj, (_Float16 *)c + j0, M, K, nc, NV, nv)
-                                 : launch_bias<TZH_WF_W8T, EPI_BIAS, _Float16>(st, num_cus, (const _Float16 *)x, wj, sj,
-                                                                              bj, (_Float16 *)c + j0, M, K, nc, NV, nv))
-                         : (gelu ? launch_bias<TZH_WF_W8T, EPI_GELU, float>(st, num_cus, (const _Float16 *)x, wj, sj,
-                                                                           bj, (float *)c + j0, M, K, nc, NV, nv)
-                                 : launch_bias<TZH_WF_W8T, EPI_BIAS, float>(st, num_cus, (const _Float16 *)x, wj, sj,
-                                                                           bj, (float *)c + j0, M, K, nc, NV, nv));
-            } else {
-                rc = c16 ? (gelu ? launch_bias<TZH_WF_F16, EPI_GELU, _Float16>(st, num_cus, (const _Float16 *)x, wj, sj,
-                                                                              bj, (_Float16 *)c + j0, M, K, nc, NV, nv)
-                                 : launch_bias<TZH_WF_F16, EPI_BIAS, _Float16>(st, num_cus, (const _Float16 *)x, wj, sj,
-                                                                              bj, (_Float16 *)c + j0, M, K, nc, NV, nv))
-                         : (gelu ? launch_bias<TZH_WF_F16, EPI_GELU, float>(st, num_cus, (const _Float16 *)x, wj, sj,
-                                                                           bj, (float *)c + j0, M, K, nc, NV, nv)
-                                 : launch_bias<TZH_WF_F16, EPI_BIAS, float>(st, num_cus, (const _Float16 *)x, wj, sj,
-                                                                           bj, (float *)c + j0, M, K, nc, NV, nv));
-            }
-            TZH_TRY(rc);
+            TZH_TRY(typed([&](auto xt, auto ct) {
+                using TC = std::remove_pointer_t<decltype(ct)>;
+                return gelu ? launch_bias<TZH_WF_W8T, EPI_GELU, TC>(st, num_cus, xt, wj, sj, bj, ct + j0, M, K, nc, NV,
+                                                                    nv, rexp)
+                            : launch_bias<TZH_WF_W8T, EPI_BIAS, TC>(st, num_cus, xt, wj, sj, bj, ct + j0, M, K, nc, NV,
+                                                                    nv, rexp);
+            }));
         }
         return TZH_OK;
     }
@@ -1176,22 +1164,11 @@ int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t 
             return tzh_fail(TZH_ERR_INVALID_ARGS, "LayerNorm epilogue needs n == 384 (got %d)", NV);
         if (!res || !gamma || !beta) return tzh_fail(TZH_ERR_INVALID_ARGS, "null residual/gamma/beta");
         if (ln_ws && !aligned16(ln_ws)) return tzh_fail(TZH_ERR_INVALID_ARGS, "LayerNorm workspace must be 16-byte aligned");
-        if (w8t && x32)
-            return c16 ? launch_ln<TZH_WF_W8T, _Float16>(st, num_cus, (const float *)x, wc, scale, bias, (_Float16 *)c,
-                                                         M, K, (const _Float16 *)res, gamma, beta, eps, ln_ws,
-                                                         ln_ws_rows)
-                       : launch_ln<TZH_WF_W8T, float>(st, num_cus, (const float *)x, wc, scale, bias, (float *)c, M, K,
-                                                      (const float *)res, gamma, beta, eps, ln_ws, ln_ws_rows);
-        if (w8t)
-            return c16 ? launch_ln<TZH_WF_W8T, _Float16>(st, num_cus, (const _Float16 *)x, wc, scale, bias,
-                                                         (_Float16 *)c, M, K, (const _Float16 *)res, gamma, beta, eps,
-                                                         ln_ws, ln_ws_rows)
-                       : launch_ln<TZH_WF_W8T, float>(st, num_cus, (const _Float16 *)x, wc, scale, bias, (float *)c, M,
-                                                      K, (const float *)res, gamma, beta, eps, ln_ws, ln_ws_rows);
-        return c16 ? launch_ln<TZH_WF_F16, _Float16>(st, num_cus, (const _Float16 *)x, wc, scale, bias, (_Float16 *)c,
-                                                     M, K, (const _Float16 *)res, gamma, beta, eps, ln_ws, ln_ws_rows)
-                   : launch_ln<TZH_WF_F16, float>(st, num_cus, (const _Float16 *)x, wc, scale, bias, (float *)c, M, K,
-                                                  (const float *)res, gamma, beta, eps, ln_ws, ln_ws_rows);
+        return typed([&](auto xt, auto ct) {
+            using TC = std::remove_pointer_t<decltype(ct)>;
+            return launch_ln<TZH_WF_W8T, TC>(st, num_cus, xt, wc, scale, bias, ct, M, K, (const TC *)res, gamma, beta,
+                                             eps, ln_ws, ln_ws_rows, rexp);
+        });
     }
     return tzh_fail(TZH_ERR_INVALID_ARGS, "unknown epilogue %d", epilogue);
 }

@@ -43,8 +43,17 @@ int tzh_ctx_scratch(tzh_ctx *ctx, size_t bytes, void **out) {
             return tzh_fail(TZH_ERR_OUT_OF_MEMORY, "scratch allocation of %zu bytes failed", want);
         }
         ctx->scratch_bytes = want;
+        ctx->scratch_allocs++;
     }
     *out = ctx->scratch;
+    return TZH_OK;
+}
+
+extern "C" int tzh_ctx_scratch_info(tzh_ctx *ctx, int64_t *bytes, int64_t *allocs) {
+    tzh_clear_error();
+    if (!ctx || !bytes || !allocs) return tzh_fail(TZH_ERR_INVALID_ARGS, "null argument");
+    *bytes = (int64_t)ctx->scratch_bytes;
+    *allocs = ctx->scratch_allocs;
     return TZH_OK;
 }
 

@@ -3,6 +3,9 @@
 // block as a ucontext fiber; blocks run one after another.
 #include "hip/hip_runtime.h"
 
+#undef dma16  // the kernels' hook (hip_runtime.h); emu::dma16 below is the queue behind it
+
+#include <setjmp.h>
 #include <ucontext.h>
 
 #include <cstdio>
@@ -23,8 +26,13 @@ dim3 g_threadIdx, g_blockIdx, g_blockDim, g_gridDim;
 
 namespace {
 enum State { RUN, AT_BLOCK, AT_WAVE, DONE };
+// A fiber starts on its own stack through makecontext/setcontext; every
+// later switch is _setjmp/_longjmp, which (unlike swapcontext) saves no
+// signal mask and so makes no system call.
 struct Fiber {
     ucontext_t uc;
+    jmp_buf jb;
+    bool started;
     State st;
 };
 constexpr size_t kStack = 512 * 1024;
@@ -37,7 +45,7 @@ struct PendingDma {
     unsigned char data[16];
 };
 std::vector<std::deque<PendingDma>> dma_q;  // per lane of the running block
-ucontext_t sched_uc;
+jmp_buf sched_jb;
 int cur = -1;
 void (*g_body)(void *) = nullptr;
 void *g_ctx = nullptr;
@@ -51,11 +59,11 @@ void to_sched(bool dying) {
 #ifdef EMU_ASAN
     void *fake = nullptr;
     __sanitizer_start_switch_fiber(dying ? nullptr : &fake, sched_bottom, sched_size);
-    swapcontext(&fibers[(size_t)cur].uc, &sched_uc);
+    if (!_setjmp(fibers[(size_t)cur].jb)) _longjmp(sched_jb, 1);
     __sanitizer_finish_switch_fiber(fake, nullptr, nullptr);
 #else
     (void)dying;
-    swapcontext(&fibers[(size_t)cur].uc, &sched_uc);
+    if (!_setjmp(fibers[(size_t)cur].jb)) _longjmp(sched_jb, 1);
 #endif
 }
 
@@ -68,16 +76,25 @@ void fiber_entry(int) {
     to_sched(true);
 }
 
+void switch_to(int i) {
+    Fiber &f = fibers[(size_t)i];
+    if (!_setjmp(sched_jb)) {
+        if (f.started) _longjmp(f.jb, 1);
+        f.started = true;
+        setcontext(&f.uc);
+    }
+}
+
 void run_fiber(int i) {
     cur = i;
     g_threadIdx = dim3((unsigned)i % g_blockDim.x, 0, 0);
 #ifdef EMU_ASAN
     void *fake = nullptr;
     __sanitizer_start_switch_fiber(&fake, stacks[(size_t)i], kStack);
-    swapcontext(&sched_uc, &fibers[(size_t)i].uc);
+    switch_to(i);
     __sanitizer_finish_switch_fiber(fake, &sched_bottom, &sched_size);
 #else
-    swapcontext(&sched_uc, &fibers[(size_t)i].uc);
+    switch_to(i);
 #endif
 }
 
@@ -121,6 +138,33 @@ void waitcnt_vm(int n) {
     }
 }
 
+uint64_t wave_uniform(uint64_t v, const char *what, const char *file, int line) {
+    const int lane = cur % 64, base = cur - lane;
+    std::memcpy(wave_slot(lane), &v, sizeof v);
+    wave_barrier();  // every live lane of the wave has written its value
+    const int n = (int)fibers.size() - base < 64 ? (int)fibers.size() - base : 64;
+    uint64_t first = v;
+    bool have = false;
+    for (int l = 0; l < n; l++) {
+        if (fibers[(size_t)(base + l)].st == DONE) continue;  // exited lanes take no part
+        uint64_t o;
+        std::memcpy(&o, wave_slot(l), sizeof o);
+        if (!have) {
+            first = o;
+            have = true;
+        } else if (o != first) {
+            std::fprintf(stderr,
+                         "EMU: kernel %s block (%u,%u,%u) wave %d: %s is not wave-uniform at %s:%d "
+                         "(lane %d has %#llx, the first live lane %#llx)\n",
+                         g_name, g_blockIdx.x, g_blockIdx.y, g_blockIdx.z, cur / 64, what, file, line, l,
+                         (unsigned long long)o, (unsigned long long)first);
+            std::abort();
+        }
+    }
+    wave_barrier();  // every lane has read the slots before they are reused
+    return first;
+}
+
 int lane_id() { return cur % 64; }
 int wave_id() { return cur / 64; }
 void *wave_slot(int lane) { return &slots[((size_t)(cur / 64) * 64 + (size_t)lane) * kSlot]; }
@@ -155,6 +199,7 @@ void launch(const char *name, dim3 grid, dim3 block, void (*body)(void *), void 
                     f.uc.uc_stack.ss_size = kStack;
                     f.uc.uc_link = nullptr;
                     makecontext(&f.uc, (void (*)())fiber_entry, 1, i);
+                    f.started = false;
                     f.st = RUN;
                 }
                 for (;;) {

@@ -312,7 +312,7 @@ def group_gemm_ln():
     # the same rows computed inside whole tiles (the emulated device has 16
     # CUs: 17 tiles = 16 whole + 1 split into 64 x 64 pieces; k > 384, since
     # tiled int8 weights with k <= 384 use two workgroups per CU unsplit)
-    for odt, k in ((np.float16, 448), (np.float32, 128)):  # f32 output: f16 codes, which split at any k
+    for odt, k in ((np.float16, 448), (np.float32, 448)):
         m, n = 16 * 128 + 100, 384
         a, q, s, bias = problem(21, m, k, n)
         a16 = a.astype(np.float16)
@@ -346,6 +346,71 @@ def group_gemm_ln():
         ref = oracle.layernorm(res.astype(np.float32) + oracle.matmul_w8a32(a16.astype(np.float32), q, s, bias), g, b,
                                1e-12)
         assert np.abs(two - ref).max() < 2e-2
+
+
+def range_problem(seed, m, k, n, scale):
+    a, q, s, _ = problem(seed, m, k, n)
+    return (a.astype(np.float64) * scale).astype(np.float32), q, s
+
+
+def normalised_error(c, a, q, s, bias=None):
+    """max |c - exact| / (sum_k |a| |q| s): the error of an f32 matmul_w8a32
+    relative to the magnitude of its terms (exact = float64)."""
+    sf = s.view(np.float16).astype(np.float64)
+    exact = (a.astype(np.float64) @ q.astype(np.float64).T) * sf
+    if bias is not None:
+        exact = exact + bias.astype(np.float64)
+    mag = (np.abs(a.astype(np.float64)) @ np.abs(q.astype(np.float64)).T) * sf
+    return float((np.abs(c.astype(np.float64) - exact) / mag).max())
+
+
+def group_range():
+    # f32 activations over the f32 range (row exponents scale each row into
+    # the f16 split's range): at every input scale the error relative to the
+    # terms' magnitude stays at the oracle's own f32 level
+    m, k, n = 37, 384, 384
+    for scale in (1e-6, 1e-3, 1.0, 3e4, 1e6):
+        a, q, s = range_problem(31, m, k, n, scale)
+        c = np.empty((m, n), np.float32)
+        check(L.tzh_matmul_w8a32(CTX, a.ctypes.data, q.ctypes.data, s.ctypes.data, None, c.ctypes.data, m, k, n))
+        ours = normalised_error(c, a, q, s)
+        orc = normalised_error(oracle.matmul_w8a32(a, q, s, None), a, q, s)
+        print(f"  scale {scale:g}: normalised error {ours:.2e} (oracle {orc:.2e})", flush=True)
+        assert np.isfinite(c).all() and ours <= max(4 * orc, 2.0 ** -22), (scale, ours, orc)
+        cn = np.empty((m, n), np.float32)
+        check(L.tzh_matmul_w8a32_noalloc(CTX, a.ctypes.data, q.ctypes.data, s.ctypes.data, None, cn.ctypes.data, m, k,
+                                         n))
+        assert np.array_equal(c, cn), scale
+    # rows of very different scales in one matrix, a zero row, a row of
+    # subnormals, and the GELU and LayerNorm epilogues of tzh_linear_w8
+    a, q, s = range_problem(32, 64 * 3 + 5, 128, 768, 1.0)
+    a[0] = 0
+    a[1] *= np.float32(2.0 ** -140)
+    a[2:] *= np.logspace(-30, 30, a.shape[0] - 2).astype(np.float32)[:, None]
+    bias = np.random.default_rng(33).uniform(-0.1, 0.1, 768).astype(np.float32)
+    c = linear(a, q, s, bias, np.float32, _abi.EPI_BIAS)
+    assert np.isfinite(c).all() and np.array_equal(c[0], bias)
+    sf = s.view(np.float16).astype(np.float64)
+    exact = (a.astype(np.float64) @ q.astype(np.float64).T) * sf
+    mag = (np.abs(a.astype(np.float64)) @ np.abs(q.astype(np.float64)).T) * sf
+    err = np.abs(c - (exact + bias)) / (mag + np.abs(exact + bias))
+    assert err[1:].max() < 2.0 ** -21, float(err[1:].max())
+    g = oracle.gelu(oracle.matmul_w8a32(a, q, s, bias))
+    cg = linear(a, q, s, bias, np.float32, _abi.EPI_BIAS_GELU)
+    assert np.isfinite(cg).all()
+    assert (np.abs(cg - g) <= 1.13 * 2.0 ** -21 * (mag + np.abs(exact)) + 2.0 ** -20 * np.abs(g) + 1e-37).all()
+    for k in (384, 448):  # the two-workgroup k <= 384 tiles; 128-row tiles with a split last round
+        m = 16 * 128 + 100
+        a, q, s = range_problem(34, m, k, 384, 1.0)
+        a *= np.logspace(-20, 20, m).astype(np.float32)[:, None]
+        rng = np.random.default_rng(35)
+        res = (rng.standard_normal((m, 384)) * np.logspace(-20, 20, m)[:, None]).astype(np.float32)
+        gm = (1 + 0.1 * rng.standard_normal(384)).astype(np.float32)
+        bt = (0.1 * rng.standard_normal(384)).astype(np.float32)
+        bias = np.zeros(384, np.float32)
+        c = linear(a, q, s, bias, np.float32, _abi.EPI_BIAS_RES_LN, res, gm, bt)
+        ref = oracle.layernorm(res + oracle.matmul_w8a32(a, q, s, bias), gm, bt, 1e-12)
+        assert np.isfinite(c).all() and np.abs(c - ref).max() < 1e-4, (k, float(np.abs(c - ref).max()))
 
 
 def group_attention():
@@ -435,6 +500,69 @@ def group_arctic():
     print(f"  arctic emu (f32 weights) vs oracle max-abs {err:.2e}", flush=True)
     assert err < 1e-5
     check(L.tzh_arctic_free(m32))
+
+
+def mixed_weights(w, f32_names):
+    """The quantized weights of `w` with the linears named in f32_names kept
+    f32 (a model that mixes MatWeight.f32 and MatWeight.q8 linears)."""
+    out = synth.quantize(w)
+    for name in f32_names:
+        out[name] = w[name]
+        del out[name + ".scale"]
+    return out
+
+
+def forward_vs_oracle(w, cfg, ids, lengths, what, tol=1e-5):
+    hw = synth.HostWeights(w, cfg)
+    m = C.c_void_p()
+    check(L.tzh_arctic_upload(CTX, C.byref(hw.struct), C.byref(m)))
+    try:
+        d = C.c_int32()
+        check(L.tzh_arctic_precision(m, C.byref(d)))
+        out = np.empty((len(lengths), 384), np.float32)
+        rc = L.tzh_arctic_forward_batch(m, out.ctypes.data, ids.ctypes.data, lengths.ctypes.data, len(lengths),
+                                        ids.shape[1])
+        if rc != 0:
+            return rc, d.value
+        ref = np.stack([oracle.arctic_forward(hw, ids[b, :Ln]) for b, Ln in enumerate(lengths)])
+        err = float(np.abs(out - ref).max())
+        print(f"  {what}: max-abs {err:.2e} vs oracle", flush=True)
+        assert np.isfinite(out).all() and err < tol, (what, err)
+        return rc, d.value
+    finally:
+        check(L.tzh_arctic_free(m))
+
+
+def group_models():
+    # models that mix f32 and int8 linears: each linear on its own format's
+    # GEMM, the forward in f32 (f32 activations for the f32 GEMM)
+    cfg = synth.Config(num_hidden_layers=2)
+    w = synth.make_arctic_f32(91, cfg, ln_random=True)
+    ids, lengths = synth.make_batch(92, 3, seq_len=40, min_len=5)
+    att = [f"encoder.layer.0.attention.self.{x}.weight" for x in ("query", "key", "value")] + \
+          ["encoder.layer.0.attention.output.dense.weight"]
+    ffn = ["encoder.layer.1.intermediate.dense.weight", "encoder.layer.1.output.dense.weight"]
+    rc, act = forward_vs_oracle(mixed_weights(w, att + ffn), cfg, ids, lengths, "f32 attention / int8 FFN, then reverse")
+    assert rc == 0 and act == _abi.F32
+    rc, act = forward_vs_oracle(mixed_weights(w, ["encoder.layer.1.attention.self.key.weight"]), cfg, ids, lengths,
+                                "QKV with an f32 key among int8 query and value")
+    assert rc == 0 and act == _abi.F32
+    # activations past the f16 range: the embedding LayerNorm's gamma makes
+    # layer 0's QKV input reach ~1e5 (the bound, sqrt(383) * 2e4, marks the
+    # model row-scaled); small QKV weights keep the attention inside its range
+    wr = dict(w)
+    wr["embeddings.LayerNorm.weight"] = (w["embeddings.LayerNorm.weight"] * 2e4).astype(np.float32)
+    for x in ("query", "key", "value"):
+        wr[f"encoder.layer.0.attention.self.{x}.weight"] = (w[f"encoder.layer.0.attention.self.{x}.weight"] *
+                                                           1e-4).astype(np.float32)
+    rc, act = forward_vs_oracle(synth.quantize(wr), cfg, ids, lengths, "row-scaled int8 GEMMs (inputs ~1e5)")
+    assert rc == 0 and act == _abi.F32
+    # ... and with full-size QKV weights the attention's inputs could pass
+    # its split's range: the forward refuses instead of returning NaN
+    wr2 = dict(w)
+    wr2["embeddings.LayerNorm.weight"] = wr["embeddings.LayerNorm.weight"]
+    rc, _ = forward_vs_oracle(synth.quantize(wr2), cfg, ids, lengths, "attention past its range")
+    assert rc == _abi.ERR_TOO_LARGE, rc
 
 
 def group_embed():
@@ -647,8 +775,9 @@ def group_gemm_fp():
             assert rc1 == 0 and rc2 == 0 and np.array_equal(fused, split), dt
 
 
-GROUPS = {"eval": group_eval, "gemm_fp": group_gemm_fp, "gemm": group_gemm, "gemm_ln": group_gemm_ln, "attention": group_attention,
-          "arctic": group_arctic, "embed": group_embed,
+GROUPS = {"eval": group_eval, "gemm_fp": group_gemm_fp, "gemm": group_gemm, "gemm_ln": group_gemm_ln, "range": group_range,
+          "attention": group_attention,
+          "arctic": group_arctic, "embed": group_embed, "models": group_models,
           "nodes": group_nodes}
 
 if __name__ == "__main__":

@@ -58,13 +58,23 @@ void launch(const char *name, dim3 grid, dim3 block, void (*body)(void *), void 
 void dma16(const void *src, void *lds_dst);
 void waitcnt_vm(int n);
 void vmem_marker();  // a vector memory op with no LDS effect (a store or a register load), in issue order
+// A value the hardware holds once per wave (an SGPR, M0): every live lane of
+// the wave must pass the same v, or the emulation aborts naming `what` and
+// the source line (on the GPU a divergent value would silently become one
+// lane's).  Returns the value of the wave's first live lane.
+uint64_t wave_uniform(uint64_t v, const char *what, const char *file, int line);
 }  // namespace emu
 
 // the hooks gemm_pipe.hip takes from its target: DMA issue and LDS barrier
 #define TZH_EMULATION 1
-inline void dma16(const char *sbase, uint32_t voff, char *lds_base) {
+// global_load_lds_dwordx4 takes its global base in an SGPR pair and its LDS
+// base in M0: both must be wave-uniform
+inline void emu_dma16(const char *sbase, uint32_t voff, char *lds_base, const char *file, int line) {
+    emu::wave_uniform((uint64_t)(uintptr_t)sbase, "dma16 global base (SGPR operand)", file, line);
+    emu::wave_uniform((uint64_t)(uintptr_t)lds_base, "dma16 LDS base (M0)", file, line);
     emu::dma16(sbase + voff, lds_base + 16 * emu::lane_id());
 }
+#define dma16(sbase, voff, lds_base) emu_dma16((sbase), (voff), (lds_base), __FILE__, __LINE__)
 inline void lds_barrier_only() { emu::syncthreads(); }
 inline void vmem_store_issued() { emu::vmem_marker(); }
 inline void vmem_load_issued() { emu::vmem_marker(); }
@@ -107,7 +117,20 @@ inline bool wave_any(bool p) {  // every lane of the emulated wave is active
     return any;
 }
 #define __builtin_amdgcn_s_waitcnt(imm) emu::waitcnt_vm(((imm)&15) | ((((imm) >> 14) & 3) << 4))
-#define __builtin_amdgcn_readfirstlane(x) (x)
+// v_readfirstlane_b32: the first live lane's value; the kernels use it only
+// on values that are already wave-uniform, which the emulation checks
+template <typename T>
+inline T emu_readfirstlane(T x, const char *file, int line) {
+    static_assert(sizeof(T) <= 8, "32/64-bit values only");
+    uint64_t v = 0;
+    std::memcpy(&v, &x, sizeof(T));
+    v = emu::wave_uniform(v, "readfirstlane operand", file, line);
+    T r;
+    std::memcpy(&r, &v, sizeof(T));
+    return r;
+}
+#define __builtin_amdgcn_readfirstlane(x) emu_readfirstlane((x), __FILE__, __LINE__)
+#define __builtin_amdgcn_ldexpf(x, e) ldexpf((x), (e))
 
 #define threadIdx (emu::g_threadIdx)
 #define blockIdx (emu::g_blockIdx)

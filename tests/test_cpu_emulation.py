@@ -34,7 +34,7 @@ def emu_env():
     return env
 
 
-GROUPS = ["eval", "attention", "gemm", "gemm_ln", "nodes", "gemm_fp"]
+GROUPS = ["eval", "attention", "gemm", "gemm_ln", "range", "models", "nodes", "gemm_fp"]
 
 
 @pytest.fixture(scope="module")

@@ -202,7 +202,7 @@ def test_quantized_embedding_tables(ctx, host):
         assert_embedding_parity(got, ref)
         h0 = gpu_hidden(m, ids, lengths, 0)
         r0 = oracle.arctic_hidden(hw, ids[0, :lengths[0]], 0)
-        assert np.abs(h0[:lengths[0]] - r0).max() < 1e-2
+        assert np.abs(h0[:lengths[0]] - r0).max() < 1e-4
     finally:
         m.deinit()
 
@@ -309,3 +309,77 @@ def test_f32_model_config1(ctx):
         m.deinit()
 
 
+
+
+def mixed_weights(w, f32_names):
+    """The quantized weights of `w` with the linears named in f32_names kept
+    f32: a model that mixes MatWeight.f32 and MatWeight.q8 linears, which the
+    reference loads matrix by matrix (arctic.zig:55-58, 258-287)."""
+    out = synth.quantize(w)
+    for name in f32_names:
+        out[name] = w[name]
+        del out[name + ".scale"]
+    return out
+
+
+ATT = ["attention.self.query.weight", "attention.self.key.weight", "attention.self.value.weight",
+       "attention.output.dense.weight"]
+FFN = ["intermediate.dense.weight", "output.dense.weight"]
+
+
+@pytest.mark.parametrize("f32_names", [
+    [f"encoder.layer.{l}.{n}" for l in (0, 2, 4) for n in ATT] + [f"encoder.layer.{l}.{n}" for l in (1, 3, 5) for n in FFN],
+    [f"encoder.layer.{l}.{n}" for l in (1, 3) for n in FFN],
+    ["encoder.layer.2.attention.self.key.weight"]])
+def test_mixed_f32_int8_models(ctx, f32_names):
+    """Each linear on its own format's GEMM (f32 weights on the f32 GEMM,
+    int8 on the int8 GEMM), the forward in f32 whatever precision is set;
+    a QKV that mixes dtypes runs as one f32 matrix."""
+    w = mixed_weights(synth.make_arctic_f32(51, CFG, ln_random=True), f32_names)
+    m = ModelWeights.fromHost(ctx, w, CFG)
+    try:
+        hw = synth.HostWeights(w, CFG)
+        m.set_precision("float16")
+        assert m.precision == "float32"
+        ids, lengths = synth.make_batch(52, 7, seq_len=200, min_len=1)
+        got = gpu_embed(m, ids, lengths)
+        ref = np.stack([oracle.arctic_forward(hw, ids[b, :L]) for b, L in enumerate(lengths)])
+        assert_embedding_parity(got, ref, max_abs=1e-5)
+        hid = gpu_hidden(m, ids, lengths, 6)
+        assert np.abs(hid[:lengths[0]] - oracle.arctic_hidden(hw, ids[0, :lengths[0]], 6)).max() < 1e-4
+    finally:
+        m.deinit()
+
+
+def test_activations_past_the_f16_range(ctx):
+    """The embedding LayerNorm's gamma (2e4) puts layer 0's QKV input near
+    1e5, past f16: the weights' bound marks the model row-scaled and its
+    int8 GEMMs scale each row into the split's range, so the forward stays
+    the f32 one.  With full-size QKV weights the attention's inputs could
+    pass its split's range too, and the forward refuses (TooLarge) instead
+    of returning NaN."""
+    w = synth.make_arctic_f32(61, CFG, ln_random=True)
+    w["embeddings.LayerNorm.weight"] = (w["embeddings.LayerNorm.weight"] * 2e4).astype(np.float32)
+    small = dict(w)
+    for n in ATT[:3]:
+        small[f"encoder.layer.0.{n}"] = (w[f"encoder.layer.0.{n}"] * 1e-4).astype(np.float32)
+    q = synth.quantize(small)
+    m = ModelWeights.fromHost(ctx, q, CFG)
+    try:
+        hw = synth.HostWeights(q, CFG)
+        ids, lengths = synth.make_batch(62, 5, seq_len=128, min_len=4)
+        h0 = gpu_hidden(m, ids, lengths, 0)
+        assert np.abs(h0).max() > 65504  # the QKV input really is past f16
+        got = gpu_embed(m, ids, lengths)
+        ref = np.stack([oracle.arctic_forward(hw, ids[b, :L]) for b, L in enumerate(lengths)])
+        assert np.isfinite(got).all()
+        assert_embedding_parity(got, ref, max_abs=1e-5)
+    finally:
+        m.deinit()
+    m = ModelWeights.fromHost(ctx, synth.quantize(w), CFG)
+    try:
+        with pytest.raises(TzhError) as ei:
+            gpu_embed(m, ids, lengths)
+        assert ei.value.code == _abi.ERR_TOO_LARGE
+    finally:
+        m.deinit()

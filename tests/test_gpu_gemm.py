@@ -2,14 +2,17 @@
 oracle's matmul_w8a32 (matmul_w8a32.zig:14-57), GELU (arctic.zig:750-756)
 and LayerNorm (layernorm.zig:26-117).
 
-Tolerance: f32 activations enter the MFMA as an exact f16 split a = hi +
-lo + r with |r| <= 2^-22 |a| + 2^-25, and the sums run in f32 in another
-order than the oracle's, so every output is checked against the bound
-    |gpu - oracle| <= s_j * sum_k (|a_ik| + 2^-4) |q_jk| * (2^-20 + k 2^-23) + 2^-22 |c_ij| + 1e-30
-which a dropped lo half (2^-12 |a|), a wrong scale/bias index or a
-transposed operand exceeds by orders of magnitude.  f16 activations (the
-opt-in model path) are exact in the MFMA; their outputs are compared with
-the oracle on the same f16 values."""
+Tolerance: each f32 activation row is scaled by the power of two 2^e that
+puts its largest magnitude M in [2^14, 2^15) and enters the MFMA as an
+exact f16 split a 2^e = hi + lo + r with |r| <= 2^-22 |a 2^e| (for |a| >=
+2^-17 M) or 2^-25 (below), and the sums run in f32 in another order than
+the oracle's, so every output is checked against the bound
+    |gpu - oracle| <= s_j * sum_k (|a_ik| + 2^-36 M_i) |q_jk| * (2^-20 + k 2^-23) + 2^-22 |c_ij| + 1e-37
+which a dropped lo half (2^-12 |a|), a wrong scale/bias index, a
+transposed operand or a missing row scale (2^-25 |a|^-1 relative error for
+small rows) exceeds.  f16 activations (the opt-in model path) are exact in
+the MFMA; their outputs are compared with the oracle on the same f16
+values."""
 import ctypes as C
 
 import numpy as np
@@ -33,8 +36,20 @@ def make_problem(seed, m, k, n, x_scale=1.0):
 
 def bound(a, q, s, c, k):
     sf = s.view(np.float16).astype(np.float64)
-    mag = (np.abs(a).astype(np.float64) + 2.0 ** -4) @ np.abs(q.astype(np.float64)).T * sf[None, :]
-    return mag * (2.0 ** -20 + k * 2.0 ** -23) + 2.0 ** -22 * np.abs(c) + 1e-30
+    a64 = np.abs(a.astype(np.float64))
+    mag = (a64 + 2.0 ** -36 * a64.max(axis=1, keepdims=True)) @ np.abs(q.astype(np.float64)).T * sf[None, :]
+    return mag * (2.0 ** -20 + k * 2.0 ** -23) + 2.0 ** -22 * np.abs(c) + 1e-37
+
+
+def normalised_error(c, a, q, s, bias=None):
+    """max |c - exact| / (sum_k |a| |q| s): the error of an f32 matmul_w8a32
+    relative to the magnitude of its terms (exact = float64)."""
+    sf = s.view(np.float16).astype(np.float64)
+    exact = (a.astype(np.float64) @ q.astype(np.float64).T) * sf
+    if bias is not None:
+        exact = exact + bias.astype(np.float64)
+    mag = (np.abs(a.astype(np.float64)) @ np.abs(q.astype(np.float64)).T) * sf
+    return float((np.abs(c.astype(np.float64) - exact) / mag).max())
 
 
 def dev(x):
@@ -101,20 +116,121 @@ def test_matmul_w8a32_null_bias_and_zero_rows(ctx):
                                  70, 128, 256))
     ref = oracle.matmul_w8a32(a, q, s, None)
     assert (np.abs(Cg.cpu().numpy() - ref) <= bound(a, q, s, ref, 128)).all()
-    # m == 0 is a no-op (matmul_w8a32.zig:24)
-    check(lib().tzh_matmul_w8a32(ctx.handle, A.data_ptr(), Q.data_ptr(), S.data_ptr(), None, Cg.data_ptr(),
-                                 0, 128, 256))
+
+
+def test_matmul_w8a32_empty_and_k0_edges(ctx):
+    """matmul_w8a32.zig:24 returns for m == 0 or n == 0 before touching c;
+    with k == 0 the sum is empty and c[i,j] = 0 * s[j] + bias[j] (40-55)."""
+    a, q, s, bias = make_problem(4, 8, 40, 128)
+    A, Q, S, B = dev(a), dev(q), dev(s.view(np.int16)), dev(bias)
+    sentinel = torch.full((8 * 128,), 7.0, device="cuda")
+    for m, k, n in [(0, 40, 128), (8, 40, 0), (0, 0, 0), (0, 65536, 65536)]:
+        check(lib().tzh_matmul_w8a32(ctx.handle, A.data_ptr(), Q.data_ptr(), S.data_ptr(), B.data_ptr(),
+                                     sentinel.data_ptr(), m, k, n))
+        assert (sentinel == 7.0).all(), (m, k, n)
+    Cg = torch.full((8, 128), float("nan"), device="cuda")
+    check(lib().tzh_matmul_w8a32(ctx.handle, A.data_ptr(), Q.data_ptr(), S.data_ptr(), B.data_ptr(), Cg.data_ptr(),
+                                 8, 0, 128))
+    assert np.array_equal(Cg.cpu().numpy(), np.broadcast_to(bias, (8, 128)))
+    check(lib().tzh_matmul_w8a32(ctx.handle, A.data_ptr(), Q.data_ptr(), S.data_ptr(), None, Cg.data_ptr(), 8, 0, 128))
+    assert (Cg == 0).all()
+    assert np.array_equal(oracle.matmul_w8a32(np.zeros((8, 0), np.float32), np.zeros((128, 0), np.int8), s, bias),
+                          np.broadcast_to(bias, (8, 128)))
 
 
 def test_matmul_w8a32_rejects_bad_arguments(ctx):
     a, q, s, bias = make_problem(4, 8, 40, 128)
     A, Q, S = dev(a), dev(q), dev(s.view(np.int16))
     Cg = torch.empty((8, 128), device="cuda")
-    for m, k, n in [(8, 0, 128), (-1, 40, 128), (8, 40, 0)]:
+    for m, k, n in [(-1, 40, 128), (8, -1, 128), (8, 40, -1)]:
         rc = lib().tzh_matmul_w8a32(ctx.handle, A.data_ptr(), Q.data_ptr(), S.data_ptr(), None, Cg.data_ptr(), m, k, n)
         assert rc == _abi.ERR_INVALID_ARGS, (m, k, n)
     rc = lib().tzh_matmul_w8a32(ctx.handle, None, Q.data_ptr(), S.data_ptr(), None, Cg.data_ptr(), 8, 40, 128)
     assert rc == _abi.ERR_INVALID_ARGS
+
+
+SCALES = [1e-6, 1e-3, 1.0, 3e4, 1e6]
+
+
+@pytest.mark.parametrize("scale", SCALES)
+def test_matmul_w8a32_over_the_f32_range(ctx, scale):
+    """Inputs N(0,1) * scale from 1e-6 to 1e6 (the f16 halves alone span
+    2^-24 .. 65504): every output within the bound, no NaN, and the error
+    relative to the terms' magnitude at the f32 oracle's own level, through
+    tzh_matmul_w8a32, tzh_matmul_w8a32_noalloc and tzh_linear_w8."""
+    m, k, n = 300, 384, 1152
+    a, q, s, _ = make_problem(40, m, k, n)
+    a = (a.astype(np.float64) * scale).astype(np.float32)
+    A, Q, S = dev(a), dev(q), dev(s.view(np.int16))
+    ref = oracle.matmul_w8a32(a, q, s, None)
+    orc = normalised_error(ref, a, q, s)
+    outs = {}
+    for name in ("tzh_matmul_w8a32", "tzh_matmul_w8a32_noalloc"):
+        Cg = torch.full((m, n), float("nan"), device="cuda")
+        check(getattr(lib(), name)(ctx.handle, A.data_ptr(), Q.data_ptr(), S.data_ptr(), None, Cg.data_ptr(), m, k, n))
+        outs[name] = Cg.cpu().numpy()
+    outs["tzh_linear_w8"] = gpu_linear(ctx, a, q, s, np.zeros(n, np.float32))
+    for name, c in outs.items():
+        ours = normalised_error(c, a, q, s)
+        assert np.isfinite(c).all(), name
+        assert (np.abs(c - ref) <= bound(a, q, s, ref, k)).all(), name
+        assert ours <= max(4 * orc, 2.0 ** -22), (name, ours, orc)
+
+
+@pytest.mark.parametrize("scale", SCALES)
+def test_linear_w8_epilogues_over_the_f32_range(ctx, scale):
+    """GELU and residual + LayerNorm epilogues of tzh_linear_w8 with f32
+    activations of every scale (LayerNorm: its 128-row tiles with a split
+    last round at k = 1536, the two-workgroup tiles at k = 384)."""
+    m, k, n = 300, 384, 1536
+    a, q, s, bias = make_problem(41, m, k, n)
+    a = (a.astype(np.float64) * scale).astype(np.float32)
+    bias = (bias * min(scale, 1.0)).astype(np.float32)
+    lin = oracle.matmul_w8a32(a, q, s, bias)
+    c = gpu_linear(ctx, a, q, s, bias, torch.float32, _abi.EPI_BIAS_GELU)
+    ref = oracle.gelu(lin)
+    tol = 1.13 * bound(a, q, s, lin, k) + 2.0 ** -20 * np.abs(ref) + 1e-37
+    assert np.isfinite(c).all() and (np.abs(c - ref) <= tol).all(), float((np.abs(c - ref) / tol).max())
+    rng = np.random.default_rng(42)
+    # 40000 rows at k = 1536: whole rounds of 128-row tiles, then the
+    # leftover tiles as pieces; 3000 rows: pieces only; k = 384: the
+    # two-workgroup tiles.  Parity on sampled rows of every region.
+    for m, k in ((40000, 1536), (3000, 1536), (777, 384)):
+        a, q, s, bias = make_problem(43 + k, m, k, 384)
+        a = (a.astype(np.float64) * scale).astype(np.float32)
+        bias = (bias * scale).astype(np.float32)
+        res = (rng.standard_normal((m, 384)) * scale).astype(np.float32)
+        gamma = (1 + 0.1 * rng.standard_normal(384)).astype(np.float32)
+        beta = (0.1 * rng.standard_normal(384)).astype(np.float32)
+        c = gpu_linear(ctx, a, q, s, bias, torch.float32, _abi.EPI_BIAS_RES_LN, res, gamma, beta)
+        rows = np.unique(np.concatenate([rng.choice(m, min(m, 400), replace=False), np.arange(m - 50, m)]))
+        a, res, c = a[rows], res[rows], c[rows]
+        pre = res + oracle.matmul_w8a32(a, q, s, bias)
+        ref = oracle.layernorm(pre, gamma, beta, 1e-12)
+        std = pre.astype(np.float64).std(axis=1, keepdims=True)
+        tol = (bound(a, q, s, pre, k) + 2.0 ** -22 * np.abs(res)).max(axis=1, keepdims=True) * 4 * \
+            np.abs(gamma)[None, :] / std + 1e-5
+        assert np.isfinite(c).all() and (np.abs(c - ref) <= tol).all(), (m, k, float((np.abs(c - ref) / tol).max()))
+
+
+def test_matmul_w8a32_rows_of_every_scale(ctx):
+    """One matrix whose rows span 1e-30 .. 1e30, a zero row and a row of
+    f32 subnormals: each row keeps its own relative accuracy."""
+    m, k, n = 197, 128, 768
+    a, q, s, bias = make_problem(44, m, k, n)
+    a[0] = 0
+    a[1] *= np.float32(2.0 ** -140)
+    a[2:] *= np.logspace(-30, 30, m - 2).astype(np.float32)[:, None]
+    A, Q, S, B = dev(a), dev(q), dev(s.view(np.int16)), dev(bias)
+    Cg = torch.empty((m, n), device="cuda")
+    check(lib().tzh_matmul_w8a32(ctx.handle, A.data_ptr(), Q.data_ptr(), S.data_ptr(), B.data_ptr(), Cg.data_ptr(),
+                                 m, k, n))
+    c = Cg.cpu().numpy()
+    assert np.isfinite(c).all() and np.array_equal(c[0], bias)
+    sf = s.view(np.float16).astype(np.float64)
+    exact = (a.astype(np.float64) @ q.astype(np.float64).T) * sf + bias
+    mag = (np.abs(a.astype(np.float64)) @ np.abs(q.astype(np.float64)).T) * sf
+    assert (np.abs(c - exact) / (mag + np.abs(exact)))[1:].max() < 2.0 ** -21
 
 
 def test_f16_activations_f16_out(ctx):
