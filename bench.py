@@ -14,7 +14,10 @@ tokens.  `roofline` describes the dominant kernel (by total time in the
 forward), timed inside the forward with HIP events recorded around every
 launch on the forward's own stream; `cpu_baseline` times the C restatement of the reference's
 batch-parallel CPU forward (forwardBatchParallel) on a sample of the same
-batch on the host cores.
+batch on the host cores.  The default (forward) line also carries `chain`
+and `gemm3`: configs 2 and 3 measured in the same run (value, time per
+step, roofline fraction of their kernels and their own CPU baselines), the
+same figures their own workloads print.
 """
 from __future__ import annotations
 
@@ -132,9 +135,11 @@ def main():
     if args.workload == "embed-docs":
         return embed_docs(args)
     if args.workload == "chain":
-        return chain(args)
+        print(json.dumps(chain(args)), flush=True)
+        return
     if args.workload == "gemm3":
-        return gemm3(args)
+        print(json.dumps(gemm3(args)), flush=True)
+        return
     cfg = synth.Config()
     weights = synth.quantize(synth.make_arctic_f32(SEED_WEIGHTS, cfg))  # N(0,0.02), gamma 1, beta 0
     ctx = tenzor_amd.Context(0)
@@ -278,8 +283,20 @@ def main():
                       f"{int(lengths[sel].sum())} real tokens), C restatement of forwardBatchParallel "
                       f"(f32, OpenMP over sequences), {dt:.1f} s",
         }
-    print(json.dumps(line), flush=True)
     model.deinit()
+    del d_ids, out
+    torch.cuda.empty_cache()
+    # configs 2 and 3 in the same run (their own workloads print the full
+    # line): value, time per step, roofline fraction and CPU baseline each
+    for name, fn in (("chain", chain), ("gemm3", gemm3)):
+        sub = fn(argparse.Namespace(steps=args.steps, warmup=args.warmup, no_cpu_baseline=args.no_cpu_baseline))
+        line[name] = {k: sub[k] for k in ("metric", "value", "unit", "ms_per_step", "dtype", "config", "roofline")}
+        if "kernels" in sub:
+            line[name]["kernels"] = sub["kernels"]
+        if "cpu_baseline" in sub:
+            line[name]["cpu_baseline"] = sub["cpu_baseline"]
+        torch.cuda.empty_cache()
+    print(json.dumps(line), flush=True)
 
 
 CHAIN_N = 16384
@@ -389,7 +406,8 @@ def chain(args):
                       f"passes with two temporaries (oracle.c), one thread; {dt:.1f} s; GPU vs CPU on the sample: "
                       f"max {int(ulp)} ulp",
         }
-    print(json.dumps(line), flush=True)
+    ctx.close()
+    return line
 
 
 def gemm3(args):
@@ -499,7 +517,8 @@ def gemm3(args):
             "sample": f"{len(rows)} random rows of X through the pair (oracle.c: matmul_w8a32, GELU, matmul_w8a32, "
                       f"residual, LayerNorm), one thread; {dt:.1f} s; GPU vs CPU on the sample: max-abs {err:.2e}",
         }
-    print(json.dumps(line), flush=True)
+    ctx.close()
+    return line
 
 
 DOCS = 256

@@ -181,6 +181,7 @@ inline T atomicExch(T *p, T v) {
 
 using std::max;
 using std::min;
+using std::sqrt;  // sqrt(float) in float, as HIP's overload computes it (not via double)
 using std::isnan;
 using std::isinf;
 using std::isfinite;

@@ -37,6 +37,12 @@ def emu_env():
 GROUPS = ["eval", "attention", "gemm", "gemm_ln", "range", "models", "nodes", "gemm_fp"]
 
 
+# test_gpu_eval.py's whole sequence in one process, in file order, with the
+# generated kernels and the cases kept off the GPU (replay_plugin.py)
+REPLAY = ["python", "-m", "pytest", "-p", "tests.cpu_emu.replay_plugin", "-m", "gpu", "-q", "-p", "no:cacheprovider",
+          "tests/test_gpu_eval.py", "--deselect", "tests/test_gpu_eval.py::test_config2_chain_full_size"]
+
+
 @pytest.fixture(scope="module")
 def emu_runs(emu_env):
     """All groups started at once (each is single-threaded), so the module
@@ -44,6 +50,9 @@ def emu_runs(emu_env):
     procs = {g: subprocess.Popen(["python", os.path.join(EMU, "emu_checks.py"), g], stdout=subprocess.PIPE,
                                  stderr=subprocess.STDOUT, text=True, env=emu_env, cwd=ROOT)
              for g in GROUPS}
+    procs["replay_eval"] = subprocess.Popen(REPLAY, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                                            env=dict(emu_env, TZH_EMU_LIB=os.path.join(EMU, "libtenzor_hip_emu.so")),
+                                            cwd=ROOT)
     yield procs
     for p in procs.values():
         if p.poll() is None:
@@ -56,6 +65,13 @@ def test_kernels_under_emulation(emu_runs, group):
     out, _ = emu_runs[group].communicate(timeout=1200)
     assert emu_runs[group].returncode == 0, out[-4000:]
     assert "EMU CHECKS PASSED" in out
+
+
+def test_gpu_eval_sequence_replayed_under_emulation(emu_runs):
+    """Every test of test_gpu_eval.py (the deep-tree case included, which
+    stays off the GPU) in one process against the emulation."""
+    out, _ = emu_runs["replay_eval"].communicate(timeout=1200)
+    assert emu_runs["replay_eval"].returncode == 0, out[-4000:]
 
 
 def test_cpp_host_api_under_emulation(emu_env, tmp_path):

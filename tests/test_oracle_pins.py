@@ -395,3 +395,93 @@ def test_eval_errors():
     nodes[-1].shape[1] = 4  # corrupt the result shape
     rc, _ = oracle.eval_tape(nodes, [np.zeros((2, 3), np.float32), np.zeros(3, np.float32)])
     assert rc == _abi.ERR_SHAPE
+
+
+# ------------------------------------------------------------------ A12-A15 executor in f64
+# The reference runs the same op set on f64 slices (elementwise.zig:13-207,
+# simd.zig:107-315, reduce.zig:13-96).  The oracle's f64 mode (orc_eval with
+# F64, orc_unary_f64 / orc_binary_f64) is pinned against numpy / torch in
+# float64 with bounds a few f64 ulp wide: evaluating in f32 (errors near
+# 2^-24), dropping a term or swapping an operand fails them.
+def H64(a):
+    return HT(np.asarray(a, np.float64), np.float64)
+
+
+def run64(expr):
+    return run(expr, np.float64)
+
+
+def test_f64_unary_ops_vs_float64_references():
+    x = np.linspace(-5, 5, 2001)
+    xp = np.abs(x) + 0.01
+    t = torch.from_numpy(x)
+    exact = {  # correctly rounded (or one-rounding) float64 references
+        "neg": (x, -x), "abs": (x, np.abs(x)), "sqrt": (xp, np.sqrt(xp)), "floor": (x, np.floor(x)),
+        "ceil": (x, np.ceil(x)), "relu": (x, np.maximum(x, 0)),
+    }
+    for op, (inp, ref) in exact.items():
+        rc, out = run64(UnaryExpr(op, H64(inp)))
+        assert rc == 0 and out.dtype == np.float64 and np.array_equal(out, ref), op
+    libm = {"exp": (x, np.exp(x)), "log": (xp, np.log(xp)), "sin": (x, np.sin(x)), "cos": (x, np.cos(x)),
+            "rsqrt": (xp, 1 / np.sqrt(xp))}
+    for op, (inp, ref) in libm.items():
+        rc, out = run64(UnaryExpr(op, H64(inp)))
+        assert rc == 0
+        np.testing.assert_allclose(out, ref, rtol=4e-16, atol=0, err_msg=op)
+    closed = {  # the reference's forms (2 sigmoid(2x) - 1 tanh, simd.zig) against torch / numpy
+        "tanh": torch.tanh(t).numpy(), "sigmoid": torch.sigmoid(t).numpy(),
+        "silu": torch.nn.functional.silu(t).numpy(), "softplus": np.logaddexp(0, x),
+        "gelu": torch.nn.functional.gelu(t, approximate="tanh").numpy(),
+    }
+    for op, ref in closed.items():
+        rc, out = run64(UnaryExpr(op, H64(x)))
+        assert rc == 0
+        np.testing.assert_allclose(out, ref, rtol=1e-14, atol=1e-15, err_msg=op)
+    rc, r = run64(UnaryExpr("round", H64([0.5, -0.5, 1.5, 2.5, -2.5, 0.49999999999999994])))
+    assert rc == 0 and r.tolist() == [1, -1, 2, 3, -3, 0]  # half away from zero
+    # f64 really is f64: 1 + 2^-40 survives, an f32 evaluation loses it
+    rc, out = run64(BinaryExpr("add", H64([1.0]), H64([2.0 ** -40])))
+    assert rc == 0 and out[0] == 1 + 2.0 ** -40
+
+
+def test_f64_binary_ops_and_broadcasts_vs_numpy():
+    rng = np.random.default_rng(71)
+    a = rng.uniform(0.1, 3, 257)
+    b = rng.uniform(-2, 2, 257)
+    for op, ref in {"add": a + b, "sub": a - b, "mul": a * b, "div": a / b, "max": np.maximum(a, b),
+                    "min": np.minimum(a, b)}.items():
+        rc, out = run64(BinaryExpr(op, H64(a), H64(b)))
+        assert rc == 0 and np.array_equal(out, ref), op
+    rc, out = run64(BinaryExpr("pow", H64(a), H64(b)))
+    np.testing.assert_allclose(out, np.power(a, b), rtol=4e-16, atol=0)
+    rc, out = run64(BinaryExpr("sub", H64(a), ScalarExpr(0.25, "float64")))
+    assert rc == 0 and np.array_equal(out, a - 0.25)
+    for ls, rs in [((4, 6), (6,)), ((4, 6), (4, 1)), ((2, 1, 5), (3, 1)), ((2, 3, 4, 5), (3, 1, 5))]:
+        x = rng.standard_normal(ls)
+        y = rng.standard_normal(rs)
+        rc, out = run64(BinaryExpr("sub", H64(x), H64(y)).mul(H64(y)))
+        assert rc == 0 and np.array_equal(out, (x - y) * y), (ls, rs)
+
+
+def test_f64_reductions_and_chain_vs_numpy():
+    rng = np.random.default_rng(72)
+    x = rng.uniform(0.5, 1.5, (5, 7, 9))
+    for op, fn in {"sum": np.sum, "mean": np.mean, "prod": np.prod, "reduce_max": np.max,
+                   "reduce_min": np.min}.items():
+        for ax in (0, 1, 2):
+            rc, out = run64(ReduceExpr(op, H64(x), (ax,)))
+            assert rc == 0
+            np.testing.assert_allclose(out, fn(x, axis=ax), rtol=1e-14, atol=0, err_msg=f"{op} axis {ax}")
+        rc, out = run64(ReduceExpr(op, H64(x)))
+        np.testing.assert_allclose(out, fn(x), rtol=1e-13, atol=0, err_msg=op)
+    # the config-2 chain in f64: exp((a + b) * c), b broadcast over rows
+    a = rng.uniform(-1, 1, (33, 65))
+    bb = rng.uniform(-1, 1, 65)
+    c = rng.uniform(-1, 1, (33, 65))
+    rc, out = run64(BinaryExpr("add", H64(a), H64(bb)).mul(H64(c)).exp())
+    assert rc == 0
+    np.testing.assert_allclose(out, np.exp((a + bb) * c), rtol=4e-16, atol=0)
+    # a reduction feeding more elementwise work
+    rc, out = run64(BinaryExpr("mul", ReduceExpr("sum", H64(a), (0,)), H64(bb)).exp())
+    assert rc == 0
+    np.testing.assert_allclose(out, np.exp(a.sum(axis=0) * bb), rtol=1e-14, atol=0)
