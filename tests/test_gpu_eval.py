@@ -163,6 +163,38 @@ def test_deep_tree_materialises_and_matches(ctx):
     assert ((ulp_diff(out, ref) <= 8) | (np.abs(out - ref) < 1e-6)).all()
 
 
+@pytest.mark.parametrize("case", ["right_deep_sigmoid", "balanced_depth5", "right_deep_f64"])
+def test_right_deep_trees_cut_by_depth(ctx, case):
+    """Trees whose inline evaluation needs a deeper value stack than a
+    generated kernel keeps (executor.zig:551-578 evaluates any nesting by
+    materialising children): the planner cuts the deepest subtrees into
+    temporaries; results must equal the oracle's three-address evaluation."""
+    rng = np.random.default_rng(41)
+    if case == "right_deep_sigmoid":
+        xs = [T(rng.standard_normal((17, 40)).astype(np.float32)) for _ in range(6)]
+        row = T(rng.standard_normal(40).astype(np.float32))
+        e = BinaryExpr("mul", xs[0], row)
+        for i, x in enumerate(xs[1:]):
+            inner = UnaryExpr("sigmoid", e)
+            e = BinaryExpr("sub" if i % 2 else "mul", x, inner)  # the right operand is the deep one
+    elif case == "balanced_depth5":
+        def tree(level):
+            if level == 0:
+                return T(rng.uniform(-1, 1, (9, 130)).astype(np.float32))
+            return BinaryExpr("add" if level % 2 else "mul", tree(level - 1), tree(level - 1))
+        e = tree(5)  # 32 leaves, a stack of depth 6 inline
+    else:
+        xs = [T(rng.standard_normal((5, 70)), torch.float64) for _ in range(7)]
+        e = xs[0]
+        for x in xs[1:]:
+            e = BinaryExpr("add", x, UnaryExpr("sin", e))
+    out, ref = run_both(e, ctx)
+    if case == "right_deep_f64":
+        np.testing.assert_allclose(out, ref, rtol=1e-13, atol=1e-14)
+    else:
+        assert ((ulp_diff(out, ref) <= 8) | (np.abs(out - ref) < 1e-6)).all()
+
+
 def test_long_chain_over_32_nodes(ctx):
     x = T(np.linspace(-1, 1, 4097, dtype=np.float32))
     e = x
