@@ -33,10 +33,9 @@ int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t 
                             int32_t w_format, const uint16_t *scale, const float *bias, void *c, int32_t c_dtype,
                             int64_t m, int64_t k, int64_t n, int64_t n_valid, int32_t epilogue, const void *res,
                             const float *gamma, const float *beta, float eps, float *ln_ws, int64_t ln_ws_rows,
-                            const int *rexp);
+                            bool row_scale);
 int tzh_attention_launch(hipStream_t st, int num_cus, unsigned *queue, const void *qkv, void *out, int32_t dtype,
                          const int *cu_seqlens, const int *order, int batch, int n_heads, int hidden);
-int tzh_row_exp_launch(hipStream_t st, const float *a, int64_t m, int64_t k, int *e);
 
 namespace {
 
@@ -236,12 +235,10 @@ struct tzh_model {
     int64_t ln_ws_rows = 0;
     // Range of the f32 forward's f16 hi/lo splits (set at upload from the
     // weights): row_scaled when some int8 GEMM's input bound reaches 2^15
-    // (those GEMMs then run row-scaled, with rexp holding the row
-    // exponents); attn_bound, the bound of the attention's split inputs
-    // (|q| log2(e)/sqrt(32), |k|, |v|) over the layers
+    // (the int8 GEMMs then run row-scaled); attn_bound, the bound of the
+    // attention's split inputs (|q| log2(e)/sqrt(32), |k|, |v|) over the layers
     bool row_scaled = false;
     float attn_bound = 0.0f;
-    int *rexp = nullptr;
     uint32_t *tok_ids = nullptr;
     int32_t *tok_pos = nullptr;
     int *meta = nullptr;  // device: cu[batch+1] | order[batch]
@@ -416,12 +413,11 @@ int check_config(const tzh_arctic_config &c) {
 }
 
 void free_workspace(tzh_model *m) {
-    void *bufs[] = {m->h, m->h1, m->qkv, m->attn, m->inter, m->ln_ws, m->tok_ids, m->tok_pos, m->meta, m->rexp};
+    void *bufs[] = {m->h, m->h1, m->qkv, m->attn, m->inter, m->ln_ws, m->tok_ids, m->tok_pos, m->meta};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     m->h = m->h1 = m->qkv = m->attn = m->inter = nullptr;
     m->ln_ws = nullptr;
-    m->rexp = nullptr;
     m->ln_ws_rows = 0;
     m->tok_ids = nullptr;
     m->tok_pos = nullptr;
@@ -489,7 +485,6 @@ int ensure_workspace(tzh_model *m, int64_t tokens, int batch, size_t es) {
     // a split partial round is at most a third of the CUs' 128-row tiles
     m->ln_ws_rows = std::min<int64_t>((T + 127) / 128, m->ctx->num_cus / 3 + 1) * 128;
     TZH_TRY(get((void **)&m->ln_ws, (size_t)m->ln_ws_rows * H * 4));
-    if (m->row_scaled) TZH_TRY(get((void **)&m->rexp, (size_t)T * 4));
     TZH_TRY(get((void **)&m->tok_ids, (size_t)T * 4));
     TZH_TRY(get((void **)&m->tok_pos, (size_t)T * 4));
     TZH_TRY(get((void **)&m->meta, (size_t)(2 * B + 1) * 4));
@@ -941,20 +936,13 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
                 return tzh_fail(TZH_ERR_INVALID_ARGS, "layer %d: weight format %d cannot run with activation type %d", li,
                                 l->fmt, act);
         float *const hf = (float *)m->h, *const h1f = (float *)m->h1;
-        // row-scaled int8 GEMMs (set_range): the row exponents of input x [T, k]
+        // row-scaled int8 GEMMs when the weights do not bound their inputs
+        // inside the split's range (set_range)
         const bool rs = m->row_scaled && act == TZH_F32;
-        auto rexp_of = [&](const void *x, int64_t k, const int **e) -> int {
-            *e = nullptr;
-            if (!rs) return TZH_OK;
-            *e = m->rexp;
-            return tzh_row_exp_launch(st, (const float *)x, T, k, m->rexp);
-        };
-        const int *ex = nullptr;
         TZH_TRY(stage("qkv", [&]() {
             if (d.qkv.fmt == TZH_WF_F32) return linear_f32w(st, hf, d.qkv, (float *)m->qkv, T, H, 3 * H, -1, nullptr);
-            TZH_TRY(rexp_of(m->h, H, &ex));
             return tzh_linear_codes_launch(st, cus, m->h, act, d.qkv.w, d.qkv.fmt, d.qkv.s, d.qkv.b, m->qkv, act, T,
-                                           H, 3 * H, 3 * H, TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f, nullptr, 0, ex);
+                                           H, 3 * H, 3 * H, TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f, nullptr, 0, rs);
         }));
         TZH_TRY(stage("attention", [&]() {
             return tzh_attention_launch(st, m->ctx->num_cus, m->ctx->work_queue, m->qkv, m->attn, act, d_cu, d_order,
@@ -965,27 +953,24 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
                 TZH_TRY(linear_f32w(st, (const float *)m->attn, d.o, (float *)m->inter, T, H, H, -1, hf));
                 return layernorm_rows(st, (const float *)m->inter, d.ln1_g, d.ln1_b, h1f, T, H, eps);
             }
-            TZH_TRY(rexp_of(m->attn, H, &ex));
             return tzh_linear_codes_launch(st, cus, m->attn, act, d.o.w, d.o.fmt, d.o.s, d.o.b, m->h1, act, T, H, H,
                                            H, TZH_EPI_BIAS_RES_LN, m->h, d.ln1_g, d.ln1_b, eps, m->ln_ws,
-                                           m->ln_ws_rows, ex);
+                                           m->ln_ws_rows, rs);
         }));
         TZH_TRY(stage("ffn1_gelu", [&]() {
             if (d.ffn1.fmt == TZH_WF_F32) return linear_f32w(st, h1f, d.ffn1, (float *)m->inter, T, H, 1536, TZH_OP_GELU, nullptr);
-            TZH_TRY(rexp_of(m->h1, H, &ex));
             return tzh_linear_codes_launch(st, cus, m->h1, act, d.ffn1.w, d.ffn1.fmt, d.ffn1.s, d.ffn1.b, m->inter,
                                            act, T, H, 1536, 1536, TZH_EPI_BIAS_GELU, nullptr, nullptr, nullptr, 0.0f,
-                                           nullptr, 0, ex);
+                                           nullptr, 0, rs);
         }));
         TZH_TRY(stage("ffn2_ln", [&]() {
             if (d.ffn2.fmt == TZH_WF_F32) {
                 TZH_TRY(linear_f32w(st, (const float *)m->inter, d.ffn2, (float *)m->attn, T, 1536, H, -1, h1f));
                 return layernorm_rows(st, (const float *)m->attn, d.ln2_g, d.ln2_b, hf, T, H, eps);
             }
-            TZH_TRY(rexp_of(m->inter, 1536, &ex));
             return tzh_linear_codes_launch(st, cus, m->inter, act, d.ffn2.w, d.ffn2.fmt, d.ffn2.s, d.ffn2.b, m->h,
                                            act, T, 1536, H, H, TZH_EPI_BIAS_RES_LN, m->h1, d.ln2_g, d.ln2_b, eps,
-                                           m->ln_ws, m->ln_ws_rows, ex);
+                                           m->ln_ws, m->ln_ws_rows, rs);
         }));
     }
     if (outputs) {

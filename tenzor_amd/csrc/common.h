@@ -162,6 +162,14 @@ __device__ __forceinline__ void lane_swap16(uint32_t &a, uint32_t &b) {
 }
 #endif
 
+// The value of another lane of the wave by a DPP lane pattern (gfx9
+// encodings): 0xB1 quad_perm [1,0,3,2] (lane ^ 1), 0x4E quad_perm [2,3,0,1]
+// (lane ^ 2), 0x141 row_half_mirror (lane 7 - i of each group of eight).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
 // Maximum over the four lanes l % 16 + 16j (j = 0..3), left in all four:
 // two row swaps instead of LDS-routed shuffles.
 __device__ __forceinline__ float max_over_rows(float x) {

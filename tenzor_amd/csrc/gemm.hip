@@ -14,11 +14,13 @@
 //
 // f32 activations enter the MFMA as f16 halves hi + lo.  So that this is the
 // reference's f32 arithmetic for rows of any scale (f16 alone spans 2^-24 ..
-// 65504), row_exp_kernel first finds each row's largest magnitude and an
-// exponent e that puts it in [2^14, 2^15); the GEMM splits X[t,:] * 2^e[t]
-// and multiplies the sums by 2^-e[t] before the scale and bias.  Both steps
-// are exact (v_ldexp_f32), so the products carry the split's 2^-22 relative
-// residual for every value within 2^17 of its row's largest.
+// 65504), the GEMM runs row-scaled: it splits X[t,:] * 2^e with e an exact
+// power-of-two exponent per row that it chooses stage by stage from the
+// row's largest magnitude (lowered, with the sums rescaled exactly, when a
+// later stage holds larger values), and multiplies the sums by 2^-e before
+// the scale and bias (linear_pipe_kernel in gemm_pipe.hip).  So the products
+// carry the split's 2^-22 relative residual for every value within 2^17 of
+// its row's largest.
 #include "common.h"
 
 #include <algorithm>
@@ -30,47 +32,7 @@ int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t 
                             int32_t w_format, const uint16_t *scale, const float *bias, void *c, int32_t c_dtype,
                             int64_t m, int64_t k, int64_t n, int64_t n_valid, int32_t epilogue, const void *res,
                             const float *gamma, const float *beta, float eps, float *ln_ws, int64_t ln_ws_rows,
-                            const int *rexp);
-
-namespace {
-
-// e[r] for the rows of a [m, k] (row pitch k): max_j |a[r, j]| * 2^e[r] lies
-// in [2^14, 2^15); 0 for a row of zeros or one whose largest magnitude is not
-// finite (inf and NaN then reach the sums as they are).  One wave per row.
-__global__ void __launch_bounds__(256) row_exp_kernel(const float *__restrict__ a, int64_t m, int64_t k,
-                                                      int *__restrict__ e) {
-    const int lane = threadIdx.x & 63;
-    const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
-    if (r >= m) return;  // whole waves: the shuffles below see every lane
-    const float *row = a + r * k;
-    float mx = 0.0f;
-    if ((k & 3) == 0 && ((uintptr_t)row & 15) == 0) {
-        for (int64_t j = 4 * lane; j < k; j += 256) {
-            const f32x4_t v = *(const f32x4_t *)(row + j);
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-        }
-    } else {
-        for (int64_t j = lane; j < k; j += 64) mx = fmaxf(mx, fabsf(row[j]));
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    if (lane == 0) {
-        int ex = 0;  // mx = f * 2^ex, f in [0.5, 1)
-        (void)frexpf(mx, &ex);
-        e[r] = (mx > 0.0f && isfinite(mx)) ? 15 - ex : 0;
-    }
-}
-
-}  // namespace
-
-// Row exponents of an f32 activation matrix [m, k] (row pitch k) for the
-// row-scaled GEMM (tzh_linear_codes_launch's rexp).
-int tzh_row_exp_launch(hipStream_t st, const float *a, int64_t m, int64_t k, int *e) {
-    if (m <= 0) return TZH_OK;
-    hipLaunchKernelGGL(row_exp_kernel, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, st, a, m, k, e);
-    TZH_LAUNCHED("row_exp_kernel");
-    return TZH_OK;
-}
+                            bool row_scale);
 
 namespace {
 
@@ -123,12 +85,12 @@ int noalloc_scratch(tzh_ctx *ctx, void **out) {
 }
 
 // The workspace a linear needs: tiled codes, then (k % 64 != 0 or a
-// misaligned a) the zero-padded activation rows, then (f32 activations) the
-// row exponents, then (LayerNorm epilogue) the rows of a split partial round.
+// misaligned a) the zero-padded activation rows, then (LayerNorm epilogue)
+// the rows of a split partial round.
 struct Workspace {
-    size_t codes = 0, a = 0, e = 0, ws = 0;
+    size_t codes = 0, a = 0, ws = 0;
     int64_t ws_rows = 0;
-    size_t total() const { return codes + a + e + ws; }
+    size_t total() const { return codes + a + ws; }
 };
 
 Workspace workspace_of(const tzh_ctx *ctx, const void *a, int32_t a_dtype, int64_t m, int64_t k, int64_t n, bool ln) {
@@ -136,7 +98,6 @@ Workspace workspace_of(const tzh_ctx *ctx, const void *a, int32_t a_dtype, int64
     Workspace w;
     w.codes = round256((size_t)n_pad * (size_t)k_pad);
     if (k != k_pad || !al16(a)) w.a = round256((size_t)m * (size_t)k_pad * (a_dtype == TZH_F32 ? 4 : 2));
-    if (a_dtype == TZH_F32) w.e = round256((size_t)m * 4);
     w.ws_rows = ln ? std::min<int64_t>((m + 127) / 128, ctx->num_cus / 3 + 1) * 128 : 0;
     w.ws = (size_t)w.ws_rows * 384 * 4;
     return w;
@@ -190,8 +151,6 @@ int linear(tzh_ctx *ctx, const void *a, int32_t a_dtype, const int8_t *wq, const
     void *scratch = scratch_ptr;
     if (!scratch) TZH_TRY(tzh_ctx_scratch(ctx, wsz.total(), &scratch));
     uint8_t *codes = (uint8_t *)scratch;
-    int *rexp = wsz.e ? (int *)((char *)scratch + codes_bytes + a_bytes) : nullptr;
-    if (rexp) TZH_TRY(tzh_row_exp_launch(ctx->stream, (const float *)a, m, k, rexp));
     TZH_TRY(tzh_tile_codes_w8_launch(ctx->stream, wq, codes, n, k, n_pad, k_pad));
     const void *x = a;
     if (pad_a) {
@@ -207,9 +166,10 @@ int linear(tzh_ctx *ctx, const void *a, int32_t a_dtype, const int8_t *wq, const
         TZH_LAUNCHED("pad_cols_kernel");
         x = xp;
     }
-    float *ws = ws_rows ? (float *)((char *)scratch + codes_bytes + a_bytes + wsz.e) : nullptr;
+    float *ws = ws_rows ? (float *)((char *)scratch + codes_bytes + a_bytes) : nullptr;
     return tzh_linear_codes_launch(ctx->stream, ctx->num_cus, x, a_dtype, codes, TZH_WF_W8T, scale, bias, c, c_dtype,
-                                   m, k_pad, n_pad, n, epilogue, residual, gamma, beta, eps, ws, ws_rows, rexp);
+                                   m, k_pad, n_pad, n, epilogue, residual, gamma, beta, eps, ws, ws_rows,
+                                   a_dtype == TZH_F32);
 }
 
 }  // namespace
@@ -245,8 +205,8 @@ extern "C" int tzh_matmul_w8a32_noalloc(tzh_ctx *ctx, const float *a, const int8
     if (need > kNoAllocScratchBytes)
         return tzh_fail(TZH_ERR_TOO_LARGE,
                         "tzh_matmul_w8a32_noalloc needs %zu bytes of workspace for m=%lld k=%lld n=%lld; its static "
-                        "workspace holds %zu (the tiled codes, n_pad * k_pad bytes, the row exponents, m * 4 bytes, "
-                        "plus m * k_pad * 4 when k %% 64 != 0 or a is not 16-byte aligned)",
+                        "workspace holds %zu (the tiled codes, n_pad * k_pad bytes, plus m * k_pad * 4 when k %% 64 "
+                        "!= 0 or a is not 16-byte aligned)",
                         need, (long long)m, (long long)k, (long long)n, kNoAllocScratchBytes);
     void *ws = nullptr;
     TZH_TRY(noalloc_scratch(ctx, &ws));

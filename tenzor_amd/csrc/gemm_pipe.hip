@@ -302,18 +302,25 @@ __device__ __forceinline__ void store4<float>(float *p, float a, float b, float 
 // pre-normalisation rows of a split LayerNorm tile (see launch_ln).
 enum { EPI_BIAS = 0, EPI_GELU = 1, EPI_LN = 2, EPI_RES = 3 };
 
-// RS (f32 activations only): row t of X enters the split as X[t,:] * 2^e[t]
-// with e = rexp[t] (row_exp_kernel: the row's largest magnitude lands in
-// [2^14, 2^15)), exact, and the epilogue takes the sums times 2^-e[t],
-// exact too; so the hi/lo split keeps its 2^-22 relative residual for every
-// value within 2^17 of its row's largest, whatever the row's scale, and no
-// finite row overflows the f16 halves.
+// Row scaling (RS; f32 activations only).  Each activation row enters the
+// split as X[t,:] * 2^e with e an exact power-of-two exponent per row and
+// unit, chosen online: the split of a stage takes the row's largest
+// magnitude M over that stage (the eight lanes that hold the row's 64
+// values reduce it), and the row's first stage with M > 0 sets e so that
+// M 2^e lies in [2^14, 2^15); a later stage whose maximum would reach 2^15
+// at the current e lowers e to that stage's choice.  Every stage's e goes
+// to LDS (a ring of three), and each wave that accumulates the row
+// multiplies its sums by 2^(e_new - e_old) when e drops, before that
+// stage's MFMAs (exact: a power of two); the epilogue multiplies the sums by
+// 2^-e.  So the hi/lo split keeps its 2^-22 relative residual for every
+// value within 2^17 of the row's largest so far, whatever the row's scale,
+// no finite row overflows the f16 halves, and the sums are f32 sums of the
+// products.  A row's inf or NaN reaches the sums as NaN.
 template <int EPI, typename TC, typename P, typename TR = TC, typename TX = _Float16, bool RS = false>
 __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     const TX *__restrict__ X, const void *__restrict__ Wc, const uint16_t *__restrict__ scale,
     const float *__restrict__ bias, TC *__restrict__ C, int M, int K, int N, const TR *__restrict__ R,
-    const float *__restrict__ gamma, const float *__restrict__ beta, float eps, int ldc, int n_valid,
-    const int *__restrict__ rexp) {
+    const float *__restrict__ gamma, const float *__restrict__ beta, float eps, int ldc, int n_valid) {
     using FX = typename P::FX;
     using FW = typename P::FW;
     constexpr int BM = P::BM, BN = P::BN, BK = P::BK, NS = P::NS, TMF = P::TMF, TNF = P::TNF;
@@ -334,9 +341,12 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     __shared__ __attribute__((aligned(16))) char st3[NS > 3 ? P::STAGE : 16];
     __shared__ __attribute__((aligned(16))) float par[NPAR][MAXN];
     __shared__ float stat0[LN ? BM * P::WN : 1], stat1[LN ? BM * P::WN : 1];
-    // RS: the row exponents of the two most recent units (unit parity),
-    // written by the split of a unit's first stage, read by its epilogue
-    __shared__ int rx[RS ? 2 * BM : 1];
+    // RS: the row exponents stage t was split with, in slot t % 3 (written by
+    // the split of stage t in step t - 1; read in step t by the waves that
+    // multiply the stage, by the split of stage t + 1 (which writes slot
+    // (t + 1) % 3) and, at a unit's last stage, by its epilogue)
+    constexpr int kUnset = -100000;  // no nonzero value in the row yet (its sums are exact zeros)
+    __shared__ int e_st[RS ? 3 : 1][RS ? BM : 1];
     // f16 output goes through LDS, except from the f32-activation LayerNorm
     // kernel, which has no registers to spare for the staging
     constexpr bool STAGED = std::is_same<TC, _Float16>::value && !(XF32 && LN);
@@ -484,28 +494,6 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
             // kept in registers across the whole kernel
             int ln = lane;
             asm volatile("" : "+v"(ln));
-            // RS: the split rows' exponents come from rexp at the split of a
-            // unit's first stage (no ring loads are in flight then: the
-            // compute step that follows issues the next ones), which also
-            // leaves them in rx for the unit's later splits and its epilogue
-            // (the eight lanes of a row are in one wave)
-            int ex[RS ? ROWS_W * GPR / 64 : 1] = {};
-            if constexpr (RS) {
-                const int u = t / KT;
-                if (t % KT == 0) {
-                    const int m0 = unit_m0(u);
-#pragma unroll
-                    for (int c = 0; c < ROWS_W * GPR / 64; c++) {
-                        const int g = c * 64 + ln, r = wu * ROWS_W + g / GPR;
-                        ex[c] = rexp[m0 + r < M ? m0 + r : M - 1];
-                        if (g % GPR == 0) rx[(u & 1) * BM + r] = ex[c];
-                    }
-                } else {
-#pragma unroll
-                    for (int c = 0; c < ROWS_W * GPR / 64; c++)
-                        ex[c] = rx[(u & 1) * BM + wu * ROWS_W + (c * 64 + ln) / GPR];
-                }
-            }
 #pragma unroll
             for (int c = 0; c < ROWS_W * GPR / 64; c++) {
                 const int g = c * 64 + ln, r = wu * ROWS_W + g / GPR, p = g % GPR;
@@ -513,12 +501,29 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                 f32x4_t *c0 = (f32x4_t *)(row + (((2 * p) ^ FX::swz(r)) << 4));
                 f32x4_t *c1 = (f32x4_t *)(row + (((2 * p + 1) ^ FX::swz(r)) << 4));
                 f32x4_t x0 = *c0, x1 = *c1;
-                if constexpr (RS)
+                if constexpr (RS) {
+                    // the row's largest magnitude over this stage: the GPR
+                    // consecutive lanes that hold its groups of eight
+                    float mx = fmaxf(fmaxf(fmaxf(fabsf(x0[0]), fabsf(x0[1])), fmaxf(fabsf(x0[2]), fabsf(x0[3]))),
+                                     fmaxf(fmaxf(fabsf(x1[0]), fabsf(x1[1])), fmaxf(fabsf(x1[2]), fabsf(x1[3]))));
+                    static_assert(GPR == 4 || GPR == 8, "a row's lanes: a quad or an aligned group of eight");
+                    mx = fmaxf(mx, dpp_f32<0xB1>(mx));  // lane ^ 1
+                    mx = fmaxf(mx, dpp_f32<0x4E>(mx));  // lane ^ 2
+                    if constexpr (GPR == 8) mx = fmaxf(mx, dpp_f32<0x141>(mx));  // the other quad of the eight
+                    const int prev = t % KT == 0 ? kUnset : e_st[(t + 2) % 3][r];
+                    int e = prev;
+                    if (mx > 0.0f && mx < INFINITY) {  // zero, inf and NaN rows keep theirs
+                        const int want = 15 - __builtin_amdgcn_frexp_expf(mx);  // mx 2^want in [2^14, 2^15)
+                        e = prev == kUnset || want < prev ? want : prev;
+                    }
+                    if (p == 0) e_st[t % 3][r] = e;
+                    const int es = e == kUnset ? 0 : e;
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
-                        x0[q] = __builtin_amdgcn_ldexpf(x0[q], ex[c]);
-                        x1[q] = __builtin_amdgcn_ldexpf(x1[q], ex[c]);
+                        x0[q] = __builtin_amdgcn_ldexpf(x0[q], es);
+                        x1[q] = __builtin_amdgcn_ldexpf(x1[q], es);
                     }
+                }
                 half8_t hi, lo;
                 split_f32x8(x0, x1, hi, lo);
                 *(half8_t *)c0 = hi;
@@ -535,7 +540,23 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     // null: none
     constexpr int KS = XF32 ? 2 : 1;
     constexpr int XPER = (P::LX + KS - 1) / KS, WPER = (P::LW + KS - 1) / KS;
-    auto compute = [&](const char *buf, char *nb) __attribute__((always_inline)) {
+    auto compute = [&](const char *buf, char *nb, int t) __attribute__((always_inline)) {
+        if constexpr (RS)
+            if (t % KT != 0) {
+                // a row whose exponent dropped at stage t: its sums so far
+                // times 2^(e_t - e_{t-1}), before this stage's products
+#pragma unroll
+                for (int b = 0; b < TMF; b++) {
+                    const int row = wm * TMF * 32 + b * 32 + l31;
+                    const int en = e_st[t % 3][row], ep = e_st[(t + 2) % 3][row];
+                    const int d = ep != kUnset && en != ep ? en - ep : 0;
+                    if (wave_any(d != 0))
+#pragma unroll
+                        for (int a = 0; a < TNF; a++)
+#pragma unroll
+                            for (int q = 0; q < 16; q++) acc[a][b][q] = __builtin_amdgcn_ldexpf(acc[a][b][q], d);
+                }
+            }
         u32x4_t wraw[TNF];
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ks++) {
@@ -583,10 +604,16 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
     auto epilogue = [&](int i) __attribute__((always_inline)) {
         const int m0 = unit_m0(i), n0 = unit_n0(i);
         const bool st32 = STAGED32 && cvec && n0 + BN <= n_valid;  // uniform
-        // RS: the sums of token fragment b times 2^-e of its row
+        // RS: the sums of token fragment b times 2^-e of its row (the
+        // exponent of the unit's last stage)
+        const int tl = (i + 1) * KT - 1;
+        auto neg_e = [&](int b) __attribute__((always_inline)) {
+            const int e = RS ? e_st[tl % 3][wm * TMF * 32 + b * 32 + l31] : 0;
+            return e == kUnset ? 0 : -e;
+        };
         auto unscale = [&](int b) __attribute__((always_inline)) {
             if constexpr (RS) {
-                const int e = -rx[(i & 1) * BM + wm * TMF * 32 + b * 32 + l31];
+                const int e = neg_e(b);
 #pragma unroll
                 for (int a = 0; a < TNF; a++)
 #pragma unroll
@@ -663,7 +690,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
                 int t = m0 + wm * TMF * 32 + b * 32 + l31;
                 t = t < M ? t : M - 1;
                 // RS: the sums times 2^-e of the fragment's row
-                const int ne = RS ? -rx[(i & 1) * BM + wm * TMF * 32 + b * 32 + l31] : 0;
+                const int ne = neg_e(b);
                 float sum = 0.0f;
 #pragma unroll
                 for (int a = 0; a < TNF; a++) {
@@ -804,7 +831,7 @@ __global__ void __launch_bounds__(P::THREADS) linear_pipe_kernel(
         lds_barrier_only();  // every wave's stage s landed (and split); stage s-1 fully read
         const int kt = s % KT;
         const bool more = s + NS - 1 < S;
-        compute(bufs[j], more ? bufs[(j + NS - 1) % NS] : nullptr);
+        compute(bufs[j], more ? bufs[(j + NS - 1) % NS] : nullptr, s);
         if (more) advance();
         // (before this step's epilogue, whose stores the wait would
         // otherwise include, and whose registers the split would add to)
@@ -898,7 +925,7 @@ struct NoDeduce {
 template <int EPI, typename TC, typename P, typename TR = TC, typename TX>
 int launch(hipStream_t st, int num_cus, const TX *x, const void *wc, const uint16_t *scale, const float *bias, TC *c,
            int M, int K, int N, const typename NoDeduce<TR>::type *res, const float *gamma, const float *beta,
-           float eps, int ldc, int n_valid, const int *rexp) {
+           float eps, int ldc, int n_valid, bool rs) {
     const int nbm = (M + P::BM - 1) / P::BM;
     const int nbn = N / P::BN;
     constexpr bool f32_out = std::is_same<TC, float>::value && EPI != EPI_RES && EPI != EPI_LN;
@@ -908,17 +935,20 @@ int launch(hipStream_t st, int num_cus, const TX *x, const void *wc, const uint1
     // (blocks without a unit return at once); beyond that, one per slot.
     const int64_t spread = (int64_t)kXcds * ((nbm + kXcds - 1) / kXcds) * nbn;
     const int grid = spread < slots ? (int)spread : slots;
-    if constexpr (sizeof(TX) == 4) {
-        if (rexp) {
+    // row scaling: every configuration but the 128-row LayerNorm tiles (whose
+    // registers it would spill; launch_ln takes the 64-row ones instead)
+    constexpr bool rs_ok = !(EPI == EPI_LN && P::BM == 128);
+    if constexpr (sizeof(TX) == 4 && rs_ok) {
+        if (rs) {
             hipLaunchKernelGGL((linear_pipe_kernel<EPI, TC, P, TR, TX, true>), dim3(grid), dim3(P::THREADS), 0, st, x,
-                               wc, scale, bias, c, M, K, N, res, gamma, beta, eps, ldc, n_valid, rexp);
+                               wc, scale, bias, c, M, K, N, res, gamma, beta, eps, ldc, n_valid);
             TZH_LAUNCHED("linear_pipe_kernel");
             return TZH_OK;
         }
     }
-    if (rexp) return tzh_fail(TZH_ERR_INVALID_ARGS, "row scaling needs f32 activations");
+    if (rs) return tzh_fail(TZH_ERR_INVALID_ARGS, "row scaling needs f32 activations and a tile that supports it");
     hipLaunchKernelGGL((linear_pipe_kernel<EPI, TC, P, TR, TX, false>), dim3(grid), dim3(P::THREADS), 0, st, x, wc,
-                       scale, bias, c, M, K, N, res, gamma, beta, eps, ldc, n_valid, nullptr);
+                       scale, bias, c, M, K, N, res, gamma, beta, eps, ldc, n_valid);
     TZH_LAUNCHED("linear_pipe_kernel");
     return TZH_OK;
 }
@@ -990,8 +1020,8 @@ __global__ void __launch_bounds__(256) ln_rows_kernel(const float *__restrict__ 
 }
 
 // bias + residual + LayerNorm over 384-wide rows.  Tiled int8 weights with
-// k <= 384 use the short-k configuration (two workgroups per CU, above).
-// Otherwise the 128-row tiles run in
+// k <= 384, and row-scaled calls at any k, use the short-k configuration
+// (two workgroups per CU, above).  Otherwise the 128-row tiles run in
 // whole rounds of one tile per CU slot; when the rows left over for a
 // partial last round would keep only a few CUs busy (at most slots / 3
 // tiles), those tiles are instead cut into 64 x 64, 128 x 64 or 128 x 128
@@ -1003,14 +1033,14 @@ __global__ void __launch_bounds__(256) ln_rows_kernel(const float *__restrict__ 
 template <int WF, typename TC, typename TX>
 int launch_ln(hipStream_t st, int num_cus, const TX *x, const void *wc, const uint16_t *scale, const float *bias,
               TC *c, int M, int K, const TC *res, const float *gamma, const float *beta, float eps, float *ws,
-              int64_t ws_rows, const int *rexp) {
+              int64_t ws_rows, bool rs) {
     using C = Cfgs<WF, (int)sizeof(TX)>;
     constexpr int N = C::Ln::BN, BM = C::Ln::BM;
     constexpr bool f32_out = false;  // LayerNorm outputs are not staged when f32
     constexpr bool staged = std::is_same<TC, _Float16>::value && sizeof(TX) == 2;  // as the kernel decides
-    if (K <= 384)
+    if (K <= 384 || rs)  // row-scaled: the 64-row tiles at any k
         return launch<EPI_LN, TC, typename C::LnShortK>(st, num_cus, x, wc, scale, bias, c, M, K, N, res, gamma, beta,
-                                                        eps, N, N, rexp);
+                                                        eps, N, N, rs);
     const int slots = num_cus * C::Ln::blocks_per_cu(true, staged, f32_out);
     const int panels = (M + BM - 1) / BM;
     const int full = panels / slots * slots;
@@ -1026,20 +1056,19 @@ int launch_ln(hipStream_t st, int num_cus, const TX *x, const void *wc, const ui
     const int m_main = per ? full * BM : M;
     if (m_main > 0)
         TZH_TRY((launch<EPI_LN, TC, typename C::Ln>(st, num_cus, x, wc, scale, bias, c, m_main, K, N, res, gamma, beta,
-                                                     eps, N, N, rexp)));
+                                                     eps, N, N, rs)));
     if (!per) return TZH_OK;
     const TX *xt = x + (size_t)m_main * K;
     const TC *rt = res + (size_t)m_main * N;
-    const int *et = rexp ? rexp + m_main : nullptr;
     if (per == 12)
         TZH_TRY((launch<EPI_RES, float, typename C::Piece64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N,
-                                                                  rt, nullptr, nullptr, 0.f, N, N, et)));
+                                                                  rt, nullptr, nullptr, 0.f, N, N, rs)));
     else if (per == 6)
         TZH_TRY((launch<EPI_RES, float, typename C::Piece128x64, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K,
-                                                                      N, rt, nullptr, nullptr, 0.f, N, N, et)));
+                                                                      N, rt, nullptr, nullptr, 0.f, N, N, rs)));
     else
         TZH_TRY((launch<EPI_RES, float, typename C::Piece128, TC>(st, num_cus, xt, wc, scale, bias, ws, tail_rows, K, N,
-                                                                   rt, nullptr, nullptr, 0.f, N, N, et)));
+                                                                   rt, nullptr, nullptr, 0.f, N, N, rs)));
     hipLaunchKernelGGL(ln_rows_kernel<TC>, dim3((unsigned)((tail_rows + 31) / 32)), dim3(256), 0, st, ws, tail_rows,
                        gamma, beta, eps, c + (size_t)m_main * N);
     TZH_LAUNCHED("ln_rows_kernel");
@@ -1048,13 +1077,13 @@ int launch_ln(hipStream_t st, int num_cus, const TX *x, const void *wc, const ui
 
 template <int WF, int EPI, typename TC, typename TX>
 int launch_bias(hipStream_t st, int num_cus, const TX *x, const void *wc, const uint16_t *scale, const float *bias,
-                TC *c, int M, int K, int N, int ldc, int n_valid, const int *rexp) {
+                TC *c, int M, int K, int N, int ldc, int n_valid, bool rs) {
     using C = Cfgs<WF, (int)sizeof(TX)>;
     if (N % C::Bias::BN == 0)
         return launch<EPI, TC, typename C::Bias>(st, num_cus, x, wc, scale, bias, c, M, K, N, nullptr, nullptr,
-                                                 nullptr, 0.f, ldc, n_valid, rexp);
+                                                 nullptr, 0.f, ldc, n_valid, rs);
     return launch<EPI, TC, typename C::Narrow>(st, num_cus, x, wc, scale, bias, c, M, K, N, nullptr, nullptr, nullptr,
-                                               0.f, ldc, n_valid, rexp);
+                                               0.f, ldc, n_valid, rs);
 }
 
 // int8 codes q[r][j] (n rows of k) -> biased codes u = q + 128 stage-tiled
@@ -1111,13 +1140,13 @@ int tzh_tile_codes_w8_launch(hipStream_t st, const int8_t *q, uint8_t *out, int6
 // entries; C rows are n_valid apart); the bias epilogues run n in chunks of
 // up to 1536 columns.  ln_ws (f32, ln_ws_rows rows of 384; may be null) lets
 // the LayerNorm epilogue split a partial last round of tiles (see
-// launch_ln).  rexp (f32 activations; may be null): the row exponents of
-// row_exp_kernel, which scale each row into the split's range.
+// launch_ln).  row_scale (f32 activations): each row scaled into the
+// split's range by an exact power of two (see linear_pipe_kernel).
 int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t x_dtype, const void *wc,
                             int32_t w_format, const uint16_t *scale, const float *bias, void *c, int32_t c_dtype,
                             int64_t m, int64_t k, int64_t n, int64_t n_valid, int32_t epilogue, const void *res,
                             const float *gamma, const float *beta, float eps, float *ln_ws, int64_t ln_ws_rows,
-                            const int *rexp) {
+                            bool row_scale) {
     if (m < 0 || k <= 0 || n <= 0 || n_valid <= 0 || n_valid > n) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad GEMM shape");
     if (m == 0) return TZH_OK;  // matmul_w8a32.zig:24
     if (m > (int64_t)1 << 30 || k > 65536 || n > 65536) return tzh_fail(TZH_ERR_TOO_LARGE, "GEMM shape too large");
@@ -1134,7 +1163,7 @@ int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t 
     if (w_format != TZH_WF_W8T) return tzh_fail(TZH_ERR_INVALID_ARGS, "unknown weight format %d", w_format);
     if (N % kWtBlock) return tzh_fail(TZH_ERR_INVALID_ARGS, "tiled int8 weights need n %% 384 == 0 (n=%d)", N);
     if (c16 && NV != N) return tzh_fail(TZH_ERR_INVALID_ARGS, "f16 output needs every column (n_valid == n)");
-    if (rexp && !x32) return tzh_fail(TZH_ERR_INVALID_ARGS, "row scaling needs f32 activations");
+    if (row_scale && !x32) return tzh_fail(TZH_ERR_INVALID_ARGS, "row scaling needs f32 activations");
     // one call per (activation type, output type): f(x, c) with typed pointers
     auto typed = [&](auto &&f) -> int {
         if (x32)
@@ -1152,9 +1181,9 @@ int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t 
             TZH_TRY(typed([&](auto xt, auto ct) {
                 using TC = std::remove_pointer_t<decltype(ct)>;
                 return gelu ? launch_bias<TZH_WF_W8T, EPI_GELU, TC>(st, num_cus, xt, wj, sj, bj, ct + j0, M, K, nc, NV,
-                                                                    nv, rexp)
+                                                                    nv, row_scale)
                             : launch_bias<TZH_WF_W8T, EPI_BIAS, TC>(st, num_cus, xt, wj, sj, bj, ct + j0, M, K, nc, NV,
-                                                                    nv, rexp);
+                                                                    nv, row_scale);
             }));
         }
         return TZH_OK;
@@ -1167,7 +1196,7 @@ int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t 
         return typed([&](auto xt, auto ct) {
             using TC = std::remove_pointer_t<decltype(ct)>;
             return launch_ln<TZH_WF_W8T, TC>(st, num_cus, xt, wc, scale, bias, ct, M, K, (const TC *)res, gamma, beta,
-                                             eps, ln_ws, ln_ws_rows, rexp);
+                                             eps, ln_ws, ln_ws_rows, row_scale);
         });
     }
     return tzh_fail(TZH_ERR_INVALID_ARGS, "unknown epilogue %d", epilogue);

@@ -399,7 +399,27 @@ def group_range():
     cg = linear(a, q, s, bias, np.float32, _abi.EPI_BIAS_GELU)
     assert np.isfinite(cg).all()
     assert (np.abs(cg - g) <= 1.13 * 2.0 ** -21 * (mag + np.abs(exact)) + 2.0 ** -20 * np.abs(g) + 1e-37).all()
-    for k in (384, 448):  # the two-workgroup k <= 384 tiles; 128-row tiles with a split last round
+    # rows whose scale changes along k (the row exponent drops at a later
+    # stage, with the sums so far rescaled), rows that start with zeros, and
+    # every epilogue
+    m, k = 70, 448
+    a, q, s = range_problem(36, m, k, 768, 1.0)
+    prof = np.ones((m, k), np.float32)
+    prof[0::5, :64] = 1e-3
+    prof[0::5, 64:] = 1e3           # larger from the second stage on
+    prof[1::5, :192] = 0.0          # zeros, then ordinary values
+    prof[2::5, :] = np.logspace(-20, 20, k).astype(np.float32)  # growing all the way
+    prof[3::5, 200:] = 1e-9         # large first, then tiny
+    a *= prof
+    bias = np.random.default_rng(37).uniform(-0.1, 0.1, 768).astype(np.float32)
+    c = linear(a, q, s, bias, np.float32, _abi.EPI_BIAS)
+    sf = s.view(np.float16).astype(np.float64)
+    exact = (a.astype(np.float64) @ q.astype(np.float64).T) * sf
+    mag = (np.abs(a.astype(np.float64)) @ np.abs(q.astype(np.float64)).T) * sf
+    err = np.abs(c - (exact + bias)) / (mag + np.abs(exact + bias))
+    print(f"  rows changing scale along k: relative error {err.max():.2e}", flush=True)
+    assert np.isfinite(c).all() and err.max() < 2.0 ** -21, float(err.max())
+    for k in (384, 448):  # the two-workgroup tiles (row-scaled LayerNorm GEMMs at any k)
         m = 16 * 128 + 100
         a, q, s = range_problem(34, m, k, 384, 1.0)
         a *= np.logspace(-20, 20, m).astype(np.float32)[:, None]

@@ -107,6 +107,27 @@ inline void lane_swap16(uint32_t &a, uint32_t &b) {
         b = other[0];  // the odd-row partner's a
 }
 inline void wave_lds_order() { emu::wave_barrier(); }
+// v_mov_b32 with a DPP lane pattern, every lane active and every row and
+// bank enabled: quad_perm (ctrl < 0x100), row_mirror (0x140) and
+// row_half_mirror (0x141); others abort
+inline int __builtin_amdgcn_update_dpp(int, int src, int ctrl, int, int, bool) {
+    const int lane = emu::lane_id();
+    int from;
+    if (ctrl < 0x100)
+        from = (lane & ~3) | ((ctrl >> (2 * (lane & 3))) & 3);
+    else if (ctrl == 0x140)
+        from = (lane & ~15) | (15 - (lane & 15));
+    else if (ctrl == 0x141)
+        from = (lane & ~7) | (7 - (lane & 7));
+    else
+        __builtin_trap();
+    std::memcpy(emu::wave_slot(lane), &src, sizeof src);
+    emu::wave_barrier();
+    int r;
+    std::memcpy(&r, emu::wave_slot(from), sizeof r);
+    emu::wave_barrier();
+    return r;
+}
 inline bool wave_any(bool p) {  // every lane of the emulated wave is active
     const int lane = emu::lane_id();
     *(unsigned char *)emu::wave_slot(lane) = p ? 1 : 0;
@@ -131,6 +152,12 @@ inline T emu_readfirstlane(T x, const char *file, int line) {
 }
 #define __builtin_amdgcn_readfirstlane(x) emu_readfirstlane((x), __FILE__, __LINE__)
 #define __builtin_amdgcn_ldexpf(x, e) ldexpf((x), (e))
+// v_frexp_exp_i32_f32: the exponent of frexp (x = f 2^e, f in [0.5, 1))
+inline int __builtin_amdgcn_frexp_expf(float x) {
+    int e = 0;
+    (void)frexpf(x, &e);
+    return e;
+}
 
 #define threadIdx (emu::g_threadIdx)
 #define blockIdx (emu::g_blockIdx)

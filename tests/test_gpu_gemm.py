@@ -213,6 +213,35 @@ def test_linear_w8_epilogues_over_the_f32_range(ctx, scale):
         assert np.isfinite(c).all() and (np.abs(c - ref) <= tol).all(), (m, k, float((np.abs(c - ref) / tol).max()))
 
 
+@pytest.mark.parametrize("epi", [_abi.EPI_BIAS, _abi.EPI_BIAS_GELU])
+def test_rows_changing_scale_along_k(ctx, epi):
+    """Row scaling is chosen stage by stage: rows that grow by 1e6 after
+    their first 64 values, rows of zeros then ordinary values, rows growing
+    from 1e-20 to 1e20 along k, rows large then tiny; the sums accumulated
+    so far are rescaled exactly when a row's exponent drops."""
+    m, k, n = 700, 448, 768
+    a, q, s, bias = make_problem(45, m, k, n)
+    prof = np.ones((m, k), np.float32)
+    prof[0::5, :64] = 1e-3
+    prof[0::5, 64:] = 1e3
+    prof[1::5, :192] = 0.0
+    prof[2::5, :] = np.logspace(-20, 20, k).astype(np.float32)
+    prof[3::5, 200:] = 1e-9
+    a = a * prof
+    c = gpu_linear(ctx, a, q, s, bias, torch.float32, epi)
+    lin = oracle.matmul_w8a32(a, q, s, bias)
+    sf = s.view(np.float16).astype(np.float64)
+    exact = (a.astype(np.float64) @ q.astype(np.float64).T) * sf + bias
+    mag = (np.abs(a.astype(np.float64)) @ np.abs(q.astype(np.float64)).T) * sf
+    assert np.isfinite(c).all()
+    if epi == _abi.EPI_BIAS:
+        assert (np.abs(c - exact) / (mag + np.abs(exact))).max() < 2.0 ** -21
+    else:
+        ref = oracle.gelu(lin)
+        tol = 1.13 * 2.0 ** -21 * (mag + np.abs(exact)) + 2.0 ** -20 * np.abs(ref) + 1e-37
+        assert (np.abs(c - ref) <= tol).all()
+
+
 def test_matmul_w8a32_rows_of_every_scale(ctx):
     """One matrix whose rows span 1e-30 .. 1e30, a zero row and a row of
     f32 subnormals: each row keeps its own relative accuracy."""
