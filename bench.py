@@ -115,6 +115,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--forward-only", action="store_true",
+                    help="leave configs 2 and 3 out of the forward line (for kernel traces of the forward alone)")
     ap.add_argument("--cpu-sample-stride", type=int, default=1, help="every k-th sequence of the batch")
     ap.add_argument("--workload", choices=["forward", "chain", "gemm3", "embed-docs"], default="forward")
     ap.add_argument("--precision", choices=["fp32", "fp16"], default="fp32",
@@ -288,7 +290,7 @@ def main():
     torch.cuda.empty_cache()
     # configs 2 and 3 in the same run (their own workloads print the full
     # line): value, time per step, roofline fraction and CPU baseline each
-    for name, fn in (("chain", chain), ("gemm3", gemm3)):
+    for name, fn in () if args.forward_only else (("chain", chain), ("gemm3", gemm3)):
         sub = fn(argparse.Namespace(steps=args.steps, warmup=args.warmup, no_cpu_baseline=args.no_cpu_baseline))
         line[name] = {k: sub[k] for k in ("metric", "value", "unit", "ms_per_step", "dtype", "config", "roofline")}
         if "kernels" in sub:

@@ -15,8 +15,8 @@ Subcommands:
 
     python bench_profile.py gemm
         The config-3 GEMM pair (T = 65536: 384 -> 1536 + GELU, then
-        1536 -> 384 + residual + LayerNorm; f16 activations, int8 weights in
-        the model's device format) three times, for `rocprofv3 --pmc` passes.
+        1536 -> 384 + residual + LayerNorm; f32 activations, int8 weights,
+        through tzh_linear_w8) three times, for `rocprofv3` passes.
 
     python bench_profile.py counters DIR [DIR ...]
         Per-kernel averages of the counters in those runs' CSV output, with
@@ -158,7 +158,7 @@ COMMANDS = """Commands (on one MI355X; rocprofv3 runs from /tmp with TMPDIR=/tmp
 PYTHONPATH=<repo>, the program right after `--`):
 
     rocprofv3 --kernel-trace --stats --output-format csv -d <out>/trace -o fwd -- \\
-        python3 <repo>/bench.py --steps 5 --warmup 2 --no-cpu-baseline > <out>/trace.log
+        python3 <repo>/bench.py --steps 5 --warmup 2 --no-cpu-baseline --forward-only > <out>/trace.log
     rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/fetch -o f -- \\
         python3 <repo>/bench_profile.py run
     rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/write -o w -- \\
