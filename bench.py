@@ -46,6 +46,8 @@ KERNELS = {
     "ffn1_gelu": "linear_pipe_kernel bias+GELU, 384 -> 1536",
     "ffn2_ln": "linear_pipe_kernel bias+residual+LayerNorm, 1536 -> 384, + split last round "
                "(linear_pipe_kernel residual pieces, ln_rows_kernel)",
+    "ffn": "mlp_fused_kernel: the feed-forward block in one kernel, 384 -> 1536 + GELU -> 384 + residual + "
+           "LayerNorm, the intermediate kept on chip",
     "embed_ln": "embed_ln_kernel", "pack_ids": "pack_ids_kernel", "cls_l2": "cls_l2_kernel",
 }
 
@@ -99,6 +101,11 @@ def stage_work(T, lengths, es=4):
         weights = N * K + N * (2 + 4) + (2 * N * 4 if res else 0)
         moved = T * K * es + T * N * es + (T * N * es if res else 0) + weights
         w[name] = (2.0 * T * K * N, float(T * per_tok + weights), float(moved))
+    # the fused feed-forward block: the two linears' op-boundary bytes (the
+    # reference writes and re-reads the intermediate); it moves X in, Y out,
+    # X again as the residual, and reads its f16 weight pack
+    f1, f2 = w["ffn1_gelu"], w["ffn2_ln"]
+    w["ffn"] = (f1[0] + f2[0], f1[1] + f2[1], float(3 * T * H * es + 2 * (2 * H * I)))
     L2 = float((lengths.astype(np.float64) ** 2).sum())
     # per head QK^T and PV: 2 * L^2 * 32 flops each; 12 heads
     w["attention"] = (4.0 * L2 * H, float(T * 6144), float(T * 3 * H * es + T * H * es))
@@ -256,6 +263,11 @@ def main():
             "algorithmic_flops": int(dom["flops"]),
             "bytes_moved": int(dom["bytes16"]),
             "moved_GBps": round(dom["bytes16"] / secs / 1e9, 1),
+            # the f32 products run as f16 MFMAs on the hi/lo halves: two per
+            # product in the GEMMs, three in attention; the matrix cores'
+            # share of that work
+            "mfma_frac_f32_split": round((3.0 if dom_name == "attention" else 2.0) * dom["flops"] / secs / 1e12 /
+                                         F16_PEAK_TFLOPS, 4),
         },
         "forward_roofline_frac": round(fwd_roof_us / (ms_per_step * 1e3), 4),
         "stage_us": {k: round(v["avg_us"], 1) for k, v in stages.items()},

@@ -25,7 +25,8 @@ Subcommands:
 Dispatches are mapped to forward stages by kernel and launch order: both
 LayerNorm GEMMs are linear_pipe_kernel<2> (with f32 activations the k = 384
 one has a tile configuration of its own); the one launched after attention
-is attn_out_ln and the one after ffn1_gelu is ffn2_ln.  The
+is attn_out_ln and the one after ffn1_gelu is ffn2_ln; mlp_fused_kernel, the
+fused feed-forward block, is the stage ffn.  The
 pieces of a split partial round (the residual-only GEMM) and their row
 LayerNorm belong to the LayerNorm GEMM launched just before them.
 
@@ -44,7 +45,7 @@ import re
 import sys
 
 CAL_BYTES = 1 << 30
-STAGES = ("pack_ids", "embed_ln", "qkv", "attention", "attn_out_ln", "ffn1_gelu", "ffn2_ln", "cls_l2")
+STAGES = ("pack_ids", "embed_ln", "qkv", "attention", "attn_out_ln", "ffn", "ffn1_gelu", "ffn2_ln", "cls_l2")
 
 
 def epi_of(kernel: str) -> int | None:
@@ -66,6 +67,8 @@ def stage_of(kernel: str, prev: str | None) -> str | None:
         return "attention"
     if "cls_l2_kernel" in kernel:
         return "cls_l2"
+    if "mlp_fused_kernel" in kernel:
+        return "ffn"
     epi = epi_of(kernel)
     if epi == 0:
         return "qkv"
@@ -229,6 +232,8 @@ def summarize(trace: str | None, fetch: str | None, write: str | None, bench_log
         out.append("|---|---:|---:|---:|---:|")
         for st in STAGES:
             n, us = t.get(st, (0, float("nan")))
+            if n == 0 and st not in fs and st not in ws:
+                continue  # a stage this precision does not run (fused or split feed-forward)
             rd = fs[st] * 1024 * f_scale if st in fs and f_scale else None
             wr = ws[st] * 1024 * w_scale if st in ws and w_scale else None
             data[key][st] = {"instances": n, "avg_us": None if n == 0 else round(us, 2),
@@ -257,8 +262,10 @@ def summarize(trace: str | None, fetch: str | None, write: str | None, bench_log
                                          "ms_per_step": steps[prec]}
                                   for prec, key in (("fp32", "stages"), ("fp16", "stages_fp16"))}
     if trace:
-        out += ["Both LayerNorm GEMMs are linear_pipe_kernel<2> (in the fp32 forward the O-projection",
-                "with its own tile configuration); the rows above separate them by launch order.",
+        out += ["The fp32 forward runs each feed-forward block as one kernel (mlp_fused_kernel, stage",
+                "ffn); the fp16 forward runs the GEMM pair (ffn1_gelu, ffn2_ln).  Both LayerNorm GEMMs",
+                "are linear_pipe_kernel<2> (in the fp32 forward the O-projection with its own tile",
+                "configuration); the rows above separate them by launch order.",
                 "The counter runs (bench_profile.py run) make one fp32",
                 "forward.  rocprofv3's own kernel summary of the trace run (bench.py: the fp16",
                 "forward first, 5 timed + 2 warmup, then the fp32 one, 5 timed + 2 warmup + 3",

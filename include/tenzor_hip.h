@@ -432,6 +432,24 @@ int tzh_arctic_last_launch_count(tzh_model *model);
 int tzh_arctic_set_precision(tzh_model *model, int32_t dtype);
 int tzh_arctic_precision(tzh_model *model, int32_t *dtype);
 
+/* The feed-forward block of one encoder layer (replaces feedForward,
+ * arctic.zig:760-811): output = LayerNorm(input + (GELU(input W1^T s1 + b1)
+ * W2^T s2 + b2)) with the layer's intermediate and output linears and its
+ * output LayerNorm, for device f32 input and output [seq_len, hidden]
+ * (16-byte aligned, not overlapping; layer in [0, num_hidden_layers)),
+ * in f32 whatever tzh_arctic_set_precision chose, enqueued on the model's
+ * stream.  A layer whose two linears are int8 runs it as one kernel, the
+ * 1536-wide intermediate kept on chip, unless the model's weights call for
+ * row scaling; other layers run the GEMM pair. */
+int tzh_arctic_feed_forward(tzh_model *model, int32_t layer, const float *input, float *output, int64_t seq_len);
+
+/* Fused feed-forward switch (no counterpart in the reference): enable = 0
+ * makes the forward and tzh_arctic_feed_forward run every feed-forward block
+ * as the GEMM pair (GELU epilogue, then residual + LayerNorm epilogue) even
+ * where the single kernel applies; nonzero (the default) restores it.  The
+ * two agree to the f32 rounding of their different summation orders. */
+int tzh_arctic_set_ffn_fusion(tzh_model *model, int32_t enable);
+
 /* Launch tracing (no counterpart in the reference, whose CPU path has no
  * kernels to time): with timing enabled (enable = n >= 1), every later
  * forward records a HIP event on the model's stream before its first and
@@ -445,7 +463,8 @@ int tzh_arctic_set_timing(tzh_model *model, int32_t enable);
  * us[i] (microseconds between the events around stage i, divided by the
  * times it was issued) and names[i]
  * (static stage names: "pack_ids", "embed_ln", "qkv", "attention",
- * "attn_out_ln", "ffn1_gelu", "ffn2_ln", "cls_l2", "hidden_f32"), at most
+ * "attn_out_ln", "ffn" (the fused feed-forward kernel) or "ffn1_gelu" and
+ * "ffn2_ln" (the GEMM pair), "cls_l2", "hidden_f32"), at most
  * `capacity` entries; *count = number of launches (0 if the last forward was
  * not timed).  Waits for that forward to finish.  Either array may be NULL. */
 int tzh_arctic_launch_times(tzh_model *model, float *us, const char **names, int32_t capacity, int32_t *count);

@@ -161,6 +161,8 @@ PROTOTYPES = {
     "tzh_arctic_set_timing": (C.c_int, [vp, i32]),
     "tzh_arctic_set_precision": (C.c_int, [vp, i32]),
     "tzh_arctic_precision": (C.c_int, [vp, C.POINTER(i32)]),
+    "tzh_arctic_feed_forward": (C.c_int, [vp, i32, vp, vp, i64]),
+    "tzh_arctic_set_ffn_fusion": (C.c_int, [vp, i32]),
     "tzh_arctic_launch_times": (C.c_int, [vp, C.POINTER(f32), C.POINTER(C.c_char_p), i32, C.POINTER(i32)]),
     "tzh_tenzor_name_hash": (C.c_uint64, [C.c_char_p, i64]),
     "tzh_tenzor_open": (C.c_int, [C.c_char_p, pp]),

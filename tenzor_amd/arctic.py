@@ -67,6 +67,11 @@ class ModelWeights:
             raise ValueError(f"precision must be float32 or float16, not {dtype!r}")
         check(lib().tzh_arctic_set_precision(self.handle, codes[dtype]))
 
+    def set_ffn_fusion(self, enable: bool) -> None:
+        """Run each feed-forward block as one kernel where it applies (the
+        default) or, with False, as the GEMM pair (no reference counterpart)."""
+        check(lib().tzh_arctic_set_ffn_fusion(self.handle, 1 if enable else 0))
+
     @property
     def precision(self) -> str:
         d = C.c_int32()
@@ -106,6 +111,18 @@ def forward(output, token_ids, weights: ModelWeights, ctx: Context | None = None
         raise ValueError("output must hold hidden_size floats")
     check(lib().tzh_arctic_forward(weights.handle, C.c_void_p(output.data_ptr()),
                                    C.c_void_p(token_ids.data_ptr()), int(token_ids.numel())))
+
+
+def feedForward(output, input, weights: ModelWeights, layer: int, seq_len: int) -> None:
+    """arctic.feedForward (arctic.zig:760-811) of encoder layer `layer`:
+    output = LayerNorm(input + GELU(input W1^T + b1) W2^T + b2) for device
+    f32 tensors input and output of seq_len * hidden_size floats (distinct
+    buffers), in f32."""
+    n = int(seq_len) * weights.config.hidden_size
+    if input.numel() < n or output.numel() < n:
+        raise ValueError("input and output must hold seq_len * hidden_size floats")
+    check(lib().tzh_arctic_feed_forward(weights.handle, int(layer), C.c_void_p(input.data_ptr()),
+                                        C.c_void_p(output.data_ptr()), int(seq_len)))
 
 
 def forwardBatch(outputs, ids, lengths, weights: ModelWeights, ctx: Context | None = None) -> None:

@@ -19,7 +19,7 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libtenzor_hip.so"
 SOURCES = ["runtime.cpp", "safetensors.cpp", "ew.hip", "gemm.hip", "gemm_pipe.hip", "ew_jit.cpp", "attention.hip", "arctic.hip",
-           "tokenizer.cpp", "embed.hip", "tenzor_file.cpp", "gemm_fp.hip"]
+           "tokenizer.cpp", "embed.hip", "tenzor_file.cpp", "gemm_fp.hip", "mlp.hip"]
 
 # -ffp-contract=off: every multiply and add rounds separately unless a kernel
 # asks for an FMA explicitly (bit-exact elementwise chains).

@@ -36,6 +36,11 @@ int tzh_linear_codes_launch(hipStream_t st, int num_cus, const void *x, int32_t 
                             bool row_scale);
 int tzh_attention_launch(hipStream_t st, int num_cus, unsigned *queue, const void *qkv, void *out, int32_t dtype,
                          const int *cu_seqlens, const int *order, int batch, int n_heads, int hidden);
+size_t tzh_mlp_pack_bytes();
+int tzh_mlp_pack_launch(hipStream_t st, const void *w1, const void *w2, void *out);
+int tzh_mlp_fused_launch(hipStream_t st, int num_cus, const float *x, const void *pack, const uint16_t *s1,
+                         const float *b1, const uint16_t *s2, const float *b2, const float *gamma, const float *beta,
+                         float eps, float *y, int64_t t);
 
 namespace {
 
@@ -212,6 +217,9 @@ struct DevLinear {
 struct DevLayer {
     DevLinear qkv, o, ffn1, ffn2;
     float *ln1_g = nullptr, *ln1_b = nullptr, *ln2_g = nullptr, *ln2_b = nullptr;
+    // both feed-forward linears int8: their codes widened to f16 in the
+    // fragment order of the fused feed-forward kernel (mlp.hip)
+    void *mlp = nullptr;
 };
 
 }  // namespace
@@ -239,6 +247,9 @@ struct tzh_model {
     // attention's split inputs (|q| log2(e)/sqrt(32), |k|, |v|) over the layers
     bool row_scaled = false;
     float attn_bound = 0.0f;
+    // f32 forwards run the feed-forward block as one kernel (mlp.hip) where
+    // the layer has its pack and no row scaling (tzh_arctic_set_ffn_fusion)
+    bool fuse_ffn = true;
     uint32_t *tok_ids = nullptr;
     int32_t *tok_pos = nullptr;
     int *meta = nullptr;  // device: cu[batch+1] | order[batch]
@@ -463,6 +474,37 @@ int layernorm_rows(hipStream_t st, const float *x, const float *g, const float *
     return TZH_OK;
 }
 
+// The feed-forward block of layer d (feedForward, arctic.zig:760-811), y =
+// LayerNorm(x + GELU(x W1^T + b1) W2^T + b2) for x, y [T, 384] in the
+// activation type act: one kernel (mlp.hip) in f32 when both linears are
+// int8 and their inputs need no row scaling, else the GEMM pair through the
+// workspace's intermediate (`part` 1: the GELU GEMM, 2: the LayerNorm GEMM;
+// an f32 second linear writes its pre-norm rows to the workspace's attn).
+bool ffn_fused(const tzh_model *m, const DevLayer &d, int32_t act, bool rs) {
+    return m->fuse_ffn && d.mlp && act == TZH_F32 && !rs;
+}
+
+int ffn_part(tzh_model *m, const DevLayer &d, hipStream_t st, int32_t act, bool rs, const void *x, void *y, int64_t T,
+             int part) {
+    const int cus = m->ctx->num_cus;
+    const float eps = m->cfg.layer_norm_eps;
+    if (part == 0)
+        return tzh_mlp_fused_launch(st, cus, (const float *)x, d.mlp, d.ffn1.s, d.ffn1.b, d.ffn2.s, d.ffn2.b, d.ln2_g,
+                                    d.ln2_b, eps, (float *)y, T);
+    if (part == 1) {
+        if (d.ffn1.fmt == TZH_WF_F32)
+            return linear_f32w(st, (const float *)x, d.ffn1, (float *)m->inter, T, H, 1536, TZH_OP_GELU, nullptr);
+        return tzh_linear_codes_launch(st, cus, x, act, d.ffn1.w, d.ffn1.fmt, d.ffn1.s, d.ffn1.b, m->inter, act, T, H,
+                                       1536, 1536, TZH_EPI_BIAS_GELU, nullptr, nullptr, nullptr, 0.0f, nullptr, 0, rs);
+    }
+    if (d.ffn2.fmt == TZH_WF_F32) {
+        TZH_TRY(linear_f32w(st, (const float *)m->inter, d.ffn2, (float *)m->attn, T, 1536, H, -1, (const float *)x));
+        return layernorm_rows(st, (const float *)m->attn, d.ln2_g, d.ln2_b, (float *)y, T, H, eps);
+    }
+    return tzh_linear_codes_launch(st, cus, m->inter, act, d.ffn2.w, d.ffn2.fmt, d.ffn2.s, d.ffn2.b, y, act, T, 1536, H,
+                                   H, TZH_EPI_BIAS_RES_LN, x, d.ln2_g, d.ln2_b, eps, m->ln_ws, m->ln_ws_rows, rs);
+}
+
 int ensure_workspace(tzh_model *m, int64_t tokens, int batch, size_t es) {
     if (tokens <= m->cap_tokens && batch <= m->cap_batch && es <= m->cap_es) return TZH_OK;
     TZH_HIP(hipStreamSynchronize(m->ctx->stream));
@@ -618,7 +660,12 @@ int upload_weights(tzh_model *m, const tzh_arctic_weights *w) {
         TZH_TRY(upload<float>(m, &d.ln1_b, a.output_ln_beta, H));
         TZH_TRY(upload<float>(m, &d.ln2_g, f.output_ln_gamma, H));
         TZH_TRY(upload<float>(m, &d.ln2_b, f.output_ln_beta, H));
+        if (d.ffn1.fmt == TZH_WF_W8T && d.ffn2.fmt == TZH_WF_W8T) {
+            TZH_TRY(dev_alloc(m, &d.mlp, tzh_mlp_pack_bytes()));
+            TZH_TRY(tzh_mlp_pack_launch(m->ctx->stream, d.ffn1.w, d.ffn2.w, d.mlp));
+        }
     }
+    TZH_HIP(hipStreamSynchronize(m->ctx->stream));
     set_range(m, w);
     return TZH_OK;
 }
@@ -957,21 +1004,12 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
                                            H, TZH_EPI_BIAS_RES_LN, m->h, d.ln1_g, d.ln1_b, eps, m->ln_ws,
                                            m->ln_ws_rows, rs);
         }));
-        TZH_TRY(stage("ffn1_gelu", [&]() {
-            if (d.ffn1.fmt == TZH_WF_F32) return linear_f32w(st, h1f, d.ffn1, (float *)m->inter, T, H, 1536, TZH_OP_GELU, nullptr);
-            return tzh_linear_codes_launch(st, cus, m->h1, act, d.ffn1.w, d.ffn1.fmt, d.ffn1.s, d.ffn1.b, m->inter,
-                                           act, T, H, 1536, 1536, TZH_EPI_BIAS_GELU, nullptr, nullptr, nullptr, 0.0f,
-                                           nullptr, 0, rs);
-        }));
-        TZH_TRY(stage("ffn2_ln", [&]() {
-            if (d.ffn2.fmt == TZH_WF_F32) {
-                TZH_TRY(linear_f32w(st, (const float *)m->inter, d.ffn2, (float *)m->attn, T, 1536, H, -1, h1f));
-                return layernorm_rows(st, (const float *)m->attn, d.ln2_g, d.ln2_b, hf, T, H, eps);
-            }
-            return tzh_linear_codes_launch(st, cus, m->inter, act, d.ffn2.w, d.ffn2.fmt, d.ffn2.s, d.ffn2.b, m->h,
-                                           act, T, 1536, H, H, TZH_EPI_BIAS_RES_LN, m->h1, d.ln2_g, d.ln2_b, eps,
-                                           m->ln_ws, m->ln_ws_rows, rs);
-        }));
+        if (ffn_fused(m, d, act, rs)) {
+            TZH_TRY(stage("ffn", [&]() { return ffn_part(m, d, st, act, rs, m->h1, m->h, T, 0); }));
+        } else {
+            TZH_TRY(stage("ffn1_gelu", [&]() { return ffn_part(m, d, st, act, rs, m->h1, m->h, T, 1); }));
+            TZH_TRY(stage("ffn2_ln", [&]() { return ffn_part(m, d, st, act, rs, m->h1, m->h, T, 2); }));
+        }
     }
     if (outputs) {
         TZH_TRY(stage("cls_l2", [&]() -> int {
@@ -1102,6 +1140,37 @@ extern "C" int tzh_arctic_set_precision(tzh_model *m, int32_t dtype) {
         return tzh_fail(TZH_ERR_UNSUPPORTED_DTYPE, "activation precision must be F32 or F16 (got %d)", dtype);
     m->act = dtype;
     return TZH_OK;
+}
+
+extern "C" int tzh_arctic_set_ffn_fusion(tzh_model *m, int32_t enable) {
+    tzh_clear_error();
+    if (!m) return tzh_fail(TZH_ERR_INVALID_ARGS, "null model");
+    m->fuse_ffn = enable != 0;
+    return TZH_OK;
+}
+
+extern "C" int tzh_arctic_feed_forward(tzh_model *m, int32_t layer, const float *input, float *output,
+                                       int64_t seq_len) {
+    tzh_clear_error();
+    if (!m) return tzh_fail(TZH_ERR_INVALID_ARGS, "null model");
+    if (layer < 0 || layer >= (int32_t)m->layers.size())
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "layer %d out of range [0, %zu)", layer, m->layers.size());
+    if (seq_len < 0 || seq_len > ((int64_t)1 << 30)) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad token count");
+    if (seq_len == 0) return TZH_OK;
+    if (!input || !output) return tzh_fail(TZH_ERR_INVALID_ARGS, "null input or output");
+    if ((((uintptr_t)input | (uintptr_t)output) & 15) != 0)
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "input and output must be 16-byte aligned");
+    const size_t bytes = (size_t)seq_len * H * 4;
+    if ((const char *)input < (const char *)output + bytes && (const char *)output < (const char *)input + bytes)
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "input and output overlap");
+    TZH_TRY(tzh_ctx_enter(m->ctx));
+    const DevLayer &d = m->layers[(size_t)layer];
+    const bool rs = m->row_scaled;
+    hipStream_t st = m->ctx->stream;
+    if (ffn_fused(m, d, TZH_F32, rs)) return ffn_part(m, d, st, TZH_F32, rs, input, output, seq_len, 0);
+    TZH_TRY(ensure_workspace(m, seq_len, 1, 4));
+    TZH_TRY(ffn_part(m, d, st, TZH_F32, rs, input, output, seq_len, 1));
+    return ffn_part(m, d, st, TZH_F32, rs, input, output, seq_len, 2);
 }
 
 extern "C" int tzh_arctic_precision(tzh_model *m, int32_t *dtype) {

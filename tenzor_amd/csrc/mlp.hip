@@ -1,0 +1,523 @@
+// K7: the encoder layer's feed-forward block in one kernel
+// (feedForward, arctic.zig:760-811):
+//
+//   Y = LayerNorm( X + ( GELU(X W1^T s1 + b1) W2^T s2 + b2 ) )
+//
+// for X [T, 384] f32, W1 int8 codes [1536, 384] with f16 scales s1, W2
+// int8 codes [384, 1536] with scales s2 (matmul_w8a32.zig:40-55: sum of x q,
+// times the row's scale, plus bias), the tanh-form GELU (arctic.zig:750-756)
+// and a two-pass LayerNorm over each 384-wide row (layernorm.zig:26-117).
+// The 1536-wide intermediate H never leaves the chip: the unfused pair writes
+// and re-reads it as f32 (830 MB per layer at 67 590 tokens).
+//
+// Arithmetic is the reference's f32: activations are split into an exact
+// f16 pair x = hi + lo + r (|r| <= 2^-22 |x| for 2^-3 <= |x| < 65504,
+// split_f32x8), weight codes are exact in f16, and each product runs as
+// hi q + lo q through v_mfma_f32_16x16x32_f16 into an f32 accumulator.
+// The caller guarantees that X and H lie inside the split's range (the
+// model checks it from the weights at upload; rows that need scaling run
+// on the unfused GEMMs).
+//
+// Design (gfx950):
+//   - One workgroup of four waves per CU, one wave per SIMD, so every wave
+//     has the SIMD's whole register file (VGPRs and AGPRs).  Each wave owns
+//     16 tokens from the first product to the stored LayerNorm row: their X
+//     as f16 hi/lo halves in VGPRs (the MFMA B operand of the first GEMM),
+//     the raw f32 X in AGPRs (the residual), the 16 x 384 output sums in
+//     VGPRs, and the current chunk of H.  Nothing but the weights goes
+//     through LDS, and no wave waits for another except at the stage
+//     barrier of the weight ring.
+//   - The weights are widened once, at upload, to f16 in the order the
+//     MFMA reads them (mlp_pack_kernel): 1 KiB fragments in which lane l's
+//     16 bytes are its eight A-operand values, so every fragment read is one
+//     conflict-free ds_read_b128.  Widening int8 codes in registers costs
+//     eight VALU ops per fragment; measured with two MFMAs per fragment, that
+//     halved the matrix-core rate (1.0 against 1.7 PFLOP/s).
+//   - The intermediate runs in 24 chunks of 64 features; each chunk is four
+//     24 KiB stages of the ring (W1 rows of the chunk over k 0..191 and
+//     192..383, then W2 columns of the chunk for outputs 0..191 and
+//     192..383), streamed HBM/L2 -> LDS by the direct-to-LDS loads, three
+//     stages ahead.  The stage stream is the same for every 64-token panel.
+//   - The H chunk needs no transpose: the first GEMM's result tile (token
+//     lane % 16, features 4 (lane / 16) + e) is the second GEMM's B operand
+//     for a k order in which MFMA slot 8 g + i holds feature 4 g + i (i < 4)
+//     or 16 + 4 g + i - 4 (i >= 4) of a 32-feature step; the packed W2
+//     fragments follow that k order.  W2's rows are packed so that the
+//     output tile pair (2 j, 2 j + 1) leaves lane (t, g) with outputs 32 j +
+//     8 g .. 32 j + 8 g + 7 of token t: the same columns as the lane's X
+//     registers, so the residual add is lane-local and each LayerNorm row's
+//     statistics reduce over the four lanes of its token with two row swaps.
+#include "pipe.h"
+
+namespace {
+
+constexpr int kD = 384;                      // hidden size
+constexpr int kF = 1536;                     // intermediate size
+constexpr int kFC = 64;                      // intermediate features per chunk
+constexpr int kChunks = kF / kFC;            // 24
+constexpr int kWaves = 4;                    // one per SIMD
+constexpr int kTokW = 16;                    // tokens per wave
+constexpr int kBM = kWaves * kTokW;          // tokens per panel
+constexpr int kFrag = 1024;                  // bytes of one A fragment (64 lanes x 8 f16)
+constexpr int kStageFrags = 24;
+constexpr int kStage = kStageFrags * kFrag;  // 24 KiB
+constexpr int kSPC = 4;                      // stages per chunk
+constexpr int kSPP = kChunks * kSPC;         // stages per panel
+constexpr int kLW = kStageFrags / kWaves;    // direct-to-LDS loads per wave per stage
+constexpr int kXJ = kD / 32;                 // 32-wide k steps of the first GEMM
+constexpr int kYT = kD / 16;                 // 16-row output tiles of the second GEMM
+constexpr int kXL = 2 * kXJ;                 // 16-byte X loads per lane per panel
+constexpr size_t kPackHalves = (size_t)kChunks * kSPC * kStageFrags * (kFrag / 2);
+static_assert(kStageFrags % kWaves == 0, "a stage splits evenly over the waves");
+static_assert(kPackHalves * 2 == (size_t)2 * kD * kF * 2, "the pack holds both weight matrices as f16");
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// The packed f16 layout (halves): stage (c, q) at ((c * 4 + q) * 24 + f) *
+// 512 + lane * 8 + i for fragment f, lane l = 16 g + rho:
+//   q = 0, 1 (first GEMM, k steps j = 6 q + f / 4, feature tile ft = f % 4):
+//       W1[64 c + 16 ft + rho][32 j + 8 g + i]
+//   q = 2, 3 (second GEMM, output tile ot = 12 (q - 2) + f / 2, k step
+//       jj = f % 2): W2[w2_row(ot, rho)][64 c + 32 jj + w2_k(g, i)]
+__host__ __device__ constexpr int w2_row(int ot, int rho) {
+    return 32 * (ot / 2) + 8 * (rho / 4) + 4 * (ot % 2) + rho % 4;
+}
+__host__ __device__ constexpr int w2_k(int g, int i) { return i < 4 ? 4 * g + i : 16 + 4 * g + i - 4; }
+
+// W8T codes (biased u = q + 128, stage-tiled in 384-row blocks; see
+// tile_codes_w8_kernel) -> q as f16, exactly.
+__device__ __forceinline__ _Float16 w8t_code(const uint8_t *w, int k_pad, int n, int k) {
+    const size_t o = (((size_t)(n / 384) * (k_pad / 64) + k / 64) * 384 + n % 384) * 64 + k % 64;
+    return (_Float16)((int)w[o] - 128);
+}
+
+// One thread per (stage, fragment, lane): eight f16 values.
+__global__ void mlp_pack_kernel(const uint8_t *__restrict__ w1, const uint8_t *__restrict__ w2,
+                                _Float16 *__restrict__ out) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= kChunks * kSPC * kStageFrags * 64) return;
+    const int lane = idx % 64, f = idx / 64 % kStageFrags, q = idx / (64 * kStageFrags) % kSPC;
+    const int c = idx / (64 * kStageFrags * kSPC);
+    const int rho = lane % 16, g = lane / 16;
+    half8_t v;
+    if (q < 2) {
+        const int j = 6 * q + f / 4, ft = f % 4;
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = w8t_code(w1, kD, kFC * c + 16 * ft + rho, 32 * j + 8 * g + i);
+    } else {
+        const int ot = 12 * (q - 2) + f / 2, jj = f % 2;
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = w8t_code(w2, kF, w2_row(ot, rho), kFC * c + 32 * jj + w2_k(g, i));
+    }
+    *(half8_t *)(out + (size_t)idx * 8) = v;
+}
+
+// A value parked in an accumulation register (AGPR) until it is read back:
+// the raw X of a wave's tokens (its residual) stays there through the panel,
+// outside the VGPRs the products use.
+#ifdef TZH_EMULATION
+__device__ __forceinline__ float park(float v) { return v; }
+__device__ __forceinline__ float unpark(float a) { return a; }
+#else
+__device__ __forceinline__ float park(float v) {
+    float a;
+    asm("v_accvgpr_write_b32 %0, %1" : "=a"(a) : "v"(v));
+    return a;
+}
+__device__ __forceinline__ float unpark(float a) {
+    float v;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+    return v;
+}
+#endif
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) for the counts the ring can need (n =
+// 6 a + 24 b, a <= 2, b <= 2); any other n waits for everything.
+__device__ __forceinline__ void wait_vm_n(int n) {
+    switch (n) {
+    case 60: wait_vm_lgkm0<60>(); break;
+    case 54: wait_vm_lgkm0<54>(); break;
+    case 48: wait_vm_lgkm0<48>(); break;
+    case 36: wait_vm_lgkm0<36>(); break;
+    case 30: wait_vm_lgkm0<30>(); break;
+    case 24: wait_vm_lgkm0<24>(); break;
+    case 12: wait_vm_lgkm0<12>(); break;
+    case 6: wait_vm_lgkm0<6>(); break;
+    default: wait_vm_lgkm0<0>(); break;
+    }
+}
+
+__global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
+    const float *__restrict__ X, const _Float16 *__restrict__ Wp, const uint16_t *__restrict__ s1,
+    const float *__restrict__ b1, const uint16_t *__restrict__ s2, const float *__restrict__ b2,
+    const float *__restrict__ gamma, const float *__restrict__ beta, float eps, float *__restrict__ Y, int T) {
+    __shared__ __attribute__((aligned(16))) char st[4][kStage];  // the weight ring
+    __shared__ __attribute__((aligned(16))) float p1[2][kF];  // s1, b1
+    __shared__ __attribute__((aligned(16))) float p2[4][kD];  // s2, b2, gamma, beta
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wu = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tl = lane & 15, g = lane >> 4;
+    const int panels = (T + kBM - 1) / kBM;
+    const int count = blockIdx.x < panels ? (panels - 1 - blockIdx.x) / gridDim.x + 1 : 0;
+    const int S = count * kSPP;  // stages this block streams
+    if (S == 0) return;
+
+    // per-feature parameters -> LDS (visible after the first stage barrier)
+    for (int i = tid; i < kF; i += kWaves * 64) {
+        p1[0][i] = f16_bits_to_f32(s1[i]);
+        p1[1][i] = b1[i];
+    }
+    for (int i = tid; i < kD; i += kWaves * 64) {
+        p2[0][i] = f16_bits_to_f32(s2[i]);
+        p2[1][i] = b2[i];
+        p2[2][i] = gamma[i];
+        p2[3][i] = beta[i];
+    }
+
+    // The stage stream of a panel, skewed by one chunk so that the GELU of
+    // chunk p runs between the products of the second GEMM of chunk p - 1
+    // (the matrix cores would otherwise idle through it, with one wave per
+    // SIMD):
+    //   s = 0, 1:            W1 of chunk 0 (k 0..191, 192..383)
+    //   s = 4p - 2, 4p - 1:  W1 of chunk p          (p = 1 .. 23)
+    //   s = 4p, 4p + 1:      W2 of chunk p - 1      (outputs 0..191, 192..383)
+    //   s = 94, 95:          W2 of chunk 23
+    // Stage u of the block sits in ring slot u % 4; pack_stage gives the
+    // pack's stage (4 c + q) at stream position s.
+    auto pack_stage = [](int s) __attribute__((always_inline)) {
+        if (s < 2) return s;
+        if (s >= kSPP - 2) return 4 * (kChunks - 1) + 2 + (s - (kSPP - 2));
+        const int p = (s + 2) >> 2, r = (s + 2) & 3;
+        return r < 2 ? 4 * p + r : 4 * (p - 1) + r;
+    };
+    char *const ring = &st[0][0];
+    const char *const wsrc = (const char *)Wp + (size_t)wu * kLW * kFrag;
+    // where this wave's loads of a stage go: its kLW fragments of the stage
+    struct Dma {
+        const char *src;  // null: no stage to load
+        char *dst;
+    };
+    auto dma_of = [&](int u) __attribute__((always_inline)) {
+        return Dma{wsrc + (size_t)pack_stage(u % kSPP) * kStage, ring + (u & 3) * kStage + wu * kLW * kFrag};
+    };
+    auto dma_one = [&](const Dma &d, int i) __attribute__((always_inline)) {
+        if (d.src) dma16(d.src + i * kFrag, (uint32_t)lane * 16, d.dst + i * kFrag);
+    };
+
+    // X of the wave's tokens in the B-operand layout: lane (tl, g), k step
+    // j: X[t][32 j + 8 g .. 32 j + 8 g + 7] (rows past T clamped to T - 1)
+    f32x4_t xn[kXL];
+    auto load_x = [&](int panel) __attribute__((always_inline)) {
+        int t = panel * kBM + wu * kTokW + tl;
+        t = t < T ? t : T - 1;
+        const float *row = X + (size_t)t * kD + 8 * g;
+#pragma unroll
+        for (int j = 0; j < kXJ; j++) {
+            xn[2 * j] = *(const f32x4_t *)(row + 32 * j);
+            vmem_load_issued();
+            xn[2 * j + 1] = *(const f32x4_t *)(row + 32 * j + 4);
+            vmem_load_issued();
+        }
+    };
+    half8_t xh[kXJ], xl[kXJ];
+    float xr[kXJ * 8];  // parked raw X: xr[8 j + i] = X[t][32 j + 8 g + i]
+    auto split_x = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < kXJ; j++) {
+            split_f32x8(xn[2 * j], xn[2 * j + 1], xh[j], xl[j]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                xr[8 * j + i] = park(xn[2 * j][i]);
+                xr[8 * j + 4 + i] = park(xn[2 * j + 1][i]);
+            }
+        }
+    };
+
+    f32x4_t yacc[kYT];  // lane (tl, g), tile ot: outputs w2_row(ot, 4 g + e)
+    f32x4_t hacc[4];    // lane (tl, g), tile ft: features 64 c + 16 ft + 4 g + e
+    // H of chunks p (being formed) and p - 1 (being multiplied) as the
+    // second GEMM's B operand: hbh/hbl[p % 2][jj], k step jj = tiles 2 jj,
+    // 2 jj + 1
+    half8_t hbh[2][2], hbl[2][2];
+
+    // Ops this wave issued after stage u's loads when step u waits for them:
+    // the loads of stages u + 1 and u + 2 and the extra X loads and stores
+    // issued after stage u's loads, by the step that issued them (ext0: the
+    // step before this one, ext1, ext2: the two before it).  GEN: the count
+    // computed at run time; otherwise (the steps away from a panel's ends)
+    // it is two stages' loads and stage u + 3 exists.
+    int ext0 = 0, ext1 = 0, ext2 = 0;
+    auto step_begin = [&](auto genc, int u) __attribute__((always_inline)) {
+        if constexpr (!decltype(genc)::value) {
+            wait_vm_lgkm0<2 * kLW>();
+            lds_barrier_only();  // every wave's stage u landed; stage u - 1 fully read
+            return dma_of(u + 3);
+        } else {
+            const int ahead = S - 1 - u < 2 ? S - 1 - u : 2;
+            wait_vm_n(kLW * ahead + ext0 + ext1 + ext2);
+            lds_barrier_only();
+            ext2 = ext1;
+            ext1 = ext0;
+            ext0 = 0;
+            return u + 3 < S ? dma_of(u + 3) : Dma{nullptr, nullptr};
+        }
+    };
+
+    // The lane's byte offset in a fragment, recomputed in each stage (an
+    // opaque copy): the compiler otherwise keeps every fragment address of
+    // every stage in its own VGPR for the whole kernel.
+    auto lane_off = [&]() __attribute__((always_inline)) {
+        int lo = lane * 16;
+        asm volatile("" : "+v"(lo));
+        return lo;
+    };
+    // first GEMM, half q of the chunk's k: H^T tiles += W1 fragments x X.
+    // The fragments of k step jp + 1 are read before the products of step
+    // jp are issued (two register sets), so the LDS latency hides behind
+    // eight MFMAs; one of the six loads of stage u + 3 goes out per k step.
+    auto gemm1 = [&](auto qc, const char *sb, const Dma &d) __attribute__((always_inline)) {
+        constexpr int q = decltype(qc)::value;
+        constexpr int j0 = 6 * q;
+        sb += lane_off();
+        if constexpr (q == 0)
+#pragma unroll
+            for (int ft = 0; ft < 4; ft++) hacc[ft] = f32x4_t{};
+        half8_t a[2][4];
+#pragma unroll
+        for (int ft = 0; ft < 4; ft++) a[0][ft] = *(const half8_t *)(sb + ft * kFrag);
+#pragma unroll
+        for (int jp = 0; jp < 6; jp++) {
+            if (jp + 1 < 6)
+#pragma unroll
+                for (int ft = 0; ft < 4; ft++)
+                    a[(jp + 1) & 1][ft] = *(const half8_t *)(sb + ((jp + 1) * 4 + ft) * kFrag);
+            dma_one(d, jp);
+#pragma unroll
+            for (int ft = 0; ft < 4; ft++)
+                hacc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[jp & 1][ft], xh[j0 + jp], hacc[ft], 0, 0, 0);
+#pragma unroll
+            for (int ft = 0; ft < 4; ft++)
+                hacc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[jp & 1][ft], xl[j0 + jp], hacc[ft], 0, 0, 0);
+        }
+    };
+    // H = GELU(sum * s1 + b1) (matmul_w8a32.zig:55, arctic.zig:774-776) of
+    // tile ft of chunk c
+    auto gelu_tile = [&](int c, int ft) __attribute__((always_inline)) {
+        const int f = kFC * c + 16 * ft + 4 * g;
+        const f32x4_t s = *(const f32x4_t *)&p1[0][f];
+        const f32x4_t b = *(const f32x4_t *)&p1[1][f];
+        f32x4_t v;
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = gelu_fast(hacc[ft][e] * s[e] + b[e]);
+        return v;
+    };
+    // second GEMM, output tiles 12 (q - 2) .. + 11 of the chunk whose H is in
+    // buffer HB: Y^T tiles += W2 fragments x H, in six half-groups hg (tiles
+    // 4 (hg / 2) .. + 3 at k step hg % 2): each tile's two dependent products
+    // of a half-group have three other tiles' between them, the next
+    // half-group's fragments are read before this one's products are issued,
+    // and one load of stage u + 3 goes out per half-group.  gc >= 0:
+    // meanwhile k step q - 2 of chunk gc's GELU, into buffer HB ^ 1.
+    auto gemm2 = [&](auto qc, auto hbc, const char *sb, const Dma &d, int gc) __attribute__((always_inline)) {
+        constexpr int q = decltype(qc)::value, o0 = 12 * (q - 2), jg = q - 2;
+        constexpr int HB = decltype(hbc)::value;
+        sb += lane_off();
+        half8_t a[2][4];
+        f32x4_t gv[2];
+        auto read = [&](int buf, int hg) __attribute__((always_inline)) {
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                a[buf][t] = *(const half8_t *)(sb + ((4 * (hg >> 1) + t) * 2 + (hg & 1)) * kFrag);
+        };
+        read(0, 0);
+#pragma unroll
+        for (int hg = 0; hg < 6; hg++) {
+            if (hg + 1 < 6) read((hg + 1) & 1, hg + 1);
+            dma_one(d, hg);
+            const int jj = hg & 1, o = o0 + 4 * (hg >> 1);
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                yacc[o + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[hg & 1][t], hbh[HB][jj], yacc[o + t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                yacc[o + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[hg & 1][t], hbl[HB][jj], yacc[o + t], 0, 0, 0);
+            if (gc >= 0) {
+                if (hg == 1) gv[0] = gelu_tile(gc, 2 * jg);
+                if (hg == 3) gv[1] = gelu_tile(gc, 2 * jg + 1);
+                if (hg == 5) split_f32x8(gv[0], gv[1], hbh[HB ^ 1][jg], hbl[HB ^ 1][jg]);
+            }
+        }
+    };
+
+    // residual + bias, LayerNorm (arctic.zig:780-783, layernorm.zig:26-117),
+    // store; returns whether every token of the wave was stored (then all 24
+    // store instructions were issued with every lane on).  Each of the three
+    // passes forms v = x + (sum * s2 + b2) again from the accumulation
+    // registers (opaque copies, so the compiler cannot keep the 96 values of
+    // the first pass live in VGPRs next to the next panel's X); every pass
+    // forms the same v.
+    auto pre_norm = [&](int j, int h, int e, const f32x4_t &s, const f32x4_t &b) __attribute__((always_inline)) {
+        float y = yacc[2 * j + h][e];
+        asm volatile("" : "+v"(y));
+        // input + (sum * s + bias)  (arctic.zig:780-781)
+        return unpark(xr[8 * j + 4 * h + e]) + (y * s[e] + b[e]);
+    };
+    auto epilogue = [&](int panel) __attribute__((always_inline)) {
+        const int t = panel * kBM + wu * kTokW + tl;
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kXJ; j++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int n = 32 * j + 8 * g + 4 * h;
+                const f32x4_t s = *(const f32x4_t *)&p2[0][n];
+                const f32x4_t b = *(const f32x4_t *)&p2[1][n];
+#pragma unroll
+                for (int e = 0; e < 4; e++) sum += pre_norm(j, h, e, s, b);
+            }
+        const float mean = sum_over_rows(sum) / (float)kD;
+        float sq = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kXJ; j++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int n = 32 * j + 8 * g + 4 * h;
+                const f32x4_t s = *(const f32x4_t *)&p2[0][n];
+                const f32x4_t b = *(const f32x4_t *)&p2[1][n];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float d = pre_norm(j, h, e, s, b) - mean;
+                    sq += d * d;
+                }
+            }
+        const float inv_std = 1.0f / sqrtf(sum_over_rows(sq) / (float)kD + eps);
+        const bool full = panel * kBM + wu * kTokW + kTokW <= T;  // uniform
+#pragma unroll
+        for (int j = 0; j < kXJ; j++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int n = 32 * j + 8 * g + 4 * h;
+                const f32x4_t s = *(const f32x4_t *)&p2[0][n];
+                const f32x4_t b = *(const f32x4_t *)&p2[1][n];
+                const f32x4_t gg = *(const f32x4_t *)&p2[2][n];
+                const f32x4_t bt = *(const f32x4_t *)&p2[3][n];
+                f32x4_t y;
+#pragma unroll
+                for (int e = 0; e < 4; e++) y[e] = ((pre_norm(j, h, e, s, b) - mean) * inv_std) * gg[e] + bt[e];
+                if (t < T) {
+                    *(f32x4_t *)(Y + (size_t)t * kD + n) = y;
+                    vmem_store_issued();
+                }
+            }
+        return full;
+    };
+
+    // Period p of panel i (p = 0 .. 24; block stages from u0): the first
+    // GEMM of chunk p (p <= 23; two stages), then the second GEMM of chunk
+    // p - 1 (p >= 1; two stages) with chunk p's GELU between its products.
+    // PK 0: p = 0 (its GELU alone), 1: 1 <= p <= 23, 2: p = 24.  GEN: the
+    // stage waits counted at run time (the periods next to a panel's ends).
+    // PAR = p & 1: chunk p's H goes to buffer PAR, chunk p - 1's is in
+    // PAR ^ 1.  At p = 23 the next panel's X loads go out once this panel's
+    // first GEMM is done, before the loads of the stage after next (counted
+    // with the step before, after whose stage loads they are issued).
+    auto period = [&](auto pkc, auto genc, auto parc, int u0, int p, int i) __attribute__((always_inline)) {
+        constexpr int PK = decltype(pkc)::value, PAR = decltype(parc)::value;
+        constexpr int S1 = PK == 0 ? 0 : 2;  // ring slots of this period's first two stages
+        if constexpr (PK <= 1) {
+            Dma d = step_begin(genc, u0);
+            gemm1(std::integral_constant<int, 0>{}, st[S1], d);
+            d = step_begin(genc, u0 + 1);
+            gemm1(std::integral_constant<int, 1>{}, st[S1 + 1], d);
+        }
+        if constexpr (PK == 0) {
+#pragma unroll
+            for (int jj = 0; jj < 2; jj++)
+                split_f32x8(gelu_tile(0, 2 * jj), gelu_tile(0, 2 * jj + 1), hbh[0][jj], hbl[0][jj]);
+        } else {
+            constexpr int S2 = PK == 1 ? 0 : 2;  // ring slots of the second GEMM's stages
+            const int u2 = PK == 1 ? u0 + 2 : u0;
+            const int gc = PK == 1 ? p : -1;
+            Dma d = step_begin(genc, u2);
+            if (PK == 1 && p == kChunks - 1 && i + 1 < count) {
+                load_x(blockIdx.x + (i + 1) * gridDim.x);
+                ext1 += kXL;
+            }
+            gemm2(std::integral_constant<int, 2>{}, std::integral_constant<int, PAR ^ 1>{}, st[S2], d, gc);
+            d = step_begin(genc, u2 + 1);
+            gemm2(std::integral_constant<int, 3>{}, std::integral_constant<int, PAR ^ 1>{}, st[S2 + 1], d, gc);
+        }
+    };
+    using std::integral_constant;
+    using Gen = std::true_type;
+    using Mid = std::false_type;
+    using P0 = integral_constant<int, 0>;
+    using P1 = integral_constant<int, 1>;
+
+    load_x(blockIdx.x);
+#pragma unroll
+    for (int u = 0; u < 3; u++)
+        if (u < S) {
+            const Dma d = dma_of(u);
+#pragma unroll
+            for (int k = 0; k < kLW; k++) dma_one(d, k);
+        }
+    split_x();
+    for (int i = 0; i < count; i++) {
+        const int panel = blockIdx.x + i * gridDim.x;
+#pragma unroll
+        for (int o = 0; o < kYT; o++) yacc[o] = f32x4_t{};
+        const int ub = i * kSPP;
+        period(P0{}, Gen{}, P0{}, ub, 0, i);
+        period(P1{}, Gen{}, P1{}, ub + 2, 1, i);
+        for (int p = 2; p < kChunks - 2; p += 2) {
+            period(P1{}, Mid{}, P0{}, ub + 4 * p - 2, p, i);
+            period(P1{}, Mid{}, P1{}, ub + 4 * p + 2, p + 1, i);
+        }
+        period(P1{}, Mid{}, P0{}, ub + 4 * (kChunks - 2) - 2, kChunks - 2, i);
+        period(P1{}, Gen{}, P1{}, ub + 4 * (kChunks - 1) - 2, kChunks - 1, i);
+        period(integral_constant<int, 2>{}, Gen{}, P0{}, ub + kSPP - 2, kChunks, i);
+        const bool full = epilogue(panel);
+        ext0 = full ? kXL : 0;  // the stores, after the loads of the panel's last step
+        if (i + 1 < count) split_x();
+    }
+}
+
+}  // namespace
+
+// W8T codes of the two feed-forward linears (w1: 1536 rows of 384, w2: 384
+// rows of 1536) -> the f16 fragment pack of mlp_fused_kernel
+// (tzh_mlp_pack_bytes bytes, 16-byte aligned).
+size_t tzh_mlp_pack_bytes() { return kPackHalves * 2; }
+
+int tzh_mlp_pack_launch(hipStream_t st, const void *w1, const void *w2, void *out) {
+    if (!w1 || !w2 || !out || ((uintptr_t)out & 15)) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad MLP pack operands");
+    const int threads = kChunks * kSPC * kStageFrags * 64;
+    hipLaunchKernelGGL(mlp_pack_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                       (const uint8_t *)w1, (const uint8_t *)w2, (_Float16 *)out);
+    TZH_LAUNCHED("mlp_pack_kernel");
+    return TZH_OK;
+}
+
+// Y = LayerNorm(X + GELU(X W1^T s1 + b1) W2^T s2 + b2) for X, Y [t, 384]
+// f32 (16-byte aligned, not overlapping) with the pack of W1 and W2.
+int tzh_mlp_fused_launch(hipStream_t st, int num_cus, const float *x, const void *pack, const uint16_t *s1,
+                         const float *b1, const uint16_t *s2, const float *b2, const float *gamma, const float *beta,
+                         float eps, float *y, int64_t t) {
+    if (t < 0 || t > ((int64_t)1 << 30)) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad token count %lld", (long long)t);
+    if (t == 0) return TZH_OK;
+    if (!x || !pack || !s1 || !b1 || !s2 || !b2 || !gamma || !beta || !y)
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "null MLP operand");
+    if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)pack) & 15)
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "MLP operands must be 16-byte aligned");
+    const char *xb = (const char *)x, *yb = (const char *)y;
+    const size_t bytes = (size_t)t * kD * 4;
+    if (xb < yb + bytes && yb < xb + bytes) return tzh_fail(TZH_ERR_INVALID_ARGS, "MLP input and output overlap");
+    const int64_t panels = (t + kBM - 1) / kBM;
+    const int grid = (int)(panels < num_cus ? panels : num_cus);
+    hipLaunchKernelGGL(mlp_fused_kernel, dim3((unsigned)grid), dim3(kWaves * 64), 0, st, x, (const _Float16 *)pack, s1,
+                       b1, s2, b2, gamma, beta, eps, y, (int)t);
+    TZH_LAUNCHED("mlp_fused_kernel");
+    return TZH_OK;
+}

@@ -585,6 +585,58 @@ def group_models():
     assert rc == _abi.ERR_TOO_LARGE, rc
 
 
+def ffn_oracle(w, layer, x, eps):
+    """The reference's feedForward (arctic.zig:760-811) on the oracle's
+    pieces: LayerNorm(x + (gelu(x W1^T s1 + b1) W2^T s2 + b2))."""
+    p = f"encoder.layer.{layer}."
+    h = oracle.matmul_w8a32(x, w[p + "intermediate.dense.weight"], w[p + "intermediate.dense.weight.scale"],
+                            w[p + "intermediate.dense.bias"])
+    y = oracle.matmul_w8a32(oracle.gelu(h), w[p + "output.dense.weight"], w[p + "output.dense.weight.scale"],
+                            w[p + "output.dense.bias"])
+    return oracle.layernorm(x + y, w[p + "output.LayerNorm.weight"], w[p + "output.LayerNorm.bias"], eps)
+
+
+def group_mlp():
+    # the feed-forward block as one kernel (mlp.hip) and as the GEMM pair,
+    # through tzh_arctic_feed_forward, against the oracle.  Run with two
+    # emulated CUs (TZH_EMU_CUS=2, as tests/test_cpu_emulation.py does),
+    # 300 tokens make 5 panels of 64 on two blocks (3 and 2 panels: the
+    # weight ring runs on across panels), the last holding 44 tokens (two
+    # full waves, one partial, one with none).
+    cfg = synth.Config(num_hidden_layers=2)
+    w = synth.quantize(synth.make_arctic_f32(5150, cfg, ln_random=True))
+    hw = synth.HostWeights(w, cfg)
+    m = C.c_void_p()
+    check(L.tzh_arctic_upload(CTX, C.byref(hw.struct), C.byref(m)))
+    rng = np.random.default_rng(5151)
+    try:
+        for t, layer in ((1, 0), (17, 1), (64, 0), (300, 1)):
+            x = aligned_empty((t, 384), np.float32)
+            x[...] = rng.standard_normal((t, 384), dtype=np.float32)
+            x[t // 2] = 0.0  # a zero row
+            ref = ffn_oracle(w, layer, x, cfg.layer_norm_eps)
+            outs = []
+            for fused in (1, 0):
+                check(L.tzh_arctic_set_ffn_fusion(m, fused))
+                y = aligned_empty((t, 384), np.float32)
+                y[...] = np.nan
+                check(L.tzh_arctic_feed_forward(m, layer, x.ctypes.data, y.ctypes.data, t))
+                err = float(np.abs(y - ref).max())
+                print(f"  feed-forward t={t} layer {layer} {'fused' if fused else 'GEMM pair'}: max-abs {err:.2e} "
+                      f"vs oracle", flush=True)
+                assert np.isfinite(y).all() and err < 2e-5, (t, fused, err)
+                outs.append(y)
+            assert float(np.abs(outs[0] - outs[1]).max()) < 2e-5
+        check(L.tzh_arctic_set_ffn_fusion(m, 1))
+        x = aligned_empty((32, 384), np.float32)
+        x[...] = 1.0
+        assert L.tzh_arctic_feed_forward(m, 0, x.ctypes.data, x.ctypes.data, 32) == _abi.ERR_INVALID_ARGS
+        assert L.tzh_arctic_feed_forward(m, 2, x.ctypes.data, x.ctypes.data + 32 * 384 * 4, 1) == _abi.ERR_INVALID_ARGS
+        check(L.tzh_arctic_feed_forward(m, 0, x.ctypes.data, None, 0))
+    finally:
+        check(L.tzh_arctic_free(m))
+
+
 def group_embed():
     # tokenizer -> chunks of every document -> one batched forward -> the
     # chunk pooling kernel, against the same forward on the oracle's chunks
@@ -797,7 +849,7 @@ def group_gemm_fp():
 
 GROUPS = {"eval": group_eval, "gemm_fp": group_gemm_fp, "gemm": group_gemm, "gemm_ln": group_gemm_ln, "range": group_range,
           "attention": group_attention,
-          "arctic": group_arctic, "embed": group_embed, "models": group_models,
+          "arctic": group_arctic, "embed": group_embed, "models": group_models, "mlp": group_mlp,
           "nodes": group_nodes}
 
 if __name__ == "__main__":

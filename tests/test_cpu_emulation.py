@@ -34,7 +34,11 @@ def emu_env():
     return env
 
 
-GROUPS = ["eval", "attention", "gemm", "gemm_ln", "range", "models", "nodes", "gemm_fp"]
+GROUPS = ["eval", "attention", "gemm", "gemm_ln", "range", "models", "nodes", "gemm_fp", "mlp"]
+# emulated CU count per group (default 16): two CUs give the fused
+# feed-forward kernel blocks of several panels at a size the emulation
+# runs in about a minute
+GROUP_ENV = {"mlp": {"TZH_EMU_CUS": "2"}}
 
 
 # test_gpu_eval.py's whole sequence in one process, in file order, with the
@@ -48,7 +52,8 @@ def emu_runs(emu_env):
     """All groups started at once (each is single-threaded), so the module
     takes as long as the slowest group."""
     procs = {g: subprocess.Popen(["python", os.path.join(EMU, "emu_checks.py"), g], stdout=subprocess.PIPE,
-                                 stderr=subprocess.STDOUT, text=True, env=emu_env, cwd=ROOT)
+                                 stderr=subprocess.STDOUT, text=True, env=dict(emu_env, **GROUP_ENV.get(g, {})),
+                                 cwd=ROOT)
              for g in GROUPS}
     procs["replay_eval"] = subprocess.Popen(REPLAY, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
                                             env=dict(emu_env, TZH_EMU_LIB=os.path.join(EMU, "libtenzor_hip_emu.so")),
