@@ -318,13 +318,17 @@ CHAIN_BYTES = 3 * CHAIN_N * CHAIN_N * 4 + CHAIN_N * 4  # A, c read, out written,
 
 
 def kernel_events(launch, reps):
-    """Average duration (us) of `launch()` bracketed by events on torch's
-    current stream, the stream the library enqueues on (tzh_ctx made with
-    the torch stream)."""
+    """Average device duration (us) of `launch()` bracketed by events on
+    torch's current stream, the stream the library enqueues on (tzh_ctx made
+    with the torch stream).  A GPU spin (torch.cuda._sleep) is queued ahead
+    of each pair of events, so that the host's time to issue the launch (a
+    Python call that builds and uploads its program) passes while the GPU
+    spins instead of between the two events."""
     import torch
 
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     for a, b in ev:
+        torch.cuda._sleep(2_000_000)
         a.record()
         launch()
         b.record()
