@@ -405,7 +405,7 @@ def counters(dirs: list[str]) -> str:
             per.setdefault(k, {}).setdefault(cname, {})[(d, did)] = v
     out = []
     for k, cs in per.items():
-        if not any(x in k for x in ("linear_pipe_kernel", "ln_rows_kernel", "attn_varlen")):
+        if not any(x in k for x in ("linear_pipe_kernel", "ln_rows_kernel", "attn_varlen", "mlp_fused_kernel")):
             continue
         out.append(f"### `{k}`")
         out.append("")

@@ -352,17 +352,8 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
 
     // residual + bias, LayerNorm (arctic.zig:780-783, layernorm.zig:26-117),
     // store; returns whether every token of the wave was stored (then all 24
-    // store instructions were issued with every lane on).  Each of the three
-    // passes forms v = x + (sum * s2 + b2) again from the accumulation
-    // registers (opaque copies, so the compiler cannot keep the 96 values of
-    // the first pass live in VGPRs next to the next panel's X); every pass
-    // forms the same v.
-    auto pre_norm = [&](int j, int h, int e, const f32x4_t &s, const f32x4_t &b) __attribute__((always_inline)) {
-        float y = yacc[2 * j + h][e];
-        asm volatile("" : "+v"(y));
-        // input + (sum * s + bias)  (arctic.zig:780-781)
-        return unpark(xr[8 * j + 4 * h + e]) + (y * s[e] + b[e]);
-    };
+    // store instructions were issued with every lane on).  The pre-norm row
+    // replaces the sums in place.
     auto epilogue = [&](int panel) __attribute__((always_inline)) {
         const int t = panel * kBM + wu * kTokW + tl;
         float sum = 0.0f;
@@ -374,22 +365,21 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
                 const f32x4_t s = *(const f32x4_t *)&p2[0][n];
                 const f32x4_t b = *(const f32x4_t *)&p2[1][n];
 #pragma unroll
-                for (int e = 0; e < 4; e++) sum += pre_norm(j, h, e, s, b);
+                for (int e = 0; e < 4; e++) {
+                    // input + (sum * s + bias)  (arctic.zig:780-781)
+                    const float v = unpark(xr[8 * j + 4 * h + e]) + (yacc[2 * j + h][e] * s[e] + b[e]);
+                    yacc[2 * j + h][e] = v;
+                    sum += v;
+                }
             }
         const float mean = sum_over_rows(sum) / (float)kD;
         float sq = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kXJ; j++)
+        for (int o = 0; o < kYT; o++)
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const int n = 32 * j + 8 * g + 4 * h;
-                const f32x4_t s = *(const f32x4_t *)&p2[0][n];
-                const f32x4_t b = *(const f32x4_t *)&p2[1][n];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float d = pre_norm(j, h, e, s, b) - mean;
-                    sq += d * d;
-                }
+            for (int e = 0; e < 4; e++) {
+                const float d = yacc[o][e] - mean;
+                sq += d * d;
             }
         const float inv_std = 1.0f / sqrtf(sum_over_rows(sq) / (float)kD + eps);
         const bool full = panel * kBM + wu * kTokW + kTokW <= T;  // uniform
@@ -398,13 +388,11 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int n = 32 * j + 8 * g + 4 * h;
-                const f32x4_t s = *(const f32x4_t *)&p2[0][n];
-                const f32x4_t b = *(const f32x4_t *)&p2[1][n];
                 const f32x4_t gg = *(const f32x4_t *)&p2[2][n];
                 const f32x4_t bt = *(const f32x4_t *)&p2[3][n];
                 f32x4_t y;
 #pragma unroll
-                for (int e = 0; e < 4; e++) y[e] = ((pre_norm(j, h, e, s, b) - mean) * inv_std) * gg[e] + bt[e];
+                for (int e = 0; e < 4; e++) y[e] = ((yacc[2 * j + h][e] - mean) * inv_std) * gg[e] + bt[e];
                 if (t < T) {
                     *(f32x4_t *)(Y + (size_t)t * kD + n) = y;
                     vmem_store_issued();
