@@ -11,6 +11,7 @@
 //
 //   auto w = tenzor::arctic::ModelWeights::fromSafeTensors(ctx, "model.safetensors");  // arctic.zig:113
 //   tenzor::arctic::forwardBatch(outputs, ids, lengths, stride, w);                    // arctic.zig:902-1013
+//   tenzor::arctic::feedForward(output, input, w, layer, seq_len);                     // arctic.zig:760-811
 //   tenzor::io::Tokenizer tok; tok.loadVocab("vocab.txt");                             // tokenizer.zig:17-51
 //   tenzor::arctic::embedDocuments(outputs, docs, tok.handle(), w);                    // main.zig:786-933
 //
@@ -711,6 +712,13 @@ inline void forward(float *output, const uint32_t *token_ids, int64_t seq_len, c
 inline void forwardBatch(float *outputs, const uint32_t *ids, const std::vector<int32_t> &lengths, int64_t stride,
                          const ModelWeights &weights) {
     check(tzh_arctic_forward_batch(weights.handle(), outputs, ids, lengths.data(), (int32_t)lengths.size(), stride));
+}
+
+// arctic.feedForward (arctic.zig:760-811) of encoder layer `layer`: device
+// f32 input and output [seq_len, hidden] (distinct buffers), f32 arithmetic.
+inline void feedForward(float *output, const float *input, const ModelWeights &weights, int32_t layer,
+                        int64_t seq_len) {
+    check(tzh_arctic_feed_forward(weights.handle(), layer, input, output, seq_len));
 }
 
 // The embed command's document path (main.zig:786-933) for several

@@ -350,6 +350,35 @@ int main(int argc, char **argv) {
             EXPECT(max_abs <= 1e-3 && min_cos >= 0.9999);
             for (int j = 0; j < 384; j++) EXPECT(one[j] == got[j]);  // same kernels, same sums
         });
+        run("arctic feed-forward: one kernel = the GEMM pair to f32 rounding", [&] {  // arctic.zig:760-811
+            auto weights = arctic::ModelWeights::fromSafeTensors(ctx, dir + "/model.safetensors");
+            const int64_t n = 100;
+            std::vector<float> x((size_t)n * 384);
+            for (size_t i = 0; i < x.size(); i++) x[i] = std::sin(0.37f * (float)i) * 1.5f;
+            void *d_x = nullptr, *d_y = nullptr, *d_z = nullptr;
+            check(tzh_malloc(ctx.handle(), x.size() * 4, &d_x));
+            check(tzh_malloc(ctx.handle(), x.size() * 4, &d_y));
+            check(tzh_malloc(ctx.handle(), x.size() * 4, &d_z));
+            check(tzh_memcpy_h2d(ctx.handle(), d_x, x.data(), x.size() * 4));
+            arctic::feedForward((float *)d_y, (const float *)d_x, weights, 0, n);
+            check(tzh_arctic_set_ffn_fusion(weights.handle(), 0));
+            arctic::feedForward((float *)d_z, (const float *)d_x, weights, 0, n);
+            check(tzh_arctic_set_ffn_fusion(weights.handle(), 1));
+            std::vector<float> y(x.size()), z(x.size());
+            check(tzh_memcpy_d2h(ctx.handle(), y.data(), d_y, y.size() * 4));
+            check(tzh_memcpy_d2h(ctx.handle(), z.data(), d_z, z.size() * 4));
+            tzh_free(ctx.handle(), d_x);
+            tzh_free(ctx.handle(), d_y);
+            tzh_free(ctx.handle(), d_z);
+            double max_abs = 0;
+            bool finite = true;
+            for (size_t i = 0; i < y.size(); i++) {
+                finite = finite && std::isfinite(y[i]) && std::isfinite(z[i]);
+                max_abs = std::max(max_abs, (double)std::fabs(y[i] - z[i]));
+            }
+            std::printf("  feed-forward: fused vs GEMM pair max-abs %.3g\n", max_abs);
+            EXPECT(finite && max_abs <= 2e-5);
+        });
     }
 
     std::printf(g_failed ? "FAILED %d\n" : "ALL PASSED\n", g_failed);
