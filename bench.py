@@ -48,6 +48,9 @@ KERNELS = {
                "(linear_pipe_kernel residual pieces, ln_rows_kernel)",
     "ffn": "mlp_fused_kernel: the feed-forward block in one kernel, 384 -> 1536 + GELU -> 384 + residual + "
            "LayerNorm, the intermediate kept on chip",
+    "attn_ffn": "mlp_fused_kernel<true>: O-projection 384 -> 384 + residual + LayerNorm, then the feed-forward "
+                "block (384 -> 1536 + GELU -> 384 + residual + LayerNorm) in one kernel, h1 and the intermediate "
+                "kept on chip",
     "embed_ln": "embed_ln_kernel", "pack_ids": "pack_ids_kernel", "cls_l2": "cls_l2_kernel",
 }
 
@@ -106,6 +109,10 @@ def stage_work(T, lengths, es=4):
     # X again as the residual, and reads its f16 weight pack
     f1, f2 = w["ffn1_gelu"], w["ffn2_ln"]
     w["ffn"] = (f1[0] + f2[0], f1[1] + f2[1], float(3 * T * H * es + 2 * (2 * H * I)))
+    # ... preceded by the O-projection + LayerNorm (op-boundary bytes of the
+    # three linears; it moves the context and h in and h out)
+    o = w["attn_out_ln"]
+    w["attn_ffn"] = (o[0] + f1[0] + f2[0], o[1] + f1[1] + f2[1], float(3 * T * H * es + 2 * (2 * H * I + H * H)))
     L2 = float((lengths.astype(np.float64) ** 2).sum())
     # per head QK^T and PV: 2 * L^2 * 32 flops each; 12 heads
     w["attention"] = (4.0 * L2 * H, float(T * 6144), float(T * 3 * H * es + T * H * es))

@@ -26,7 +26,8 @@ Dispatches are mapped to forward stages by kernel and launch order: both
 LayerNorm GEMMs are linear_pipe_kernel<2> (with f32 activations the k = 384
 one has a tile configuration of its own); the one launched after attention
 is attn_out_ln and the one after ffn1_gelu is ffn2_ln; mlp_fused_kernel, the
-fused feed-forward block, is the stage ffn.  The
+fused feed-forward block, is the stage ffn, and in its O-projection mode
+(template argument true) the stage attn_ffn.  The
 pieces of a split partial round (the residual-only GEMM) and their row
 LayerNorm belong to the LayerNorm GEMM launched just before them.
 
@@ -45,7 +46,8 @@ import re
 import sys
 
 CAL_BYTES = 1 << 30
-STAGES = ("pack_ids", "embed_ln", "qkv", "attention", "attn_out_ln", "ffn", "ffn1_gelu", "ffn2_ln", "cls_l2")
+STAGES = ("pack_ids", "embed_ln", "qkv", "attention", "attn_out_ln", "attn_ffn", "ffn", "ffn1_gelu", "ffn2_ln",
+          "cls_l2")
 
 
 def epi_of(kernel: str) -> int | None:
@@ -68,7 +70,8 @@ def stage_of(kernel: str, prev: str | None) -> str | None:
     if "cls_l2_kernel" in kernel:
         return "cls_l2"
     if "mlp_fused_kernel" in kernel:
-        return "ffn"
+        # <true>: the O-projection mode (mangled ...kernelILb1E...)
+        return "attn_ffn" if ("ILb1E" in kernel or "<true>" in kernel) else "ffn"
     epi = epi_of(kernel)
     if epi == 0:
         return "qkv"
@@ -262,14 +265,15 @@ def summarize(trace: str | None, fetch: str | None, write: str | None, bench_log
                                          "ms_per_step": steps[prec]}
                                   for prec, key in (("fp32", "stages"), ("fp16", "stages_fp16"))}
     if trace:
-        out += ["The fp32 forward runs each feed-forward block as one kernel (mlp_fused_kernel, stage",
-                "ffn); the fp16 forward runs the GEMM pair (ffn1_gelu, ffn2_ln).  Both LayerNorm GEMMs",
-                "are linear_pipe_kernel<2> (in the fp32 forward the O-projection with its own tile",
-                "configuration); the rows above separate them by launch order.",
-                "The counter runs (bench_profile.py run) make one fp32",
-                "forward.  rocprofv3's own kernel summary of the trace run (bench.py: the fp16",
-                "forward first, 5 timed + 2 warmup, then the fp32 one, 5 timed + 2 warmup + 3",
-                "with per-launch events):", ""]
+        out += ["The fp32 forward runs each layer's O-projection, its LayerNorm and the feed-forward",
+                "block as one kernel (mlp_fused_kernel<true>, stage attn_ffn); the fp16 forward runs",
+                "the O-projection and the GEMM pair (attn_out_ln, ffn1_gelu, ffn2_ln), whose two",
+                "LayerNorm GEMMs are both linear_pipe_kernel<2>; the rows above separate them by",
+                "launch order.  The stage rows average the plain forwards of the trace run.  The",
+                "counter runs (bench_profile.py run) make one fp32 forward.  rocprofv3's own kernel",
+                "summary of the trace run (bench.py: the fp16 forward first, 5 timed + 2 warmup, then",
+                "the fp32 one, 5 timed + 2 warmup + 3 with per-launch events, which issue each stage",
+                "10 times back to back):", ""]
         out += kernel_stats_table(trace)
     out += ["", "```json", json.dumps(data, indent=1), "```", ""]
     return "\n".join(out)

@@ -445,9 +445,10 @@ int tzh_arctic_feed_forward(tzh_model *model, int32_t layer, const float *input,
 
 /* Fused feed-forward switch (no counterpart in the reference): enable = 0
  * makes the forward and tzh_arctic_feed_forward run every feed-forward block
- * as the GEMM pair (GELU epilogue, then residual + LayerNorm epilogue) even
- * where the single kernel applies; nonzero (the default) restores it.  The
- * two agree to the f32 rounding of their different summation orders. */
+ * as the GEMM pair (GELU epilogue, then residual + LayerNorm epilogue), and
+ * the forward every O-projection as its own GEMM, even where one kernel
+ * applies; nonzero (the default) restores them.  They agree to the f32
+ * rounding of their different summation orders. */
 int tzh_arctic_set_ffn_fusion(tzh_model *model, int32_t enable);
 
 /* Launch tracing (no counterpart in the reference, whose CPU path has no
@@ -463,8 +464,10 @@ int tzh_arctic_set_timing(tzh_model *model, int32_t enable);
  * us[i] (microseconds between the events around stage i, divided by the
  * times it was issued) and names[i]
  * (static stage names: "pack_ids", "embed_ln", "qkv", "attention",
- * "attn_out_ln", "ffn" (the fused feed-forward kernel) or "ffn1_gelu" and
- * "ffn2_ln" (the GEMM pair), "cls_l2", "hidden_f32"), at most
+ * "attn_out_ln" and "ffn" (the fused feed-forward kernel), or "attn_ffn"
+ * (the O-projection, its LayerNorm and the feed-forward block as one
+ * kernel), or "attn_out_ln", "ffn1_gelu" and "ffn2_ln" (the GEMM pair),
+ * "cls_l2", "hidden_f32"), at most
  * `capacity` entries; *count = number of launches (0 if the last forward was
  * not timed).  Waits for that forward to finish.  Either array may be NULL. */
 int tzh_arctic_launch_times(tzh_model *model, float *us, const char **names, int32_t capacity, int32_t *count);

@@ -40,7 +40,10 @@ size_t tzh_mlp_pack_bytes();
 int tzh_mlp_pack_launch(hipStream_t st, const void *w1, const void *w2, void *out);
 int tzh_mlp_fused_launch(hipStream_t st, int num_cus, const float *x, const void *pack, const uint16_t *s1,
                          const float *b1, const uint16_t *s2, const float *b2, const float *gamma, const float *beta,
-                         float eps, float *y, int64_t t);
+                         float eps, float *y, int64_t t, const float *ctx, const float *res, const void *opack,
+                         const uint16_t *so, const float *bo, const float *gamma1, const float *beta1);
+size_t tzh_mlp_opack_bytes();
+int tzh_mlp_opack_launch(hipStream_t st, const void *wo, void *out);
 
 namespace {
 
@@ -218,8 +221,10 @@ struct DevLayer {
     DevLinear qkv, o, ffn1, ffn2;
     float *ln1_g = nullptr, *ln1_b = nullptr, *ln2_g = nullptr, *ln2_b = nullptr;
     // both feed-forward linears int8: their codes widened to f16 in the
-    // fragment order of the fused feed-forward kernel (mlp.hip)
-    void *mlp = nullptr;
+    // fragment order of the fused feed-forward kernel (mlp.hip); mlp_o: the
+    // O-projection's too, when it is int8 as well (the kernel then starts
+    // from the attention context)
+    void *mlp = nullptr, *mlp_o = nullptr;
 };
 
 }  // namespace
@@ -490,7 +495,8 @@ int ffn_part(tzh_model *m, const DevLayer &d, hipStream_t st, int32_t act, bool 
     const float eps = m->cfg.layer_norm_eps;
     if (part == 0)
         return tzh_mlp_fused_launch(st, cus, (const float *)x, d.mlp, d.ffn1.s, d.ffn1.b, d.ffn2.s, d.ffn2.b, d.ln2_g,
-                                    d.ln2_b, eps, (float *)y, T);
+                                    d.ln2_b, eps, (float *)y, T, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                    nullptr);
     if (part == 1) {
         if (d.ffn1.fmt == TZH_WF_F32)
             return linear_f32w(st, (const float *)x, d.ffn1, (float *)m->inter, T, H, 1536, TZH_OP_GELU, nullptr);
@@ -663,6 +669,10 @@ int upload_weights(tzh_model *m, const tzh_arctic_weights *w) {
         if (d.ffn1.fmt == TZH_WF_W8T && d.ffn2.fmt == TZH_WF_W8T) {
             TZH_TRY(dev_alloc(m, &d.mlp, tzh_mlp_pack_bytes()));
             TZH_TRY(tzh_mlp_pack_launch(m->ctx->stream, d.ffn1.w, d.ffn2.w, d.mlp));
+            if (d.o.fmt == TZH_WF_W8T) {
+                TZH_TRY(dev_alloc(m, &d.mlp_o, tzh_mlp_opack_bytes()));
+                TZH_TRY(tzh_mlp_opack_launch(m->ctx->stream, d.o.w, d.mlp_o));
+            }
         }
     }
     TZH_HIP(hipStreamSynchronize(m->ctx->stream));
@@ -995,6 +1005,20 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
             return tzh_attention_launch(st, m->ctx->num_cus, m->ctx->work_queue, m->qkv, m->attn, act, d_cu, d_order,
                                         batch, 12, H);
         }));
+        // the O-projection, its LayerNorm and the feed-forward block as one
+        // kernel (mlp.hip) where the layer has both packs: (attn, h) -> h1,
+        // then h and h1 trade places, so the next layer reads its input from
+        // h (the stage writes no buffer it reads: timing repeats leave the
+        // result unchanged)
+        if (ffn_fused(m, d, act, rs) && d.mlp_o) {
+            TZH_TRY(stage("attn_ffn", [&]() {
+                return tzh_mlp_fused_launch(st, cus, nullptr, d.mlp, d.ffn1.s, d.ffn1.b, d.ffn2.s, d.ffn2.b, d.ln2_g,
+                                            d.ln2_b, eps, h1f, T, (const float *)m->attn, hf, d.mlp_o, d.o.s, d.o.b,
+                                            d.ln1_g, d.ln1_b);
+            }));
+            std::swap(m->h, m->h1);
+            continue;
+        }
         TZH_TRY(stage("attn_out_ln", [&]() {
             if (d.o.fmt == TZH_WF_F32) {
                 TZH_TRY(linear_f32w(st, (const float *)m->attn, d.o, (float *)m->inter, T, H, H, -1, hf));

@@ -112,6 +112,22 @@ __global__ void mlp_pack_kernel(const uint8_t *__restrict__ w1, const uint8_t *_
     *(half8_t *)(out + (size_t)idx * 8) = v;
 }
 
+// The O-projection's codes (W_o [384, 384] in W8T) -> its 12 stages, one per
+// 32-wide k step s, fragment f = output tile ot (rows ordered as W2's, so
+// that its sums land in the lanes of X's columns): lane l = 16 g + rho,
+// value i = W_o[w2_row(ot, rho)][32 s + 8 g + i].
+constexpr int kOStages = kD / 32;
+__global__ void mlp_opack_kernel(const uint8_t *__restrict__ wo, _Float16 *__restrict__ out) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= kOStages * kStageFrags * 64) return;
+    const int lane = idx % 64, ot = idx / 64 % kStageFrags, st = idx / (64 * kStageFrags);
+    const int rho = lane % 16, g = lane / 16;
+    half8_t v;
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = w8t_code(wo, kD, w2_row(ot, rho), 32 * st + 8 * g + i);
+    *(half8_t *)(out + (size_t)idx * 8) = v;
+}
+
 // A value parked in an accumulation register (AGPR) until it is read back:
 // the raw X of a wave's tokens (its residual) stays there through the panel,
 // outside the VGPRs the products use.
@@ -147,20 +163,50 @@ __device__ __forceinline__ void wait_vm_n(int n) {
     }
 }
 
+// Where one wave's loads of a ring stage go (its kLW fragments of the
+// stage).  ALWAYS: the stage exists; otherwise src null means no stage.
+template <bool ALWAYS>
+struct StageDma {
+    static constexpr bool kAlways = ALWAYS;
+    const char *src;
+    char *dst;
+};
+
+// The attention output's side of an encoder layer, for the O-projection
+// mode of mlp_fused_kernel: the attention context, the layer's input (the
+// first LayerNorm's residual), W_o's stages (mlp_opack_kernel), its scales
+// and bias, and the first LayerNorm's gamma and beta.
+struct OProj {
+    const float *ctx, *res;
+    const _Float16 *wp;
+    const uint16_t *s;
+    const float *b, *gamma, *beta;
+};
+
+// OP: the O-projection mode.  Each panel first forms X = LayerNorm(res +
+// (ctx W_o^T s_o + b_o)) (arctic.zig:716-746) in registers, from 12 more
+// weight stages (W_o's, streamed ahead of the feed-forward's) and the
+// first LayerNorm in the lanes, then runs the feed-forward block on it.
+template <bool OP>
 __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     const float *__restrict__ X, const _Float16 *__restrict__ Wp, const uint16_t *__restrict__ s1,
     const float *__restrict__ b1, const uint16_t *__restrict__ s2, const float *__restrict__ b2,
-    const float *__restrict__ gamma, const float *__restrict__ beta, float eps, float *__restrict__ Y, int T) {
+    const float *__restrict__ gamma, const float *__restrict__ beta, float eps, float *__restrict__ Y, int T,
+    OProj op) {
+    constexpr int kO = OP ? kOStages : 0;  // O-projection stages at the head of each panel
+    constexpr int kSP = kO + kSPP;         // stages per panel
+    static_assert(kSP % 4 == 0, "a panel's stages fill whole turns of the ring");
     __shared__ __attribute__((aligned(16))) char st[4][kStage];  // the weight ring
     __shared__ __attribute__((aligned(16))) float p1[2][kF];  // s1, b1
     __shared__ __attribute__((aligned(16))) float p2[4][kD];  // s2, b2, gamma, beta
+    __shared__ __attribute__((aligned(16))) float p0[OP ? 4 : 1][OP ? kD : 4];  // s_o, b_o, LayerNorm 1
 
-    const int tid = threadIdx.x, lane = tid & 63;
+    // (lane quantities are formed where they are used, from lane_now())
+    const int tid = threadIdx.x;
     const int wu = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int tl = lane & 15, g = lane >> 4;
     const int panels = (T + kBM - 1) / kBM;
     const int count = blockIdx.x < panels ? (panels - 1 - blockIdx.x) / gridDim.x + 1 : 0;
-    const int S = count * kSPP;  // stages this block streams
+    const int S = count * kSP;  // stages this block streams
     if (S == 0) return;
 
     // per-feature parameters -> LDS (visible after the first stage barrier)
@@ -173,6 +219,12 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         p2[1][i] = b2[i];
         p2[2][i] = gamma[i];
         p2[3][i] = beta[i];
+        if constexpr (OP) {
+            p0[0][i] = f16_bits_to_f32(op.s[i]);
+            p0[1][i] = op.b[i];
+            p0[2][i] = op.gamma[i];
+            p0[3][i] = op.beta[i];
+        }
     }
 
     // The stage stream of a panel, skewed by one chunk so that the GELU of
@@ -183,8 +235,9 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     //   s = 4p - 2, 4p - 1:  W1 of chunk p          (p = 1 .. 23)
     //   s = 4p, 4p + 1:      W2 of chunk p - 1      (outputs 0..191, 192..383)
     //   s = 94, 95:          W2 of chunk 23
-    // Stage u of the block sits in ring slot u % 4; pack_stage gives the
-    // pack's stage (4 c + q) at stream position s.
+    // (after the O-projection's kO stages in the O-projection mode).  Stage
+    // u of the block sits in ring slot u % 4; pack_stage gives the pack's
+    // stage (4 c + q) at feed-forward stream position s.
     auto pack_stage = [](int s) __attribute__((always_inline)) {
         if (s < 2) return s;
         if (s >= kSPP - 2) return 4 * (kChunks - 1) + 2 + (s - (kSPP - 2));
@@ -193,25 +246,27 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     };
     char *const ring = &st[0][0];
     const char *const wsrc = (const char *)Wp + (size_t)wu * kLW * kFrag;
-    // where this wave's loads of a stage go: its kLW fragments of the stage
-    struct Dma {
-        const char *src;  // null: no stage to load
-        char *dst;
-    };
+    const char *const osrc = OP ? (const char *)op.wp + (size_t)wu * kLW * kFrag : nullptr;
     auto dma_of = [&](int u) __attribute__((always_inline)) {
-        return Dma{wsrc + (size_t)pack_stage(u % kSPP) * kStage, ring + (u & 3) * kStage + wu * kLW * kFrag};
+        const int sp = u % kSP;
+        const char *src = OP && sp < kO ? osrc + (size_t)sp * kStage : wsrc + (size_t)pack_stage(sp - kO) * kStage;
+        return StageDma<true>{src, ring + (u & 3) * kStage + wu * kLW * kFrag};
     };
-    auto dma_one = [&](const Dma &d, int i) __attribute__((always_inline)) {
-        if (d.src) dma16(d.src + i * kFrag, (uint32_t)lane * 16, d.dst + i * kFrag);
+    auto dma_one = [&](const auto &d, int i) __attribute__((always_inline)) {
+        if (std::decay_t<decltype(d)>::kAlways || d.src)
+            dma16(d.src + i * kFrag, (uint32_t)lane_now() * 16, d.dst + i * kFrag);
     };
 
-    // X of the wave's tokens in the B-operand layout: lane (tl, g), k step
-    // j: X[t][32 j + 8 g .. 32 j + 8 g + 7] (rows past T clamped to T - 1)
+    // Rows of the wave's tokens in the B-operand layout: lane (tl, g), k
+    // step j: src[t][32 j + 8 g .. 32 j + 8 g + 7] (rows past T clamped to
+    // T - 1).  load_x: the activation a panel starts from (X, or the
+    // attention context in the O-projection mode).
     f32x4_t xn[kXL];
-    auto load_x = [&](int panel) __attribute__((always_inline)) {
-        int t = panel * kBM + wu * kTokW + tl;
+    auto load_rows = [&](const float *src, int panel) __attribute__((always_inline)) {
+        const int ln = lane_now();
+        int t = panel * kBM + wu * kTokW + (ln & 15);
         t = t < T ? t : T - 1;
-        const float *row = X + (size_t)t * kD + 8 * g;
+        const float *row = src + (size_t)t * kD + 8 * (ln >> 4);
 #pragma unroll
         for (int j = 0; j < kXJ; j++) {
             xn[2 * j] = *(const f32x4_t *)(row + 32 * j);
@@ -220,17 +275,21 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
             vmem_load_issued();
         }
     };
+    auto load_x = [&](int panel) __attribute__((always_inline)) { load_rows(OP ? op.ctx : X, panel); };
     half8_t xh[kXJ], xl[kXJ];
     float xr[kXJ * 8];  // parked raw X: xr[8 j + i] = X[t][32 j + 8 g + i]
-    auto split_x = [&]() __attribute__((always_inline)) {
+    // xn -> the f16 halves xh, xl; PARK: xn is the feed-forward's X, kept as
+    // its residual (the attention context of the O-projection mode is not)
+    auto split_x = [&](auto parkc) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < kXJ; j++) {
             split_f32x8(xn[2 * j], xn[2 * j + 1], xh[j], xl[j]);
+            if constexpr (decltype(parkc)::value)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                xr[8 * j + i] = park(xn[2 * j][i]);
-                xr[8 * j + 4 + i] = park(xn[2 * j + 1][i]);
-            }
+                for (int i = 0; i < 4; i++) {
+                    xr[8 * j + i] = park(xn[2 * j][i]);
+                    xr[8 * j + 4 + i] = park(xn[2 * j + 1][i]);
+                }
         }
     };
 
@@ -244,39 +303,43 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     // Ops this wave issued after stage u's loads when step u waits for them:
     // the loads of stages u + 1 and u + 2 and the extra X loads and stores
     // issued after stage u's loads, by the step that issued them (ext0: the
-    // step before this one, ext1, ext2: the two before it).  GEN: the count
-    // computed at run time; otherwise (the steps away from a panel's ends)
-    // it is two stages' loads and stage u + 3 exists.
+    // step before this one, ext1, ext2: the two before it).  Step kinds:
+    // MID (the steps away from a panel's ends): two stages' loads, and stage
+    // u + 3 exists; GEN: the count computed at run time, stage u + 3 exists
+    // (a panel's first steps); END: both at run time (its last steps).
     int ext0 = 0, ext1 = 0, ext2 = 0;
-    auto step_begin = [&](auto genc, int u) __attribute__((always_inline)) {
-        if constexpr (!decltype(genc)::value) {
+    auto step_begin = [&](auto kindc, int u) __attribute__((always_inline)) {
+        constexpr int K = decltype(kindc)::value;
+        if constexpr (K == 0) {
             wait_vm_lgkm0<2 * kLW>();
             lds_barrier_only();  // every wave's stage u landed; stage u - 1 fully read
             return dma_of(u + 3);
         } else {
-            const int ahead = S - 1 - u < 2 ? S - 1 - u : 2;
+            const int ahead = K == 1 || S - 1 - u >= 2 ? 2 : S - 1 - u;
             wait_vm_n(kLW * ahead + ext0 + ext1 + ext2);
             lds_barrier_only();
             ext2 = ext1;
             ext1 = ext0;
             ext0 = 0;
-            return u + 3 < S ? dma_of(u + 3) : Dma{nullptr, nullptr};
+            if constexpr (K == 1) {
+                return dma_of(u + 3);
+            } else {
+                if (u + 3 >= S) return StageDma<false>{nullptr, nullptr};
+                const StageDma<true> d = dma_of(u + 3);
+                return StageDma<false>{d.src, d.dst};
+            }
         }
     };
 
     // The lane's byte offset in a fragment, recomputed in each stage (an
     // opaque copy): the compiler otherwise keeps every fragment address of
     // every stage in its own VGPR for the whole kernel.
-    auto lane_off = [&]() __attribute__((always_inline)) {
-        int lo = lane * 16;
-        asm volatile("" : "+v"(lo));
-        return lo;
-    };
+    auto lane_off = [&]() __attribute__((always_inline)) { return lane_now() * 16; };
     // first GEMM, half q of the chunk's k: H^T tiles += W1 fragments x X.
     // The fragments of k step jp + 1 are read before the products of step
     // jp are issued (two register sets), so the LDS latency hides behind
     // eight MFMAs; one of the six loads of stage u + 3 goes out per k step.
-    auto gemm1 = [&](auto qc, const char *sb, const Dma &d) __attribute__((always_inline)) {
+    auto gemm1 = [&](auto qc, const char *sb, const auto &d) __attribute__((always_inline)) {
         constexpr int q = decltype(qc)::value;
         constexpr int j0 = 6 * q;
         sb += lane_off();
@@ -293,6 +356,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
                 for (int ft = 0; ft < 4; ft++)
                     a[(jp + 1) & 1][ft] = *(const half8_t *)(sb + ((jp + 1) * 4 + ft) * kFrag);
             dma_one(d, jp);
+            sched_fence();
 #pragma unroll
             for (int ft = 0; ft < 4; ft++)
                 hacc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[jp & 1][ft], xh[j0 + jp], hacc[ft], 0, 0, 0);
@@ -304,7 +368,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     // H = GELU(sum * s1 + b1) (matmul_w8a32.zig:55, arctic.zig:774-776) of
     // tile ft of chunk c
     auto gelu_tile = [&](int c, int ft) __attribute__((always_inline)) {
-        const int f = kFC * c + 16 * ft + 4 * g;
+        const int f = kFC * c + 16 * ft + 4 * (lane_now() >> 4);
         const f32x4_t s = *(const f32x4_t *)&p1[0][f];
         const f32x4_t b = *(const f32x4_t *)&p1[1][f];
         f32x4_t v;
@@ -319,7 +383,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     // half-group's fragments are read before this one's products are issued,
     // and one load of stage u + 3 goes out per half-group.  gc >= 0:
     // meanwhile k step q - 2 of chunk gc's GELU, into buffer HB ^ 1.
-    auto gemm2 = [&](auto qc, auto hbc, const char *sb, const Dma &d, int gc) __attribute__((always_inline)) {
+    auto gemm2 = [&](auto qc, auto hbc, const char *sb, const auto &d, int gc) __attribute__((always_inline)) {
         constexpr int q = decltype(qc)::value, o0 = 12 * (q - 2), jg = q - 2;
         constexpr int HB = decltype(hbc)::value;
         sb += lane_off();
@@ -335,6 +399,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         for (int hg = 0; hg < 6; hg++) {
             if (hg + 1 < 6) read((hg + 1) & 1, hg + 1);
             dma_one(d, hg);
+            sched_fence();
             const int jj = hg & 1, o = o0 + 4 * (hg >> 1);
 #pragma unroll
             for (int t = 0; t < 4; t++)
@@ -350,12 +415,82 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         }
     };
 
+    // O-projection mode, k step j of W_o (the panel's stage j): Y^T tiles of
+    // the 384 outputs += W_o fragments x ctx, in six groups of four tiles
+    // (hi then lo products, so each tile's two have three others between
+    // them), the next group's fragments read before this group's products,
+    // one load of stage u + 3 per group
+    auto gemm_o = [&](int j, const char *sb, const auto &d) __attribute__((always_inline)) {
+        sb += lane_off();
+        half8_t a[2][4];
+        auto read = [&](int buf, int og) __attribute__((always_inline)) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) a[buf][t] = *(const half8_t *)(sb + (4 * og + t) * kFrag);
+        };
+        read(0, 0);
+#pragma unroll
+        for (int og = 0; og < 6; og++) {
+            if (og + 1 < 6) read((og + 1) & 1, og + 1);
+            dma_one(d, og);
+            sched_fence();
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                yacc[4 * og + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[og & 1][t], xh[j], yacc[4 * og + t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                yacc[4 * og + t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[og & 1][t], xl[j], yacc[4 * og + t], 0, 0, 0);
+        }
+    };
+    // O-projection mode: X = LayerNorm(res + (sum * s_o + b_o)) (arctic.zig:
+    // 716-746, the two-pass LayerNorm of layernorm.zig:26-117) into xn, from
+    // the sums in yacc and res in xn; the pre-norm row replaces the sums
+    auto layernorm1 = [&]() __attribute__((always_inline)) {
+        const int g = lane_now() >> 4;
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kXJ; j++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int n = 32 * j + 8 * g + 4 * h;
+                const f32x4_t s = *(const f32x4_t *)&p0[0][n];
+                const f32x4_t b = *(const f32x4_t *)&p0[1][n];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    // input + (sum * s + bias)  (arctic.zig:720)
+                    const float v = xn[2 * j + h][e] + (yacc[2 * j + h][e] * s[e] + b[e]);
+                    yacc[2 * j + h][e] = v;
+                    sum += v;
+                }
+            }
+        const float mean = sum_over_rows(sum) / (float)kD;
+        float sq = 0.0f;
+#pragma unroll
+        for (int o = 0; o < kYT; o++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float d = yacc[o][e] - mean;
+                sq += d * d;
+            }
+        const float inv_std = 1.0f / sqrtf(sum_over_rows(sq) / (float)kD + eps);
+#pragma unroll
+        for (int j = 0; j < kXJ; j++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int n = 32 * j + 8 * g + 4 * h;
+                const f32x4_t gg = *(const f32x4_t *)&p0[2][n];
+                const f32x4_t bt = *(const f32x4_t *)&p0[3][n];
+#pragma unroll
+                for (int e = 0; e < 4; e++) xn[2 * j + h][e] = ((yacc[2 * j + h][e] - mean) * inv_std) * gg[e] + bt[e];
+            }
+    };
+
     // residual + bias, LayerNorm (arctic.zig:780-783, layernorm.zig:26-117),
     // store; returns whether every token of the wave was stored (then all 24
     // store instructions were issued with every lane on).  The pre-norm row
     // replaces the sums in place.
     auto epilogue = [&](int panel) __attribute__((always_inline)) {
-        const int t = panel * kBM + wu * kTokW + tl;
+        const int ln = lane_now(), g = ln >> 4;
+        const int t = panel * kBM + wu * kTokW + (ln & 15);
         float sum = 0.0f;
 #pragma unroll
         for (int j = 0; j < kXJ; j++)
@@ -404,19 +539,19 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     // Period p of panel i (p = 0 .. 24; block stages from u0): the first
     // GEMM of chunk p (p <= 23; two stages), then the second GEMM of chunk
     // p - 1 (p >= 1; two stages) with chunk p's GELU between its products.
-    // PK 0: p = 0 (its GELU alone), 1: 1 <= p <= 23, 2: p = 24.  GEN: the
-    // stage waits counted at run time (the periods next to a panel's ends).
+    // PK 0: p = 0 (its GELU alone), 1: 1 <= p <= 23, 2: p = 24.  KIND: the
+    // step kind of its stages (GEN, END next to a panel's ends, else MID).
     // PAR = p & 1: chunk p's H goes to buffer PAR, chunk p - 1's is in
     // PAR ^ 1.  At p = 23 the next panel's X loads go out once this panel's
     // first GEMM is done, before the loads of the stage after next (counted
     // with the step before, after whose stage loads they are issued).
-    auto period = [&](auto pkc, auto genc, auto parc, int u0, int p, int i) __attribute__((always_inline)) {
+    auto period = [&](auto pkc, auto kindc, auto parc, int u0, int p, int i) __attribute__((always_inline)) {
         constexpr int PK = decltype(pkc)::value, PAR = decltype(parc)::value;
         constexpr int S1 = PK == 0 ? 0 : 2;  // ring slots of this period's first two stages
         if constexpr (PK <= 1) {
-            Dma d = step_begin(genc, u0);
+            auto d = step_begin(kindc, u0);
             gemm1(std::integral_constant<int, 0>{}, st[S1], d);
-            d = step_begin(genc, u0 + 1);
+            d = step_begin(kindc, u0 + 1);
             gemm1(std::integral_constant<int, 1>{}, st[S1 + 1], d);
         }
         if constexpr (PK == 0) {
@@ -427,19 +562,20 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
             constexpr int S2 = PK == 1 ? 0 : 2;  // ring slots of the second GEMM's stages
             const int u2 = PK == 1 ? u0 + 2 : u0;
             const int gc = PK == 1 ? p : -1;
-            Dma d = step_begin(genc, u2);
+            auto d = step_begin(kindc, u2);
             if (PK == 1 && p == kChunks - 1 && i + 1 < count) {
                 load_x(blockIdx.x + (i + 1) * gridDim.x);
                 ext1 += kXL;
             }
             gemm2(std::integral_constant<int, 2>{}, std::integral_constant<int, PAR ^ 1>{}, st[S2], d, gc);
-            d = step_begin(genc, u2 + 1);
+            d = step_begin(kindc, u2 + 1);
             gemm2(std::integral_constant<int, 3>{}, std::integral_constant<int, PAR ^ 1>{}, st[S2 + 1], d, gc);
         }
     };
     using std::integral_constant;
-    using Gen = std::true_type;
-    using Mid = std::false_type;
+    using Mid = integral_constant<int, 0>;
+    using Gen = integral_constant<int, 1>;
+    using End = integral_constant<int, 2>;
     using P0 = integral_constant<int, 0>;
     using P1 = integral_constant<int, 1>;
 
@@ -447,16 +583,38 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
 #pragma unroll
     for (int u = 0; u < 3; u++)
         if (u < S) {
-            const Dma d = dma_of(u);
+            const auto d = dma_of(u);
 #pragma unroll
             for (int k = 0; k < kLW; k++) dma_one(d, k);
         }
-    split_x();
+    split_x(std::integral_constant<bool, !OP>{});
     for (int i = 0; i < count; i++) {
         const int panel = blockIdx.x + i * gridDim.x;
 #pragma unroll
         for (int o = 0; o < kYT; o++) yacc[o] = f32x4_t{};
-        const int ub = i * kSPP;
+        int ub = i * kSP;
+        if constexpr (OP) {
+            // the O-projection's stages (waits counted at run time: the first
+            // three follow the last panel's stores, the last issues the
+            // residual's loads), then the first LayerNorm
+#pragma unroll
+            for (int j = 0; j < kO; j++) {
+                const auto d = step_begin(Gen{}, ub + j);
+                if (j == kO - 1) {
+                    // the residual, once the context's first halves are done
+                    // with (counted with the step before, after whose stage
+                    // loads it is issued)
+                    load_rows(op.res, panel);
+                    ext1 += kXL;
+                }
+                gemm_o(j, st[j & 3], d);
+            }
+            layernorm1();
+            split_x(std::true_type{});
+#pragma unroll
+            for (int o = 0; o < kYT; o++) yacc[o] = f32x4_t{};
+            ub += kO;
+        }
         period(P0{}, Gen{}, P0{}, ub, 0, i);
         period(P1{}, Gen{}, P1{}, ub + 2, 1, i);
         for (int p = 2; p < kChunks - 2; p += 2) {
@@ -464,11 +622,11 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
             period(P1{}, Mid{}, P1{}, ub + 4 * p + 2, p + 1, i);
         }
         period(P1{}, Mid{}, P0{}, ub + 4 * (kChunks - 2) - 2, kChunks - 2, i);
-        period(P1{}, Gen{}, P1{}, ub + 4 * (kChunks - 1) - 2, kChunks - 1, i);
-        period(integral_constant<int, 2>{}, Gen{}, P0{}, ub + kSPP - 2, kChunks, i);
+        period(P1{}, End{}, P1{}, ub + 4 * (kChunks - 1) - 2, kChunks - 1, i);
+        period(integral_constant<int, 2>{}, End{}, P0{}, ub + kSPP - 2, kChunks, i);
         const bool full = epilogue(panel);
         ext0 = full ? kXL : 0;  // the stores, after the loads of the panel's last step
-        if (i + 1 < count) split_x();
+        if (i + 1 < count) split_x(std::integral_constant<bool, !OP>{});
     }
 }
 
@@ -488,24 +646,54 @@ int tzh_mlp_pack_launch(hipStream_t st, const void *w1, const void *w2, void *ou
     return TZH_OK;
 }
 
+// W_o's codes (W8T, [384, 384]) -> the O-projection's stages for
+// mlp_fused_kernel (tzh_mlp_opack_bytes bytes, 16-byte aligned).
+size_t tzh_mlp_opack_bytes() { return (size_t)kOStages * kStage; }
+
+int tzh_mlp_opack_launch(hipStream_t st, const void *wo, void *out) {
+    if (!wo || !out || ((uintptr_t)out & 15)) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad O-projection pack operands");
+    const int threads = kOStages * kStageFrags * 64;
+    hipLaunchKernelGGL(mlp_opack_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, (const uint8_t *)wo,
+                       (_Float16 *)out);
+    TZH_LAUNCHED("mlp_opack_kernel");
+    return TZH_OK;
+}
+
 // Y = LayerNorm(X + GELU(X W1^T s1 + b1) W2^T s2 + b2) for X, Y [t, 384]
-// f32 (16-byte aligned, not overlapping) with the pack of W1 and W2.
+// f32 (16-byte aligned, not overlapping) with the pack of W1 and W2.  With
+// the O-projection (opack non-null): X = LayerNorm(res + (ctx W_o^T s_o +
+// b_o)) with gamma1, beta1 is formed on chip first, from ctx and res [t,
+// 384] f32 (x unused).  Y may be res itself (each token's residual row is
+// read, and its output row written, by the same wave, in that order) but
+// may not overlap ctx or overlap res partly.
 int tzh_mlp_fused_launch(hipStream_t st, int num_cus, const float *x, const void *pack, const uint16_t *s1,
                          const float *b1, const uint16_t *s2, const float *b2, const float *gamma, const float *beta,
-                         float eps, float *y, int64_t t) {
+                         float eps, float *y, int64_t t, const float *ctx, const float *res, const void *opack,
+                         const uint16_t *so, const float *bo, const float *gamma1, const float *beta1) {
     if (t < 0 || t > ((int64_t)1 << 30)) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad token count %lld", (long long)t);
     if (t == 0) return TZH_OK;
-    if (!x || !pack || !s1 || !b1 || !s2 || !b2 || !gamma || !beta || !y)
+    const bool op = opack != nullptr;
+    if (op) x = ctx;  // the activations the kernel loads
+    if (!x || !pack || !s1 || !b1 || !s2 || !b2 || !gamma || !beta || !y ||
+        (op && (!res || !so || !bo || !gamma1 || !beta1)))
         return tzh_fail(TZH_ERR_INVALID_ARGS, "null MLP operand");
-    if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)pack) & 15)
+    if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)pack | (op ? (uintptr_t)res | (uintptr_t)opack : 0)) & 15)
         return tzh_fail(TZH_ERR_INVALID_ARGS, "MLP operands must be 16-byte aligned");
-    const char *xb = (const char *)x, *yb = (const char *)y;
     const size_t bytes = (size_t)t * kD * 4;
-    if (xb < yb + bytes && yb < xb + bytes) return tzh_fail(TZH_ERR_INVALID_ARGS, "MLP input and output overlap");
+    auto overlap = [&](const void *a, const void *b) {
+        return (const char *)a < (const char *)b + bytes && (const char *)b < (const char *)a + bytes;
+    };
+    if (overlap(x, y) || (op && res != y && overlap(res, y)))
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "MLP input and output overlap");
     const int64_t panels = (t + kBM - 1) / kBM;
     const int grid = (int)(panels < num_cus ? panels : num_cus);
-    hipLaunchKernelGGL(mlp_fused_kernel, dim3((unsigned)grid), dim3(kWaves * 64), 0, st, x, (const _Float16 *)pack, s1,
-                       b1, s2, b2, gamma, beta, eps, y, (int)t);
+    const OProj o{ctx, res, (const _Float16 *)opack, so, bo, gamma1, beta1};
+    if (op)
+        hipLaunchKernelGGL(mlp_fused_kernel<true>, dim3((unsigned)grid), dim3(kWaves * 64), 0, st, x,
+                           (const _Float16 *)pack, s1, b1, s2, b2, gamma, beta, eps, y, (int)t, o);
+    else
+        hipLaunchKernelGGL(mlp_fused_kernel<false>, dim3((unsigned)grid), dim3(kWaves * 64), 0, st, x,
+                           (const _Float16 *)pack, s1, b1, s2, b2, gamma, beta, eps, y, (int)t, o);
     TZH_LAUNCHED("mlp_fused_kernel");
     return TZH_OK;
 }

@@ -36,6 +36,29 @@ __device__ __forceinline__ void vmem_load_issued() {}
 __device__ __forceinline__ void wave_lds_order() { asm volatile("" ::: "memory"); }
 #endif
 
+// Scheduling fence: the compiler moves no instruction across it, so the
+// fragment reads and ring loads issued before it go out before the matrix
+// products after it (left to itself, it issues each group's reads right
+// before the products that consume them, exposing the LDS latency).
+__device__ __forceinline__ void sched_fence() {
+#ifndef TZH_EMULATION
+    __builtin_amdgcn_sched_barrier(0);
+#endif
+}
+
+// This lane's index in its wave, formed from nothing (v_mbcnt over a full
+// mask) and opaque to the compiler: values derived from it are recomputed
+// where they are used instead of being held in registers through a kernel.
+__device__ __forceinline__ int lane_now() {
+#ifdef TZH_EMULATION
+    return emu::lane_id();
+#else
+    int l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    asm volatile("" : "+v"(l));
+    return l;
+#endif
+}
+
 // s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding; expcnt left at its maximum).
 template <int N>
 __device__ __forceinline__ void wait_vm_lgkm0() {

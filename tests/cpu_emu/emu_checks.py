@@ -627,6 +627,20 @@ def group_mlp():
                 assert np.isfinite(y).all() and err < 2e-5, (t, fused, err)
                 outs.append(y)
             assert float(np.abs(outs[0] - outs[1]).max()) < 2e-5
+        # the forward, whose O-projection, LayerNorm and feed-forward block
+        # run as one kernel (about 280 tokens: 5 panels on the two blocks),
+        # and with the fusion off, against the oracle
+        ids, lengths = synth.make_batch(5152, 6, seq_len=64, min_len=30)
+        ref = np.stack([oracle.arctic_forward(hw, ids[b, :Ln]) for b, Ln in enumerate(lengths)])
+        for fused in (1, 0):
+            check(L.tzh_arctic_set_ffn_fusion(m, fused))
+            out = np.empty((len(lengths), 384), np.float32)
+            check(L.tzh_arctic_forward_batch(m, out.ctypes.data, ids.ctypes.data, lengths.ctypes.data, len(lengths),
+                                             ids.shape[1]))
+            err = float(np.abs(out - ref).max())
+            print(f"  forward {int(lengths.sum())} tokens {'fused' if fused else 'unfused'}: max-abs {err:.2e} "
+                  f"vs oracle", flush=True)
+            assert np.isfinite(out).all() and err < 1e-5, (fused, err)
         check(L.tzh_arctic_set_ffn_fusion(m, 1))
         x = aligned_empty((32, 384), np.float32)
         x[...] = 1.0
