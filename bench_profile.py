@@ -27,7 +27,8 @@ LayerNorm GEMMs are linear_pipe_kernel<2> (with f32 activations the k = 384
 one has a tile configuration of its own); the one launched after attention
 is attn_out_ln and the one after ffn1_gelu is ffn2_ln; mlp_fused_kernel, the
 fused feed-forward block, is the stage ffn, and in its O-projection mode
-(template argument true) the stage attn_ffn.  The
+(template argument true) the stage attn_ffn; mlp_tail_kernel, which
+finishes the rows of its split last round, belongs to the same stage.  The
 pieces of a split partial round (the residual-only GEMM) and their row
 LayerNorm belong to the LayerNorm GEMM launched just before them.
 
@@ -72,6 +73,8 @@ def stage_of(kernel: str, prev: str | None) -> str | None:
     if "mlp_fused_kernel" in kernel:
         # <true>: the O-projection mode (mangled ...kernelILb1E...)
         return "attn_ffn" if ("ILb1E" in kernel or "<true>" in kernel) else "ffn"
+    if "mlp_tail_kernel" in kernel:  # the rows of the fused kernel's split last round
+        return prev if prev in ("attn_ffn", "ffn") else None
     epi = epi_of(kernel)
     if epi == 0:
         return "qkv"
@@ -101,8 +104,8 @@ def _instances(seq):
     instances per forward precision: {"fp32" | "fp16": {stage: [summed
     value of each instance]}}.  A forward runs from one pack_ids dispatch to
     the next; its precision is that of its attention kernel.  A dispatch that
-    continues the previous stage (the pieces of a split LayerNorm round)
-    adds to that stage's current instance.  Forwards that launch a stage
+    continues the previous stage (the pieces of a split LayerNorm round, the
+    fused kernel's split-round rows) adds to that stage's current instance.  Forwards that launch a stage
     twice in a row (bench.py's per-launch timing forwards repeat each stage)
     are left out, so that instances and averages are those of plain
     forwards."""
@@ -124,7 +127,7 @@ def _instances(seq):
             fwd, prec, repeated = {}, None, False
         if st == "attention":
             prec = "fp32" if "attn_varlen_f32_kernel" in name else "fp16"
-        if st == prev and (epi_of(name) == 3 or "ln_rows_kernel" in name):
+        if st == prev and (epi_of(name) == 3 or "ln_rows_kernel" in name or "mlp_tail_kernel" in name):
             fwd[st][-1] += v
         else:
             repeated = repeated or st == prev

@@ -439,8 +439,10 @@ int tzh_arctic_precision(tzh_model *model, int32_t *dtype);
  * (16-byte aligned, not overlapping; layer in [0, num_hidden_layers)),
  * in f32 whatever tzh_arctic_set_precision chose, enqueued on the model's
  * stream.  A layer whose two linears are int8 runs it as one kernel, the
- * 1536-wide intermediate kept on chip, unless the model's weights call for
- * row scaling; other layers run the GEMM pair. */
+ * 1536-wide intermediate kept on chip (its last, partial round of 64-token
+ * panels split by chunks over the idle CUs and finished by a second, small
+ * kernel), unless the model's weights call for row scaling; other layers
+ * run the GEMM pair. */
 int tzh_arctic_feed_forward(tzh_model *model, int32_t layer, const float *input, float *output, int64_t seq_len);
 
 /* Fused feed-forward switch (no counterpart in the reference): enable = 0
@@ -466,7 +468,8 @@ int tzh_arctic_set_timing(tzh_model *model, int32_t enable);
  * (static stage names: "pack_ids", "embed_ln", "qkv", "attention",
  * "attn_out_ln" and "ffn" (the fused feed-forward kernel), or "attn_ffn"
  * (the O-projection, its LayerNorm and the feed-forward block as one
- * kernel), or "attn_out_ln", "ffn1_gelu" and "ffn2_ln" (the GEMM pair),
+ * kernel; both fused stages include the kernel that finishes the rows of a
+ * split last round), or "attn_out_ln", "ffn1_gelu" and "ffn2_ln" (the GEMM pair),
  * "cls_l2", "hidden_f32"), at most
  * `capacity` entries; *count = number of launches (0 if the last forward was
  * not timed).  Waits for that forward to finish.  Either array may be NULL. */

@@ -41,7 +41,9 @@ int tzh_mlp_pack_launch(hipStream_t st, const void *w1, const void *w2, void *ou
 int tzh_mlp_fused_launch(hipStream_t st, int num_cus, const float *x, const void *pack, const uint16_t *s1,
                          const float *b1, const uint16_t *s2, const float *b2, const float *gamma, const float *beta,
                          float eps, float *y, int64_t t, const float *ctx, const float *res, const void *opack,
-                         const uint16_t *so, const float *bo, const float *gamma1, const float *beta1);
+                         const uint16_t *so, const float *bo, const float *gamma1, const float *beta1, void *scratch,
+                         size_t scratch_bytes);
+size_t tzh_mlp_tail_bytes(int num_cus);
 size_t tzh_mlp_opack_bytes();
 int tzh_mlp_opack_launch(hipStream_t st, const void *wo, void *out);
 
@@ -253,8 +255,11 @@ struct tzh_model {
     bool row_scaled = false;
     float attn_bound = 0.0f;
     // f32 forwards run the feed-forward block as one kernel (mlp.hip) where
-    // the layer has its pack and no row scaling (tzh_arctic_set_ffn_fusion)
+    // the layer has its pack and no row scaling (tzh_arctic_set_ffn_fusion);
+    // mlp_tail: that kernel's scratch for splitting its last round of panels
     bool fuse_ffn = true;
+    void *mlp_tail = nullptr;
+    size_t mlp_tail_bytes = 0;
     uint32_t *tok_ids = nullptr;
     int32_t *tok_pos = nullptr;
     int *meta = nullptr;  // device: cu[batch+1] | order[batch]
@@ -496,7 +501,7 @@ int ffn_part(tzh_model *m, const DevLayer &d, hipStream_t st, int32_t act, bool 
     if (part == 0)
         return tzh_mlp_fused_launch(st, cus, (const float *)x, d.mlp, d.ffn1.s, d.ffn1.b, d.ffn2.s, d.ffn2.b, d.ln2_g,
                                     d.ln2_b, eps, (float *)y, T, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
-                                    nullptr);
+                                    nullptr, m->mlp_tail, m->mlp_tail_bytes);
     if (part == 1) {
         if (d.ffn1.fmt == TZH_WF_F32)
             return linear_f32w(st, (const float *)x, d.ffn1, (float *)m->inter, T, H, 1536, TZH_OP_GELU, nullptr);
@@ -669,6 +674,10 @@ int upload_weights(tzh_model *m, const tzh_arctic_weights *w) {
         if (d.ffn1.fmt == TZH_WF_W8T && d.ffn2.fmt == TZH_WF_W8T) {
             TZH_TRY(dev_alloc(m, &d.mlp, tzh_mlp_pack_bytes()));
             TZH_TRY(tzh_mlp_pack_launch(m->ctx->stream, d.ffn1.w, d.ffn2.w, d.mlp));
+            if (!m->mlp_tail) {
+                m->mlp_tail_bytes = tzh_mlp_tail_bytes(m->ctx->num_cus);
+                TZH_TRY(dev_alloc(m, &m->mlp_tail, m->mlp_tail_bytes));
+            }
             if (d.o.fmt == TZH_WF_W8T) {
                 TZH_TRY(dev_alloc(m, &d.mlp_o, tzh_mlp_opack_bytes()));
                 TZH_TRY(tzh_mlp_opack_launch(m->ctx->stream, d.o.w, d.mlp_o));
@@ -1014,7 +1023,7 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
             TZH_TRY(stage("attn_ffn", [&]() {
                 return tzh_mlp_fused_launch(st, cus, nullptr, d.mlp, d.ffn1.s, d.ffn1.b, d.ffn2.s, d.ffn2.b, d.ln2_g,
                                             d.ln2_b, eps, h1f, T, (const float *)m->attn, hf, d.mlp_o, d.o.s, d.o.b,
-                                            d.ln1_g, d.ln1_b);
+                                            d.ln1_g, d.ln1_b, m->mlp_tail, m->mlp_tail_bytes);
             }));
             std::swap(m->h, m->h1);
             continue;

@@ -47,6 +47,8 @@
 //     8 g .. 32 j + 8 g + 7 of token t: the same columns as the lane's X
 //     registers, so the residual add is lane-local and each LayerNorm row's
 //     statistics reduce over the four lanes of its token with two row swaps.
+#include <algorithm>
+
 #include "pipe.h"
 
 namespace {
@@ -183,6 +185,20 @@ struct OProj {
     const float *b, *gamma, *beta;
 };
 
+// The last, partial round of panels split by intermediate chunks over the
+// CUs the round would leave idle.  Panels 0 .. full - 1 run whole, dealt
+// round robin over the blocks; with parts > 1, each later panel runs as
+// `parts` parts of kChunks / parts chunks each (block b: panel full + b /
+// parts, part b % parts).  A part stores its raw output sums (codes times
+// H, before scale and bias) to sums[(tp parts + part) 64 + token][384]
+// (tp = panel - full); in the O-projection mode part 0 also stores X (the
+// feed-forward's residual, formed on chip) to xs[tp 64 + token][384].
+// mlp_tail_kernel adds the parts and finishes the rows.
+struct TailSplit {
+    int full, parts;
+    float *sums, *xs;
+};
+
 // OP: the O-projection mode.  Each panel first forms X = LayerNorm(res +
 // (ctx W_o^T s_o + b_o)) (arctic.zig:716-746) in registers, from 12 more
 // weight stages (W_o's, streamed ahead of the feed-forward's) and the
@@ -192,7 +208,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     const float *__restrict__ X, const _Float16 *__restrict__ Wp, const uint16_t *__restrict__ s1,
     const float *__restrict__ b1, const uint16_t *__restrict__ s2, const float *__restrict__ b2,
     const float *__restrict__ gamma, const float *__restrict__ beta, float eps, float *__restrict__ Y, int T,
-    OProj op) {
+    OProj op, TailSplit ts) {
     constexpr int kO = OP ? kOStages : 0;  // O-projection stages at the head of each panel
     constexpr int kSP = kO + kSPP;         // stages per panel
     static_assert(kSP % 4 == 0, "a panel's stages fill whole turns of the ring");
@@ -205,8 +221,13 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     const int tid = threadIdx.x;
     const int wu = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int panels = (T + kBM - 1) / kBM;
-    const int count = blockIdx.x < panels ? (panels - 1 - blockIdx.x) / gridDim.x + 1 : 0;
-    const int S = count * kSP;  // stages this block streams
+    const int count = (int)blockIdx.x < ts.full ? (ts.full - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+    // this block's part of a split panel, if any: chunks c0 .. c0 + nc - 1
+    const bool tail = ts.parts > 1 && (int)blockIdx.x < (panels - ts.full) * ts.parts;
+    const int tpanel = ts.full + (int)blockIdx.x / ts.parts, tpart = (int)blockIdx.x % ts.parts;
+    const int nc = kChunks / ts.parts, c0 = tpart * nc;
+    const int SF = count * kSP;                          // stages of the whole panels
+    const int S = SF + (tail ? kO + kSPC * nc : 0);  // stages this block streams
     if (S == 0) return;
 
     // per-feature parameters -> LDS (visible after the first stage barrier)
@@ -235,21 +256,32 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     //   s = 4p - 2, 4p - 1:  W1 of chunk p          (p = 1 .. 23)
     //   s = 4p, 4p + 1:      W2 of chunk p - 1      (outputs 0..191, 192..383)
     //   s = 94, 95:          W2 of chunk 23
-    // (after the O-projection's kO stages in the O-projection mode).  Stage
-    // u of the block sits in ring slot u % 4; pack_stage gives the pack's
-    // stage (4 c + q) at feed-forward stream position s.
-    auto pack_stage = [](int s) __attribute__((always_inline)) {
-        if (s < 2) return s;
-        if (s >= kSPP - 2) return 4 * (kChunks - 1) + 2 + (s - (kSPP - 2));
-        const int p = (s + 2) >> 2, r = (s + 2) & 3;
-        return r < 2 ? 4 * p + r : 4 * (p - 1) + r;
+    // (after the O-projection's kO stages in the O-projection mode; a part
+    // of a split panel streams the same for its chunks c0 .. c0 + n - 1).
+    // Stage u of the block sits in ring slot u % 4; pack_stage gives the
+    // pack's stage (4 c + q) at feed-forward stream position s.
+    auto pack_stage = [](int s, int cb, int n) __attribute__((always_inline)) {
+        // (selects, not branches: one wave per SIMD has nothing to hide a
+        // branch behind)
+        const int p = cb + ((s + 2) >> 2), r = (s + 2) & 3, last = kSPC * n - 2;
+        int v = r < 2 ? 4 * p + r : 4 * (p - 1) + r;
+        v = s < 2 ? 4 * cb + s : v;
+        return s >= last ? 4 * (cb + n - 1) + 2 + (s - last) : v;
     };
     char *const ring = &st[0][0];
     const char *const wsrc = (const char *)Wp + (size_t)wu * kLW * kFrag;
     const char *const osrc = OP ? (const char *)op.wp + (size_t)wu * kLW * kFrag : nullptr;
-    auto dma_of = [&](int u) __attribute__((always_inline)) {
-        const int sp = u % kSP;
-        const char *src = OP && sp < kO ? osrc + (size_t)sp * kStage : wsrc + (size_t)pack_stage(sp - kO) * kStage;
+    // stage u's loads; WHOLE: u is a feed-forward stage of a whole panel
+    auto dma_of = [&](int u, auto wholec) __attribute__((always_inline)) {
+        const char *src;
+        if constexpr (decltype(wholec)::value) {
+            src = wsrc + (size_t)pack_stage(u % kSP - kO, 0, kChunks) * kStage;
+        } else {
+            const bool tl = u >= SF;
+            const int sp = tl ? u - SF : u % kSP;
+            src = OP && sp < kO ? osrc + (size_t)sp * kStage
+                                : wsrc + (size_t)pack_stage(sp - kO, tl ? c0 : 0, tl ? nc : kChunks) * kStage;
+        }
         return StageDma<true>{src, ring + (u & 3) * kStage + wu * kLW * kFrag};
     };
     auto dma_one = [&](const auto &d, int i) __attribute__((always_inline)) {
@@ -313,7 +345,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         if constexpr (K == 0) {
             wait_vm_lgkm0<2 * kLW>();
             lds_barrier_only();  // every wave's stage u landed; stage u - 1 fully read
-            return dma_of(u + 3);
+            return dma_of(u + 3, std::true_type{});  // (the middle steps load their own panel's stages)
         } else {
             const int ahead = K == 1 || S - 1 - u >= 2 ? 2 : S - 1 - u;
             wait_vm_n(kLW * ahead + ext0 + ext1 + ext2);
@@ -322,10 +354,10 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
             ext1 = ext0;
             ext0 = 0;
             if constexpr (K == 1) {
-                return dma_of(u + 3);
+                return dma_of(u + 3, std::false_type{});
             } else {
                 if (u + 3 >= S) return StageDma<false>{nullptr, nullptr};
-                const StageDma<true> d = dma_of(u + 3);
+                const StageDma<true> d = dma_of(u + 3, std::false_type{});
                 return StageDma<false>{d.src, d.dst};
             }
         }
@@ -541,11 +573,12 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     // p - 1 (p >= 1; two stages) with chunk p's GELU between its products.
     // PK 0: p = 0 (its GELU alone), 1: 1 <= p <= 23, 2: p = 24.  KIND: the
     // step kind of its stages (GEN, END next to a panel's ends, else MID).
-    // PAR = p & 1: chunk p's H goes to buffer PAR, chunk p - 1's is in
-    // PAR ^ 1.  At p = 23 the next panel's X loads go out once this panel's
-    // first GEMM is done, before the loads of the stage after next (counted
-    // with the step before, after whose stage loads they are issued).
-    auto period = [&](auto pkc, auto kindc, auto parc, int u0, int p, int i) __attribute__((always_inline)) {
+    // PAR: chunk p's H goes to buffer PAR, chunk p - 1's is in PAR ^ 1 (p &
+    // 1, or p - c0 for a part).  At p = 23 the loads of panel nextp's X
+    // (if nextp >= 0) go out once this panel's first GEMM is done, before
+    // the loads of the stage after next (counted with the step before, after
+    // whose stage loads they are issued).
+    auto period = [&](auto pkc, auto kindc, auto parc, int u0, int p, int nextp) __attribute__((always_inline)) {
         constexpr int PK = decltype(pkc)::value, PAR = decltype(parc)::value;
         constexpr int S1 = PK == 0 ? 0 : 2;  // ring slots of this period's first two stages
         if constexpr (PK <= 1) {
@@ -557,14 +590,14 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         if constexpr (PK == 0) {
 #pragma unroll
             for (int jj = 0; jj < 2; jj++)
-                split_f32x8(gelu_tile(0, 2 * jj), gelu_tile(0, 2 * jj + 1), hbh[0][jj], hbl[0][jj]);
+                split_f32x8(gelu_tile(p, 2 * jj), gelu_tile(p, 2 * jj + 1), hbh[0][jj], hbl[0][jj]);
         } else {
             constexpr int S2 = PK == 1 ? 0 : 2;  // ring slots of the second GEMM's stages
             const int u2 = PK == 1 ? u0 + 2 : u0;
             const int gc = PK == 1 ? p : -1;
             auto d = step_begin(kindc, u2);
-            if (PK == 1 && p == kChunks - 1 && i + 1 < count) {
-                load_x(blockIdx.x + (i + 1) * gridDim.x);
+            if (PK == 1 && p == kChunks - 1 && nextp >= 0) {
+                load_x(nextp);
                 ext1 += kXL;
             }
             gemm2(std::integral_constant<int, 2>{}, std::integral_constant<int, PAR ^ 1>{}, st[S2], d, gc);
@@ -579,55 +612,145 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     using P0 = integral_constant<int, 0>;
     using P1 = integral_constant<int, 1>;
 
-    load_x(blockIdx.x);
+    // the O-projection's stages (waits counted at run time: the first three
+    // follow the last panel's stores, the last issues the residual's loads),
+    // then the first LayerNorm
+    auto o_phase = [&](int panel, int ub) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < kO; j++) {
+            const auto d = step_begin(Gen{}, ub + j);
+            if (j == kO - 1) {
+                // the residual, once the context's first halves are done
+                // with (counted with the step before, after whose stage
+                // loads it is issued)
+                load_rows(op.res, panel);
+                ext1 += kXL;
+            }
+            gemm_o(j, st[j & 3], d);
+        }
+        layernorm1();
+        split_x(std::true_type{});
+#pragma unroll
+        for (int o = 0; o < kYT; o++) yacc[o] = f32x4_t{};
+    };
+
+    load_x(count > 0 ? (int)blockIdx.x : tpanel);
 #pragma unroll
     for (int u = 0; u < 3; u++)
         if (u < S) {
-            const auto d = dma_of(u);
+            const auto d = dma_of(u, std::false_type{});
 #pragma unroll
             for (int k = 0; k < kLW; k++) dma_one(d, k);
         }
     split_x(std::integral_constant<bool, !OP>{});
     for (int i = 0; i < count; i++) {
         const int panel = blockIdx.x + i * gridDim.x;
+        const int nextp = i + 1 < count ? panel + (int)gridDim.x : (tail ? tpanel : -1);
 #pragma unroll
         for (int o = 0; o < kYT; o++) yacc[o] = f32x4_t{};
         int ub = i * kSP;
         if constexpr (OP) {
-            // the O-projection's stages (waits counted at run time: the first
-            // three follow the last panel's stores, the last issues the
-            // residual's loads), then the first LayerNorm
-#pragma unroll
-            for (int j = 0; j < kO; j++) {
-                const auto d = step_begin(Gen{}, ub + j);
-                if (j == kO - 1) {
-                    // the residual, once the context's first halves are done
-                    // with (counted with the step before, after whose stage
-                    // loads it is issued)
-                    load_rows(op.res, panel);
-                    ext1 += kXL;
-                }
-                gemm_o(j, st[j & 3], d);
-            }
-            layernorm1();
-            split_x(std::true_type{});
-#pragma unroll
-            for (int o = 0; o < kYT; o++) yacc[o] = f32x4_t{};
+            o_phase(panel, ub);
             ub += kO;
         }
-        period(P0{}, Gen{}, P0{}, ub, 0, i);
-        period(P1{}, Gen{}, P1{}, ub + 2, 1, i);
+        period(P0{}, Gen{}, P0{}, ub, 0, nextp);
+        period(P1{}, Gen{}, P1{}, ub + 2, 1, nextp);
         for (int p = 2; p < kChunks - 2; p += 2) {
-            period(P1{}, Mid{}, P0{}, ub + 4 * p - 2, p, i);
-            period(P1{}, Mid{}, P1{}, ub + 4 * p + 2, p + 1, i);
+            period(P1{}, Mid{}, P0{}, ub + 4 * p - 2, p, nextp);
+            period(P1{}, Mid{}, P1{}, ub + 4 * p + 2, p + 1, nextp);
         }
-        period(P1{}, Mid{}, P0{}, ub + 4 * (kChunks - 2) - 2, kChunks - 2, i);
-        period(P1{}, End{}, P1{}, ub + 4 * (kChunks - 1) - 2, kChunks - 1, i);
-        period(integral_constant<int, 2>{}, End{}, P0{}, ub + kSPP - 2, kChunks, i);
+        period(P1{}, Mid{}, P0{}, ub + 4 * (kChunks - 2) - 2, kChunks - 2, nextp);
+        period(P1{}, End{}, P1{}, ub + 4 * (kChunks - 1) - 2, kChunks - 1, nextp);
+        period(integral_constant<int, 2>{}, End{}, P0{}, ub + kSPP - 2, kChunks, nextp);
         const bool full = epilogue(panel);
         ext0 = full ? kXL : 0;  // the stores, after the loads of the panel's last step
-        if (i + 1 < count) split_x(std::integral_constant<bool, !OP>{});
+        if (nextp >= 0) split_x(std::integral_constant<bool, !OP>{});
     }
+    if (tail) {
+        // this block's part of a split panel: its chunks' periods (every
+        // step's wait counted at run time; the stream ends with the part),
+        // then its raw sums (and, part 0, X) to the scratch
+#pragma unroll
+        for (int o = 0; o < kYT; o++) yacc[o] = f32x4_t{};
+        int ub = SF;
+        if constexpr (OP) {
+            o_phase(tpanel, ub);
+            ub += kO;
+            if (tpart == 0) {
+                // X, the residual, now (not parked through the part); issued
+                // after the last O step's stage loads, counted with that step
+                const int ln = lane_now(), g = ln >> 4;
+                float *const px = ts.xs + ((size_t)(tpanel - ts.full) * kBM + wu * kTokW + (ln & 15)) * kD;
+#pragma unroll
+                for (int j = 0; j < kXJ; j++)
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        f32x4_t x;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) x[e] = unpark(xr[8 * j + 4 * h + e]);
+                        *(f32x4_t *)(px + 32 * j + 8 * g + 4 * h) = x;
+                        vmem_store_issued();
+                    }
+                ext0 += kXL;
+            }
+        }
+        period(P0{}, End{}, P0{}, ub, c0, -1);
+        for (int pr = 1; pr < nc; pr += 2) {
+            period(P1{}, End{}, P1{}, ub + 4 * pr - 2, c0 + pr, -1);
+            if (pr + 1 < nc) period(P1{}, End{}, P0{}, ub + 4 * pr + 2, c0 + pr + 1, -1);
+        }
+        if (nc & 1)
+            period(integral_constant<int, 2>{}, End{}, P1{}, ub + kSPC * nc - 2, c0 + nc, -1);
+        else
+            period(integral_constant<int, 2>{}, End{}, P0{}, ub + kSPC * nc - 2, c0 + nc, -1);
+        const int ln = lane_now(), g = ln >> 4;
+        float *const ps =
+            ts.sums + (((size_t)(tpanel - ts.full) * ts.parts + tpart) * kBM + wu * kTokW + (ln & 15)) * kD;
+#pragma unroll
+        for (int j = 0; j < kXJ; j++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                *(f32x4_t *)(ps + 32 * j + 8 * g + 4 * h) = yacc[2 * j + h];
+                vmem_store_issued();
+            }
+    }
+}
+
+// Rows t0 .. T - 1 of the split panels (the tail parts of mlp_fused_kernel):
+// Y = LayerNorm(X + ((sum over parts) * s2 + b2)) with the parts' sums added
+// in part order (arctic.zig:780-783; the LayerNorm of layernorm.zig:26-117,
+// two-pass as in the fused kernel's epilogue); xs: X's row t0 + r at r.
+// One wave per row, lane l holding columns 6 l .. 6 l + 5.
+__global__ void __launch_bounds__(256) mlp_tail_kernel(const float *__restrict__ sums, const float *__restrict__ xs,
+                                                       int parts, const uint16_t *__restrict__ s2,
+                                                       const float *__restrict__ b2, const float *__restrict__ gamma,
+                                                       const float *__restrict__ beta, float eps,
+                                                       float *__restrict__ Y, int t0, int T) {
+    const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (t0 + row >= T) return;
+    const int lane = threadIdx.x & 63, tp = row / kBM, tok = row % kBM;
+    const int n0 = 6 * lane;
+    float acc[6];
+    for (int p = 0; p < parts; p++) {
+        const float *sr = sums + (((size_t)tp * parts + p) * kBM + tok) * kD + n0;
+#pragma unroll
+        for (int e = 0; e < 6; e++) acc[e] = p == 0 ? sr[e] : acc[e] + sr[e];
+    }
+    const float *xr = xs + (size_t)row * kD + n0;
+    float v[6], sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 6; e++) {
+        v[e] = xr[e] + (acc[e] * f16_bits_to_f32(s2[n0 + e]) + b2[n0 + e]);
+        sum += v[e];
+    }
+    const float mean = wave_sum(sum) / (float)kD;
+    float sq = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 6; e++) sq += (v[e] - mean) * (v[e] - mean);
+    const float inv_std = 1.0f / sqrtf(wave_sum(sq) / (float)kD + eps);
+    float *yr = Y + (size_t)(t0 + row) * kD + n0;
+#pragma unroll
+    for (int e = 0; e < 6; e++) yr[e] = ((v[e] - mean) * inv_std) * gamma[n0 + e] + beta[n0 + e];
 }
 
 }  // namespace
@@ -659,17 +782,54 @@ int tzh_mlp_opack_launch(hipStream_t st, const void *wo, void *out) {
     return TZH_OK;
 }
 
+namespace {
+
+// The split of the last round for t tokens on num_cus CUs: the most parts
+// (a divisor of the 24 chunks) whose blocks fit the CUs the round leaves
+// idle, when the scratch holds their sums; otherwise none (parts = 1).
+TailSplit choose_tail(int64_t t, int num_cus, size_t scratch_bytes) {
+    const int panels = (int)((t + kBM - 1) / kBM);
+    const int rest = panels % num_cus;
+    TailSplit ts{panels, 1, nullptr, nullptr};
+    if (rest == 0) return ts;
+    for (int parts : {24, 12, 8, 6, 4, 3, 2}) {
+        const size_t need = (size_t)rest * (parts + 1) * kBM * kD * 4;
+        if (rest * parts <= num_cus && need <= scratch_bytes) {
+            ts.full = panels - rest;
+            ts.parts = parts;
+            return ts;
+        }
+    }
+    return ts;
+}
+
+}  // namespace
+
+// Scratch bytes the split of the last round can use on num_cus CUs, at most
+// (any token count).
+size_t tzh_mlp_tail_bytes(int num_cus) {
+    size_t most = 0;
+    for (int rest = 1; rest <= num_cus / 2; rest++) {
+        const TailSplit ts = choose_tail((int64_t)rest * kBM, num_cus, (size_t)-1);
+        most = std::max(most, (size_t)rest * (ts.parts + 1) * kBM * kD * 4);
+    }
+    return most;
+}
+
 // Y = LayerNorm(X + GELU(X W1^T s1 + b1) W2^T s2 + b2) for X, Y [t, 384]
 // f32 (16-byte aligned, not overlapping) with the pack of W1 and W2.  With
 // the O-projection (opack non-null): X = LayerNorm(res + (ctx W_o^T s_o +
 // b_o)) with gamma1, beta1 is formed on chip first, from ctx and res [t,
 // 384] f32 (x unused).  Y may be res itself (each token's residual row is
 // read, and its output row written, by the same wave, in that order) but
-// may not overlap ctx or overlap res partly.
+// may not overlap ctx or overlap res partly.  scratch (16-byte aligned,
+// overlapping none of them; may be null): room for the split of the last
+// round (tzh_mlp_tail_bytes); without enough, that round runs whole panels.
 int tzh_mlp_fused_launch(hipStream_t st, int num_cus, const float *x, const void *pack, const uint16_t *s1,
                          const float *b1, const uint16_t *s2, const float *b2, const float *gamma, const float *beta,
                          float eps, float *y, int64_t t, const float *ctx, const float *res, const void *opack,
-                         const uint16_t *so, const float *bo, const float *gamma1, const float *beta1) {
+                         const uint16_t *so, const float *bo, const float *gamma1, const float *beta1, void *scratch,
+                         size_t scratch_bytes) {
     if (t < 0 || t > ((int64_t)1 << 30)) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad token count %lld", (long long)t);
     if (t == 0) return TZH_OK;
     const bool op = opack != nullptr;
@@ -685,15 +845,31 @@ int tzh_mlp_fused_launch(hipStream_t st, int num_cus, const float *x, const void
     };
     if (overlap(x, y) || (op && res != y && overlap(res, y)))
         return tzh_fail(TZH_ERR_INVALID_ARGS, "MLP input and output overlap");
-    const int64_t panels = (t + kBM - 1) / kBM;
-    const int grid = (int)(panels < num_cus ? panels : num_cus);
+    if (num_cus < 1) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad CU count %d", num_cus);
+    if ((uintptr_t)scratch & 15) return tzh_fail(TZH_ERR_INVALID_ARGS, "MLP scratch must be 16-byte aligned");
+    const int panels = (int)((t + kBM - 1) / kBM);
+    TailSplit ts = choose_tail(t, num_cus, scratch ? scratch_bytes : 0);
+    const int rest = panels - ts.full;
+    int grid = panels < num_cus ? panels : num_cus;
+    if (ts.parts > 1) {
+        ts.sums = (float *)scratch;
+        ts.xs = op ? ts.sums + (size_t)rest * ts.parts * kBM * kD : nullptr;
+        grid = ts.full > 0 ? num_cus : rest * ts.parts;
+    }
     const OProj o{ctx, res, (const _Float16 *)opack, so, bo, gamma1, beta1};
     if (op)
         hipLaunchKernelGGL(mlp_fused_kernel<true>, dim3((unsigned)grid), dim3(kWaves * 64), 0, st, x,
-                           (const _Float16 *)pack, s1, b1, s2, b2, gamma, beta, eps, y, (int)t, o);
+                           (const _Float16 *)pack, s1, b1, s2, b2, gamma, beta, eps, y, (int)t, o, ts);
     else
         hipLaunchKernelGGL(mlp_fused_kernel<false>, dim3((unsigned)grid), dim3(kWaves * 64), 0, st, x,
-                           (const _Float16 *)pack, s1, b1, s2, b2, gamma, beta, eps, y, (int)t, o);
+                           (const _Float16 *)pack, s1, b1, s2, b2, gamma, beta, eps, y, (int)t, o, ts);
     TZH_LAUNCHED("mlp_fused_kernel");
+    if (ts.parts > 1) {
+        const int t0 = ts.full * kBM, rows = (int)t - t0;
+        hipLaunchKernelGGL(mlp_tail_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, ts.sums,
+                           op ? (const float *)ts.xs : x + (size_t)t0 * kD, ts.parts, s2, b2, gamma, beta, eps, y, t0,
+                           (int)t);
+        TZH_LAUNCHED("mlp_tail_kernel");
+    }
     return TZH_OK;
 }

@@ -468,12 +468,19 @@ def group_attention():
                     assert (np.abs(got - ref) <= tol).all(), (lengths, dt, bi, h, float(np.abs(got - ref).max()))
 
 
-def group_arctic():
+def arctic_model(seed=1234):
     cfg = synth.Config()
-    w = synth.quantize(synth.make_arctic_f32(1234, cfg, ln_random=True))
-    hw = synth.HostWeights(w, cfg)
+    hw = synth.HostWeights(synth.quantize(synth.make_arctic_f32(seed, cfg, ln_random=True)), cfg)
     m = C.c_void_p()
     check(L.tzh_arctic_upload(CTX, C.byref(hw.struct), C.byref(m)))
+    return hw, m
+
+
+def group_arctic():
+    # the f32 forward (the fused O-projection + feed-forward kernel), its
+    # hidden states, and on a small batch and the GEMM pair (cheaper to
+    # emulate) packed = padded ids bit for bit and the bad-id count
+    hw, m = arctic_model()
     ids, lengths = synth.make_batch(21, 3, seq_len=40, min_len=5)
     out = np.empty((3, 384), np.float32)
     check(L.tzh_arctic_forward_batch(m, out.ctypes.data, ids.ctypes.data, lengths.ctypes.data, 3, 40))
@@ -485,26 +492,38 @@ def group_arctic():
     check(L.tzh_arctic_hidden(m, hid.ctypes.data, ids.ctypes.data, lengths.ctypes.data, 3, 40, 1))
     r1 = oracle.arctic_hidden(hw, ids[0, :lengths[0]], 1)
     assert np.abs(hid[:lengths[0]] - r1).max() < 1e-4
-    # the opt-in f16 activations
+    check(L.tzh_arctic_set_ffn_fusion(m, 0))
+    ids, lengths = synth.make_batch(22, 3, seq_len=12, min_len=3)
+    small = np.empty((3, 384), np.float32)
+    check(L.tzh_arctic_forward_batch(m, small.ctypes.data, ids.ctypes.data, lengths.ctypes.data, 3, 12))
+    flat, _ = synth.packed(ids, lengths)
+    out2 = np.empty((3, 384), np.float32)
+    check(L.tzh_arctic_forward_batch(m, out2.ctypes.data, flat.ctypes.data, lengths.ctypes.data, 3, 0))
+    assert np.array_equal(small, out2)
+    bad = ids.copy()
+    bad[1, 2] = 99999
+    check(L.tzh_arctic_forward_batch(m, out2.ctypes.data, bad.ctypes.data, lengths.ctypes.data, 3, 12))
+    n = C.c_int32()
+    check(L.tzh_arctic_bad_id_count(m, C.byref(n)))
+    assert n.value == 1
+    check(L.tzh_arctic_free(m))
+
+
+def group_arctic_f16w():
+    # the opt-in f16 activations, and the f32 model (MatWeight.f32 linears on
+    # the f32 GEMM, two layers)
+    hw, m = arctic_model()
+    ids, lengths = synth.make_batch(21, 3, seq_len=40, min_len=5)
+    ref = np.stack([oracle.arctic_forward(hw, ids[b, :Ln]) for b, Ln in enumerate(lengths)])
+    r1 = oracle.arctic_hidden(hw, ids[0, :lengths[0]], 1)
+    hid = np.empty((int(lengths.sum()), 384), np.float32)
     check(L.tzh_arctic_set_precision(m, _abi.F16))
     out16 = np.empty((3, 384), np.float32)
     check(L.tzh_arctic_forward_batch(m, out16.ctypes.data, ids.ctypes.data, lengths.ctypes.data, 3, 40))
     assert np.abs(out16 - ref).max() < 1e-3
     check(L.tzh_arctic_hidden(m, hid.ctypes.data, ids.ctypes.data, lengths.ctypes.data, 3, 40, 1))
     assert np.abs(hid[:lengths[0]] - r1).max() < 2e-2
-    check(L.tzh_arctic_set_precision(m, _abi.F32))
-    flat, _ = synth.packed(ids, lengths)
-    out2 = np.empty((3, 384), np.float32)
-    check(L.tzh_arctic_forward_batch(m, out2.ctypes.data, flat.ctypes.data, lengths.ctypes.data, 3, 0))
-    assert np.array_equal(out, out2)
-    bad = ids.copy()
-    bad[1, 2] = 99999
-    check(L.tzh_arctic_forward_batch(m, out2.ctypes.data, bad.ctypes.data, lengths.ctypes.data, 3, 40))
-    n = C.c_int32()
-    check(L.tzh_arctic_bad_id_count(m, C.byref(n)))
-    assert n.value == 1
     check(L.tzh_arctic_free(m))
-    # the f32 model (MatWeight.f32 linears on the f32 GEMM), two layers
     cfg2 = synth.Config(num_hidden_layers=2)
     w32 = synth.make_arctic_f32(77, cfg2, ln_random=True)
     hw32 = synth.HostWeights(w32, cfg2)
@@ -600,9 +619,10 @@ def group_mlp():
     # the feed-forward block as one kernel (mlp.hip) and as the GEMM pair,
     # through tzh_arctic_feed_forward, against the oracle.  Run with two
     # emulated CUs (TZH_EMU_CUS=2, as tests/test_cpu_emulation.py does),
-    # 300 tokens make 5 panels of 64 on two blocks (3 and 2 panels: the
-    # weight ring runs on across panels), the last holding 44 tokens (two
-    # full waves, one partial, one with none).
+    # 300 tokens make 5 panels of 64 on two blocks: two whole panels each
+    # (the weight ring runs on across panels), then the fifth, holding 44
+    # tokens (two full waves, one partial, one with none), split into two
+    # parts of 12 chunks; 1 to 64 tokens make one panel, split the same way.
     cfg = synth.Config(num_hidden_layers=2)
     w = synth.quantize(synth.make_arctic_f32(5150, cfg, ln_random=True))
     hw = synth.HostWeights(w, cfg)
@@ -647,6 +667,40 @@ def group_mlp():
         assert L.tzh_arctic_feed_forward(m, 0, x.ctypes.data, x.ctypes.data, 32) == _abi.ERR_INVALID_ARGS
         assert L.tzh_arctic_feed_forward(m, 2, x.ctypes.data, x.ctypes.data + 32 * 384 * 4, 1) == _abi.ERR_INVALID_ARGS
         check(L.tzh_arctic_feed_forward(m, 0, x.ctypes.data, None, 0))
+    finally:
+        check(L.tzh_arctic_free(m))
+
+
+def group_mlp_split():
+    # The fused kernel's split last round (mlp.hip, TailSplit) with 24
+    # emulated CUs (TZH_EMU_CUS=24, as tests/test_cpu_emulation.py does):
+    # 1, 2 and 3 panels split into 24, 12 and 8 parts (one, two and three
+    # chunks each), through tzh_arctic_feed_forward and, with the
+    # O-projection at the kernel's head, the forward; against the oracle.
+    cfg = synth.Config(num_hidden_layers=2)
+    w = synth.quantize(synth.make_arctic_f32(5160, cfg, ln_random=True))
+    hw = synth.HostWeights(w, cfg)
+    m = C.c_void_p()
+    check(L.tzh_arctic_upload(CTX, C.byref(hw.struct), C.byref(m)))
+    rng = np.random.default_rng(5161)
+    try:
+        for t, layer in ((1, 0), (100, 1), (130, 0)):
+            x = aligned_empty((t, 384), np.float32)
+            x[...] = rng.standard_normal((t, 384), dtype=np.float32)
+            y = aligned_empty((t, 384), np.float32)
+            y[...] = np.nan
+            check(L.tzh_arctic_feed_forward(m, layer, x.ctypes.data, y.ctypes.data, t))
+            err = float(np.abs(y - ffn_oracle(w, layer, x, cfg.layer_norm_eps)).max())
+            print(f"  split feed-forward t={t}: max-abs {err:.2e} vs oracle", flush=True)
+            assert np.isfinite(y).all() and err < 2e-5, (t, err)
+        for seed, n, seq, lo in ((5162, 2, 30, 10), (5163, 3, 64, 40)):
+            ids, lengths = synth.make_batch(seed, n, seq_len=seq, min_len=lo)
+            ref = np.stack([oracle.arctic_forward(hw, ids[b, :Ln]) for b, Ln in enumerate(lengths)])
+            out = np.empty((n, 384), np.float32)
+            check(L.tzh_arctic_forward_batch(m, out.ctypes.data, ids.ctypes.data, lengths.ctypes.data, n, seq))
+            err = float(np.abs(out - ref).max())
+            print(f"  split forward {int(lengths.sum())} tokens: max-abs {err:.2e} vs oracle", flush=True)
+            assert np.isfinite(out).all() and err < 1e-5, err
     finally:
         check(L.tzh_arctic_free(m))
 
@@ -863,7 +917,8 @@ def group_gemm_fp():
 
 GROUPS = {"eval": group_eval, "gemm_fp": group_gemm_fp, "gemm": group_gemm, "gemm_ln": group_gemm_ln, "range": group_range,
           "attention": group_attention,
-          "arctic": group_arctic, "embed": group_embed, "models": group_models, "mlp": group_mlp,
+          "arctic": group_arctic, "arctic_f16w": group_arctic_f16w, "embed": group_embed, "models": group_models, "mlp": group_mlp,
+          "mlp_split": group_mlp_split,
           "nodes": group_nodes}
 
 if __name__ == "__main__":

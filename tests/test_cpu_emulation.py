@@ -34,11 +34,15 @@ def emu_env():
     return env
 
 
-GROUPS = ["eval", "attention", "gemm", "gemm_ln", "range", "models", "nodes", "gemm_fp", "mlp"]
+GROUPS = ["eval", "attention", "gemm", "gemm_ln", "range", "models", "nodes", "gemm_fp", "mlp", "mlp_split", "arctic",
+          "arctic_f16w"]
 # emulated CU count per group (default 16): two CUs give the fused
 # feed-forward kernel blocks of several panels at a size the emulation
-# runs in about a minute
-GROUP_ENV = {"mlp": {"TZH_EMU_CUS": "2"}}
+# runs in about a minute (and a last round split in two); 24 CUs split
+# one to three panels into 24, 12 and 8 parts; with four, the small
+# forwards of group arctic split their two panels in two, not eight (each
+# part repeats its panel's O-projection, which the emulation pays for)
+GROUP_ENV = {"mlp": {"TZH_EMU_CUS": "2"}, "mlp_split": {"TZH_EMU_CUS": "24"}, "arctic": {"TZH_EMU_CUS": "4"}}
 
 
 # test_gpu_eval.py's whole sequence in one process, in file order, with the

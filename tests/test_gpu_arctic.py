@@ -20,6 +20,13 @@ from tests.conftest import GOLDEN, cosine
 
 pytestmark = pytest.mark.gpu
 CFG = synth.Config()
+# A sequence's embedding in two batch compositions (alone, in another order):
+# the same to f32 rounding.  The fused feed-forward kernel splits its last
+# round of 64-token panels over idle CUs and adds the parts' sums in another
+# order than a whole panel's, so which tokens land there changes the
+# rounding (about 3e-8 on these unit-norm embeddings).  A given batch is
+# deterministic, bit for bit.
+COMPOSITION_TOL = 1e-6
 
 
 @pytest.fixture(scope="module")
@@ -129,7 +136,7 @@ def test_config4_batch32_seq128(model, host):
 
 def test_config5_headline_batch(model, host):
     """B=256, lengths U[16,512]: full batch on the GPU, oracle on a sample
-    (incl. the longest and shortest), exact invariants on all of it."""
+    (incl. the longest and shortest), invariants on all of it."""
     ids, lengths = synth.make_batch(5, 256, seq_len=512)
     got = gpu_embed(model, ids, lengths)
     assert np.isfinite(got).all()
@@ -139,10 +146,12 @@ def test_config5_headline_batch(model, host):
     assert_embedding_parity(got[sample], ref)
     # packed input == padded input, bit for bit
     assert np.array_equal(gpu_embed(model, ids, lengths, packed=True), got)
-    # batch order invariance, bit for bit
+    # batch order invariance: within f32 rounding (another order puts other
+    # tokens in the split last round of the fused feed-forward kernel, whose
+    # parts' sums are added in another order)
     perm = np.random.default_rng(0).permutation(256)
     got_p = gpu_embed(model, ids[perm], lengths[perm])
-    assert np.array_equal(got_p, got[perm])
+    assert float(np.abs(got_p - got[perm]).max()) < COMPOSITION_TOL
 
 
 def test_single_sequence_forward(model, host):
@@ -167,7 +176,7 @@ def test_host_slice_entry_points(model, host):
     assert np.array_equal(out, gpu_embed(model, ids, lengths))
     one = np.zeros(CFG.hidden_size, np.float32)
     check(lib().tzh_arctic_forward_host(model.handle, one.ctypes.data, seqs[2].ctypes.data, len(seqs[2])))
-    assert np.array_equal(one, out[2])
+    assert float(np.abs(one - out[2]).max()) < COMPOSITION_TOL  # alone: another batch composition
     ref = np.stack([oracle.arctic_forward(host, s) for s in seqs[:2]])
     assert_embedding_parity(out[:2], ref)
     with pytest.raises(TzhError):

@@ -84,7 +84,10 @@ def test_documents_batch_equals_single(model, vocab):
     together, _ = embed_docs(model, tok, docs)
     for d, doc in enumerate(docs):
         alone, _ = embed_docs(model, tok, [doc])
-        assert np.array_equal(alone[0], together[d]), d
+        # another batch composition: the same to f32 rounding (the fused
+        # feed-forward kernel's split last round adds its parts' sums in
+        # another order than a whole panel's)
+        assert float(np.abs(alone[0] - together[d]).max()) < 1e-6, d
 
 
 def test_document_end_to_end_vs_oracle(model, host, vocab):
