@@ -40,7 +40,9 @@ TRAFFIC_PROFILE = "arctic_b256_stage_profile.md"
 
 
 KERNELS = {
-    "qkv": "linear_pipe_kernel bias, 384 -> 1152",  # f32 activations split hi/lo (fp32)
+    # f32 forward: the fused kernel's QKV mode (X in registers, weights streamed through LDS); fp16:
+    # linear_pipe_kernel
+    "qkv": "mlp_fused_kernel<2> (fp32; linear_pipe_kernel with --precision fp16): bias, 384 -> 1152",
     "attention": "attn_varlen_f32_kernel (attn_varlen_kernel with --precision fp16)",
     "attn_out_ln": "linear_pipe_kernel bias+residual+LayerNorm, 384 -> 384, 64-row tiles, two workgroups per CU",
     "ffn1_gelu": "linear_pipe_kernel bias+GELU, 384 -> 1536",

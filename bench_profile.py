@@ -26,9 +26,10 @@ Dispatches are mapped to forward stages by kernel and launch order: both
 LayerNorm GEMMs are linear_pipe_kernel<2> (with f32 activations the k = 384
 one has a tile configuration of its own); the one launched after attention
 is attn_out_ln and the one after ffn1_gelu is ffn2_ln; mlp_fused_kernel, the
-fused feed-forward block, is the stage ffn, and in its O-projection mode
-(template argument true) the stage attn_ffn; mlp_tail_kernel, which
-finishes the rows of its split last round, belongs to the same stage.  The
+fused feed-forward block, is the stage ffn, in its O-projection mode
+(template argument 1) the stage attn_ffn and in its QKV mode (2) the stage
+qkv; mlp_tail_kernel, which finishes the rows of a split last round,
+belongs to the stage before it.  The
 pieces of a split partial round (the residual-only GEMM) and their row
 LayerNorm belong to the LayerNorm GEMM launched just before them.
 
@@ -71,8 +72,11 @@ def stage_of(kernel: str, prev: str | None) -> str | None:
     if "cls_l2_kernel" in kernel:
         return "cls_l2"
     if "mlp_fused_kernel" in kernel:
-        # <true>: the O-projection mode (mangled ...kernelILb1E...)
-        return "attn_ffn" if ("ILb1E" in kernel or "<true>" in kernel) else "ffn"
+        # the template mode (mangled ...kernelILi<mode>E...): 1 the O-projection
+        # mode, 2 the QKV mode, 0 the feed-forward block alone
+        if "ILi1E" in kernel or "<1>" in kernel:
+            return "attn_ffn"
+        return "qkv" if ("ILi2E" in kernel or "<2>" in kernel) else "ffn"
     if "mlp_tail_kernel" in kernel:  # the rows of the fused kernel's split last round
         return prev if prev in ("attn_ffn", "ffn") else None
     epi = epi_of(kernel)

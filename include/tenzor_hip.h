@@ -448,8 +448,8 @@ int tzh_arctic_feed_forward(tzh_model *model, int32_t layer, const float *input,
 /* Fused feed-forward switch (no counterpart in the reference): enable = 0
  * makes the forward and tzh_arctic_feed_forward run every feed-forward block
  * as the GEMM pair (GELU epilogue, then residual + LayerNorm epilogue), and
- * the forward every O-projection as its own GEMM, even where one kernel
- * applies; nonzero (the default) restores them.  They agree to the f32
+ * the forward every O-projection and QKV projection on the int8 GEMM, even
+ * where the fused kernel applies; nonzero (the default) restores them.  They agree to the f32
  * rounding of their different summation orders. */
 int tzh_arctic_set_ffn_fusion(tzh_model *model, int32_t enable);
 

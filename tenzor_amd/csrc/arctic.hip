@@ -44,6 +44,10 @@ int tzh_mlp_fused_launch(hipStream_t st, int num_cus, const float *x, const void
                          const uint16_t *so, const float *bo, const float *gamma1, const float *beta1, void *scratch,
                          size_t scratch_bytes);
 size_t tzh_mlp_tail_bytes(int num_cus);
+size_t tzh_qkv_pack_bytes();
+int tzh_qkv_pack_launch(hipStream_t st, const void *w, void *out);
+int tzh_qkv_fused_launch(hipStream_t st, int num_cus, const float *x, const void *pack, const uint16_t *s,
+                         const float *b, float *y, int64_t t);
 size_t tzh_mlp_opack_bytes();
 int tzh_mlp_opack_launch(hipStream_t st, const void *wo, void *out);
 
@@ -227,6 +231,8 @@ struct DevLayer {
     // O-projection's too, when it is int8 as well (the kernel then starts
     // from the attention context)
     void *mlp = nullptr, *mlp_o = nullptr;
+    // qkvp: W_qkv in the fragment order of the same kernel's QKV mode
+    void *qkvp = nullptr;
 };
 
 }  // namespace
@@ -683,6 +689,10 @@ int upload_weights(tzh_model *m, const tzh_arctic_weights *w) {
                 TZH_TRY(tzh_mlp_opack_launch(m->ctx->stream, d.o.w, d.mlp_o));
             }
         }
+        if (d.qkv.fmt == TZH_WF_W8T) {
+            TZH_TRY(dev_alloc(m, &d.qkvp, tzh_qkv_pack_bytes()));
+            TZH_TRY(tzh_qkv_pack_launch(m->ctx->stream, d.qkv.w, d.qkvp));
+        }
     }
     TZH_HIP(hipStreamSynchronize(m->ctx->stream));
     set_range(m, w);
@@ -1007,6 +1017,10 @@ int run_forward(tzh_model *m, float *outputs, float *hidden_out, const uint32_t 
         const bool rs = m->row_scaled && act == TZH_F32;
         TZH_TRY(stage("qkv", [&]() {
             if (d.qkv.fmt == TZH_WF_F32) return linear_f32w(st, hf, d.qkv, (float *)m->qkv, T, H, 3 * H, -1, nullptr);
+            // int8 QKV of the f32 forward on the fused kernel's QKV mode
+            // (X in registers, the weights streamed through LDS)
+            if (m->fuse_ffn && d.qkvp && act == TZH_F32 && !rs)
+                return tzh_qkv_fused_launch(st, cus, hf, d.qkvp, d.qkv.s, d.qkv.b, (float *)m->qkv, T);
             return tzh_linear_codes_launch(st, cus, m->h, act, d.qkv.w, d.qkv.fmt, d.qkv.s, d.qkv.b, m->qkv, act, T,
                                            H, 3 * H, 3 * H, TZH_EPI_BIAS, nullptr, nullptr, nullptr, 0.0f, nullptr, 0, rs);
         }));

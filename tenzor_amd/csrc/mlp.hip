@@ -130,6 +130,25 @@ __global__ void mlp_opack_kernel(const uint8_t *__restrict__ wo, _Float16 *__res
     *(half8_t *)(out + (size_t)idx * 8) = v;
 }
 
+// The attention's input projection (QKV mode): W_qkv [1152, 384] in 18
+// chunks of 64 rows, two stages each (k 0..191, 192..383), in the first
+// GEMM's fragment layout: stage 2 c + q, fragment f (k step jp = f / 4,
+// row tile ft = f % 4), lane l = 16 g + rho, value i =
+// W_qkv[64 c + 16 ft + rho][32 (6 q + jp) + 8 g + i].
+constexpr int kFQ = 3 * kD;          // 1152 outputs
+constexpr int kQChunks = kFQ / kFC;  // 18
+__global__ void qkv_pack_kernel(const uint8_t *__restrict__ w, _Float16 *__restrict__ out) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= 2 * kQChunks * kStageFrags * 64) return;
+    const int lane = idx % 64, f = idx / 64 % kStageFrags, sq = idx / (64 * kStageFrags);
+    const int c = sq / 2, q = sq % 2, rho = lane % 16, g = lane / 16;
+    const int j = 6 * q + f / 4, ft = f % 4;
+    half8_t v;
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = w8t_code(w, kD, kFC * c + 16 * ft + rho, 32 * j + 8 * g + i);
+    *(half8_t *)(out + (size_t)idx * 8) = v;
+}
+
 // A value parked in an accumulation register (AGPR) until it is read back:
 // the raw X of a wave's tokens (its residual) stays there through the panel,
 // outside the VGPRs the products use.
@@ -149,8 +168,9 @@ __device__ __forceinline__ float unpark(float a) {
 }
 #endif
 
-// s_waitcnt vmcnt(n) lgkmcnt(0) for the counts the ring can need (n =
-// 6 a + 24 b, a <= 2, b <= 2); any other n waits for everything.
+// s_waitcnt vmcnt(n) lgkmcnt(0) for the counts the feed-forward modes' ring
+// can need (n = 6 a + 24 b, a <= 2, b <= 2); any other n waits for
+// everything.
 __device__ __forceinline__ void wait_vm_n(int n) {
     switch (n) {
     case 60: wait_vm_lgkm0<60>(); break;
@@ -162,6 +182,43 @@ __device__ __forceinline__ void wait_vm_n(int n) {
     case 12: wait_vm_lgkm0<12>(); break;
     case 6: wait_vm_lgkm0<6>(); break;
     default: wait_vm_lgkm0<0>(); break;
+    }
+}
+
+// The QKV mode's counts (two stages' loads, stores in fours, X loads in
+// 24s): s_waitcnt vmcnt(n') lgkmcnt(0) for n' = n rounded down to a
+// multiple of 4 (at most 60), which waits for at most three more ops than
+// needed; a four-level tree of uniform branches.
+__device__ __forceinline__ void wait_vm_n4(int n) {
+    const int k = (n > 63 ? 63 : n) >> 2;  // 0 .. 15
+    if (k & 8) {
+        if (k & 4) {
+            if (k & 2) {
+                if (k & 1) wait_vm_lgkm0<60>(); else wait_vm_lgkm0<56>();
+            } else {
+                if (k & 1) wait_vm_lgkm0<52>(); else wait_vm_lgkm0<48>();
+            }
+        } else {
+            if (k & 2) {
+                if (k & 1) wait_vm_lgkm0<44>(); else wait_vm_lgkm0<40>();
+            } else {
+                if (k & 1) wait_vm_lgkm0<36>(); else wait_vm_lgkm0<32>();
+            }
+        }
+    } else {
+        if (k & 4) {
+            if (k & 2) {
+                if (k & 1) wait_vm_lgkm0<28>(); else wait_vm_lgkm0<24>();
+            } else {
+                if (k & 1) wait_vm_lgkm0<20>(); else wait_vm_lgkm0<16>();
+            }
+        } else {
+            if (k & 2) {
+                if (k & 1) wait_vm_lgkm0<12>(); else wait_vm_lgkm0<8>();
+            } else {
+                if (k & 1) wait_vm_lgkm0<4>(); else wait_vm_lgkm0<0>();
+            }
+        }
     }
 }
 
@@ -199,18 +256,24 @@ struct TailSplit {
     float *sums, *xs;
 };
 
-// OP: the O-projection mode.  Each panel first forms X = LayerNorm(res +
-// (ctx W_o^T s_o + b_o)) (arctic.zig:716-746) in registers, from 12 more
-// weight stages (W_o's, streamed ahead of the feed-forward's) and the
-// first LayerNorm in the lanes, then runs the feed-forward block on it.
-template <bool OP>
+// MODE 0: the feed-forward block.  MODE 1 (OP), the O-projection mode:
+// each panel first forms X = LayerNorm(res + (ctx W_o^T s_o + b_o))
+// (arctic.zig:716-746) in registers, from 12 more weight stages (W_o's,
+// streamed ahead of the feed-forward's) and the first LayerNorm in the
+// lanes, then runs the feed-forward block on it.  MODE 2 (QKV): the first
+// GEMM alone over W_qkv (qkv_pack_kernel), Y [T, 1152] = X W_qkv^T s1 + b1
+// (arctic.zig:639-650, matmul_w8a32.zig:40-55), each 64-column chunk
+// stored from the accumulators.
+template <int MODE>
 __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     const float *__restrict__ X, const _Float16 *__restrict__ Wp, const uint16_t *__restrict__ s1,
     const float *__restrict__ b1, const uint16_t *__restrict__ s2, const float *__restrict__ b2,
     const float *__restrict__ gamma, const float *__restrict__ beta, float eps, float *__restrict__ Y, int T,
     OProj op, TailSplit ts) {
-    constexpr int kO = OP ? kOStages : 0;  // O-projection stages at the head of each panel
-    constexpr int kSP = kO + kSPP;         // stages per panel
+    constexpr bool OP = MODE == 1, QKV = MODE == 2;
+    constexpr int kO = OP ? kOStages : 0;           // O-projection stages at the head of each panel
+    constexpr int kSP = QKV ? 2 * kQChunks : kO + kSPP;  // stages per panel
+    constexpr int kNC = QKV ? kQChunks : kChunks;   // chunks per panel
     static_assert(kSP % 4 == 0, "a panel's stages fill whole turns of the ring");
     __shared__ __attribute__((aligned(16))) char st[4][kStage];  // the weight ring
     __shared__ __attribute__((aligned(16))) float p1[2][kF];  // s1, b1
@@ -225,17 +288,17 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     // this block's part of a split panel, if any: chunks c0 .. c0 + nc - 1
     const bool tail = ts.parts > 1 && (int)blockIdx.x < (panels - ts.full) * ts.parts;
     const int tpanel = ts.full + (int)blockIdx.x / ts.parts, tpart = (int)blockIdx.x % ts.parts;
-    const int nc = kChunks / ts.parts, c0 = tpart * nc;
-    const int SF = count * kSP;                          // stages of the whole panels
-    const int S = SF + (tail ? kO + kSPC * nc : 0);  // stages this block streams
+    const int nc = kNC / ts.parts, c0 = tpart * nc;
+    const int SF = count * kSP;  // stages of the whole panels
+    const int S = SF + (tail ? (QKV ? 2 * nc : kO + kSPC * nc) : 0);  // stages this block streams
     if (S == 0) return;
 
     // per-feature parameters -> LDS (visible after the first stage barrier)
-    for (int i = tid; i < kF; i += kWaves * 64) {
+    for (int i = tid; i < (QKV ? kFQ : kF); i += kWaves * 64) {
         p1[0][i] = f16_bits_to_f32(s1[i]);
         p1[1][i] = b1[i];
     }
-    for (int i = tid; i < kD; i += kWaves * 64) {
+    for (int i = tid; i < (QKV ? 0 : kD); i += kWaves * 64) {
         p2[0][i] = f16_bits_to_f32(s2[i]);
         p2[1][i] = b2[i];
         p2[2][i] = gamma[i];
@@ -274,7 +337,10 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     // stage u's loads; WHOLE: u is a feed-forward stage of a whole panel
     auto dma_of = [&](int u, auto wholec) __attribute__((always_inline)) {
         const char *src;
-        if constexpr (decltype(wholec)::value) {
+        if constexpr (QKV) {
+            // (QKV mode: the pack's stages in order, a part's from 2 c0)
+            src = wsrc + (size_t)(decltype(wholec)::value ? u % kSP : (u >= SF ? 2 * c0 + u - SF : u % kSP)) * kStage;
+        } else if constexpr (decltype(wholec)::value) {
             src = wsrc + (size_t)pack_stage(u % kSP - kO, 0, kChunks) * kStage;
         } else {
             const bool tl = u >= SF;
@@ -348,7 +414,10 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
             return dma_of(u + 3, std::true_type{});  // (the middle steps load their own panel's stages)
         } else {
             const int ahead = K == 1 || S - 1 - u >= 2 ? 2 : S - 1 - u;
-            wait_vm_n(kLW * ahead + ext0 + ext1 + ext2);
+            if constexpr (QKV)
+                wait_vm_n4(kLW * ahead + ext0 + ext1 + ext2);
+            else
+                wait_vm_n(kLW * ahead + ext0 + ext1 + ext2);
             lds_barrier_only();
             ext2 = ext1;
             ext1 = ext0;
@@ -361,6 +430,19 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
                 return StageDma<false>{d.src, d.dst};
             }
         }
+    };
+
+    // QKV mode, a middle step: its wait counts two stages' loads and the
+    // chunk stores issued after stage u's loads (EXTRA: 8 at a chunk's first
+    // stage, 4 at its second), and the record of extra ops moves on as in
+    // the counted steps, for the panel's last steps
+    auto step_mid_q = [&](int u, auto extrac) __attribute__((always_inline)) {
+        wait_vm_lgkm0<2 * kLW + decltype(extrac)::value>();
+        lds_barrier_only();
+        ext2 = ext1;
+        ext1 = ext0;
+        ext0 = 0;
+        return dma_of(u + 3, std::true_type{});
     };
 
     // The lane's byte offset in a fragment, recomputed in each stage (an
@@ -568,6 +650,51 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         return full;
     };
 
+    // QKV mode: chunk c's 64 columns of the panel's rows, sum * s + b
+    // (matmul_w8a32.zig:55).  Rows past T are clamped to T - 1: those lanes
+    // hold row T - 1's own values (the same X row, the same products), so
+    // every store goes out and the stage waits count four per chunk.
+    auto qkv_store = [&](int c, int panel) __attribute__((always_inline)) {
+        const int ln = lane_now(), g = ln >> 4;
+        int t = panel * kBM + wu * kTokW + (ln & 15);
+        t = t < T ? t : T - 1;
+        float *const row = Y + (size_t)t * kFQ + kFC * c + 4 * g;
+#pragma unroll
+        for (int ft = 0; ft < 4; ft++) {
+            const int f = kFC * c + 16 * ft + 4 * g;
+            const f32x4_t sc = *(const f32x4_t *)&p1[0][f];
+            const f32x4_t bs = *(const f32x4_t *)&p1[1][f];
+            f32x4_t v;
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] = hacc[ft][e] * sc[e] + bs[e];
+            *(f32x4_t *)(row + 16 * ft) = v;
+            vmem_store_issued();
+        }
+        ext0 += 4;  // after this step's stage loads
+    };
+    // QKV mode, chunk c of a panel (stages u, u + 1): the first GEMM's two
+    // halves, then the chunk's stores.  KIND as for the periods; with nextp
+    // >= 0 the next panel's X loads go out in the second step (counted with
+    // the first).
+    auto qkv_chunk = [&](auto kindc, int u, int c, int panel, int nextp) __attribute__((always_inline)) {
+        if constexpr (decltype(kindc)::value == 0) {
+            auto d = step_mid_q(u, std::integral_constant<int, 8>{});
+            gemm1(std::integral_constant<int, 0>{}, ring + (u & 3) * kStage, d);
+            d = step_mid_q(u + 1, std::integral_constant<int, 4>{});
+            gemm1(std::integral_constant<int, 1>{}, ring + ((u + 1) & 3) * kStage, d);
+        } else {
+            auto d = step_begin(kindc, u);
+            gemm1(std::integral_constant<int, 0>{}, ring + (u & 3) * kStage, d);
+            d = step_begin(kindc, u + 1);
+            if (nextp >= 0) {
+                load_x(nextp);
+                ext1 += kXL;
+            }
+            gemm1(std::integral_constant<int, 1>{}, ring + ((u + 1) & 3) * kStage, d);
+        }
+        qkv_store(c, panel);
+    };
+
     // Period p of panel i (p = 0 .. 24; block stages from u0): the first
     // GEMM of chunk p (p <= 23; two stages), then the second GEMM of chunk
     // p - 1 (p >= 1; two stages) with chunk p's GELU between its products.
@@ -642,7 +769,28 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
 #pragma unroll
             for (int k = 0; k < kLW; k++) dma_one(d, k);
         }
-    split_x(std::integral_constant<bool, !OP>{});
+    split_x(std::integral_constant<bool, MODE == 0>{});
+    if constexpr (QKV) {
+        // whole panels: the first three chunks count their waits at run time
+        // (the last panel's stores, the next panel's X loads in chunk 1), the
+        // last two as the block's stream may end
+        for (int i = 0; i < count; i++) {
+            const int panel = blockIdx.x + i * gridDim.x;
+            const int nextp = i + 1 < count ? panel + (int)gridDim.x : (tail ? tpanel : -1);
+            const int ub = i * kSP;
+            qkv_chunk(Gen{}, ub, 0, panel, -1);
+            qkv_chunk(Gen{}, ub + 2, 1, panel, nextp);
+            qkv_chunk(Gen{}, ub + 4, 2, panel, -1);
+            for (int c = 3; c < kQChunks - 2; c++) qkv_chunk(Mid{}, ub + 2 * c, c, panel, -1);
+            qkv_chunk(End{}, ub + 2 * (kQChunks - 2), kQChunks - 2, panel, -1);
+            qkv_chunk(End{}, ub + 2 * (kQChunks - 1), kQChunks - 1, panel, -1);
+            if (nextp >= 0) split_x(std::false_type{});
+        }
+        // this block's part of a split panel: its chunks' columns
+        if (tail)
+            for (int cr = 0; cr < nc; cr++) qkv_chunk(End{}, SF + 2 * cr, c0 + cr, tpanel, -1);
+        return;
+    }
     for (int i = 0; i < count; i++) {
         const int panel = blockIdx.x + i * gridDim.x;
         const int nextp = i + 1 < count ? panel + (int)gridDim.x : (tail ? tpanel : -1);
@@ -664,7 +812,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         period(integral_constant<int, 2>{}, End{}, P0{}, ub + kSPP - 2, kChunks, nextp);
         const bool full = epilogue(panel);
         ext0 = full ? kXL : 0;  // the stores, after the loads of the panel's last step
-        if (nextp >= 0) split_x(std::integral_constant<bool, !OP>{});
+        if (nextp >= 0) split_x(std::integral_constant<bool, MODE == 0>{});
     }
     if (tail) {
         // this block's part of a split panel: its chunks' periods (every
@@ -858,10 +1006,10 @@ int tzh_mlp_fused_launch(hipStream_t st, int num_cus, const float *x, const void
     }
     const OProj o{ctx, res, (const _Float16 *)opack, so, bo, gamma1, beta1};
     if (op)
-        hipLaunchKernelGGL(mlp_fused_kernel<true>, dim3((unsigned)grid), dim3(kWaves * 64), 0, st, x,
+        hipLaunchKernelGGL(mlp_fused_kernel<1>, dim3((unsigned)grid), dim3(kWaves * 64), 0, st, x,
                            (const _Float16 *)pack, s1, b1, s2, b2, gamma, beta, eps, y, (int)t, o, ts);
     else
-        hipLaunchKernelGGL(mlp_fused_kernel<false>, dim3((unsigned)grid), dim3(kWaves * 64), 0, st, x,
+        hipLaunchKernelGGL(mlp_fused_kernel<0>, dim3((unsigned)grid), dim3(kWaves * 64), 0, st, x,
                            (const _Float16 *)pack, s1, b1, s2, b2, gamma, beta, eps, y, (int)t, o, ts);
     TZH_LAUNCHED("mlp_fused_kernel");
     if (ts.parts > 1) {
@@ -871,5 +1019,48 @@ int tzh_mlp_fused_launch(hipStream_t st, int num_cus, const float *x, const void
                            (int)t);
         TZH_LAUNCHED("mlp_tail_kernel");
     }
+    return TZH_OK;
+}
+
+// W_qkv's codes (W8T, [1152, 384]) -> the QKV mode's stages
+// (tzh_qkv_pack_bytes bytes, 16-byte aligned).
+size_t tzh_qkv_pack_bytes() { return (size_t)2 * kQChunks * kStage; }
+
+int tzh_qkv_pack_launch(hipStream_t st, const void *w, void *out) {
+    if (!w || !out || ((uintptr_t)out & 15)) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad QKV pack operands");
+    const int threads = 2 * kQChunks * kStageFrags * 64;
+    hipLaunchKernelGGL(qkv_pack_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, (const uint8_t *)w,
+                       (_Float16 *)out);
+    TZH_LAUNCHED("qkv_pack_kernel");
+    return TZH_OK;
+}
+
+// Y [t, 1152] = X W_qkv^T s + b for X [t, 384] f32 (16-byte aligned, not
+// overlapping Y) with the QKV pack, on the fused kernel's QKV mode: the
+// last, partial round of panels split by chunks over the idle CUs (the
+// parts write disjoint columns; nothing to add up).
+int tzh_qkv_fused_launch(hipStream_t st, int num_cus, const float *x, const void *pack, const uint16_t *s,
+                         const float *b, float *y, int64_t t) {
+    if (t < 0 || t > ((int64_t)1 << 30)) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad token count %lld", (long long)t);
+    if (t == 0) return TZH_OK;
+    if (!x || !pack || !s || !b || !y) return tzh_fail(TZH_ERR_INVALID_ARGS, "null QKV operand");
+    if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)pack) & 15)
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "QKV operands must be 16-byte aligned");
+    if ((const char *)x < (const char *)(y + (size_t)t * kFQ) && (const char *)y < (const char *)(x + (size_t)t * kD))
+        return tzh_fail(TZH_ERR_INVALID_ARGS, "QKV input and output overlap");
+    if (num_cus < 1) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad CU count %d", num_cus);
+    const int panels = (int)((t + kBM - 1) / kBM), rest = panels % num_cus;
+    TailSplit ts{panels, 1, nullptr, nullptr};
+    if (rest > 0)
+        for (int parts : {18, 9, 6, 3, 2})
+            if (rest * parts <= num_cus) {
+                ts.full = panels - rest;
+                ts.parts = parts;
+                break;
+            }
+    const int grid = ts.parts > 1 ? (ts.full > 0 ? num_cus : rest * ts.parts) : std::min(panels, num_cus);
+    hipLaunchKernelGGL(mlp_fused_kernel<2>, dim3((unsigned)grid), dim3(kWaves * 64), 0, st, x, (const _Float16 *)pack,
+                       s, b, nullptr, nullptr, nullptr, nullptr, 0.0f, y, (int)t, OProj{}, ts);
+    TZH_LAUNCHED("mlp_fused_kernel");
     return TZH_OK;
 }
