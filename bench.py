@@ -50,7 +50,7 @@ KERNELS = {
                "(linear_pipe_kernel residual pieces, ln_rows_kernel)",
     "ffn": "mlp_fused_kernel: the feed-forward block in one kernel, 384 -> 1536 + GELU -> 384 + residual + "
            "LayerNorm, the intermediate kept on chip",
-    "attn_ffn": "mlp_fused_kernel<true>: O-projection 384 -> 384 + residual + LayerNorm, then the feed-forward "
+    "attn_ffn": "mlp_fused_kernel<1>: O-projection 384 -> 384 + residual + LayerNorm, then the feed-forward "
                 "block (384 -> 1536 + GELU -> 384 + residual + LayerNorm) in one kernel, h1 and the intermediate "
                 "kept on chip",
     "embed_ln": "embed_ln_kernel", "pack_ids": "pack_ids_kernel", "cls_l2": "cls_l2_kernel",

@@ -406,6 +406,10 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     // u + 3 exists; GEN: the count computed at run time, stage u + 3 exists
     // (a panel's first steps); END: both at run time (its last steps).
     int ext0 = 0, ext1 = 0, ext2 = 0;
+    // QKV mode: of those, the ops each step issued after its last stage load
+    // (its stores go out between its loads; those before the last load of
+    // stage u do not count for u's wait)
+    int pst0 = 0, pst1 = 0, pst2 = 0;
     auto step_begin = [&](auto kindc, int u) __attribute__((always_inline)) {
         constexpr int K = decltype(kindc)::value;
         if constexpr (K == 0) {
@@ -415,13 +419,16 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         } else {
             const int ahead = K == 1 || S - 1 - u >= 2 ? 2 : S - 1 - u;
             if constexpr (QKV)
-                wait_vm_n4(kLW * ahead + ext0 + ext1 + ext2);
+                wait_vm_n4(kLW * ahead + ext0 + ext1 + pst2);
             else
                 wait_vm_n(kLW * ahead + ext0 + ext1 + ext2);
             lds_barrier_only();
             ext2 = ext1;
             ext1 = ext0;
             ext0 = 0;
+            pst2 = pst1;
+            pst1 = pst0;
+            pst0 = 0;
             if constexpr (K == 1) {
                 return dma_of(u + 3, std::false_type{});
             } else {
@@ -432,16 +439,21 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         }
     };
 
-    // QKV mode, a middle step: its wait counts two stages' loads and the
-    // chunk stores issued after stage u's loads (EXTRA: 8 at a chunk's first
-    // stage, 4 at its second), and the record of extra ops moves on as in
-    // the counted steps, for the panel's last steps
-    auto step_mid_q = [&](int u, auto extrac) __attribute__((always_inline)) {
-        wait_vm_lgkm0<2 * kLW + decltype(extrac)::value>();
+    // QKV mode, a middle step: every step stores two of the last chunk's
+    // four vectors, one after its third load and one after its last, so its
+    // wait counts two stages' loads, the store after stage u's last load
+    // and the two stores of each of the two steps since: 17.  The records
+    // of extra ops move on as in the counted steps, for the panel's last
+    // steps.
+    auto step_mid_q = [&](int u) __attribute__((always_inline)) {
+        wait_vm_lgkm0<2 * kLW + 5>();
         lds_barrier_only();
         ext2 = ext1;
         ext1 = ext0;
         ext0 = 0;
+        pst2 = pst1;
+        pst1 = pst0;
+        pst0 = 0;
         return dma_of(u + 3, std::true_type{});
     };
 
@@ -452,8 +464,9 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     // first GEMM, half q of the chunk's k: H^T tiles += W1 fragments x X.
     // The fragments of k step jp + 1 are read before the products of step
     // jp are issued (two register sets), so the LDS latency hides behind
-    // eight MFMAs; one of the six loads of stage u + 3 goes out per k step.
-    auto gemm1 = [&](auto qc, const char *sb, const auto &d) __attribute__((always_inline)) {
+    // eight MFMAs; one of the six loads of stage u + 3 goes out per k step,
+    // then hook(jp) (the QKV mode's stores).
+    auto gemm1 = [&](auto qc, const char *sb, const auto &d, auto hook) __attribute__((always_inline)) {
         constexpr int q = decltype(qc)::value;
         constexpr int j0 = 6 * q;
         sb += lane_off();
@@ -470,6 +483,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
                 for (int ft = 0; ft < 4; ft++)
                     a[(jp + 1) & 1][ft] = *(const half8_t *)(sb + ((jp + 1) * 4 + ft) * kFrag);
             dma_one(d, jp);
+            hook(jp);
             sched_fence();
 #pragma unroll
             for (int ft = 0; ft < 4; ft++)
@@ -650,49 +664,72 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         return full;
     };
 
-    // QKV mode: chunk c's 64 columns of the panel's rows, sum * s + b
-    // (matmul_w8a32.zig:55).  Rows past T are clamped to T - 1: those lanes
-    // hold row T - 1's own values (the same X row, the same products), so
-    // every store goes out and the stage waits count four per chunk.
-    auto qkv_store = [&](int c, int panel) __attribute__((always_inline)) {
-        const int ln = lane_now(), g = ln >> 4;
-        int t = panel * kBM + wu * kTokW + (ln & 15);
-        t = t < T ? t : T - 1;
-        float *const row = Y + (size_t)t * kFQ + kFC * c + 4 * g;
+    // QKV mode: a chunk's outputs, sum * s + b (matmul_w8a32.zig:55), wait
+    // in registers (vq: lane (tl, g), vector k = columns 16 k + 4 g .. + 3
+    // of token tl of chunk pend_c of panel pend_panel) and go out one at a
+    // time during the next chunk's steps, so that the stores trickle
+    // between the matrix products instead of stalling the wave in a burst.
+    // Rows past T are clamped to T - 1: those lanes hold row T - 1's own
+    // values (the same X row, the same products), so every store goes out.
+    f32x4_t vq[4];
+    bool pend = false;
+    int pend_panel = 0, pend_c = 0;
+    auto qkv_finish = [&](int c, int panel) __attribute__((always_inline)) {
+        const int g = lane_now() >> 4;
 #pragma unroll
-        for (int ft = 0; ft < 4; ft++) {
-            const int f = kFC * c + 16 * ft + 4 * g;
+        for (int k = 0; k < 4; k++) {
+            const int f = kFC * c + 16 * k + 4 * g;
             const f32x4_t sc = *(const f32x4_t *)&p1[0][f];
             const f32x4_t bs = *(const f32x4_t *)&p1[1][f];
-            f32x4_t v;
 #pragma unroll
-            for (int e = 0; e < 4; e++) v[e] = hacc[ft][e] * sc[e] + bs[e];
-            *(f32x4_t *)(row + 16 * ft) = v;
-            vmem_store_issued();
+            for (int e = 0; e < 4; e++) vq[k][e] = hacc[k][e] * sc[e] + bs[e];
         }
-        ext0 += 4;  // after this step's stage loads
+        pend = true;
+        pend_panel = panel;
+        pend_c = c;
+    };
+    // store vector k of the pending chunk; POST: after the step's last load
+    auto qkv_put = [&](int k, bool post) __attribute__((always_inline)) {
+        if (!pend) return;
+        const int ln = lane_now();
+        int t = pend_panel * kBM + wu * kTokW + (ln & 15);
+        t = t < T ? t : T - 1;
+        *(f32x4_t *)(Y + (size_t)t * kFQ + kFC * pend_c + 16 * k + 4 * (ln >> 4)) = vq[k];
+        vmem_store_issued();
+        ext0 += 1;
+        if (post) pst0 += 1;
     };
     // QKV mode, chunk c of a panel (stages u, u + 1): the first GEMM's two
-    // halves, then the chunk's stores.  KIND as for the periods; with nextp
-    // >= 0 the next panel's X loads go out in the second step (counted with
-    // the first).
+    // halves, storing the last chunk's vectors 0, 1 during the first and 2,
+    // 3 during the second (after loads 3 and 6 of each), then this chunk's
+    // outputs.  KIND as for the periods; with nextp >= 0 the next panel's X
+    // loads go out in the second step (counted with the first).
     auto qkv_chunk = [&](auto kindc, int u, int c, int panel, int nextp) __attribute__((always_inline)) {
+        auto hook_a = [&](int jp) __attribute__((always_inline)) {
+            if (jp == 2) qkv_put(0, false);
+            if (jp == 5) qkv_put(1, true);
+        };
+        auto hook_b = [&](int jp) __attribute__((always_inline)) {
+            if (jp == 2) qkv_put(2, false);
+            if (jp == 5) qkv_put(3, true);
+        };
         if constexpr (decltype(kindc)::value == 0) {
-            auto d = step_mid_q(u, std::integral_constant<int, 8>{});
-            gemm1(std::integral_constant<int, 0>{}, ring + (u & 3) * kStage, d);
-            d = step_mid_q(u + 1, std::integral_constant<int, 4>{});
-            gemm1(std::integral_constant<int, 1>{}, ring + ((u + 1) & 3) * kStage, d);
+            auto d = step_mid_q(u);
+            gemm1(std::integral_constant<int, 0>{}, ring + (u & 3) * kStage, d, hook_a);
+            d = step_mid_q(u + 1);
+            gemm1(std::integral_constant<int, 1>{}, ring + ((u + 1) & 3) * kStage, d, hook_b);
         } else {
             auto d = step_begin(kindc, u);
-            gemm1(std::integral_constant<int, 0>{}, ring + (u & 3) * kStage, d);
+            gemm1(std::integral_constant<int, 0>{}, ring + (u & 3) * kStage, d, hook_a);
             d = step_begin(kindc, u + 1);
             if (nextp >= 0) {
                 load_x(nextp);
                 ext1 += kXL;
+                pst1 += kXL;
             }
-            gemm1(std::integral_constant<int, 1>{}, ring + ((u + 1) & 3) * kStage, d);
+            gemm1(std::integral_constant<int, 1>{}, ring + ((u + 1) & 3) * kStage, d, hook_b);
         }
-        qkv_store(c, panel);
+        qkv_finish(c, panel);
     };
 
     // Period p of panel i (p = 0 .. 24; block stages from u0): the first
@@ -710,9 +747,9 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         constexpr int S1 = PK == 0 ? 0 : 2;  // ring slots of this period's first two stages
         if constexpr (PK <= 1) {
             auto d = step_begin(kindc, u0);
-            gemm1(std::integral_constant<int, 0>{}, st[S1], d);
+            gemm1(std::integral_constant<int, 0>{}, st[S1], d, [](int) {});
             d = step_begin(kindc, u0 + 1);
-            gemm1(std::integral_constant<int, 1>{}, st[S1 + 1], d);
+            gemm1(std::integral_constant<int, 1>{}, st[S1 + 1], d, [](int) {});
         }
         if constexpr (PK == 0) {
 #pragma unroll
@@ -789,6 +826,9 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         // this block's part of a split panel: its chunks' columns
         if (tail)
             for (int cr = 0; cr < nc; cr++) qkv_chunk(End{}, SF + 2 * cr, c0 + cr, tpanel, -1);
+        // the last chunk's vectors (no wait follows them)
+#pragma unroll
+        for (int k = 0; k < 4; k++) qkv_put(k, true);
         return;
     }
     for (int i = 0; i < count; i++) {
