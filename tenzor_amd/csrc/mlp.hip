@@ -47,6 +47,16 @@
 //     8 g .. 32 j + 8 g + 7 of token t: the same columns as the lane's X
 //     registers, so the residual add is lane-local and each LayerNorm row's
 //     statistics reduce over the four lanes of its token with two row swaps.
+//   - Two more modes share the ring and the first GEMM: the O-projection
+//     mode runs the attention output's projection, residual and LayerNorm
+//     (arctic.zig:716-746) at the head of each panel, so the layer's h1 is
+//     formed in registers; the QKV mode runs the attention's input
+//     projection (the first GEMM alone over W_qkv, each 64-column chunk
+//     stored from its accumulators).
+//   - Blocks deal the panels round robin; the last, partial round is split
+//     by chunks over the CUs it would leave idle (TailSplit): a part sums
+//     its chunks only, and mlp_tail_kernel adds the parts (in the QKV mode
+//     the parts write disjoint columns, with nothing to add).
 #include <algorithm>
 
 #include "pipe.h"
