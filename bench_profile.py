@@ -273,7 +273,9 @@ def summarize(trace: str | None, fetch: str | None, write: str | None, bench_log
                                   for prec, key in (("fp32", "stages"), ("fp16", "stages_fp16"))}
     if trace:
         out += ["The fp32 forward runs each layer's O-projection, its LayerNorm and the feed-forward",
-                "block as one kernel (mlp_fused_kernel<true>, stage attn_ffn); the fp16 forward runs",
+                "block as one kernel (mlp_fused_kernel<1>, stage attn_ffn, with mlp_tail_kernel for a",
+                "split last round) and its QKV projection on the same kernel's QKV mode",
+                "(mlp_fused_kernel<2>, stage qkv); the fp16 forward runs linear_pipe_kernel for QKV,",
                 "the O-projection and the GEMM pair (attn_out_ln, ffn1_gelu, ffn2_ln), whose two",
                 "LayerNorm GEMMs are both linear_pipe_kernel<2>; the rows above separate them by",
                 "launch order.  The stage rows average the plain forwards of the trace run.  The",
