@@ -275,12 +275,19 @@ struct TailSplit {
 // (arctic.zig:639-650, matmul_w8a32.zig:40-55), each 64-column chunk
 // stored from the accumulators.
 template <int MODE>
-__global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
+__global__ void __launch_bounds__((MODE == 2 ? 2 : 1) * kWaves * 64) mlp_fused_kernel(
     const float *__restrict__ X, const _Float16 *__restrict__ Wp, const uint16_t *__restrict__ s1,
     const float *__restrict__ b1, const uint16_t *__restrict__ s2, const float *__restrict__ b2,
     const float *__restrict__ gamma, const float *__restrict__ beta, float eps, float *__restrict__ Y, int T,
     OProj op, TailSplit ts) {
     constexpr bool OP = MODE == 1, QKV = MODE == 2;
+    // waves of a block: the QKV mode, at about 290 registers a wave, runs
+    // two waves per SIMD on 128-token panels (the same weight stream feeds
+    // twice the tokens, and each SIMD has a second wave to issue MFMAs
+    // while one waits); its loads per wave per stage halve
+    constexpr int kWv = QKV ? 2 * kWaves : kWaves;
+    constexpr int kLWv = kStageFrags / kWv;
+    constexpr int kBMv = kWv * kTokW;
     constexpr int kO = OP ? kOStages : 0;           // O-projection stages at the head of each panel
     constexpr int kSP = QKV ? 2 * kQChunks : kO + kSPP;  // stages per panel
     constexpr int kNC = QKV ? kQChunks : kChunks;   // chunks per panel
@@ -293,7 +300,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     // (lane quantities are formed where they are used, from lane_now())
     const int tid = threadIdx.x;
     const int wu = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int panels = (T + kBM - 1) / kBM;
+    const int panels = (T + kBMv - 1) / kBMv;
     const int count = (int)blockIdx.x < ts.full ? (ts.full - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
     // this block's part of a split panel, if any: chunks c0 .. c0 + nc - 1
     const bool tail = ts.parts > 1 && (int)blockIdx.x < (panels - ts.full) * ts.parts;
@@ -304,11 +311,11 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     if (S == 0) return;
 
     // per-feature parameters -> LDS (visible after the first stage barrier)
-    for (int i = tid; i < (QKV ? kFQ : kF); i += kWaves * 64) {
+    for (int i = tid; i < (QKV ? kFQ : kF); i += kWv * 64) {
         p1[0][i] = f16_bits_to_f32(s1[i]);
         p1[1][i] = b1[i];
     }
-    for (int i = tid; i < (QKV ? 0 : kD); i += kWaves * 64) {
+    for (int i = tid; i < (QKV ? 0 : kD); i += kWv * 64) {
         p2[0][i] = f16_bits_to_f32(s2[i]);
         p2[1][i] = b2[i];
         p2[2][i] = gamma[i];
@@ -342,8 +349,8 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         return s >= last ? 4 * (cb + n - 1) + 2 + (s - last) : v;
     };
     char *const ring = &st[0][0];
-    const char *const wsrc = (const char *)Wp + (size_t)wu * kLW * kFrag;
-    const char *const osrc = OP ? (const char *)op.wp + (size_t)wu * kLW * kFrag : nullptr;
+    const char *const wsrc = (const char *)Wp + (size_t)wu * kLWv * kFrag;
+    const char *const osrc = OP ? (const char *)op.wp + (size_t)wu * kLWv * kFrag : nullptr;
     // stage u's loads; WHOLE: u is a feed-forward stage of a whole panel
     auto dma_of = [&](int u, auto wholec) __attribute__((always_inline)) {
         const char *src;
@@ -358,10 +365,10 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
             src = OP && sp < kO ? osrc + (size_t)sp * kStage
                                 : wsrc + (size_t)pack_stage(sp - kO, tl ? c0 : 0, tl ? nc : kChunks) * kStage;
         }
-        return StageDma<true>{src, ring + (u & 3) * kStage + wu * kLW * kFrag};
+        return StageDma<true>{src, ring + (u & 3) * kStage + wu * kLWv * kFrag};
     };
     auto dma_one = [&](const auto &d, int i) __attribute__((always_inline)) {
-        if (std::decay_t<decltype(d)>::kAlways || d.src)
+        if (i < kLWv && (std::decay_t<decltype(d)>::kAlways || d.src))
             dma16(d.src + i * kFrag, (uint32_t)lane_now() * 16, d.dst + i * kFrag);
     };
 
@@ -372,7 +379,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     f32x4_t xn[kXL];
     auto load_rows = [&](const float *src, int panel) __attribute__((always_inline)) {
         const int ln = lane_now();
-        int t = panel * kBM + wu * kTokW + (ln & 15);
+        int t = panel * kBMv + wu * kTokW + (ln & 15);
         t = t < T ? t : T - 1;
         const float *row = src + (size_t)t * kD + 8 * (ln >> 4);
 #pragma unroll
@@ -423,15 +430,15 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     auto step_begin = [&](auto kindc, int u) __attribute__((always_inline)) {
         constexpr int K = decltype(kindc)::value;
         if constexpr (K == 0) {
-            wait_vm_lgkm0<2 * kLW>();
+            wait_vm_lgkm0<2 * kLWv>();
             lds_barrier_only();  // every wave's stage u landed; stage u - 1 fully read
             return dma_of(u + 3, std::true_type{});  // (the middle steps load their own panel's stages)
         } else {
             const int ahead = K == 1 || S - 1 - u >= 2 ? 2 : S - 1 - u;
             if constexpr (QKV)
-                wait_vm_n4(kLW * ahead + ext0 + ext1 + pst2);
+                wait_vm_n4(kLWv * ahead + ext0 + ext1 + pst2);
             else
-                wait_vm_n(kLW * ahead + ext0 + ext1 + ext2);
+                wait_vm_n(kLWv * ahead + ext0 + ext1 + ext2);
             lds_barrier_only();
             ext2 = ext1;
             ext1 = ext0;
@@ -450,13 +457,14 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     };
 
     // QKV mode, a middle step: every step stores two of the last chunk's
-    // four vectors, one after its third load and one after its last, so its
-    // wait counts two stages' loads, the store after stage u's last load
-    // and the two stores of each of the two steps since: 17.  The records
+    // four vectors, after its third and sixth groups' loads, so its wait
+    // counts two stages' loads, the stores after stage u's last load (one
+    // with six loads a step, both with three) and the two stores of each
+    // of the two steps since: 17 with four waves, 12 with eight.  The records
     // of extra ops move on as in the counted steps, for the panel's last
     // steps.
     auto step_mid_q = [&](int u) __attribute__((always_inline)) {
-        wait_vm_lgkm0<2 * kLW + 5>();
+        wait_vm_lgkm0<2 * kLWv + (kLWv == 3 ? 2 : 1) + 4>();
         lds_barrier_only();
         ext2 = ext1;
         ext1 = ext0;
@@ -628,7 +636,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     // replaces the sums in place.
     auto epilogue = [&](int panel) __attribute__((always_inline)) {
         const int ln = lane_now(), g = ln >> 4;
-        const int t = panel * kBM + wu * kTokW + (ln & 15);
+        const int t = panel * kBMv + wu * kTokW + (ln & 15);
         float sum = 0.0f;
 #pragma unroll
         for (int j = 0; j < kXJ; j++)
@@ -655,7 +663,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
                 sq += d * d;
             }
         const float inv_std = 1.0f / sqrtf(sum_over_rows(sq) / (float)kD + eps);
-        const bool full = panel * kBM + wu * kTokW + kTokW <= T;  // uniform
+        const bool full = panel * kBMv + wu * kTokW + kTokW <= T;  // uniform
 #pragma unroll
         for (int j = 0; j < kXJ; j++)
 #pragma unroll
@@ -702,7 +710,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     auto qkv_put = [&](int k, bool post) __attribute__((always_inline)) {
         if (!pend) return;
         const int ln = lane_now();
-        int t = pend_panel * kBM + wu * kTokW + (ln & 15);
+        int t = pend_panel * kBMv + wu * kTokW + (ln & 15);
         t = t < T ? t : T - 1;
         *(f32x4_t *)(Y + (size_t)t * kFQ + kFC * pend_c + 16 * k + 4 * (ln >> 4)) = vq[k];
         vmem_store_issued();
@@ -716,11 +724,11 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
     // loads go out in the second step (counted with the first).
     auto qkv_chunk = [&](auto kindc, int u, int c, int panel, int nextp) __attribute__((always_inline)) {
         auto hook_a = [&](int jp) __attribute__((always_inline)) {
-            if (jp == 2) qkv_put(0, false);
+            if (jp == 2) qkv_put(0, 2 >= kLWv - 1);
             if (jp == 5) qkv_put(1, true);
         };
         auto hook_b = [&](int jp) __attribute__((always_inline)) {
-            if (jp == 2) qkv_put(2, false);
+            if (jp == 2) qkv_put(2, 2 >= kLWv - 1);
             if (jp == 5) qkv_put(3, true);
         };
         if constexpr (decltype(kindc)::value == 0) {
@@ -814,24 +822,30 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
         if (u < S) {
             const auto d = dma_of(u, std::false_type{});
 #pragma unroll
-            for (int k = 0; k < kLW; k++) dma_one(d, k);
+            for (int k = 0; k < kLWv; k++) dma_one(d, k);
         }
     split_x(std::integral_constant<bool, MODE == 0>{});
     if constexpr (QKV) {
         // whole panels: the first three chunks count their waits at run time
-        // (the last panel's stores, the next panel's X loads in chunk 1), the
-        // last two as the block's stream may end
+        // (the last panel's stores), the last two as the block's stream may
+        // end.  The next panel's X is loaded after the panel (two waves a
+        // SIMD leave no registers to hold it through the panel); the wait
+        // for it before its split retires every op before it, so it needs no
+        // count of its own.
         for (int i = 0; i < count; i++) {
             const int panel = blockIdx.x + i * gridDim.x;
             const int nextp = i + 1 < count ? panel + (int)gridDim.x : (tail ? tpanel : -1);
             const int ub = i * kSP;
             qkv_chunk(Gen{}, ub, 0, panel, -1);
-            qkv_chunk(Gen{}, ub + 2, 1, panel, nextp);
+            qkv_chunk(Gen{}, ub + 2, 1, panel, -1);
             qkv_chunk(Gen{}, ub + 4, 2, panel, -1);
             for (int c = 3; c < kQChunks - 2; c++) qkv_chunk(Mid{}, ub + 2 * c, c, panel, -1);
             qkv_chunk(End{}, ub + 2 * (kQChunks - 2), kQChunks - 2, panel, -1);
             qkv_chunk(End{}, ub + 2 * (kQChunks - 1), kQChunks - 1, panel, -1);
-            if (nextp >= 0) split_x(std::false_type{});
+            if (nextp >= 0) {
+                load_x(nextp);
+                split_x(std::false_type{});
+            }
         }
         // this block's part of a split panel: its chunks' columns
         if (tail)
@@ -878,7 +892,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
                 // X, the residual, now (not parked through the part); issued
                 // after the last O step's stage loads, counted with that step
                 const int ln = lane_now(), g = ln >> 4;
-                float *const px = ts.xs + ((size_t)(tpanel - ts.full) * kBM + wu * kTokW + (ln & 15)) * kD;
+                float *const px = ts.xs + ((size_t)(tpanel - ts.full) * kBMv + wu * kTokW + (ln & 15)) * kD;
 #pragma unroll
                 for (int j = 0; j < kXJ; j++)
 #pragma unroll
@@ -903,7 +917,7 @@ __global__ void __launch_bounds__(kWaves * 64) mlp_fused_kernel(
             period(integral_constant<int, 2>{}, End{}, P0{}, ub + kSPC * nc - 2, c0 + nc, -1);
         const int ln = lane_now(), g = ln >> 4;
         float *const ps =
-            ts.sums + (((size_t)(tpanel - ts.full) * ts.parts + tpart) * kBM + wu * kTokW + (ln & 15)) * kD;
+            ts.sums + (((size_t)(tpanel - ts.full) * ts.parts + tpart) * kBMv + wu * kTokW + (ln & 15)) * kD;
 #pragma unroll
         for (int j = 0; j < kXJ; j++)
 #pragma unroll
@@ -1099,7 +1113,8 @@ int tzh_qkv_fused_launch(hipStream_t st, int num_cus, const float *x, const void
     if ((const char *)x < (const char *)(y + (size_t)t * kFQ) && (const char *)y < (const char *)(x + (size_t)t * kD))
         return tzh_fail(TZH_ERR_INVALID_ARGS, "QKV input and output overlap");
     if (num_cus < 1) return tzh_fail(TZH_ERR_INVALID_ARGS, "bad CU count %d", num_cus);
-    const int panels = (int)((t + kBM - 1) / kBM), rest = panels % num_cus;
+    constexpr int kBMq = 2 * kBM;  // the QKV mode's panels (eight waves)
+    const int panels = (int)((t + kBMq - 1) / kBMq), rest = panels % num_cus;
     TailSplit ts{panels, 1, nullptr, nullptr};
     if (rest > 0)
         for (int parts : {18, 9, 6, 3, 2})
@@ -1109,7 +1124,7 @@ int tzh_qkv_fused_launch(hipStream_t st, int num_cus, const float *x, const void
                 break;
             }
     const int grid = ts.parts > 1 ? (ts.full > 0 ? num_cus : rest * ts.parts) : std::min(panels, num_cus);
-    hipLaunchKernelGGL(mlp_fused_kernel<2>, dim3((unsigned)grid), dim3(kWaves * 64), 0, st, x, (const _Float16 *)pack,
+    hipLaunchKernelGGL(mlp_fused_kernel<2>, dim3((unsigned)grid), dim3(2 * kWaves * 64), 0, st, x, (const _Float16 *)pack,
                        s, b, nullptr, nullptr, nullptr, nullptr, 0.0f, y, (int)t, OProj{}, ts);
     TZH_LAUNCHED("mlp_fused_kernel");
     return TZH_OK;
