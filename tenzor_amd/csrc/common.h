@@ -196,10 +196,16 @@ __device__ __forceinline__ float sum_over_rows(float x) {
 // f32 -> f16 pair x = hi + lo + r for 8 values: hi = f16(x), lo = f16(x - hi),
 // both round-to-nearest-even (x - hi is exact in f32, so lo is x - hi
 // rounded once).  |r| <= 2^-22 |x| for |x| >= 2^-3 (x - hi is then an f16
-// normal) and <= 2^-25 below; valid for |x| < 65504.  On the GPU the low halves come from
-// v_fma_mixlo/mixhi_f16 (fma(-hi, 1, x) formed exactly from the f16 hi and
-// the f32 x, rounded once to f16), one instruction per value instead of a
-// widen, a subtract and a narrow.
+// normal) and <= 2^-25 below; valid for |x| < 65504.  On the GPU the low
+// halves come from v_fma_mixlo/mixhi_f16 (fma(-hi, 1, x) formed exactly from
+// the f16 hi and the f32 x, rounded once to f16), one instruction per value
+// instead of a widen, a subtract and a narrow (the compiler's own selection
+// takes 1.5 and, at the fused kernels' register counts, spills).  The
+// compiler does not count inline asm as a VALU write, so it keeps no wait
+// states between these writes and an MFMA reading the result, which the
+// MFMA needs (two after a VALU write); each asm block therefore ends with
+// "s_nop 1".  (No MFMA reads the outputs' registers as its accumulator
+// input just before: scanned in the generated code.)
 __device__ __forceinline__ uint32_t split_lo_pair(uint32_t hi2, float a, float b) {
 #ifdef TZH_EMULATION
     const half2_t h = __builtin_bit_cast(half2_t, hi2);
@@ -207,8 +213,11 @@ __device__ __forceinline__ uint32_t split_lo_pair(uint32_t hi2, float a, float b
     return __builtin_bit_cast(uint32_t, l);
 #else
     uint32_t d;
-    asm("v_fma_mixlo_f16 %0, -%1, %3, %2 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(hi2), "v"(a), "v"(1.0f));
-    asm("v_fma_mixhi_f16 %0, -%1, %3, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(d) : "v"(hi2), "v"(b), "v"(1.0f));
+    asm("v_fma_mixlo_f16 %0, -%1, %4, %2 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, -%1, %4, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "s_nop 1"
+        : "=&v"(d)
+        : "v"(hi2), "v"(a), "v"(b), "v"(1.0f));
     return d;
 #endif
 }
@@ -220,11 +229,27 @@ __device__ __forceinline__ void split_f32x8(const f32x4_t &a, const f32x4_t &b, 
         h[i] = __builtin_bit_cast(uint32_t, half2_t{(_Float16)a[2 * i], (_Float16)a[2 * i + 1]});
         h[2 + i] = __builtin_bit_cast(uint32_t, half2_t{(_Float16)b[2 * i], (_Float16)b[2 * i + 1]});
     }
+#ifdef TZH_EMULATION
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         l[i] = split_lo_pair(h[i], a[2 * i], a[2 * i + 1]);
         l[2 + i] = split_lo_pair(h[2 + i], b[2 * i], b[2 * i + 1]);
     }
+#else
+    // the four pairs in one block, one trailing s_nop (see split_lo_pair)
+    asm("v_fma_mixlo_f16 %0, -%4, %16, %8 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, -%4, %16, %9 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixlo_f16 %1, -%5, %16, %10 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %1, -%5, %16, %11 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixlo_f16 %2, -%6, %16, %12 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %2, -%6, %16, %13 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixlo_f16 %3, -%7, %16, %14 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %3, -%7, %16, %15 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "s_nop 1"
+        : "=&v"(l[0]), "=&v"(l[1]), "=&v"(l[2]), "=&v"(l[3])
+        : "v"(h[0]), "v"(h[1]), "v"(h[2]), "v"(h[3]), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(b[0]),
+          "v"(b[1]), "v"(b[2]), "v"(b[3]), "v"(1.0f));
+#endif
     typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
     hi = __builtin_bit_cast(half8_t, u32x4v{h[0], h[1], h[2], h[3]});
     lo = __builtin_bit_cast(half8_t, u32x4v{l[0], l[1], l[2], l[3]});
