@@ -236,8 +236,12 @@ __device__ __forceinline__ void split_f32x8(const f32x4_t &a, const f32x4_t &b, 
         l[2 + i] = split_lo_pair(h[2 + i], b[2 * i], b[2 * i + 1]);
     }
 #else
-    // the four pairs in one block, one trailing s_nop (see split_lo_pair)
-    asm("v_fma_mixlo_f16 %0, -%4, %16, %8 op_sel_hi:[1,0,0]\n\t"
+    // the four pairs in one block, one trailing s_nop (see split_lo_pair).
+    // The leading s_nop keeps the first write at least seven wait states
+    // after an MFMA that read the output register as its accumulator input
+    // (the register allocator reuses such a register for l[0] right away).
+    asm("s_nop 2\n\t"
+        "v_fma_mixlo_f16 %0, -%4, %16, %8 op_sel_hi:[1,0,0]\n\t"
         "v_fma_mixhi_f16 %0, -%4, %16, %9 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
         "v_fma_mixlo_f16 %1, -%5, %16, %10 op_sel_hi:[1,0,0]\n\t"
         "v_fma_mixhi_f16 %1, -%5, %16, %11 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
