@@ -204,8 +204,8 @@ __device__ __forceinline__ float sum_over_rows(float x) {
 // compiler does not count inline asm as a VALU write, so it keeps no wait
 // states between these writes and an MFMA reading the result, which the
 // MFMA needs (two after a VALU write); each asm block therefore ends with
-// "s_nop 1".  (No MFMA reads the outputs' registers as its accumulator
-// input just before: scanned in the generated code.)
+// "s_nop 1" (split_f32x8's also starts with one, below).
+// tests/test_asm_hazards.py scans the generated code for both distances.
 __device__ __forceinline__ uint32_t split_lo_pair(uint32_t hi2, float a, float b) {
 #ifdef TZH_EMULATION
     const half2_t h = __builtin_bit_cast(half2_t, hi2);
