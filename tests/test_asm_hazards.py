@@ -7,7 +7,7 @@ a VALU write, so it keeps no wait states between such a write and an MFMA
 that reads the register (gfx950 needs two after a VALU write).  The f16
 hi/lo split's v_fma_mixlo/mixhi (common.h) is inline asm and feeds MFMA
 operands directly in the attention and fused feed-forward kernels; its asm
-blocks end with s_nop 1.  This test compiles those sources to gfx950
+blocks end with s_nop 1.  This test compiles every kernel source to gfx950
 assembly and scans every MFMA's source registers against the inline asm
 writes just before it, so a schedule or helper change cannot bring the
 hazard back unnoticed.  (An 8-wave attention variant read stale P
@@ -26,7 +26,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "tenzor_amd", "csrc")
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
-SOURCES = ["attention.hip", "mlp.hip", "gemm_pipe.hip"]
+SOURCES = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))  # every kernel source
 NEED = 2  # wait states between a VALU write and an MFMA read of the register
 NEED_WAR = 7  # wait states between a 16x16 MFMA's accumulator read and a VALU write of it
 
